@@ -1,0 +1,452 @@
+// fst_accept.hip — greedy and rejection-sampling acceptance for gfx950.
+//
+// Rows: target rows r = s*(k+1)+i (i = 0..k) of n_seq sequences, then (for
+// rejection sampling) draft rows n_seq*(k+1) + s*k + i.  Each row of V logits
+// is split into kChunks chunks processed by one workgroup each.
+//
+// Greedy (src/fst_engine.cpp:6021-6063): argmax per target row with the
+// reference's sequential semantics (first maximum wins, NaN skipped, a NaN at
+// index 0 pins the result to 0), then the longest matching prefix and bonus.
+//
+// Rejection sampling: probabilities in exact 2^-32 fixed point
+// E = floor(exp(l - max) * 2^32) with the shared fst_expf, integer sums, and
+// 128-bit integer comparisons/prefix sums, so the accept decisions and the
+// resampled token are identical to the CPU oracle for identical logits.
+#include "fst_internal.h"
+#include "../../include/fst_exact_math.h"
+
+namespace fst {
+
+constexpr int kChunks = 64;
+typedef unsigned __int128 u128;
+
+struct AccWs {
+    float* part_max;          // [R][kChunks]
+    int* part_idx;            // [R][kChunks]
+    unsigned long long* part_sum;  // [R][kChunks]
+    unsigned long long* part_res;  // [n_seq][kChunks][2] (u128 as lo, hi)
+    unsigned long long* dec;       // [n_seq][8]
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static AccWs carve(void* ws, int n_seq, int k) {
+    const int R = n_seq * (k + 1) + n_seq * k;
+    char* p = (char*)ws;
+    AccWs w;
+    w.part_max = (float*)p; p += align256(sizeof(float) * R * kChunks);
+    w.part_idx = (int*)p; p += align256(sizeof(int) * R * kChunks);
+    w.part_sum = (unsigned long long*)p; p += align256(8ull * R * kChunks);
+    w.part_res = (unsigned long long*)p; p += align256(16ull * n_seq * kChunks);
+    w.dec = (unsigned long long*)p;
+    return w;
+}
+
+size_t accept_ws_bytes(int n_seq, int k, int V) {
+    (void)V;
+    const int R = n_seq * (k + 1) + n_seq * k;
+    return align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
+           align256(8ull * R * kChunks) + align256(16ull * n_seq * kChunks) + align256(64ull * n_seq) +
+           256;
+}
+
+__device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int n_tgt_rows,
+                                                int r, int V) {
+    return r < n_tgt_rows ? target + (size_t)r * V : draft + (size_t)(r - n_tgt_rows) * V;
+}
+
+// (max over non-NaN of x*inv_t, lowest index attaining it) per (row, chunk).
+__global__ __launch_bounds__(256) void acc_stats_kernel(const float* __restrict__ target,
+                                                        const float* __restrict__ draft, int n_tgt_rows,
+                                                        int V, float inv_t, float* __restrict__ part_max,
+                                                        int* __restrict__ part_idx) {
+    const int c = blockIdx.x, r = blockIdx.y;
+    const float* row = row_ptr(target, draft, n_tgt_rows, r, V);
+    const int clen = (V + kChunks - 1) / kChunks;
+    const int b0 = c * clen, b1 = min(V, b0 + clen);
+    float best = 0.0f;
+    int bi = 0x7fffffff;
+    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) {
+        const float l = row[v] * inv_t;
+        if (l != l) continue;
+        if (bi == 0x7fffffff || l > best) { best = l; bi = v; }
+    }
+    __shared__ float sm[256];
+    __shared__ int si[256];
+    sm[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+        if ((int)threadIdx.x < off) {
+            const float ob = sm[threadIdx.x + off];
+            const int oi = si[threadIdx.x + off];
+            const int mi = si[threadIdx.x];
+            if (oi != 0x7fffffff &&
+                (mi == 0x7fffffff || ob > sm[threadIdx.x] || (ob == sm[threadIdx.x] && oi < mi))) {
+                sm[threadIdx.x] = ob;
+                si[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        part_max[(size_t)r * kChunks + c] = sm[0];
+        part_idx[(size_t)r * kChunks + c] = si[0] == 0x7fffffff ? -1 : si[0];
+    }
+}
+
+__device__ void row_reduce(const float* part_max, const int* part_idx, int r, float* mx, int* idx) {
+    float best = 0.0f;
+    int bi = -1;
+    for (int c = 0; c < kChunks; ++c) {
+        const int i = part_idx[(size_t)r * kChunks + c];
+        if (i < 0) continue;
+        const float m = part_max[(size_t)r * kChunks + c];
+        if (bi < 0 || m > best || (m == best && i < bi)) { best = m; bi = i; }
+    }
+    *mx = best;
+    *idx = bi;
+}
+
+// One wave per sequence; lane i (< k+1) resolves target row i.
+__global__ __launch_bounds__(64) void acc_greedy_final_kernel(const float* __restrict__ target, int k,
+                                                              int V, const float* __restrict__ part_max,
+                                                              const int* __restrict__ part_idx,
+                                                              const int32_t* __restrict__ draft,
+                                                              int32_t* __restrict__ n_acc,
+                                                              int32_t* __restrict__ tokens) {
+    const int s = blockIdx.x, lane = threadIdx.x;
+    __shared__ int pred[64];
+    if (lane <= k) {
+        const int r = s * (k + 1) + lane;
+        const float x0 = target[(size_t)r * V];
+        int am;
+        if (x0 != x0) {
+            am = 0;
+        } else {
+            float mx;
+            row_reduce(part_max, part_idx, r, &mx, &am);
+            if (am < 0) am = 0;
+        }
+        pred[lane] = am;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        int n = 0;
+        while (n < k && pred[n] == draft[s * k + n]) ++n;
+        for (int i = 0; i < n; ++i) tokens[s * (k + 1) + i] = draft[s * k + i];
+        tokens[s * (k + 1) + n] = pred[n];
+        for (int i = n + 1; i <= k; ++i) tokens[s * (k + 1) + i] = -1;
+        n_acc[s] = n;
+    }
+}
+
+__device__ __forceinline__ unsigned long long fixed_prob(float x, float inv_t, float mx, int any) {
+    const float l = x * inv_t;
+    if (!any || l != l) return 0ull;
+    if (l == mx) return 4294967296ull;
+    const float d = l - mx;
+    if (d != d) return 0ull;
+    return (unsigned long long)fst_prob_fixed(d);
+}
+
+__device__ __forceinline__ void row_max_any(const float* part_max, const int* part_idx, int r, float* mx,
+                                            int* any) {
+    int idx;
+    row_reduce(part_max, part_idx, r, mx, &idx);
+    *any = idx >= 0;
+}
+
+// Chunk sums of E for every row.
+__global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__ target,
+                                                       const float* __restrict__ draft, int n_tgt_rows,
+                                                       int V, float inv_t,
+                                                       const float* __restrict__ part_max,
+                                                       const int* __restrict__ part_idx,
+                                                       unsigned long long* __restrict__ part_sum) {
+    const int c = blockIdx.x, r = blockIdx.y;
+    __shared__ float s_mx;
+    __shared__ int s_any;
+    if (threadIdx.x == 0) {
+        float mx;
+        int any;
+        row_max_any(part_max, part_idx, r, &mx, &any);
+        s_mx = mx;
+        s_any = any;
+    }
+    __syncthreads();
+    const float mx = s_mx;
+    const int any = s_any;
+    const float* row = row_ptr(target, draft, n_tgt_rows, r, V);
+    const int clen = (V + kChunks - 1) / kChunks;
+    const int b0 = c * clen, b1 = min(V, b0 + clen);
+    unsigned long long acc = 0;
+    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) acc += fixed_prob(row[v], inv_t, mx, any);
+    __shared__ unsigned long long sm[256];
+    sm[threadIdx.x] = acc;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+        if ((int)threadIdx.x < off) sm[threadIdx.x] += sm[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part_sum[(size_t)r * kChunks + c] = sm[0];
+}
+
+// dec layout per sequence: [0] n_acc, [1] sampling target row, [2] mode
+// (0: residual vs draft row, 1: sample from target row), [3] U', [4] Sp, [5] Sq,
+// [6] draft row.
+__global__ __launch_bounds__(64) void acc_decide_kernel(
+    const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
+    float inv_t, const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base,
+    const float* __restrict__ part_max, const int* __restrict__ part_idx,
+    const unsigned long long* __restrict__ part_sum, unsigned long long* __restrict__ dec,
+    int32_t* __restrict__ n_acc, int32_t* __restrict__ tokens) {
+    const int s = blockIdx.x, lane = threadIdx.x;
+    const int n_tgt = n_seq * (k + 1);
+    __shared__ int accept[64];
+    __shared__ unsigned long long Sp_s[64], Sq_s[64];
+    if (lane < k) {
+        const int rt = s * (k + 1) + lane, rd = n_tgt + s * k + lane;
+        unsigned long long Sp = 0, Sq = 0;
+        for (int c = 0; c < kChunks; ++c) {
+            Sp += part_sum[(size_t)rt * kChunks + c];
+            Sq += part_sum[(size_t)rd * kChunks + c];
+        }
+        float mp, mq;
+        int ap, aq;
+        row_max_any(part_max, part_idx, rt, &mp, &ap);
+        row_max_any(part_max, part_idx, rd, &mq, &aq);
+        const int x = draft[s * k + lane];
+        int ok = 0;
+        if (x >= 0 && x < V) {
+            const unsigned long long P = fixed_prob(target[(size_t)rt * V + x], inv_t, mp, ap);
+            const unsigned long long Q = fixed_prob(draftl[(size_t)(rd - n_tgt) * V + x], inv_t, mq, aq);
+            const uint32_t U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 0);
+            const u128 lhs = (u128)U * (u128)Q * (u128)Sp;
+            const u128 rhs = ((u128)P * (u128)Sq) << 24;
+            ok = lhs < rhs;
+        }
+        accept[lane] = ok;
+        Sp_s[lane] = Sp;
+        Sq_s[lane] = Sq;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        int n = 0;
+        while (n < k && accept[n]) ++n;
+        unsigned long long* d = dec + (size_t)s * 8;
+        d[0] = (unsigned long long)n;
+        d[1] = (unsigned long long)(s * (k + 1) + n);
+        d[3] = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)n, 1);
+        if (n < k) {
+            d[2] = 0;
+            d[4] = Sp_s[n];
+            d[5] = Sq_s[n];
+            d[6] = (unsigned long long)(n_tgt + s * k + n);
+        } else {
+            unsigned long long Sp = 0;
+            const int rt = s * (k + 1) + k;
+            for (int c = 0; c < kChunks; ++c) Sp += part_sum[(size_t)rt * kChunks + c];
+            d[2] = 1;
+            d[4] = Sp;
+            d[5] = 0;
+            d[6] = 0;
+        }
+        for (int i = 0; i < n; ++i) tokens[s * (k + 1) + i] = draft[s * k + i];
+        for (int i = n; i <= k; ++i) tokens[s * (k + 1) + i] = -1;
+        n_acc[s] = n;
+    }
+}
+
+__device__ __forceinline__ u128 res_value(const float* trow, const float* drow, int v, float inv_t,
+                                          float mp, int ap, float mq, int aq, unsigned long long Sp,
+                                          unsigned long long Sq, int mode) {
+    const unsigned long long P = fixed_prob(trow[v], inv_t, mp, ap);
+    if (mode) return (u128)P;
+    const unsigned long long Q = fixed_prob(drow[v], inv_t, mq, aq);
+    const u128 a = (u128)P * Sq, b = (u128)Q * Sp;
+    return a > b ? a - b : (u128)0;
+}
+
+struct RowCtx {
+    const float* trow;
+    const float* drow;
+    float mp, mq;
+    int ap, aq, mode;
+    unsigned long long Sp, Sq;
+};
+
+__device__ void load_rowctx(const float* target, const float* draftl, int n_tgt, int V,
+                            const float* part_max, const int* part_idx, const unsigned long long* d,
+                            RowCtx& rc) {
+    const int rt = (int)d[1];
+    rc.mode = (int)d[2];
+    rc.Sp = d[4];
+    rc.Sq = d[5];
+    rc.trow = target + (size_t)rt * V;
+    row_max_any(part_max, part_idx, rt, &rc.mp, &rc.ap);
+    if (rc.mode == 0) {
+        const int rd = (int)d[6];
+        rc.drow = draftl + (size_t)(rd - n_tgt) * V;
+        row_max_any(part_max, part_idx, rd, &rc.mq, &rc.aq);
+    } else {
+        rc.drow = nullptr;
+        rc.mq = 0.0f;
+        rc.aq = 0;
+    }
+}
+
+// Residual (or target) chunk sums for the one sampling row of each sequence.
+__global__ __launch_bounds__(256) void acc_res_chunks_kernel(
+    const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
+    float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
+    const unsigned long long* __restrict__ dec, unsigned long long* __restrict__ part_res) {
+    const int c = blockIdx.x, s = blockIdx.y;
+    __shared__ RowCtx rc;
+    if (threadIdx.x == 0) load_rowctx(target, draftl, n_seq * (k + 1), V, part_max, part_idx,
+                                      dec + (size_t)s * 8, rc);
+    __syncthreads();
+    const int clen = (V + kChunks - 1) / kChunks;
+    const int b0 = c * clen, b1 = min(V, b0 + clen);
+    u128 acc = 0;
+    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256)
+        acc += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+    __shared__ u128 sm[256];
+    sm[threadIdx.x] = acc;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+        if ((int)threadIdx.x < off) sm[threadIdx.x] += sm[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        unsigned long long* o = part_res + ((size_t)s * kChunks + c) * 2;
+        o[0] = (unsigned long long)sm[0];
+        o[1] = (unsigned long long)(sm[0] >> 64);
+    }
+}
+
+// Inverse-CDF pick: first v with prefix > target, where target = (U' * total) >> 24.
+__global__ __launch_bounds__(256) void acc_sample_kernel(
+    const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
+    float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
+    const unsigned long long* __restrict__ part_sum, unsigned long long* __restrict__ dec,
+    const unsigned long long* __restrict__ part_res, int32_t* __restrict__ tokens) {
+    const int s = blockIdx.x, tid = threadIdx.x;
+    __shared__ RowCtx rc;
+    __shared__ u128 s_target, s_before;
+    __shared__ int s_chunk;
+    __shared__ u128 tsum[256];
+    __shared__ int s_tok;
+    unsigned long long* d = dec + (size_t)s * 8;
+    if (tid == 0) {
+        load_rowctx(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
+        const unsigned long long U2 = d[3];
+        u128 tot = 0;
+        u128 cs[kChunks];
+        for (int c = 0; c < kChunks; ++c) {
+            const unsigned long long* o = part_res + ((size_t)s * kChunks + c) * 2;
+            cs[c] = ((u128)o[1] << 64) | (u128)o[0];
+            tot += cs[c];
+        }
+        if (rc.mode == 0 && tot == 0) {
+            // residual is identically zero: sample from the target row instead
+            rc.mode = 1;
+            tot = 0;
+            const int rt = (int)d[1];
+            for (int c = 0; c < kChunks; ++c) {
+                cs[c] = part_sum[(size_t)rt * kChunks + c];
+                tot += cs[c];
+            }
+        }
+        s_chunk = -1;
+        s_tok = 0;
+        if (tot != 0) {
+            const u128 tg = ((u128)U2 * tot) >> 24;
+            u128 run = 0;
+            for (int c = 0; c < kChunks; ++c) {
+                if (run + cs[c] > tg) {
+                    s_chunk = c;
+                    s_before = run;
+                    break;
+                }
+                run += cs[c];
+            }
+            s_target = tg;
+        }
+    }
+    __syncthreads();
+    const int c = s_chunk;
+    if (c >= 0) {
+        const int clen = (V + kChunks - 1) / kChunks;
+        const int b0 = c * clen, b1 = min(V, b0 + clen);
+        // thread tid owns the contiguous run [b0 + tid*per, ...)
+        const int per = (clen + 255) / 256;
+        const int v0 = b0 + tid * per, v1 = min(b1, v0 + per);
+        u128 acc = 0;
+        for (int v = v0; v < v1; ++v)
+            acc += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+        tsum[tid] = acc;
+        __syncthreads();
+        if (tid == 0) {
+            u128 run = s_before;
+            int owner = -1;
+            for (int i = 0; i < 256; ++i) {
+                if (run + tsum[i] > s_target) { owner = i; break; }
+                run += tsum[i];
+            }
+            tsum[0] = run;
+            s_tok = owner;
+        }
+        __syncthreads();
+        if (tid == s_tok) {
+            u128 run = tsum[0];
+            int tok = v1 - 1;
+            for (int v = v0; v < v1; ++v) {
+                run += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq,
+                                 rc.mode);
+                if (run > s_target) { tok = v; break; }
+            }
+            s_tok = tok;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            const int n = (int)d[0];
+            tokens[s * (k + 1) + n] = s_tok >= 0 ? s_tok : 0;
+        }
+    } else if (tid == 0) {
+        const int n = (int)d[0];
+        tokens[s * (k + 1) + n] = 0;
+    }
+}
+
+void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k, int V,
+                          const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* ws) {
+    AccWs w = carve(ws, n_seq, k);
+    const int R = n_seq * (k + 1);
+    hipLaunchKernelGGL(acc_stats_kernel, dim3(kChunks, R), dim3(256), 0, st, target, nullptr, R, V, 1.0f,
+                       w.part_max, w.part_idx);
+    hipLaunchKernelGGL(acc_greedy_final_kernel, dim3(n_seq), dim3(64), 0, st, target, k, V, w.part_max,
+                       w.part_idx, draft, n_acc, tokens);
+}
+
+void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
+                              int n_seq, int k, int V, const int32_t* draft, float inv_t,
+                              uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,
+                              void* ws) {
+    AccWs w = carve(ws, n_seq, k);
+    const int n_tgt = n_seq * (k + 1);
+    const int R = n_tgt + n_seq * k;
+    hipLaunchKernelGGL(acc_stats_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
+                       inv_t, w.part_max, w.part_idx);
+    hipLaunchKernelGGL(acc_sums_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
+                       inv_t, w.part_max, w.part_idx, w.part_sum);
+    hipLaunchKernelGGL(acc_decide_kernel, dim3(n_seq), dim3(64), 0, st, target, draft_logits, n_seq, k, V,
+                       inv_t, draft, seed, seq_base, w.part_max, w.part_idx, w.part_sum, w.dec, n_acc,
+                       tokens);
+    hipLaunchKernelGGL(acc_res_chunks_kernel, dim3(kChunks, n_seq), dim3(256), 0, st, target, draft_logits,
+                       n_seq, k, V, inv_t, w.part_max, w.part_idx, w.dec, w.part_res);
+    hipLaunchKernelGGL(acc_sample_kernel, dim3(n_seq), dim3(256), 0, st, target, draft_logits, n_seq, k, V,
+                       inv_t, w.part_max, w.part_idx, w.part_sum, w.dec, w.part_res, tokens);
+}
+
+}  // namespace fst

@@ -1,0 +1,670 @@
+// fst_api.cpp — host runtime behind include/fst_hip.h.
+//
+// A context owns one HIP stream, the resident expert banks of every layer,
+// the router weights, and device scratch sized for max_tokens.  Every MoE call
+// is a fixed chain of launches on that stream (router -> bucket -> prep ->
+// gate/up -> prep -> down -> combine) with no host synchronisation inside;
+// host-pointer entry points add one H2D copy, one D2H copy and one sync.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/fst_exact_math.h"
+#include "../../include/fst_hip.h"
+#include "fst_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define FST_HIP_TRY(expr)                                                                         \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            return fail(FST_EHIP, std::string(#expr " failed: ") + hipGetErrorString(e_));       \
+    } while (0)
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace
+
+struct fst_ctx {
+    fst_config cfg{};
+    hipStream_t st = nullptr;
+    fst::Geometry geo{};
+    size_t expert_bytes = 0, expert_stride = 0;
+    uint8_t* bank = nullptr;                 // [L][E+1] experts
+    std::vector<std::vector<char>> uploaded; // [L][E+1]
+    std::vector<int> n_uploaded;             // [L]
+    uint16_t* router = nullptr;              // [L][E][hd]
+    float* bias = nullptr;                   // [L][E]
+    std::vector<char> has_router, has_bias;
+    std::vector<int32_t*> hash;              // [L] (lid < n_hash_layers)
+    fst::Scratch s{};
+    std::vector<void*> allocs;
+    // acceptance staging (grown on demand)
+    void* acc_ws = nullptr;
+    size_t acc_ws_cap = 0;
+    float* acc_logits = nullptr;
+    size_t acc_logits_cap = 0;
+    int32_t* acc_io = nullptr;
+    size_t acc_io_cap = 0;
+    // profiling
+    bool profiling = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<const char*> ev_names;
+    int n_ev = 0;
+    fst_timings last{};
+
+    ~fst_ctx() {
+        if (st) hipStreamSynchronize(st);
+        for (void* p : allocs) hipFree(p);
+        for (int32_t* p : hash)
+            if (p) hipFree(p);
+        if (acc_ws) hipFree(acc_ws);
+        if (acc_logits) hipFree(acc_logits);
+        if (acc_io) hipFree(acc_io);
+        for (hipEvent_t e : ev) hipEventDestroy(e);
+        if (st) hipStreamDestroy(st);
+    }
+
+    template <typename T>
+    int dalloc(T** p, size_t count) {
+        void* q = nullptr;
+        size_t bytes = std::max<size_t>(256, count * sizeof(T));
+        hipError_t e = hipMalloc(&q, bytes);
+        if (e != hipSuccess)
+            return fail(FST_ENOMEM, "hipMalloc(" + std::to_string(bytes) + ") failed: " + hipGetErrorString(e));
+        allocs.push_back(q);
+        *p = static_cast<T*>(q);
+        return FST_OK;
+    }
+
+    fst::LayerView layer(int lid) const {
+        fst::LayerView L;
+        L.bank = bank + (size_t)lid * (cfg.n_experts + 1) * expert_stride;
+        L.expert_stride = expert_stride;
+        L.router_nk = router + (size_t)lid * cfg.n_experts * cfg.hidden_dim;
+        L.router_bias = has_bias[lid] ? bias + (size_t)lid * cfg.n_experts : nullptr;
+        L.hash = hash[lid];
+        return L;
+    }
+
+    // profiling marks: mark(name) after a launch closes the interval opened by the previous mark
+    void mark_begin() {
+        n_ev = 0;
+        if (!profiling) return;
+        hipEventRecord(ev[0], st);
+        n_ev = 1;
+    }
+    void mark(const char* name) {
+        if (!profiling || n_ev >= (int)ev.size()) return;
+        hipEventRecord(ev[n_ev], st);
+        ev_names[n_ev] = name;
+        ++n_ev;
+    }
+    void collect() {
+        last.n = 0;
+        if (!profiling || n_ev < 2) return;
+        hipEventSynchronize(ev[n_ev - 1]);
+        for (int i = 1; i < n_ev && last.n < 16; ++i) {
+            float ms = 0.0f;
+            hipEventElapsedTime(&ms, ev[i - 1], ev[i]);
+            last.name[last.n] = ev_names[i];
+            last.ms[last.n] = ms;
+            ++last.n;
+        }
+    }
+};
+
+extern "C" {
+
+void fst_config_default(fst_config* c) {
+    if (!c) return;
+    std::memset(c, 0, sizeof(*c));
+    c->hidden_dim = 4096;
+    c->inter_dim = 2048;
+    c->n_experts = 256;
+    c->top_k = 6;
+    c->n_layers = 1;
+    c->max_tokens = 64;
+    c->codec = FST_CODEC_Q4K;
+    c->has_shared = 1;
+    c->score_func = FST_SCORE_SIGMOID;
+    c->route_scale = 1.0f;
+    c->round_logits_bf16 = 0;
+    c->n_hash_layers = 0;
+    c->vocab_size = 129280;
+    c->swiglu_limit = 0.0f;
+    c->device = 0;
+}
+
+const char* fst_last_error(void) { return g_err.c_str(); }
+int fst_abi_version(void) { return FST_ABI_VERSION; }
+
+size_t fst_expert_bytes(const fst_config* c) {
+    if (!c) return 0;
+    const size_t w = (size_t)c->hidden_dim * c->inter_dim;
+    if (c->codec == FST_CODEC_Q4K) return 3 * (w / 256) * 144;
+    if (c->codec == FST_CODEC_MXFP4) return 3 * (w / 32) * 17;
+    return 0;
+}
+
+int fst_create(const fst_config* cfg, fst_ctx** out) {
+    if (!cfg || !out) return fail(FST_EINVAL, "fst_create: null argument");
+    *out = nullptr;
+    const fst_config& c = *cfg;
+    if (c.codec != FST_CODEC_Q4K)
+        return fail(FST_EINVAL, "fst_create: only the Q4_K codec has a fused FFN path");
+    if (c.hidden_dim <= 0 || c.hidden_dim % 512 || c.inter_dim <= 0 || c.inter_dim % 256)
+        return fail(FST_EINVAL, "fst_create: hidden_dim must be a multiple of 512, inter_dim of 256");
+    if (c.hidden_dim % 64 || c.inter_dim % 64)
+        return fail(FST_EINVAL, "fst_create: dims must be multiples of 64");
+    if (c.n_experts <= 0 || c.n_experts > 1024)
+        return fail(FST_EINVAL, "fst_create: n_experts must be in [1, 1024]");
+    if (c.top_k <= 0 || c.top_k > fst::kMaxTopK || c.top_k > c.n_experts)
+        return fail(FST_EINVAL, "fst_create: top_k must be in [1, min(16, n_experts)]");
+    if (c.max_tokens <= 0 || c.max_tokens > fst::kMaxTokens)
+        return fail(FST_EINVAL, "fst_create: max_tokens must be in [1, 64]");
+    if (c.n_layers <= 0) return fail(FST_EINVAL, "fst_create: n_layers must be >= 1");
+    if (c.score_func != FST_SCORE_SIGMOID && c.score_func != FST_SCORE_SQRTSOFTPLUS)
+        return fail(FST_EINVAL, "fst_create: unknown score_func");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+        return fail(FST_ENODEV, "fst_create: no HIP device");
+    if (c.device < 0 || c.device >= ndev) return fail(FST_ENODEV, "fst_create: device ordinal out of range");
+    FST_HIP_TRY(hipSetDevice(c.device));
+    hipDeviceProp_t prop;
+    FST_HIP_TRY(hipGetDeviceProperties(&prop, c.device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(FST_ENODEV, std::string("fst_create: device is ") + prop.gcnArchName + ", need gfx950");
+
+    fst_ctx* x = new fst_ctx();
+    x->cfg = c;
+    int rc = FST_OK;
+    auto bail = [&](int code) {
+        delete x;
+        return code;
+    };
+    if (hipStreamCreateWithFlags(&x->st, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(FST_EHIP, "hipStreamCreate failed"));
+    x->geo.hd = c.hidden_dim;
+    x->geo.inter = c.inter_dim;
+    x->geo.E = c.n_experts;
+    x->geo.tk = c.top_k;
+    x->geo.codec = c.codec;
+    x->geo.score_func = c.score_func;
+    x->geo.round_logits_bf16 = c.round_logits_bf16;
+    x->geo.route_scale = c.route_scale;
+    x->geo.swiglu_limit = c.swiglu_limit;
+    x->geo.vocab = c.vocab_size;
+    x->expert_bytes = fst_expert_bytes(&c);
+    x->expert_stride = align_up(x->expert_bytes, 4096);
+    const int L = c.n_layers, E = c.n_experts, hd = c.hidden_dim, inter = c.inter_dim;
+    if ((rc = x->dalloc(&x->bank, (size_t)L * (E + 1) * x->expert_stride))) return bail(rc);
+    if ((rc = x->dalloc(&x->router, (size_t)L * E * hd))) return bail(rc);
+    if ((rc = x->dalloc(&x->bias, (size_t)L * E))) return bail(rc);
+    x->uploaded.assign(L, std::vector<char>(E + 1, 0));
+    x->n_uploaded.assign(L, 0);
+    x->has_router.assign(L, 0);
+    x->has_bias.assign(L, 0);
+    x->hash.assign(L, nullptr);
+
+    fst::Scratch& s = x->s;
+    const int T = c.max_tokens, tk = c.top_k;
+    s.max_tokens = T;
+    s.max_pairs = T * tk + T;
+    s.max_slots = std::min(E, T * tk) + 1;
+    const int P = s.max_pairs, S = s.max_slots;
+    if ((rc = x->dalloc(&s.h, (size_t)T * hd)) || (rc = x->dalloc(&s.out, (size_t)T * hd)) ||
+        (rc = x->dalloc(&s.out_routed, (size_t)T * hd)) || (rc = x->dalloc(&s.out_shared, (size_t)T * hd)) ||
+        (rc = x->dalloc(&s.ids, T)) || (rc = x->dalloc(&s.logits, (size_t)T * E)) ||
+        (rc = x->dalloc(&s.eids, (size_t)T * tk)) || (rc = x->dalloc(&s.wts, (size_t)T * tk)) ||
+        (rc = x->dalloc(&s.meta, fst::META_WORDS)) || (rc = x->dalloc(&s.slot_eid, S)) ||
+        (rc = x->dalloc(&s.slot_M, S)) || (rc = x->dalloc(&s.slot_off, S)) ||
+        (rc = x->dalloc(&s.pair_tok, P)) || (rc = x->dalloc(&s.pair_of, (size_t)T * tk)) ||
+        (rc = x->dalloc(&s.pair_shared, T)) || (rc = x->dalloc(&s.x16p, (size_t)T * hd)) ||
+        (rc = x->dalloc(&s.sxp, (size_t)T * (hd / 256) * 4)) || (rc = x->dalloc(&s.xs, T)) ||
+        (rc = x->dalloc(&s.act, (size_t)P * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
+        (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
+        (rc = x->dalloc(&s.y, (size_t)P * hd)))
+        return bail(rc);
+    if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess)
+        return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));
+    x->ev.resize(17);
+    x->ev_names.assign(17, "");
+    for (auto& e : x->ev)
+        if (hipEventCreate(&e) != hipSuccess) return bail(fail(FST_EHIP, "hipEventCreate failed"));
+    if (hipStreamSynchronize(x->st) != hipSuccess) return bail(fail(FST_EHIP, "hipStreamSynchronize failed"));
+    *out = x;
+    return FST_OK;
+}
+
+void fst_destroy(fst_ctx* ctx) { delete ctx; }
+void* fst_stream(fst_ctx* ctx) { return ctx ? (void*)ctx->st : nullptr; }
+
+int fst_sync(fst_ctx* ctx) {
+    if (!ctx) return fail(FST_EINVAL, "fst_sync: null context");
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
+}
+
+int fst_set_profiling(fst_ctx* ctx, int on) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    ctx->profiling = on != 0;
+    return FST_OK;
+}
+
+int fst_last_timings(fst_ctx* ctx, fst_timings* out) {
+    if (!ctx || !out) return fail(FST_EINVAL, "null argument");
+    ctx->collect();
+    *out = ctx->last;
+    return FST_OK;
+}
+
+int fst_last_active_experts(fst_ctx* ctx, int* n) {
+    if (!ctx || !n) return fail(FST_EINVAL, "null argument");
+    int m[fst::META_WORDS];
+    FST_HIP_TRY(hipMemcpyAsync(m, ctx->s.meta, sizeof(m), hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    *n = m[fst::META_N_ROUTED];
+    return FST_OK;
+}
+
+void* fst_device_alloc(fst_ctx* ctx, size_t bytes) {
+    if (!ctx) {
+        fail(FST_EINVAL, "null context");
+        return nullptr;
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, std::max<size_t>(bytes, 256)) != hipSuccess) {
+        fail(FST_ENOMEM, "hipMalloc(" + std::to_string(bytes) + ") failed");
+        return nullptr;
+    }
+    return p;
+}
+
+void fst_device_free(fst_ctx* ctx, void* p) {
+    if (ctx) hipStreamSynchronize(ctx->st);
+    if (p) hipFree(p);
+}
+
+int fst_copy_to_device(fst_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || !dst || !src) return fail(FST_EINVAL, "null argument");
+    FST_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
+}
+
+int fst_copy_to_host(fst_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || !dst || !src) return fail(FST_EINVAL, "null argument");
+    FST_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
+}
+
+// ------------------------------------------------------------- residency
+
+static int check_lid(fst_ctx* ctx, int lid) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (lid < 0 || lid >= ctx->cfg.n_layers) return fail(FST_EINVAL, "layer id out of range");
+    return FST_OK;
+}
+
+int fst_upload_expert(fst_ctx* ctx, int lid, int eid, const void* packed, size_t bytes) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    if (eid < 0 || eid > ctx->cfg.n_experts) return fail(FST_EINVAL, "expert id out of range");
+    if (eid == ctx->cfg.n_experts && !ctx->cfg.has_shared)
+        return fail(FST_EINVAL, "config has no shared expert");
+    if (!packed || bytes != ctx->expert_bytes)
+        return fail(FST_EINVAL, "expert size mismatch: got " + std::to_string(bytes) + ", expected " +
+                                    std::to_string(ctx->expert_bytes));
+    uint8_t* dst = ctx->bank + ((size_t)lid * (ctx->cfg.n_experts + 1) + eid) * ctx->expert_stride;
+    FST_HIP_TRY(hipMemcpyAsync(dst, packed, bytes, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    if (!ctx->uploaded[lid][eid]) {
+        ctx->uploaded[lid][eid] = 1;
+        ctx->n_uploaded[lid]++;
+    }
+    return FST_OK;
+}
+
+void* fst_expert_device_ptr(fst_ctx* ctx, int lid, int eid) {
+    if (!ctx || lid < 0 || lid >= ctx->cfg.n_layers || eid < 0 || eid > ctx->cfg.n_experts) return nullptr;
+    return ctx->bank + ((size_t)lid * (ctx->cfg.n_experts + 1) + eid) * ctx->expert_stride;
+}
+
+static int upload_router_common(fst_ctx* ctx, int lid, const std::vector<uint16_t>& nk, const float* bias) {
+    const int E = ctx->cfg.n_experts, hd = ctx->cfg.hidden_dim;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->router + (size_t)lid * E * hd, nk.data(), nk.size() * 2,
+                               hipMemcpyHostToDevice, ctx->st));
+    if (bias)
+        FST_HIP_TRY(hipMemcpyAsync(ctx->bias + (size_t)lid * E, bias, sizeof(float) * E, hipMemcpyHostToDevice,
+                                   ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    ctx->has_router[lid] = 1;
+    ctx->has_bias[lid] = bias != nullptr;
+    return FST_OK;
+}
+
+int fst_upload_router_bf16(fst_ctx* ctx, int lid, const uint16_t* w_kn, const float* bias) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    if (!w_kn) return fail(FST_EINVAL, "null router weights");
+    const int E = ctx->cfg.n_experts, hd = ctx->cfg.hidden_dim;
+    std::vector<uint16_t> nk((size_t)E * hd);
+    for (int k = 0; k < hd; ++k)
+        for (int e = 0; e < E; ++e) nk[(size_t)e * hd + k] = w_kn[(size_t)k * E + e];
+    return upload_router_common(ctx, lid, nk, bias);
+}
+
+int fst_upload_router_f32(fst_ctx* ctx, int lid, const float* w_kn, const float* bias) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    if (!w_kn) return fail(FST_EINVAL, "null router weights");
+    const int E = ctx->cfg.n_experts, hd = ctx->cfg.hidden_dim;
+    std::vector<uint16_t> nk((size_t)E * hd);
+    for (int k = 0; k < hd; ++k)
+        for (int e = 0; e < E; ++e) nk[(size_t)e * hd + k] = fst_f32_to_bf16(w_kn[(size_t)k * E + e]);
+    return upload_router_common(ctx, lid, nk, bias);
+}
+
+int fst_upload_hash_table(fst_ctx* ctx, int lid, const int32_t* tid2eid) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    if (lid >= ctx->cfg.n_hash_layers) return fail(FST_EINVAL, "layer is not a hash-routing layer");
+    if (!tid2eid || ctx->cfg.vocab_size <= 0) return fail(FST_EINVAL, "null table or vocab_size <= 0");
+    const size_t n = (size_t)ctx->cfg.vocab_size * ctx->cfg.top_k;
+    for (size_t i = 0; i < n; ++i)
+        if (tid2eid[i] < 0 || tid2eid[i] >= ctx->cfg.n_experts)
+            return fail(FST_EINVAL, "hash table entry out of range at " + std::to_string(i));
+    if (!ctx->hash[lid]) {
+        void* p = nullptr;
+        if (hipMalloc(&p, n * sizeof(int32_t)) != hipSuccess) return fail(FST_ENOMEM, "hipMalloc(hash) failed");
+        ctx->hash[lid] = (int32_t*)p;
+    }
+    FST_HIP_TRY(hipMemcpyAsync(ctx->hash[lid], tid2eid, n * sizeof(int32_t), hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
+}
+
+// ------------------------------------------------------------ MoE chain
+
+static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_ids, int do_router,
+                   int32_t* d_eids, float* d_wts, int tk, int use_routed, int use_shared, uint16_t* d_out,
+                   uint16_t* d_out_routed, uint16_t* d_out_shared) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    const fst_config& c = ctx->cfg;
+    if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    if (use_shared && !c.has_shared) return fail(FST_EINVAL, "config has no shared expert");
+    if (use_routed && ctx->n_uploaded[lid] - (ctx->uploaded[lid][c.n_experts] ? 1 : 0) < c.n_experts)
+        return fail(FST_ENOTREADY, "not all routed experts of layer " + std::to_string(lid) + " are uploaded");
+    if (use_shared && !ctx->uploaded[lid][c.n_experts])
+        return fail(FST_ENOTREADY, "shared expert of layer " + std::to_string(lid) + " is not uploaded");
+    if (do_router && !ctx->has_router[lid])
+        return fail(FST_ENOTREADY, "router of layer " + std::to_string(lid) + " is not uploaded");
+    if (tk < 0 || tk > c.top_k) return fail(FST_EINVAL, "tk must be in [0, top_k]");
+    fst::Geometry g = ctx->geo;
+    g.tk = use_routed ? tk : 0;
+    fst::LayerView L = ctx->layer(lid);
+    const int use_hash = do_router && lid < c.n_hash_layers && L.hash && d_ids;
+    const int ngrp = (M + 15) / 16 > 2 ? 4 : (M + 15) / 16;
+    hipStream_t st = ctx->st;
+    ctx->mark_begin();
+    if (do_router) {
+        fst::launch_router_logits(st, g, L, d_h, M, ctx->s.logits);
+        ctx->mark("router_logits");
+    }
+    fst::launch_route_bucket(st, g, L, M, ctx->s.logits, d_ids, use_hash, do_router, use_shared, d_eids, d_wts,
+                             ctx->s);
+    ctx->mark("route_bucket");
+    fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
+    ctx->mark("prep_x");
+    fst::launch_q4k_gate_up(st, g, L, ngrp, ctx->s);
+    ctx->mark("q4k_gate_up");
+    fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p, ctx->s.sx2p,
+                         ctx->s.xs2);
+    ctx->mark("prep_act");
+    fst::launch_q4k_down(st, g, L, ngrp, ctx->s);
+    ctx->mark("q4k_down");
+    fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared);
+    ctx->mark("combine");
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+static int check_meta_error(fst_ctx* ctx) {
+    int m[fst::META_WORDS];
+    FST_HIP_TRY(hipMemcpyAsync(m, ctx->s.meta, sizeof(m), hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    if (m[fst::META_ERROR] & 1) return fail(FST_EINVAL, "expert id out of range in routing");
+    if (m[fst::META_ERROR] & 2) return fail(FST_EINVAL, "input id out of vocabulary range for hash routing");
+    return FST_OK;
+}
+
+int fst_moe_layer_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_input_ids,
+                      uint16_t* d_out, int32_t* d_eids, float* d_wts) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!d_h || !d_out) return fail(FST_EINVAL, "null device buffer");
+    int32_t* e = d_eids ? d_eids : ctx->s.eids;
+    float* w = d_wts ? d_wts : ctx->s.wts;
+    return run_moe(ctx, lid, d_h, M, d_input_ids, 1, e, w, ctx->cfg.top_k, 1, ctx->cfg.has_shared, d_out,
+                   nullptr, nullptr);
+}
+
+int fst_moe_ffn_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_eids,
+                    const float* d_wts, int use_shared, uint16_t* d_out, uint16_t* d_out_routed,
+                    uint16_t* d_out_shared) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!d_h || !d_eids || !d_wts) return fail(FST_EINVAL, "null device buffer");
+    return run_moe(ctx, lid, d_h, M, nullptr, 0, const_cast<int32_t*>(d_eids), const_cast<float*>(d_wts),
+                   ctx->cfg.top_k, 1, use_shared, d_out, d_out_routed, d_out_shared);
+}
+
+int fst_moe_layer(fst_ctx* ctx, int lid, const uint16_t* h, int M, const int32_t* input_ids, uint16_t* out,
+                  int32_t* eids, float* wts) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!h || !out) return fail(FST_EINVAL, "null host buffer");
+    if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    const int hd = ctx->cfg.hidden_dim, tk = ctx->cfg.top_k;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->s.h, h, (size_t)M * hd * 2, hipMemcpyHostToDevice, ctx->st));
+    if (input_ids) FST_HIP_TRY(hipMemcpyAsync(ctx->s.ids, input_ids, M * 4, hipMemcpyHostToDevice, ctx->st));
+    if (int rc = run_moe(ctx, lid, ctx->s.h, M, input_ids ? ctx->s.ids : nullptr, 1, ctx->s.eids, ctx->s.wts,
+                         tk, 1, ctx->cfg.has_shared, ctx->s.out, nullptr, nullptr))
+        return rc;
+    FST_HIP_TRY(hipMemcpyAsync(out, ctx->s.out, (size_t)M * hd * 2, hipMemcpyDeviceToHost, ctx->st));
+    if (eids) FST_HIP_TRY(hipMemcpyAsync(eids, ctx->s.eids, (size_t)M * tk * 4, hipMemcpyDeviceToHost, ctx->st));
+    if (wts) FST_HIP_TRY(hipMemcpyAsync(wts, ctx->s.wts, (size_t)M * tk * 4, hipMemcpyDeviceToHost, ctx->st));
+    return check_meta_error(ctx);
+}
+
+int fst_router(fst_ctx* ctx, int lid, const uint16_t* h, int M, const int32_t* input_ids, int32_t* eids,
+               float* wts) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    if (!h || !eids || !wts) return fail(FST_EINVAL, "null host buffer");
+    const fst_config& c = ctx->cfg;
+    if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    if (!ctx->has_router[lid]) return fail(FST_ENOTREADY, "router not uploaded");
+    fst::LayerView L = ctx->layer(lid);
+    const int use_hash = lid < c.n_hash_layers && L.hash && input_ids;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->s.h, h, (size_t)M * c.hidden_dim * 2, hipMemcpyHostToDevice, ctx->st));
+    if (input_ids) FST_HIP_TRY(hipMemcpyAsync(ctx->s.ids, input_ids, M * 4, hipMemcpyHostToDevice, ctx->st));
+    ctx->mark_begin();
+    fst::launch_router_logits(ctx->st, ctx->geo, L, ctx->s.h, M, ctx->s.logits);
+    ctx->mark("router_logits");
+    fst::launch_route_bucket(ctx->st, ctx->geo, L, M, ctx->s.logits, input_ids ? ctx->s.ids : nullptr, use_hash,
+                             1, 0, ctx->s.eids, ctx->s.wts, ctx->s);
+    ctx->mark("route_bucket");
+    FST_HIP_TRY(hipGetLastError());
+    FST_HIP_TRY(hipMemcpyAsync(eids, ctx->s.eids, (size_t)M * c.top_k * 4, hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipMemcpyAsync(wts, ctx->s.wts, (size_t)M * c.top_k * 4, hipMemcpyDeviceToHost, ctx->st));
+    return check_meta_error(ctx);
+}
+
+static int host_ffn(fst_ctx* ctx, int lid, const uint16_t* h, uint16_t* out, int M, const int32_t* eids, int tk,
+                    const float* wts, int routed, int shared) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!h || !out) return fail(FST_EINVAL, "null host buffer");
+    const fst_config& c = ctx->cfg;
+    if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    if (routed) {
+        if (!eids || !wts) return fail(FST_EINVAL, "null eids/wts");
+        if (tk <= 0 || tk > c.top_k) return fail(FST_EINVAL, "tk must be in [1, top_k]");
+        for (int i = 0; i < M * tk; ++i)
+            if (eids[i] < 0 || eids[i] >= c.n_experts)
+                return fail(FST_EINVAL, "expert id out of range at " + std::to_string(i));
+    }
+    const int hd = c.hidden_dim;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->s.h, h, (size_t)M * hd * 2, hipMemcpyHostToDevice, ctx->st));
+    if (routed) {
+        FST_HIP_TRY(hipMemcpyAsync(ctx->s.eids, eids, (size_t)M * tk * 4, hipMemcpyHostToDevice, ctx->st));
+        FST_HIP_TRY(hipMemcpyAsync(ctx->s.wts, wts, (size_t)M * tk * 4, hipMemcpyHostToDevice, ctx->st));
+    }
+    if (int rc = run_moe(ctx, lid, ctx->s.h, M, nullptr, 0, ctx->s.eids, ctx->s.wts, routed ? tk : 0, routed,
+                         shared, ctx->s.out, nullptr, nullptr))
+        return rc;
+    FST_HIP_TRY(hipMemcpyAsync(out, ctx->s.out, (size_t)M * hd * 2, hipMemcpyDeviceToHost, ctx->st));
+    return check_meta_error(ctx);
+}
+
+int fst_expert_ffn(fst_ctx* ctx, int lid, const uint16_t* h, uint16_t* out, int M, const int32_t* eids, int tk,
+                   const float* wts) {
+    return host_ffn(ctx, lid, h, out, M, eids, tk, wts, 1, 0);
+}
+
+int fst_shared_expert(fst_ctx* ctx, int lid, const uint16_t* h, uint16_t* out, int M) {
+    return host_ffn(ctx, lid, h, out, M, nullptr, 0, nullptr, 0, 1);
+}
+
+// ------------------------------------------------------------ acceptance
+
+static int grow(void** p, size_t* cap, size_t need) {
+    if (*cap >= need) return FST_OK;
+    if (*p) hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    if (hipMalloc(p, need) != hipSuccess) return fail(FST_ENOMEM, "hipMalloc(acceptance staging) failed");
+    *cap = need;
+    return FST_OK;
+}
+
+static int check_accept_args(int n_seq, int k, int V) {
+    if (n_seq <= 0 || n_seq > 4096) return fail(FST_EINVAL, "n_seq must be in [1, 4096]");
+    if (k < 0 || k > 63) return fail(FST_EINVAL, "k must be in [0, 63]");
+    if (V <= 0) return fail(FST_EINVAL, "V must be positive");
+    return FST_OK;
+}
+
+int fst_accept_greedy_dev(fst_ctx* ctx, const float* d_target, int n_seq, int k, int V, const int32_t* d_draft,
+                          int32_t* d_n_acc, int32_t* d_tokens) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (int rc = check_accept_args(n_seq, k, V)) return rc;
+    if (int rc = grow(&ctx->acc_ws, &ctx->acc_ws_cap, fst::accept_ws_bytes(n_seq, k, V))) return rc;
+    ctx->mark_begin();
+    fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens, ctx->acc_ws);
+    ctx->mark("accept_greedy");
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* d_draft_logits, int n_seq, int k,
+                              int V, const int32_t* d_draft, float temperature, uint64_t seed, uint64_t seq_base,
+                              int32_t* d_n_acc, int32_t* d_tokens) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (int rc = check_accept_args(n_seq, k, V)) return rc;
+    if (!(temperature > 0.0f)) return fail(FST_EINVAL, "temperature must be > 0");
+    if (int rc = grow(&ctx->acc_ws, &ctx->acc_ws_cap, fst::accept_ws_bytes(n_seq, k, V))) return rc;
+    const float inv_t = 1.0f / temperature;
+    ctx->mark_begin();
+    fst::launch_accept_stochastic(ctx->st, d_target, d_draft_logits, n_seq, k, V, d_draft, inv_t, seed, seq_base,
+                                  d_n_acc, d_tokens, ctx->acc_ws);
+    ctx->mark("accept_stochastic");
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+static int accept_host(fst_ctx* ctx, const float* target, const float* draft_logits, int n_seq, int k, int V,
+                       const int32_t* draft, float temperature, uint64_t seed, uint64_t seq_base, int32_t* n_acc,
+                       int32_t* tokens, int stochastic) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (int rc = check_accept_args(n_seq, k, V)) return rc;
+    if (!target || !n_acc || !tokens || (k > 0 && !draft) || (stochastic && k > 0 && !draft_logits))
+        return fail(FST_EINVAL, "null host buffer");
+    for (int i = 0; i < n_seq * k; ++i)
+        if (draft[i] < 0 || draft[i] >= V) return fail(FST_EINVAL, "draft token out of range");
+    const size_t nt = (size_t)n_seq * (k + 1) * V, nd = stochastic ? (size_t)n_seq * k * V : 0;
+    if (int rc = grow((void**)&ctx->acc_logits, &ctx->acc_logits_cap, (nt + nd) * sizeof(float) + 256)) return rc;
+    const size_t io = (size_t)n_seq * k + n_seq + (size_t)n_seq * (k + 1);
+    if (int rc = grow((void**)&ctx->acc_io, &ctx->acc_io_cap, io * 4 + 256)) return rc;
+    int32_t* d_draft = ctx->acc_io;
+    int32_t* d_nacc = d_draft + (size_t)n_seq * k;
+    int32_t* d_tok = d_nacc + n_seq;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->acc_logits, target, nt * 4, hipMemcpyHostToDevice, ctx->st));
+    if (nd)
+        FST_HIP_TRY(hipMemcpyAsync(ctx->acc_logits + nt, draft_logits, nd * 4, hipMemcpyHostToDevice, ctx->st));
+    if (k > 0) FST_HIP_TRY(hipMemcpyAsync(d_draft, draft, (size_t)n_seq * k * 4, hipMemcpyHostToDevice, ctx->st));
+    int rc = stochastic ? fst_accept_stochastic_dev(ctx, ctx->acc_logits, ctx->acc_logits + nt, n_seq, k, V, d_draft,
+                                                    temperature, seed, seq_base, d_nacc, d_tok)
+                        : fst_accept_greedy_dev(ctx, ctx->acc_logits, n_seq, k, V, d_draft, d_nacc, d_tok);
+    if (rc) return rc;
+    FST_HIP_TRY(hipMemcpyAsync(n_acc, d_nacc, n_seq * 4, hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipMemcpyAsync(tokens, d_tok, (size_t)n_seq * (k + 1) * 4, hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
+}
+
+int fst_accept_greedy(fst_ctx* ctx, const float* target, int n_seq, int k, int V, const int32_t* draft,
+                      int32_t* n_acc, int32_t* tokens) {
+    return accept_host(ctx, target, nullptr, n_seq, k, V, draft, 1.0f, 0, 0, n_acc, tokens, 0);
+}
+
+int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_logits, int n_seq, int k, int V,
+                          const int32_t* draft, float temperature, uint64_t seed, uint64_t seq_base, int32_t* n_acc,
+                          int32_t* tokens) {
+    if (!(temperature > 0.0f)) return fail(FST_EINVAL, "temperature must be > 0");
+    return accept_host(ctx, target, draft_logits, n_seq, k, V, draft, temperature, seed, seq_base, n_acc, tokens, 1);
+}
+
+// ------------------------------------------------------------ dequant
+
+int fst_dequant(fst_ctx* ctx, int codec, const void* blocks, size_t nblocks, float* out_f32, uint16_t* out_bf16) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (codec != FST_CODEC_Q4K && codec != FST_CODEC_MXFP4) return fail(FST_EINVAL, "unknown codec");
+    if (!blocks || nblocks == 0) return fail(FST_EINVAL, "no blocks");
+    if (nblocks > (1u << 24)) return fail(FST_EINVAL, "too many blocks for one call");
+    const size_t bb = codec == FST_CODEC_Q4K ? 144 : 17, be = codec == FST_CODEC_Q4K ? 256 : 32;
+    void *din = nullptr, *df = nullptr, *db = nullptr;
+    auto cleanup = [&]() {
+        if (din) hipFree(din);
+        if (df) hipFree(df);
+        if (db) hipFree(db);
+    };
+    if (hipMalloc(&din, nblocks * bb) != hipSuccess || (out_f32 && hipMalloc(&df, nblocks * be * 4) != hipSuccess) ||
+        (out_bf16 && hipMalloc(&db, nblocks * be * 2) != hipSuccess)) {
+        cleanup();
+        return fail(FST_ENOMEM, "hipMalloc(dequant) failed");
+    }
+    int rc = FST_OK;
+    if (hipMemcpyAsync(din, blocks, nblocks * bb, hipMemcpyHostToDevice, ctx->st) != hipSuccess)
+        rc = fail(FST_EHIP, "dequant upload failed");
+    if (!rc) {
+        fst::launch_dequant(ctx->st, codec, (const uint8_t*)din, nblocks, (float*)df, (uint16_t*)db);
+        if (hipGetLastError() != hipSuccess) rc = fail(FST_EHIP, "dequant launch failed");
+    }
+    if (!rc && out_f32 && hipMemcpyAsync(out_f32, df, nblocks * be * 4, hipMemcpyDeviceToHost, ctx->st) != hipSuccess)
+        rc = fail(FST_EHIP, "dequant download failed");
+    if (!rc && out_bf16 && hipMemcpyAsync(out_bf16, db, nblocks * be * 2, hipMemcpyDeviceToHost, ctx->st) != hipSuccess)
+        rc = fail(FST_EHIP, "dequant download failed");
+    if (hipStreamSynchronize(ctx->st) != hipSuccess && !rc) rc = fail(FST_EHIP, "dequant sync failed");
+    cleanup();
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// fst_internal.h — device-side layouts and kernel launchers shared by the
+// HIP translation units of libfst_hip.so.  Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fst {
+
+// Q4_K super-block: 256 weights in 144 bytes (fp16 d, fp16 dmin, 12 bytes of
+// packed 6-bit scales/mins, 128 bytes of nibbles).
+constexpr int kQ4kBlockElems = 256;
+constexpr int kQ4kBlockBytes = 144;
+// MXFP4 block: 32 weights in 17 bytes (e8m0 scale + 16 nibble bytes).
+constexpr int kMxBlockElems = 32;
+constexpr int kMxBlockBytes = 17;
+
+constexpr int kMaxTokens = 64;      // tokens per call (4 groups of 16 MFMA rows)
+constexpr int kMaxTopK = 16;
+
+// Meta words written by the bucketing kernel and read by later kernels.
+enum MetaIdx {
+    META_N_SLOTS = 0,      // routed active slots + shared slot
+    META_N_ROUTED = 1,     // routed active slots
+    META_N_PAIRS = 2,      // (token, expert) pairs incl. shared
+    META_ERROR = 3,        // nonzero: invalid expert id seen
+    META_N_ROUTED_PAIRS = 4,
+    META_WORDS = 8
+};
+
+// Device scratch owned by a context, sized for max_tokens.
+struct Scratch {
+    int max_tokens, max_pairs, max_slots;
+    uint16_t* h;           // bf16 [T][hd] staging for host-pointer calls
+    uint16_t* out;         // bf16 [T][hd]
+    uint16_t* out_routed;  // bf16 [T][hd]
+    uint16_t* out_shared;  // bf16 [T][hd]
+    int32_t* ids;          // [T]
+    float* logits;         // [T][E]
+    int32_t* eids;         // [T][tk]
+    float* wts;            // [T][tk]
+    int* meta;             // [META_WORDS]
+    int* slot_eid;         // [S]
+    int* slot_M;           // [S]
+    int* slot_off;         // [S]
+    int* pair_tok;         // [P]
+    int* pair_of;          // [T][tk]
+    int* pair_shared;      // [T]
+    _Float16* x16p;        // [T][hd]    k-interleaved, power-of-two prescaled
+    uint4* sxp;            // [T][hd/256][4] sub-block sums (hi,lo) per lane group
+    int* xs;               // [T] prescale exponent
+    float* act;            // [P][inter]
+    _Float16* a16p;        // [P][inter]
+    uint4* sx2p;           // [P][inter/256][4]
+    int* xs2;              // [P]
+    float* y;              // [P][hd]
+};
+
+// Device expert bank: n_layers x (n_experts + 1) packed experts.
+struct LayerView {
+    const uint8_t* bank;       // expert 0 of the layer; expert e at bank + e*expert_stride
+    size_t expert_stride;
+    const uint16_t* router_nk; // bf16 [E][hd] (transposed at upload)
+    const float* router_bias;  // [E] or null
+    const int32_t* hash;       // [vocab][tk] or null
+};
+
+struct Geometry {
+    int hd, inter, E, tk, codec;
+    int score_func, round_logits_bf16;
+    float route_scale, swiglu_limit;
+    int vocab;
+};
+
+// ---- launchers (each enqueues on `st`) ----
+void launch_router_logits(hipStream_t st, const Geometry& g, const LayerView& L,
+                          const uint16_t* h, int M, float* logits);
+void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, int M,
+                         const float* logits, const int32_t* input_ids, int use_hash,
+                         int do_topk, int use_shared, int32_t* eids, float* wts,
+                         const Scratch& s);
+void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p,
+                      uint4* sxp, int* xs);
+void launch_prep_act(hipStream_t st, const float* act, const int* meta, int max_rows, int K,
+                     _Float16* a16p, uint4* sxp, int* xs);
+void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int ngrp,
+                        const Scratch& s);
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int ngrp,
+                     const Scratch& s);
+void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
+                    const float* wts, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
+void launch_dequant(hipStream_t st, int codec, const uint8_t* blocks, size_t nblocks,
+                    float* out_f32, uint16_t* out_bf16);
+
+// Acceptance.  Work buffers are carved from `ws` (bytes given by accept_ws_bytes).
+size_t accept_ws_bytes(int n_seq, int k, int V);
+void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k, int V,
+                          const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* ws);
+void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
+                              int n_seq, int k, int V, const int32_t* draft, float inv_t,
+                              uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,
+                              void* ws);
+
+}  // namespace fst

@@ -1,0 +1,172 @@
+/* fst_hip.h — C-ABI of the MI355X (gfx950) DSpark verify hot path.
+ *
+ * This library replaces, for one GPU, the four pieces of the reference
+ * engine's block-verification path:
+ *
+ *   FSTEngine::npu_router           include/fst_engine.h:413, src/fst_engine.cpp:936-1076
+ *   FSTEngine::process_expert_ffn   include/fst_engine.h:318, src/fst_engine.cpp:4068-4371
+ *   FSTEngine::process_shared_expert include/fst_engine.h:319, src/fst_engine.cpp:4373-4489
+ *   routed + shared combine         src/fst_engine.cpp:2848-2852
+ *   greedy accept/reject            src/fst_engine.cpp:6021-6063 (inline in generate_dspark)
+ *
+ * plus the expert residency the engine gets from get_expert_bo
+ * (src/fst_engine.cpp:3892-3926): all routed and shared experts of a layer
+ * are uploaded once and stay in HBM.
+ *
+ * Conventions: plain pointers and sizes only; bf16 values are uint16_t bit
+ * patterns (as bf16_t in include/fst_engine.h:16); activations are row-major
+ * [M][hidden]; eids/wts are token-major [M][top_k].  Functions return an
+ * FST_* status code; fst_last_error() gives the message of the last failure
+ * on the calling thread.  Host-pointer entry points are synchronous.  The
+ * *_dev entry points take device pointers and are asynchronous on the
+ * context's stream (fst_stream()); fst_sync() waits for them.  A context is
+ * not re-entrant: calls on one context must not overlap.
+ */
+#ifndef FST_HIP_H
+#define FST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FST_ABI_VERSION 1
+
+enum fst_status {
+    FST_OK = 0,
+    FST_EINVAL = 1,    /* bad argument, shape or state */
+    FST_ENOMEM = 2,    /* device or host allocation failed */
+    FST_EHIP = 3,      /* HIP runtime error (message says which call) */
+    FST_ENODEV = 4,    /* no usable gfx950 device */
+    FST_ENOTREADY = 5  /* weights for this layer/expert were never uploaded */
+};
+
+enum fst_codec { FST_CODEC_Q4K = 0, FST_CODEC_MXFP4 = 1 };
+enum fst_score { FST_SCORE_SIGMOID = 0, FST_SCORE_SQRTSOFTPLUS = 1 };
+
+typedef struct fst_ctx fst_ctx;
+
+/* Layer geometry and routing semantics (ModelConfig, include/fst_engine.h:127-149). */
+typedef struct fst_config {
+    int hidden_dim;        /* 4096 */
+    int inter_dim;         /* 2048 (INTER_DIM, include/fst_engine.h:92) */
+    int n_experts;         /* routed experts per layer, 256 */
+    int top_k;             /* 6 */
+    int n_layers;          /* layers with resident weights */
+    int max_tokens;        /* largest M per call, <= 64 */
+    int codec;             /* enum fst_codec */
+    int has_shared;        /* 1: one shared expert per layer */
+    int score_func;        /* enum fst_score */
+    float route_scale;     /* routed_scaling_factor: 1.0 (sigmoid configs) or 1.5 (V4) */
+    int round_logits_bf16; /* 1: round router logits to bf16 before scoring, as the NPU GEMM does */
+    int n_hash_layers;     /* layers < this use tid2eid hash routing when a table is uploaded */
+    int vocab_size;        /* 129280; used by hash tables, LM head and acceptance */
+    float swiglu_limit;    /* 0: no clamp (engine default); >0: HF clamp */
+    int device;            /* HIP device ordinal */
+} fst_config;
+
+/* Fills the DeepSeek-V4-Flash-like defaults used by the benchmark configs. */
+void fst_config_default(fst_config* cfg);
+
+const char* fst_last_error(void);
+int fst_abi_version(void);
+
+/* Bytes of one packed expert (gate|up|down, each [N rows][K/block] blocks):
+ * Q4_K 14,155,776 B, MXFP4 13,369,344 B at 4096/2048. */
+size_t fst_expert_bytes(const fst_config* cfg);
+
+int fst_create(const fst_config* cfg, fst_ctx** out);
+void fst_destroy(fst_ctx* ctx);
+void* fst_stream(fst_ctx* ctx);       /* hipStream_t of the context */
+int fst_sync(fst_ctx* ctx);
+
+/* ---- device buffers for the *_dev entry points (hipMalloc / hipMemcpy on the context stream) ---- */
+void* fst_device_alloc(fst_ctx* ctx, size_t bytes);
+void fst_device_free(fst_ctx* ctx, void* p);
+int fst_copy_to_device(fst_ctx* ctx, void* dst, const void* src, size_t bytes);
+int fst_copy_to_host(fst_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* ---- weight residency (replaces get_expert_bo / ExpertPager for the timed path) ---- */
+/* eid in [0, n_experts) uploads a routed expert; eid == n_experts the shared one. */
+int fst_upload_expert(fst_ctx* ctx, int lid, int eid, const void* packed, size_t bytes);
+/* Router weight W[K=hidden][N=n_experts] in bf16 or fp32
+ * (the reference's npu_router argument, converted with RNE).  bias may be NULL. */
+int fst_upload_router_bf16(fst_ctx* ctx, int lid, const uint16_t* w_kn, const float* bias);
+int fst_upload_router_f32(fst_ctx* ctx, int lid, const float* w_kn, const float* bias);
+/* tid2eid hash table [vocab][top_k] for lid < n_hash_layers (src/fst_engine.cpp:1015-1021). */
+int fst_upload_hash_table(fst_ctx* ctx, int lid, const int32_t* tid2eid);
+/* Device address of a resident expert (for in-place generation/inspection). */
+void* fst_expert_device_ptr(fst_ctx* ctx, int lid, int eid);
+
+/* ---- router: npu_router (include/fst_engine.h:413) ---- */
+int fst_router(fst_ctx* ctx, int lid, const uint16_t* h, int M, const int32_t* input_ids,
+               int32_t* eids, float* wts);
+
+/* ---- expert FFN: process_expert_ffn / process_shared_expert (include/fst_engine.h:318-319) ---- */
+/* out = bf16( sum_j wts[m][j] * FFN_{eids[m][j]}(h[m]) ) */
+int fst_expert_ffn(fst_ctx* ctx, int lid, const uint16_t* h, uint16_t* out, int M,
+                   const int32_t* eids, int tk, const float* wts);
+/* out = bf16( FFN_shared(h[m]) ) */
+int fst_shared_expert(fst_ctx* ctx, int lid, const uint16_t* h, uint16_t* out, int M);
+
+/* ---- fused MoE layer: router -> routed -> shared -> combine, all on device ---- */
+/* out = bf16( routed + shared ); eids/wts outputs may be NULL. */
+int fst_moe_layer(fst_ctx* ctx, int lid, const uint16_t* h, int M, const int32_t* input_ids,
+                  uint16_t* out, int32_t* eids, float* wts);
+/* Device-pointer, stream-ordered variants.  eids/wts are written (device). */
+int fst_moe_layer_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_input_ids,
+                      uint16_t* d_out, int32_t* d_eids, float* d_wts);
+/* Given routing (device eids/wts), with optional routed-only / shared-only outputs. */
+int fst_moe_ffn_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_eids,
+                    const float* d_wts, int use_shared, uint16_t* d_out,
+                    uint16_t* d_out_routed, uint16_t* d_out_shared);
+
+/* ---- acceptance (src/fst_engine.cpp:6021-6063) ---- */
+/* target: [n_seq][k+1][V] fp32, draft: [n_seq][k] int32,
+ * n_acc: [n_seq], tokens: [n_seq][k+1] (first n_acc[s]+1 valid). */
+int fst_accept_greedy(fst_ctx* ctx, const float* target, int n_seq, int k, int V,
+                      const int32_t* draft, int32_t* n_acc, int32_t* tokens);
+/* Rejection sampling (defined by this build; the reference is greedy-only):
+ * draft_logits [n_seq][k][V]; Philox uniforms keyed by (seed, seq_base + s). */
+int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_logits,
+                          int n_seq, int k, int V, const int32_t* draft, float temperature,
+                          uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens);
+int fst_accept_greedy_dev(fst_ctx* ctx, const float* d_target, int n_seq, int k, int V,
+                          const int32_t* d_draft, int32_t* d_n_acc, int32_t* d_tokens);
+int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* d_draft_logits,
+                              int n_seq, int k, int V, const int32_t* d_draft, float temperature,
+                              uint64_t seed, uint64_t seq_base, int32_t* d_n_acc, int32_t* d_tokens);
+
+/* ---- standalone dequant (bit-exact check of the codec; kernels/fst_dequant_q4k_kernel.cc) ---- */
+/* codec blocks (host) -> fp32 and/or bf16 (host); either output may be NULL. */
+int fst_dequant(fst_ctx* ctx, int codec, const void* blocks, size_t nblocks,
+                float* out_f32, uint16_t* out_bf16);
+
+/* ---- instrumentation ---- */
+typedef struct fst_timings {
+    int n;                  /* kernels recorded in the last call */
+    const char* name[16];
+    float ms[16];           /* per-kernel duration from HIP events on the context stream */
+} fst_timings;
+int fst_set_profiling(fst_ctx* ctx, int on);
+int fst_last_timings(fst_ctx* ctx, fst_timings* out);
+/* Number of distinct routed experts touched by the last MoE call (device -> host copy). */
+int fst_last_active_experts(fst_ctx* ctx, int* n_routed_active);
+
+/* ---- synthetic inputs (host-only; deterministic from a seed) ---- */
+/* One Q4_K expert: uniform nibbles and 6-bit scales/mins, d,dmin ~ |N(0, sigma)| in fp16. */
+int fst_synth_q4k_expert(uint64_t seed, uint64_t expert_id, int hd, int inter, float d_sigma,
+                         uint8_t* out);
+int fst_synth_mxfp4_expert(uint64_t seed, uint64_t expert_id, int hd, int inter, int e_lo,
+                           int e_hi, uint8_t* out);
+/* n values ~ N(mean, std) rounded to bf16 / kept fp32. */
+int fst_synth_normal_bf16(uint64_t seed, uint64_t stream, size_t n, float mean, float std,
+                          uint16_t* out);
+int fst_synth_normal_f32(uint64_t seed, uint64_t stream, size_t n, float mean, float std, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

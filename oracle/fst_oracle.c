@@ -1,0 +1,449 @@
+/* fst_oracle.c — CPU oracle for the DSpark verify hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: this is the checker used by tests/, smoke() and
+ * the cpu_baseline leg of bench.py.  The product library never links it.
+ *
+ * Built with: gcc -O2 -fopenmp -ffp-contract=off -shared -fPIC (oracle/build.sh).
+ * -ffp-contract=off matters: the canonical router sum and the exact-math
+ * functions must not be re-associated or fused by the compiler.
+ *
+ * Pins (what fixes each function independently of this code; see tests/):
+ *   fo_fp16_to_f32      exhaustive over all 65,536 codes vs numpy.float16.
+ *   fo_q4k_dequant      hand-built blocks (impulses, all scale/min patterns)
+ *                       vs closed form d*sc*q - dmin*m; ggml layout known
+ *                       answers; random blocks vs an independent numpy decode.
+ *   fo_mxfp4_dequant    closed form LUT[nib]*2^(e-127), e in {0,255} -> 0.
+ *   fo_expert_ffn       ones@ones = K and A@I known answers through the
+ *                       projections; wrong-transpose discrimination; numpy
+ *                       float64 restatement on small shapes.
+ *   fo_router           brute-force tie/bias/hash cases; logits vs float64 sum
+ *                       (within fp32 error); top-k vs numpy lexsort.
+ *   fo_accept_*         planted accepted lengths 0..k, argmax ties and NaN,
+ *                       brute-force rational arithmetic for the stochastic
+ *                       decision and residual sampling on small vocabularies;
+ *                       Philox known-answer vectors from Salmon et al.
+ */
+#include "fst_oracle.h"
+#include "../include/fst_exact_math.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 0;
+void fo_set_threads(int n) { g_threads = n; }
+int fo_get_threads(void) {
+#ifdef _OPENMP
+    return g_threads > 0 ? g_threads : omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+#ifdef _OPENMP
+#define FO_NT fo_get_threads()
+#endif
+
+float fo_fp16_to_f32(uint16_t h) { return fst_fp16_to_f32(h); }
+uint16_t fo_f32_to_bf16(float f) { return fst_f32_to_bf16(f); }
+float fo_expf(float x) { return fst_expf(x); }
+float fo_logf(float x) { return fst_logf(x); }
+float fo_sigmoidf(float x) { return fst_sigmoidf(x); }
+float fo_sqrtsoftplusf(float x) { return fst_sqrtsoftplusf(x); }
+void fo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    fst_philox_ctr c;
+    for (int i = 0; i < 4; ++i) c.v[i] = ctr[i];
+    fst_philox_ctr r = fst_philox4x32_10(c, key[0], key[1]);
+    for (int i = 0; i < 4; ++i) out[i] = r.v[i];
+}
+uint32_t fo_uniform24(uint64_t seed, uint64_t seq, uint32_t pos, uint32_t stream) {
+    return fst_uniform24(seed, seq, pos, stream);
+}
+
+/* ------------------------------------------------------------------ codecs */
+
+/* kernels/fst_dequant_q4k_kernel.cc:12-20 (get_scale_min_k4). */
+void fo_q4k_scale_min(int j, const uint8_t* q, uint8_t* sc, uint8_t* m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* kernels/fst_dequant_q4k_kernel.cc:40-100 (dequant_q4k_block): block of 144 B,
+ * d = fp16 @0, dmin = fp16 @2, scales[12] @4, qs[128] @16.  qs[32g+i] low
+ * nibble -> element 64g+i (sub-block 2g), high nibble -> 64g+32+i (2g+1).
+ * Value = d*sc*q - dmin*m computed in binary32 (d*sc, (d*sc)*q and dmin*m are
+ * exact products; one rounding in the subtraction).  The fp16 decode is the
+ * correct IEEE one (the reference's decoder at :22-38 mis-decodes subnormals). */
+int fo_q4k_dequant(const uint8_t* blocks, size_t nblocks, float* out) {
+#pragma omp parallel for num_threads(FO_NT) schedule(static)
+    for (long long b = 0; b < (long long)nblocks; ++b) {
+        const uint8_t* blk = blocks + (size_t)b * 144;
+        float* dst = out + (size_t)b * 256;
+        float d = fst_fp16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        float dmin = fst_fp16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+        const uint8_t* sc = blk + 4;
+        const uint8_t* qs = blk + 16;
+        for (int j = 0; j < 8; ++j) {
+            uint8_t s, m;
+            fo_q4k_scale_min(j, sc, &s, &m);
+            float d1 = d * (float)s;
+            float m1 = dmin * (float)m;
+            int g = j >> 1, hi = j & 1;
+            for (int i = 0; i < 32; ++i) {
+                uint8_t byte = qs[32 * g + i];
+                int q = hi ? (byte >> 4) : (byte & 0x0F);
+                dst[32 * j + i] = d1 * (float)q - m1;
+            }
+        }
+    }
+    return 0;
+}
+
+/* kernels/fst_dequant_v4_vectorized_kernel.cc:19-37,60-80 and
+ * scripts/fst_converter.py:449-482: 17-byte block = e8m0 scale byte + 16
+ * bytes of nibbles (low nibble = even element).  Value = LUT[nib]*2^(e-127);
+ * e = 0 or 255 decode to 0 as in the kernel (the converter's python decode
+ * maps them differently; the engine runs the kernel). */
+static const float FO_FP4_LUT[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                                     0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+int fo_mxfp4_dequant(const uint8_t* blocks, size_t nblocks, float* out) {
+#pragma omp parallel for num_threads(FO_NT) schedule(static)
+    for (long long b = 0; b < (long long)nblocks; ++b) {
+        const uint8_t* blk = blocks + (size_t)b * 17;
+        float* dst = out + (size_t)b * 32;
+        int e = blk[0];
+        float s = (e == 0 || e == 255) ? 0.0f : ldexpf(1.0f, e - 127);
+        for (int i = 0; i < 16; ++i) {
+            uint8_t byte = blk[1 + i];
+            dst[2 * i] = FO_FP4_LUT[byte & 15] * s;
+            dst[2 * i + 1] = FO_FP4_LUT[byte >> 4] * s;
+        }
+    }
+    return 0;
+}
+
+/* --------------------------------------------------------------------- FFN */
+
+/* src/fst_engine.cpp:4160-4194 (FST_FFN_AUDIT fp32 reference):
+ * g = h.Wg^T, u = h.Wu^T accumulated in double, act = (g/(1+exp(-g)))*u in
+ * float, y = act.Wd^T accumulated in double.  Orientation A.B^T with B[N][K]
+ * (scripts/fst_validate_gemms.py:174).  Optional SwiGLU clamp as in
+ * scripts/hf_gen_ref.py:475-484 (gate <= lim, up in [-lim, lim]). */
+void fo_expert_ffn_f32(const float* wg, const float* wu, const float* wd, int hd, int inter,
+                       const uint16_t* h, int M, float swiglu_limit, float* y) {
+    float* act = (float*)malloc(sizeof(float) * (size_t)M * inter);
+    float* hf = (float*)malloc(sizeof(float) * (size_t)M * hd);
+    for (size_t i = 0; i < (size_t)M * hd; ++i) hf[i] = fst_bf16_to_f32(h[i]);
+#pragma omp parallel for num_threads(FO_NT) schedule(static)
+    for (int n = 0; n < inter; ++n) {
+        const float* rg = wg + (size_t)n * hd;
+        const float* ru = wu + (size_t)n * hd;
+        for (int m = 0; m < M; ++m) {
+            const float* x = hf + (size_t)m * hd;
+            double g = 0.0, u = 0.0;
+            for (int k = 0; k < hd; ++k) {
+                g += (double)x[k] * (double)rg[k];
+                u += (double)x[k] * (double)ru[k];
+            }
+            float gf = (float)g, uf = (float)u;
+            if (swiglu_limit > 0.0f) {
+                if (gf > swiglu_limit) gf = swiglu_limit;
+                if (uf > swiglu_limit) uf = swiglu_limit;
+                if (uf < -swiglu_limit) uf = -swiglu_limit;
+            }
+            act[(size_t)m * inter + n] = (gf / (1.0f + expf(-gf))) * uf;
+        }
+    }
+#pragma omp parallel for num_threads(FO_NT) schedule(static)
+    for (int d = 0; d < hd; ++d) {
+        const float* rd = wd + (size_t)d * inter;
+        for (int m = 0; m < M; ++m) {
+            const float* a = act + (size_t)m * inter;
+            double s = 0.0;
+            for (int k = 0; k < inter; ++k) s += (double)a[k] * (double)rd[k];
+            y[(size_t)m * hd + d] = (float)s;
+        }
+    }
+    free(act);
+    free(hf);
+}
+
+int fo_expert_ffn(int codec, const uint8_t* expert, int hd, int inter,
+                  const uint16_t* h, int M, float swiglu_limit, float* y) {
+    size_t n_gu = (size_t)inter * hd;
+    float* wg = (float*)malloc(sizeof(float) * n_gu);
+    float* wu = (float*)malloc(sizeof(float) * n_gu);
+    float* wd = (float*)malloc(sizeof(float) * n_gu);
+    if (!wg || !wu || !wd) { free(wg); free(wu); free(wd); return 2; }
+    if (codec == 0) {
+        if (hd % 256 || inter % 256) { free(wg); free(wu); free(wd); return 1; }
+        size_t nb = n_gu / 256, bytes = nb * 144;
+        fo_q4k_dequant(expert, nb, wg);
+        fo_q4k_dequant(expert + bytes, nb, wu);
+        fo_q4k_dequant(expert + 2 * bytes, nb, wd);
+    } else if (codec == 1) {
+        if (hd % 32 || inter % 32) { free(wg); free(wu); free(wd); return 1; }
+        size_t nb = n_gu / 32, bytes = nb * 17;
+        fo_mxfp4_dequant(expert, nb, wg);
+        fo_mxfp4_dequant(expert + bytes, nb, wu);
+        fo_mxfp4_dequant(expert + 2 * bytes, nb, wd);
+    } else {
+        free(wg); free(wu); free(wd);
+        return 1;
+    }
+    fo_expert_ffn_f32(wg, wu, wd, hd, inter, h, M, swiglu_limit, y);
+    free(wg); free(wu); free(wd);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ router */
+
+/* Logits of src/fst_engine.cpp:936-960 (h[M,K] . W[K,N], bf16 inputs).  The
+ * reference leaves the fp32 summation order to the NPU; this build fixes one:
+ * bf16*bf16 products are exact in fp32, each of 64 partials is a sequential
+ * fmaf chain over a contiguous K/64 chunk, and the partials are combined by a
+ * halving tree p[j] += p[j+off] for off = 32,16,8,4,2,1. */
+void fo_router_logits(const uint16_t* h, const uint16_t* w_kn, int M, int K, int N, float* logits) {
+    int chunk = K / 64;
+#pragma omp parallel for num_threads(FO_NT) schedule(static)
+    for (int e = 0; e < N; ++e) {
+        for (int m = 0; m < M; ++m) {
+            float p[64];
+            for (int j = 0; j < 64; ++j) {
+                float acc = 0.0f;
+                for (int i = 0; i < chunk; ++i) {
+                    int k = j * chunk + i;
+                    acc = fmaf(fst_bf16_to_f32(h[(size_t)m * K + k]),
+                               fst_bf16_to_f32(w_kn[(size_t)k * N + e]), acc);
+                }
+                p[j] = acc;
+            }
+            for (int off = 32; off >= 1; off >>= 1)
+                for (int j = 0; j < off; ++j) p[j] = p[j] + p[j + off];
+            logits[(size_t)m * N + e] = p[0];
+        }
+    }
+}
+
+/* Selection and weights: src/fst_engine.cpp:974-1061.  score = sigmoid or
+ * sqrt(softplus) of the logit (optionally rounded to bf16 first, as the NPU
+ * GEMM returns bf16), top-k by score + bias with ties broken toward the lower
+ * expert id (partial_sort leaves ties unspecified), weights = unbiased scores
+ * of the chosen experts, w = v * (1/(sum+1e-12)) * route_scale.  NaN scores
+ * are never selected ahead of a number.  Hash rows (tid2eid, :1015-1021)
+ * replace the selection when given. */
+int fo_router(const uint16_t* h, const uint16_t* w_kn, const float* bias, int M, int K, int N,
+              int top_k, int score_func, float route_scale, int round_logits_bf16,
+              const int32_t* hash_row_eids, int32_t* eids, float* wts, float* logits_out) {
+    if (K % 64 || top_k <= 0 || top_k > N || top_k > 64) return 1;
+    float* lg = (float*)malloc(sizeof(float) * (size_t)M * N);
+    fo_router_logits(h, w_kn, M, K, N, lg);
+    for (int m = 0; m < M; ++m) {
+        float* row = lg + (size_t)m * N;
+        float score[1024], sel[1024];
+        char used[1024];
+        if (N > 1024) { free(lg); return 1; }
+        for (int e = 0; e < N; ++e) {
+            float x = row[e];
+            if (round_logits_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
+            row[e] = x;
+            score[e] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+            sel[e] = score[e] + (bias ? bias[e] : 0.0f);
+            used[e] = 0;
+        }
+        int idx[64];
+        if (hash_row_eids) {
+            for (int k = 0; k < top_k; ++k) idx[k] = hash_row_eids[(size_t)m * top_k + k];
+        } else {
+            for (int k = 0; k < top_k; ++k) {
+                int best = -1;
+                for (int e = 0; e < N; ++e) {
+                    if (used[e]) continue;
+                    if (best < 0) { best = e; continue; }
+                    float a = sel[e], b = sel[best];
+                    int better;
+                    if (a != a) better = 0;
+                    else if (b != b) better = 1;
+                    else better = a > b;
+                    if (better) best = e;
+                }
+                used[best] = 1;
+                idx[k] = best;
+            }
+        }
+        float sum = 0.0f;
+        for (int k = 0; k < top_k; ++k) {
+            if (idx[k] < 0 || idx[k] >= N) { free(lg); return 1; }
+            sum += score[idx[k]];
+        }
+        float inv = 1.0f / (sum + 1e-12f);
+        for (int k = 0; k < top_k; ++k) {
+            eids[(size_t)m * top_k + k] = idx[k];
+            wts[(size_t)m * top_k + k] = score[idx[k]] * inv * route_scale;
+        }
+    }
+    if (logits_out) memcpy(logits_out, lg, sizeof(float) * (size_t)M * N);
+    free(lg);
+    return 0;
+}
+
+/* ----------------------------------------------------------------- combine */
+
+/* src/fst_engine.cpp:4196-4201 (acc += w * down_out, fp32) and :2851-2852
+ * (routed + shared).  The reference truncates each stage to bf16; this build
+ * keeps fp32 to the end and rounds once (RNE). */
+void fo_combine(const float* y_routed, const float* y_shared, const float* wts,
+                int M, int tk, int hd, uint16_t* out, float* out_f32) {
+    for (int m = 0; m < M; ++m)
+        for (int d = 0; d < hd; ++d) {
+            float acc = 0.0f;
+            for (int j = 0; j < tk; ++j)
+                acc = acc + wts[(size_t)m * tk + j] * y_routed[((size_t)m * tk + j) * hd + d];
+            if (y_shared) acc = acc + y_shared[(size_t)m * hd + d];
+            if (out) out[(size_t)m * hd + d] = fst_f32_to_bf16(acc);
+            if (out_f32) out_f32[(size_t)m * hd + d] = acc;
+        }
+}
+
+/* -------------------------------------------------------------- acceptance */
+
+/* src/fst_engine.cpp:6039-6042: int argmax = 0; for v>=1: if (l[v] > max)
+ * update.  First maximum wins; NaN never compares greater, so a NaN at index
+ * 0 pins the result to 0 and NaNs elsewhere are skipped. */
+int fo_argmax(const float* l, int V) {
+    int best = 0;
+    float mx = l[0];
+    for (int v = 1; v < V; ++v)
+        if (l[v] > mx) { mx = l[v]; best = v; }
+    return best;
+}
+
+/* src/fst_engine.cpp:6021-6063: n_acc = longest prefix with pred[i]==draft[i]
+ * (i < k), bonus = pred[n_acc]; emitted = draft[0..n_acc) + bonus. */
+int fo_accept_greedy(const float* target, int k, int V, const int32_t* draft,
+                     int32_t* n_acc, int32_t* tokens) {
+    int n = 0;
+    while (n < k && fo_argmax(target + (size_t)n * V, V) == draft[n]) ++n;
+    for (int i = 0; i < n; ++i) tokens[i] = draft[i];
+    tokens[n] = fo_argmax(target + (size_t)n * V, V);
+    *n_acc = n;
+    return 0;
+}
+
+typedef unsigned __int128 u128;
+
+/* Fixed-point softmax row: E[v] = floor(exp(l[v]*inv_t - max)*2^32). */
+static uint64_t fo_softmax_fixed(const float* row, int V, float inv_t, uint64_t* E) {
+    float mx = -INFINITY;
+    int any = 0;
+    for (int v = 0; v < V; ++v) {
+        float l = row[v] * inv_t;
+        if (l != l) continue;
+        if (!any || l > mx) { mx = l; any = 1; }
+    }
+    uint64_t s = 0;
+    for (int v = 0; v < V; ++v) {
+        float l = row[v] * inv_t;
+        uint64_t e;
+        if (!any || l != l) e = 0;
+        else if (l == mx) e = 4294967296ull;
+        else {
+            float dlt = l - mx;
+            e = (dlt != dlt) ? 0 : fst_prob_fixed(dlt);
+        }
+        if (E) E[v] = e;
+        s += e;
+    }
+    return s;
+}
+
+static int fo_sample_fixed(const uint64_t* E, uint64_t S, int V, uint32_t U) {
+    if (S == 0) return 0;
+    u128 target = ((u128)U * (u128)S) >> 24;
+    u128 c = 0;
+    for (int v = 0; v < V; ++v) {
+        c += E[v];
+        if (c > target) return v;
+    }
+    return V - 1;
+}
+
+/* Speculative rejection sampling (Leviathan et al. 2023; Chen et al. 2023).
+ * The reference has no stochastic acceptance (its only sampler draws from an
+ * unseeded mt19937, src/fst_engine.cpp:4522-4523), so this build defines it:
+ *   p_i = softmax(t_i/T), q_i = softmax(d_i/T) in 2^-32 fixed point
+ *   (E = floor(exp(l-max)*2^32), S = sum E, exact integers);
+ *   u_i = U_i/2^24 from Philox(seed, seq, pos=i, stream=0);
+ *   accept x_i iff U_i*Q(x_i)*S_p < P(x_i)*S_q*2^24   (u < p/q);
+ *   on the first reject, sample from max(0, P*S_q - Q*S_p) (exact 128-bit)
+ *   by inverse CDF with target = (U'_i * sum) >> 24, U'_i from stream 1
+ *   (if that residual is all zero, sample from p_i instead);
+ *   if all k accepted, the bonus is sampled from p_k with U'_k. */
+int fo_accept_stochastic(const float* target, const float* draft_logits, int k, int V,
+                         const int32_t* draft, float temperature, uint64_t seed, uint64_t seq,
+                         int32_t* n_acc, int32_t* tokens) {
+    if (!(temperature > 0.0f)) return 1;
+    float inv_t = 1.0f / temperature;
+    uint64_t* P = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    uint64_t* Q = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    int n = 0;
+    for (; n < k; ++n) {
+        uint64_t Sp = fo_softmax_fixed(target + (size_t)n * V, V, inv_t, P);
+        uint64_t Sq = fo_softmax_fixed(draft_logits + (size_t)n * V, V, inv_t, Q);
+        int x = draft[n];
+        if (x < 0 || x >= V) { free(P); free(Q); return 1; }
+        uint32_t U = fst_uniform24(seed, seq, (uint32_t)n, 0);
+        u128 lhs = (u128)U * (u128)Q[x] * (u128)Sp;
+        u128 rhs = ((u128)P[x] * (u128)Sq) << 24;
+        if (lhs < rhs) { tokens[n] = x; continue; }
+        /* reject: residual resample */
+        uint32_t U2 = fst_uniform24(seed, seq, (uint32_t)n, 1);
+        u128 R = 0;
+        for (int v = 0; v < V; ++v) {
+            u128 a = (u128)P[v] * Sq, b = (u128)Q[v] * Sp;
+            if (a > b) R += a - b;
+        }
+        int tok;
+        if (R == 0) tok = fo_sample_fixed(P, Sp, V, U2);
+        else {
+            u128 tgt = ((u128)U2 * R) >> 24;
+            u128 c = 0;
+            tok = V - 1;
+            for (int v = 0; v < V; ++v) {
+                u128 a = (u128)P[v] * Sq, b = (u128)Q[v] * Sp;
+                if (a > b) c += a - b;
+                if (c > tgt) { tok = v; break; }
+            }
+        }
+        tokens[n] = tok;
+        *n_acc = n;
+        free(P); free(Q);
+        return 0;
+    }
+    uint64_t Sp = fo_softmax_fixed(target + (size_t)k * V, V, inv_t, P);
+    tokens[k] = fo_sample_fixed(P, Sp, V, fst_uniform24(seed, seq, (uint32_t)k, 1));
+    *n_acc = k;
+    free(P); free(Q);
+    return 0;
+}
+
+/* ----------------------------------------------------------------- RMSNorm */
+
+/* src/fst_engine.cpp:89-91 (rms_cpu): r = 1/sqrt(mean(x^2)+eps), out =
+ * bf16(x*r*w); this build rounds RNE and accumulates the mean in double. */
+void fo_rmsnorm(const float* x, const uint16_t* w, int M, int d, float eps, uint16_t* out) {
+    for (int m = 0; m < M; ++m) {
+        double ss = 0.0;
+        for (int j = 0; j < d; ++j) ss += (double)x[(size_t)m * d + j] * x[(size_t)m * d + j];
+        float r = (float)(1.0 / sqrt(ss / d + eps));
+        for (int j = 0; j < d; ++j)
+            out[(size_t)m * d + j] = fst_f32_to_bf16(x[(size_t)m * d + j] * r * fst_bf16_to_f32(w[j]));
+    }
+}
