@@ -1,0 +1,220 @@
+#!/usr/bin/env python3
+"""Benchmark: block-8 MoE-layer verify on one MI355X.
+
+One step = one pass of the verify hot path over one batch of 8 verify tokens:
+router GEMM 4096x256 + top-6 + 256 routed / 1 shared Q4_K SwiGLU experts
+(4096->2048->4096) + weighted combine + greedy acceptance (k=7, V=129,280)
+over resident target logits.  All weights and inputs are resident in HBM
+before the timed region; 16 different hidden batches are cycled so routing
+changes from step to step (no warm Infinity-Cache replay of one expert set).
+
+Prints one JSON line (rank 0) with the metric, the roofline of the dominant
+kernel (HIP-event timed on the library stream) and the CPU oracle baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HD, INTER, E, TK, M = 4096, 2048, 256, 6, 8
+K_DRAFT, VOCAB = 7, 129280
+SEED = 20260101
+N_BATCH = 16
+PROJ_BYTES = INTER * (HD // 256) * 144          # one Q4_K projection, 4,718,592 B
+EXPERT_BYTES = 3 * PROJ_BYTES                    # 14,155,776 B
+ROUTER_BYTES = HD * E * 2
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def setup(fa):
+    ctx = fa.Context(n_experts=E, top_k=TK, max_tokens=64)
+    t0 = time.time()
+    for e in range(E + 1):
+        ctx.upload_expert(0, e, fa.synth_q4k_expert(SEED, e))
+    w = fa.synth_normal_bf16(SEED, 1000, (HD, E), 0.0, 0.02)
+    ctx.upload_router_bf16(0, w)
+    log("uploaded %d experts (%.2f GB) in %.1fs" % (E + 1, (E + 1) * EXPERT_BYTES / 1e9, time.time() - t0))
+    hs = fa.synth_normal_bf16(SEED, 3000, (N_BATCH, M, HD))
+    logits = fa.synth_normal_f32(SEED, 4000, (1, K_DRAFT + 1, VOCAB), 0.0, 2.0)
+    draft = np.array([[int(np.argmax(logits[0, i])) if i < 3 else (i * 7919) % VOCAB
+                       for i in range(K_DRAFT)]], np.int32)
+    bufs = {
+        "h": ctx.to_device(hs),
+        "out": ctx.dev_alloc(M * HD * 2),
+        "eids": ctx.dev_alloc(M * TK * 4),
+        "wts": ctx.dev_alloc(M * TK * 4),
+        "logits": ctx.to_device(logits),
+        "draft": ctx.to_device(draft),
+        "nacc": ctx.dev_alloc(4),
+        "tok": ctx.dev_alloc((K_DRAFT + 1) * 4),
+    }
+    return ctx, w, hs, logits, draft, bufs
+
+
+def step(fa, ctx, bufs, i):
+    L = fa.lib()
+    hp = bufs["h"] + (i % N_BATCH) * M * HD * 2
+    fa._check(L.fst_moe_layer_dev(ctx.h, 0, hp, M, None, bufs["out"], bufs["eids"], bufs["wts"]))
+    fa._check(L.fst_accept_greedy_dev(ctx.h, bufs["logits"], 1, K_DRAFT, VOCAB, bufs["draft"], bufs["nacc"],
+                                      bufs["tok"]))
+
+
+def cpu_baseline(hs, w, threads):
+    """CPU oracle on one verify step (batch 0): router + every routed expert
+    touched + shared expert + combine, fp64-accumulated, `threads` OpenMP threads."""
+    import fastar_amd as fa
+    from oracle import pyoracle as po
+    po.set_threads(threads)
+    h = hs[0]
+    e, wt, _ = po.router(h, w, None, TK)
+    distinct = sorted(set(int(x) for x in e.ravel()))
+    experts = {ex: fa.synth_q4k_expert(SEED, ex) for ex in distinct + [E]}
+    t0 = time.perf_counter()
+    e, wt, _ = po.router(h, w, None, TK)
+    y = np.zeros((M, TK, HD), np.float32)
+    for ex in distinct:
+        rows = [m for m in range(M) if ex in e[m]]
+        ye = po.expert_ffn(0, experts[ex], h[rows])
+        for r, m in enumerate(rows):
+            for j in range(TK):
+                if e[m, j] == ex:
+                    y[m, j] = ye[r]
+    ys = po.expert_ffn(0, experts[E], h)
+    po.combine(y, ys, wt)
+    dt = time.perf_counter() - t0
+    return M / dt, dt, len(distinct)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calib-copy", type=int, default=0,
+                    help="also run N launches of the plain copy kernel (512 MiB) for PMC calibration")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; the verify path is not sharded across GPUs "
+              "(see DESIGN.md, 'How the path would shard'). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import fastar_amd as fa
+    L = fa.lib()
+    ctx, w, hs, logits, draft, bufs = setup(fa)
+
+    for i in range(args.warmup):
+        step(fa, ctx, bufs, i)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(fa, ctx, bufs, i)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    ms_step = dt * 1e3 / args.steps
+    value = M * args.steps / dt
+
+    # Per-kernel durations (HIP events on the library stream) and distinct experts per step.
+    ctx.set_profiling(True)
+    per = {}
+    bytes_gu, bytes_dn, dur_gu, dur_dn, n_act = [], [], [], [], []
+    nprof = min(args.steps, 64)
+    for i in range(nprof):
+        fa._check(L.fst_moe_layer_dev(ctx.h, 0, bufs["h"] + (i % N_BATCH) * M * HD * 2, M, None, bufs["out"],
+                                      bufs["eids"], bufs["wts"]))
+        tm = ctx.last_timings()
+        a = ctx.last_active_experts()
+        n_act.append(a)
+        for name, ms in tm:
+            per.setdefault(name, []).append(ms)
+        d = dict(tm)
+        bytes_gu.append((a + 1) * 2 * PROJ_BYTES)
+        bytes_dn.append((a + 1) * PROJ_BYTES)
+        dur_gu.append(d["q4k_gate_up"] * 1e-3)
+        dur_dn.append(d["q4k_down"] * 1e-3)
+    ctx.set_profiling(False)
+    fa._check(L.fst_accept_greedy_dev(ctx.h, bufs["logits"], 1, K_DRAFT, VOCAB, bufs["draft"], bufs["nacc"],
+                                      bufs["tok"]))
+    ctx.sync()
+    n_acc = int(ctx.to_host(bufs["nacc"], (1,), np.int32)[0])
+
+    gu_achieved = np.mean(bytes_gu) / np.mean(dur_gu) / 1e9
+    dn_achieved = np.mean(bytes_dn) / np.mean(dur_dn) / 1e9
+    mean_act = float(np.mean(n_act))
+    step_bytes = (mean_act + 1) * EXPERT_BYTES + ROUTER_BYTES
+    kern = {k: round(float(np.mean(v)) * 1e3, 2) for k, v in per.items()}  # microseconds
+
+    if args.calib_copy:
+        nbytes = 512 << 20
+        src = ctx.dev_alloc(nbytes)
+        dst = ctx.dev_alloc(nbytes)
+        for _ in range(args.calib_copy):
+            fa._check(L.fst_device_copy(ctx.h, dst, src, nbytes))
+        ctx.sync()
+        ctx.dev_free(src)
+        ctx.dev_free(dst)
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        v, secs, nd = cpu_baseline(hs, w, threads)
+        cpu = {"value": round(v, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": "one block-8 verify step (batch 0: router + %d routed + 1 shared Q4_K experts + "
+                         "combine) through the C oracle, %.1f s" % (nd, secs)}
+
+    res = {
+        "metric": "verified tokens/s for block-8 MoE-layer verify",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2 block-8 MoE-layer verify: router 4096x256 bf16 (sigmoid, top-6) + 256 routed + "
+                        "1 shared Q4_K SwiGLU experts 4096->2048->4096 + combine + greedy acceptance "
+                        "k=7 over V=129280",
+            "tokens_per_step": M,
+            "experts_resident": E + 1,
+            "mean_distinct_routed_experts": round(mean_act, 2),
+            "packed_bytes_per_step": int(step_bytes),
+            "operands": "Q4_K weights decoded to exact fp16 (sc*q), fp16 MFMA, fp32 accumulate",
+            "parallelism": "1 GPU",
+        },
+        "roofline": {
+            "kernel": "q4k_ffn gate+up (fused Q4_K decode, fp16 MFMA, SiLU*up)",
+            "bound": "hbm",
+            "achieved": round(gu_achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "packed_weight_GBps_step": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "down_kernel_GBps": round(dn_achieved, 1),
+        "kernel_us": kern,
+        "accepted_len_step": n_acc,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

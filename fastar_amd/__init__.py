@@ -80,6 +80,7 @@ _SIGS = {
     "fst_set_profiling": (C.c_int, [P, C.c_int]),
     "fst_last_timings": (C.c_int, [P, P]),
     "fst_last_active_experts": (C.c_int, [P, P]),
+    "fst_device_copy": (C.c_int, [P, P, P, SZ]),
     "fst_synth_q4k_expert": (C.c_int, [U64, U64, C.c_int, C.c_int, C.c_float, P]),
     "fst_synth_mxfp4_expert": (C.c_int, [U64, U64, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "fst_synth_normal_bf16": (C.c_int, [U64, U64, SZ, C.c_float, C.c_float, P]),

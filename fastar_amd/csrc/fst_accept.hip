@@ -95,20 +95,38 @@ __global__ __launch_bounds__(256) void acc_stats_kernel(const float* __restrict_
     }
 }
 
-__device__ void row_reduce(const float* part_max, const int* part_idx, int r, float* mx, int* idx) {
-    float best = 0.0f;
-    int bi = -1;
-    for (int c = 0; c < kChunks; ++c) {
-        const int i = part_idx[(size_t)r * kChunks + c];
-        if (i < 0) continue;
-        const float m = part_max[(size_t)r * kChunks + c];
-        if (bi < 0 || m > best || (m == best && i < bi)) { best = m; bi = i; }
+// Wave-parallel reduction of the kChunks (= 64) chunk partials of row r: lane
+// c reads chunk c.  Returns (max, lowest index attaining it, -1 if the row
+// has no number) in every lane.
+__device__ __forceinline__ void wave_row_argmax(const float* part_max, const int* part_idx, int r, float* mx,
+                                                int* idx) {
+    const int lane = threadIdx.x & 63;
+    float m = part_max[(size_t)r * kChunks + lane];
+    int i = part_idx[(size_t)r * kChunks + lane];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float om = __shfl_xor(m, off, 64);
+        const int oi = __shfl_xor(i, off, 64);
+        if (oi >= 0 && (i < 0 || om > m || (om == m && oi < i))) {
+            m = om;
+            i = oi;
+        }
     }
-    *mx = best;
-    *idx = bi;
+    *mx = m;
+    *idx = i;
 }
 
-// One wave per sequence; lane i (< k+1) resolves target row i.
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned lo = __shfl_xor((unsigned)v, off, 64);
+        const unsigned hi = __shfl_xor((unsigned)(v >> 32), off, 64);
+        v += ((unsigned long long)hi << 32) | lo;
+    }
+    return v;
+}
+
+// One wave per sequence: rows reduced one after another, chunks across lanes.
 __global__ __launch_bounds__(64) void acc_greedy_final_kernel(const float* __restrict__ target, int k,
                                                               int V, const float* __restrict__ part_max,
                                                               const int* __restrict__ part_idx,
@@ -117,18 +135,15 @@ __global__ __launch_bounds__(64) void acc_greedy_final_kernel(const float* __res
                                                               int32_t* __restrict__ tokens) {
     const int s = blockIdx.x, lane = threadIdx.x;
     __shared__ int pred[64];
-    if (lane <= k) {
-        const int r = s * (k + 1) + lane;
-        const float x0 = target[(size_t)r * V];
+    for (int i = 0; i <= k; ++i) {
+        const int r = s * (k + 1) + i;
+        float mx;
         int am;
-        if (x0 != x0) {
-            am = 0;
-        } else {
-            float mx;
-            row_reduce(part_max, part_idx, r, &mx, &am);
-            if (am < 0) am = 0;
+        wave_row_argmax(part_max, part_idx, r, &mx, &am);
+        if (lane == 0) {
+            const float x0 = target[(size_t)r * V];
+            pred[i] = (x0 != x0 || am < 0) ? 0 : am;
         }
-        pred[lane] = am;
     }
     __syncthreads();
     if (lane == 0) {
@@ -150,10 +165,10 @@ __device__ __forceinline__ unsigned long long fixed_prob(float x, float inv_t, f
     return (unsigned long long)fst_prob_fixed(d);
 }
 
-__device__ __forceinline__ void row_max_any(const float* part_max, const int* part_idx, int r, float* mx,
-                                            int* any) {
+__device__ __forceinline__ void wave_row_max_any(const float* part_max, const int* part_idx, int r, float* mx,
+                                                 int* any) {
     int idx;
-    row_reduce(part_max, part_idx, r, mx, &idx);
+    wave_row_argmax(part_max, part_idx, r, mx, &idx);
     *any = idx >= 0;
 }
 
@@ -167,12 +182,14 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
     const int c = blockIdx.x, r = blockIdx.y;
     __shared__ float s_mx;
     __shared__ int s_any;
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {
         float mx;
         int any;
-        row_max_any(part_max, part_idx, r, &mx, &any);
-        s_mx = mx;
-        s_any = any;
+        wave_row_max_any(part_max, part_idx, r, &mx, &any);
+        if (threadIdx.x == 0) {
+            s_mx = mx;
+            s_any = any;
+        }
     }
     __syncthreads();
     const float mx = s_mx;
@@ -194,7 +211,7 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
 
 // dec layout per sequence: [0] n_acc, [1] sampling target row, [2] mode
 // (0: residual vs draft row, 1: sample from target row), [3] U', [4] Sp, [5] Sq,
-// [6] draft row.
+// [6] draft row, [7] packed (row max bits of target | any) unused.
 __global__ __launch_bounds__(64) void acc_decide_kernel(
     const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
     float inv_t, const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base,
@@ -204,31 +221,35 @@ __global__ __launch_bounds__(64) void acc_decide_kernel(
     const int s = blockIdx.x, lane = threadIdx.x;
     const int n_tgt = n_seq * (k + 1);
     __shared__ int accept[64];
-    __shared__ unsigned long long Sp_s[64], Sq_s[64];
-    if (lane < k) {
-        const int rt = s * (k + 1) + lane, rd = n_tgt + s * k + lane;
-        unsigned long long Sp = 0, Sq = 0;
-        for (int c = 0; c < kChunks; ++c) {
-            Sp += part_sum[(size_t)rt * kChunks + c];
-            Sq += part_sum[(size_t)rd * kChunks + c];
-        }
+    __shared__ unsigned long long Sp_s[65], Sq_s[64];
+    for (int i = 0; i < k; ++i) {
+        const int rt = s * (k + 1) + i, rd = n_tgt + s * k + i;
+        const unsigned long long Sp = wave_sum_u64(part_sum[(size_t)rt * kChunks + lane]);
+        const unsigned long long Sq = wave_sum_u64(part_sum[(size_t)rd * kChunks + lane]);
         float mp, mq;
         int ap, aq;
-        row_max_any(part_max, part_idx, rt, &mp, &ap);
-        row_max_any(part_max, part_idx, rd, &mq, &aq);
-        const int x = draft[s * k + lane];
-        int ok = 0;
-        if (x >= 0 && x < V) {
-            const unsigned long long P = fixed_prob(target[(size_t)rt * V + x], inv_t, mp, ap);
-            const unsigned long long Q = fixed_prob(draftl[(size_t)(rd - n_tgt) * V + x], inv_t, mq, aq);
-            const uint32_t U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 0);
-            const u128 lhs = (u128)U * (u128)Q * (u128)Sp;
-            const u128 rhs = ((u128)P * (u128)Sq) << 24;
-            ok = lhs < rhs;
+        wave_row_max_any(part_max, part_idx, rt, &mp, &ap);
+        wave_row_max_any(part_max, part_idx, rd, &mq, &aq);
+        if (lane == 0) {
+            const int x = draft[s * k + i];
+            int ok = 0;
+            if (x >= 0 && x < V) {
+                const unsigned long long P = fixed_prob(target[(size_t)rt * V + x], inv_t, mp, ap);
+                const unsigned long long Q = fixed_prob(draftl[(size_t)(rd - n_tgt) * V + x], inv_t, mq, aq);
+                const uint32_t U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)i, 0);
+                const u128 lhs = (u128)U * (u128)Q * (u128)Sp;
+                const u128 rhs = ((u128)P * (u128)Sq) << 24;
+                ok = lhs < rhs;
+            }
+            accept[i] = ok;
+            Sp_s[i] = Sp;
+            Sq_s[i] = Sq;
         }
-        accept[lane] = ok;
-        Sp_s[lane] = Sp;
-        Sq_s[lane] = Sq;
+    }
+    {
+        const int rt = s * (k + 1) + k;
+        const unsigned long long Sp = wave_sum_u64(part_sum[(size_t)rt * kChunks + lane]);
+        if (lane == 0) Sp_s[k] = Sp;
     }
     __syncthreads();
     if (lane == 0) {
@@ -238,17 +259,13 @@ __global__ __launch_bounds__(64) void acc_decide_kernel(
         d[0] = (unsigned long long)n;
         d[1] = (unsigned long long)(s * (k + 1) + n);
         d[3] = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)n, 1);
+        d[4] = Sp_s[n];
         if (n < k) {
             d[2] = 0;
-            d[4] = Sp_s[n];
             d[5] = Sq_s[n];
             d[6] = (unsigned long long)(n_tgt + s * k + n);
         } else {
-            unsigned long long Sp = 0;
-            const int rt = s * (k + 1) + k;
-            for (int c = 0; c < kChunks; ++c) Sp += part_sum[(size_t)rt * kChunks + c];
             d[2] = 1;
-            d[4] = Sp;
             d[5] = 0;
             d[6] = 0;
         }
@@ -276,23 +293,27 @@ struct RowCtx {
     unsigned long long Sp, Sq;
 };
 
-__device__ void load_rowctx(const float* target, const float* draftl, int n_tgt, int V,
-                            const float* part_max, const int* part_idx, const unsigned long long* d,
-                            RowCtx& rc) {
+// Called by all lanes of the first wave; lane 0 stores the context.
+__device__ void load_rowctx_wave(const float* target, const float* draftl, int n_tgt, int V,
+                                 const float* part_max, const int* part_idx, const unsigned long long* d,
+                                 RowCtx& rc) {
     const int rt = (int)d[1];
-    rc.mode = (int)d[2];
-    rc.Sp = d[4];
-    rc.Sq = d[5];
-    rc.trow = target + (size_t)rt * V;
-    row_max_any(part_max, part_idx, rt, &rc.mp, &rc.ap);
-    if (rc.mode == 0) {
-        const int rd = (int)d[6];
-        rc.drow = draftl + (size_t)(rd - n_tgt) * V;
-        row_max_any(part_max, part_idx, rd, &rc.mq, &rc.aq);
-    } else {
-        rc.drow = nullptr;
-        rc.mq = 0.0f;
-        rc.aq = 0;
+    const int mode = (int)d[2];
+    float mp, mq = 0.0f;
+    int ap, aq = 0;
+    wave_row_max_any(part_max, part_idx, rt, &mp, &ap);
+    const int rd = (int)d[6];
+    if (mode == 0) wave_row_max_any(part_max, part_idx, rd, &mq, &aq);
+    if ((threadIdx.x & 63) == 0) {
+        rc.mode = mode;
+        rc.Sp = d[4];
+        rc.Sq = d[5];
+        rc.trow = target + (size_t)rt * V;
+        rc.drow = mode == 0 ? draftl + (size_t)(rd - n_tgt) * V : nullptr;
+        rc.mp = mp;
+        rc.ap = ap;
+        rc.mq = mq;
+        rc.aq = aq;
     }
 }
 
@@ -303,8 +324,8 @@ __global__ __launch_bounds__(256) void acc_res_chunks_kernel(
     const unsigned long long* __restrict__ dec, unsigned long long* __restrict__ part_res) {
     const int c = blockIdx.x, s = blockIdx.y;
     __shared__ RowCtx rc;
-    if (threadIdx.x == 0) load_rowctx(target, draftl, n_seq * (k + 1), V, part_max, part_idx,
-                                      dec + (size_t)s * 8, rc);
+    if (threadIdx.x < 64)
+        load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, dec + (size_t)s * 8, rc);
     __syncthreads();
     const int clen = (V + kChunks - 1) / kChunks;
     const int b0 = c * clen, b1 = min(V, b0 + clen);
@@ -338,8 +359,9 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
     __shared__ u128 tsum[256];
     __shared__ int s_tok;
     unsigned long long* d = dec + (size_t)s * 8;
+    if (tid < 64) load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
+    __syncthreads();
     if (tid == 0) {
-        load_rowctx(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
         const unsigned long long U2 = d[3];
         u128 tot = 0;
         u128 cs[kChunks];

@@ -52,6 +52,7 @@ struct fst_ctx {
     std::vector<int32_t*> hash;              // [L] (lid < n_hash_layers)
     fst::Scratch s{};
     std::vector<void*> allocs;
+    std::vector<uint8_t> staging;            // host repack buffer for expert uploads
     // acceptance staging (grown on demand)
     void* acc_ws = nullptr;
     size_t acc_ws_cap = 0;
@@ -168,8 +169,7 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         return fail(FST_EINVAL, "fst_create: only the Q4_K codec has a fused FFN path");
     if (c.hidden_dim <= 0 || c.hidden_dim % 512 || c.inter_dim <= 0 || c.inter_dim % 256)
         return fail(FST_EINVAL, "fst_create: hidden_dim must be a multiple of 512, inter_dim of 256");
-    if (c.hidden_dim % 64 || c.inter_dim % 64)
-        return fail(FST_EINVAL, "fst_create: dims must be multiples of 64");
+
     if (c.n_experts <= 0 || c.n_experts > 1024)
         return fail(FST_EINVAL, "fst_create: n_experts must be in [1, 1024]");
     if (c.top_k <= 0 || c.top_k > fst::kMaxTopK || c.top_k > c.n_experts)
@@ -235,7 +235,7 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.pair_tok, P)) || (rc = x->dalloc(&s.pair_of, (size_t)T * tk)) ||
         (rc = x->dalloc(&s.pair_shared, T)) || (rc = x->dalloc(&s.x16p, (size_t)T * hd)) ||
         (rc = x->dalloc(&s.sxp, (size_t)T * (hd / 256) * 4)) || (rc = x->dalloc(&s.xs, T)) ||
-        (rc = x->dalloc(&s.act, (size_t)P * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
+        (rc = x->dalloc(&s.act, (size_t)P * 2 * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
         (rc = x->dalloc(&s.y, (size_t)P * hd)))
         return bail(rc);
@@ -269,6 +269,14 @@ int fst_last_timings(fst_ctx* ctx, fst_timings* out) {
     if (!ctx || !out) return fail(FST_EINVAL, "null argument");
     ctx->collect();
     *out = ctx->last;
+    return FST_OK;
+}
+
+int fst_device_copy(fst_ctx* ctx, void* d_dst, const void* d_src, size_t bytes) {
+    if (!ctx || !d_dst || !d_src) return fail(FST_EINVAL, "null argument");
+    if (bytes % 16) return fail(FST_EINVAL, "bytes must be a multiple of 16");
+    fst::launch_copy(ctx->st, d_dst, d_src, bytes);
+    FST_HIP_TRY(hipGetLastError());
     return FST_OK;
 }
 
@@ -330,7 +338,10 @@ int fst_upload_expert(fst_ctx* ctx, int lid, int eid, const void* packed, size_t
         return fail(FST_EINVAL, "expert size mismatch: got " + std::to_string(bytes) + ", expected " +
                                     std::to_string(ctx->expert_bytes));
     uint8_t* dst = ctx->bank + ((size_t)lid * (ctx->cfg.n_experts + 1) + eid) * ctx->expert_stride;
-    FST_HIP_TRY(hipMemcpyAsync(dst, packed, bytes, hipMemcpyHostToDevice, ctx->st));
+    ctx->staging.resize(bytes);
+    fst::repack_q4k_expert(static_cast<const uint8_t*>(packed), ctx->staging.data(), ctx->cfg.hidden_dim,
+                           ctx->cfg.inter_dim);
+    FST_HIP_TRY(hipMemcpyAsync(dst, ctx->staging.data(), bytes, hipMemcpyHostToDevice, ctx->st));
     FST_HIP_TRY(hipStreamSynchronize(ctx->st));
     if (!ctx->uploaded[lid][eid]) {
         ctx->uploaded[lid][eid] = 1;
@@ -415,7 +426,6 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     g.tk = use_routed ? tk : 0;
     fst::LayerView L = ctx->layer(lid);
     const int use_hash = do_router && lid < c.n_hash_layers && L.hash && d_ids;
-    const int ngrp = (M + 15) / 16 > 2 ? 4 : (M + 15) / 16;
     hipStream_t st = ctx->st;
     ctx->mark_begin();
     if (do_router) {
@@ -427,12 +437,12 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     ctx->mark("route_bucket");
     fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
     ctx->mark("prep_x");
-    fst::launch_q4k_gate_up(st, g, L, ngrp, ctx->s);
+    fst::launch_q4k_gate_up(st, g, L, M, ctx->s);
     ctx->mark("q4k_gate_up");
-    fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p, ctx->s.sx2p,
-                         ctx->s.xs2);
+    fst::launch_prep_act(st, ctx->s.act, c.swiglu_limit, ctx->s.meta, ctx->s.max_pairs, c.inter_dim,
+                         ctx->s.a16p, ctx->s.sx2p, ctx->s.xs2);
     ctx->mark("prep_act");
-    fst::launch_q4k_down(st, g, L, ngrp, ctx->s);
+    fst::launch_q4k_down(st, g, L, M, ctx->s);
     ctx->mark("q4k_down");
     fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared);
     ctx->mark("combine");

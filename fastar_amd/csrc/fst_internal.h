@@ -25,6 +25,7 @@ enum MetaIdx {
     META_N_PAIRS = 2,      // (token, expert) pairs incl. shared
     META_ERROR = 3,        // nonzero: invalid expert id seen
     META_N_ROUTED_PAIRS = 4,
+    META_TOPK_ERROR = 5,   // set by the top-k kernel, folded into META_ERROR by bucketing
     META_WORDS = 8
 };
 
@@ -49,7 +50,7 @@ struct Scratch {
     _Float16* x16p;        // [T][hd]    k-interleaved, power-of-two prescaled
     uint4* sxp;            // [T][hd/256][4] sub-block sums (hi,lo) per lane group
     int* xs;               // [T] prescale exponent
-    float* act;            // [P][inter]
+    float* act;            // [P][2*inter] raw gate||up projections
     _Float16* a16p;        // [P][inter]
     uint4* sx2p;           // [P][inter/256][4]
     int* xs2;              // [P]
@@ -81,14 +82,17 @@ void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, 
                          const Scratch& s);
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p,
                       uint4* sxp, int* xs);
-void launch_prep_act(hipStream_t st, const float* act, const int* meta, int max_rows, int K,
-                     _Float16* a16p, uint4* sxp, int* xs);
-void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int ngrp,
-                        const Scratch& s);
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int ngrp,
-                     const Scratch& s);
+void launch_prep_act(hipStream_t st, const float* gu, float swiglu_limit, const int* meta, int max_rows,
+                     int K, _Float16* a16p, uint4* sxp, int* xs);
+// Weights must be in the wave-tiled device layout (repack_q4k_expert).
+void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
+// Host-side reorder of one packed Q4_K expert (gate|up|down, each [N][K/256]
+// blocks of 144 B) into the device layout the linear kernel streams.
+void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);
 void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
                     const float* wts, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
+void launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);
 void launch_dequant(hipStream_t st, int codec, const uint8_t* blocks, size_t nblocks,
                     float* out_f32, uint16_t* out_bf16);
 

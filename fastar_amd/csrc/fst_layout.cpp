@@ -1,0 +1,52 @@
+// fst_layout.cpp — device layout of resident Q4_K experts.
+//
+// The packed expert handed over at the ABI is the reference's byte format:
+// gate | up | down, each a row-major [N rows][K/256] array of 144-byte Q4_K
+// super-blocks (scripts/fst_converter.py:64-92 orientation, block format of
+// kernels/fst_dequant_q4k_kernel.cc).  On upload each matrix is reordered so
+// the linear kernel's 64-lane wave reads it with contiguous, fully coalesced
+// 1 KiB loads, front to back:
+//
+//   matrix = [N/16 row tiles][K/256 super-blocks] chunks of 2304 bytes;
+//   chunk (t, sb) holds super-block sb of rows 16t .. 16t+15:
+//     [0,    1024)  lane L = 16g + r: qs bytes [32g,    32g+16) of row r
+//     [1024, 2048)  lane L = 16g + r: qs bytes [32g+16, 32g+32) of row r
+//     [2048, 2304)  row r: the 16-byte header (d, dmin, 12 scale bytes)
+//
+// Every byte of every block is kept; only their order changes, so the device
+// copy holds exactly the packed expert's 14,155,776 bytes (4096/2048 shape).
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "fst_internal.h"
+
+namespace fst {
+
+static void repack_matrix(const uint8_t* src, uint8_t* dst, int N, int K) {
+    const int nsb = K / 256;
+    for (int t = 0; t < N / 16; ++t)
+        for (int sb = 0; sb < nsb; ++sb) {
+            uint8_t* chunk = dst + ((size_t)t * nsb + sb) * 2304;
+            for (int r = 0; r < 16; ++r) {
+                const uint8_t* b = src + ((size_t)(t * 16 + r) * nsb + sb) * 144;
+                std::memcpy(chunk + 2048 + 16 * r, b, 16);
+                for (int g = 0; g < 4; ++g) {
+                    const int L = 16 * g + r;
+                    std::memcpy(chunk + 16 * L, b + 16 + 32 * g, 16);
+                    std::memcpy(chunk + 1024 + 16 * L, b + 32 + 32 * g, 16);
+                }
+            }
+        }
+}
+
+void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter) {
+    const size_t proj = (size_t)inter * (hd / 256) * 144;
+    std::thread a([&] { repack_matrix(src, dst, inter, hd); });
+    std::thread b([&] { repack_matrix(src + proj, dst + proj, inter, hd); });
+    repack_matrix(src + 2 * proj, dst + 2 * proj, hd, inter);
+    a.join();
+    b.join();
+}
+
+}  // namespace fst

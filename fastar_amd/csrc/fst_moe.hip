@@ -21,6 +21,8 @@
 // hi+lo in fp16).  d and dmin scale once per 256-weight super-block.
 // Activations are prescaled per token by a power of two (exact) so the fp16
 // operand covers their range.
+#include <algorithm>
+
 #include "fst_internal.h"
 #include "../../include/fst_exact_math.h"
 
@@ -37,61 +39,65 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t b) {
 
 // ---------------------------------------------------------------- router
 
-// One wave per expert: lane j owns the contiguous K/64 chunk j, sums it with a
-// sequential fmaf chain, then the 64 partials are combined by the halving
-// tree p[j] += p[j+off] (off = 32..1) that lane 0 sees through shfl_down.
-template <int CH>
+// One wave per (expert, pair of tokens): lane j owns the contiguous K/64
+// chunk j, sums it with a sequential fmaf chain, then the 64 partials are
+// combined by the halving tree p[j] += p[j+off] (off = 32..1) that lane 0
+// sees through shfl_down.  All loads of a wave are issued before the math.
+template <int CH, int TPW>
 __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ w_nk,
                                                             const uint16_t* __restrict__ h, int M,
                                                             int K, int E, float* __restrict__ logits) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int e = blockIdx.x * 4 + wave;
+    const int t0 = blockIdx.y * TPW;
     if (e >= E) return;
-    float wv[CH];
+    uint4 wq[CH / 8], xq[TPW][CH / 8];
     const uint4* wp = reinterpret_cast<const uint4*>(w_nk + (size_t)e * K + (size_t)lane * CH);
 #pragma unroll
-    for (int i = 0; i < CH / 8; ++i) {
-        uint4 u = wp[i];
-        uint32_t q[4] = {u.x, u.y, u.z, u.w};
+    for (int i = 0; i < CH / 8; ++i) wq[i] = wp[i];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            wv[8 * i + 2 * k] = fst_bits_f32(q[k] << 16);
-            wv[8 * i + 2 * k + 1] = fst_bits_f32(q[k] & 0xffff0000u);
+    for (int t = 0; t < TPW; ++t) {
+        if (t0 + t < M) {
+            const uint4* xp = reinterpret_cast<const uint4*>(h + (size_t)(t0 + t) * K + (size_t)lane * CH);
+#pragma unroll
+            for (int i = 0; i < CH / 8; ++i) xq[t][i] = xp[i];
         }
     }
-    for (int t = 0; t < M; ++t) {
-        const uint4* xp = reinterpret_cast<const uint4*>(h + (size_t)t * K + (size_t)lane * CH);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        if (t0 + t >= M) continue;
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < CH / 8; ++i) {
-            uint4 u = xp[i];
-            uint32_t q[4] = {u.x, u.y, u.z, u.w};
+            const uint32_t wv[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+            const uint32_t xv[4] = {xq[t][i].x, xq[t][i].y, xq[t][i].z, xq[t][i].w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                acc = fmaf(fst_bits_f32(q[k] << 16), wv[8 * i + 2 * k], acc);
-                acc = fmaf(fst_bits_f32(q[k] & 0xffff0000u), wv[8 * i + 2 * k + 1], acc);
+                acc = fmaf(fst_bits_f32(xv[k] << 16), fst_bits_f32(wv[k] << 16), acc);
+                acc = fmaf(fst_bits_f32(xv[k] & 0xffff0000u), fst_bits_f32(wv[k] & 0xffff0000u), acc);
             }
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_down(acc, off, 64);
-        if (lane == 0) logits[(size_t)t * E + e] = acc;
+        if (lane == 0) logits[(size_t)(t0 + t) * E + e] = acc;
     }
 }
 
 void launch_router_logits(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h,
                           int M, float* logits) {
-    dim3 grid((g.E + 3) / 4);
+    constexpr int TPW = 2;
+    dim3 grid((g.E + 3) / 4, (M + TPW - 1) / TPW);
     if (g.hd == 4096)
-        hipLaunchKernelGGL(router_logits_kernel<64>, grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
+        hipLaunchKernelGGL((router_logits_kernel<64, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
                            g.E, logits);
     else if (g.hd == 2048)
-        hipLaunchKernelGGL(router_logits_kernel<32>, grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
+        hipLaunchKernelGGL((router_logits_kernel<32, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
                            g.E, logits);
     else if (g.hd == 1024)
-        hipLaunchKernelGGL(router_logits_kernel<16>, grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
+        hipLaunchKernelGGL((router_logits_kernel<16, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
                            g.E, logits);
     else
-        hipLaunchKernelGGL(router_logits_kernel<8>, grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
+        hipLaunchKernelGGL((router_logits_kernel<8, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
                            g.E, logits);
 }
 
@@ -113,158 +119,172 @@ __device__ __forceinline__ bool cand_better(const Cand& a, const Cand& b) {
 
 constexpr int kMaxExperts = 1024;
 
-// Single workgroup of 256 threads.  Part A: per-token top-k and weights
-// (src/fst_engine.cpp:974-1061 semantics; ties toward the lower expert id).
-// Part B: (token, expert) pairs grouped by expert in ascending expert id,
-// tokens ascending within an expert; the shared expert gets the last slot.
-__global__ __launch_bounds__(256) void route_bucket_kernel(
-    int M, int E, int tk, int score_func, int round_bf16, float route_scale,
-    const float* __restrict__ logits, const float* __restrict__ bias,
-    const int32_t* __restrict__ hash, const int32_t* __restrict__ ids, int vocab, int do_topk,
-    int use_shared, int32_t* __restrict__ eids, float* __restrict__ wts, int* __restrict__ meta,
-    int* __restrict__ slot_eid, int* __restrict__ slot_M, int* __restrict__ slot_off,
-    int* __restrict__ pair_tok, int* __restrict__ pair_of, int* __restrict__ pair_shared) {
+// One wave per token: top-k and weights (src/fst_engine.cpp:974-1061
+// semantics; ties toward the lower expert id, NaN scores last), or the hash
+// table row for hash-routed layers (:1015-1021).
+__global__ __launch_bounds__(64) void topk_kernel(int E, int tk, int score_func, int round_bf16,
+                                                  float route_scale, const float* __restrict__ logits,
+                                                  const float* __restrict__ bias,
+                                                  const int32_t* __restrict__ hash,
+                                                  const int32_t* __restrict__ ids, int vocab,
+                                                  int32_t* __restrict__ eids, float* __restrict__ wts,
+                                                  int* __restrict__ meta) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float* row = logits + (size_t)t * E;
+    if (hash) {
+        if (lane == 0) {
+            const int tok = ids ? ids[t] : -1;
+            if (tok < 0 || tok >= vocab) {
+                atomicOr(&meta[META_TOPK_ERROR], 2);
+                for (int k = 0; k < tk; ++k) {
+                    eids[(size_t)t * tk + k] = -1;
+                    wts[(size_t)t * tk + k] = 0.0f;
+                }
+                return;
+            }
+            float sc[kMaxTopK];
+            float sum = 0.0f;
+            for (int k = 0; k < tk; ++k) {
+                const int e = hash[(size_t)tok * tk + k];
+                float x = (e >= 0 && e < E) ? row[e] : 0.0f;
+                if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
+                sc[k] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+                sum += sc[k];
+                eids[(size_t)t * tk + k] = e;
+            }
+            const float inv = 1.0f / (sum + 1e-12f);
+            for (int k = 0; k < tk; ++k) wts[(size_t)t * tk + k] = sc[k] * inv * route_scale;
+        }
+        return;
+    }
+    constexpr int PER = kMaxExperts / 64;
+    Cand c[PER];
+    const int nper = (E + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        c[i].id = 0x7fffffff;
+        c[i].sel = 0.0f;
+        c[i].score = 0.0f;
+        if (i < nper && e < E) {
+            float x = row[e];
+            if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
+            const float s = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+            c[i].score = s;
+            c[i].sel = s + (bias ? bias[e] : 0.0f);
+            c[i].id = e;
+        }
+    }
+    float chosen_sc = 0.0f;
+    int chosen_id = 0;
+    float sum = 0.0f;
+    for (int k = 0; k < tk; ++k) {
+        Cand b;
+        b.id = 0x7fffffff;
+        b.sel = 0.0f;
+        b.score = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (i < nper && cand_better(c[i], b)) b = c[i];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            Cand o;
+            o.sel = __shfl_xor(b.sel, off, 64);
+            o.score = __shfl_xor(b.score, off, 64);
+            o.id = __shfl_xor(b.id, off, 64);
+            if (cand_better(o, b)) b = o;
+        }
+        if (lane == k) {
+            chosen_sc = b.score;
+            chosen_id = b.id;
+        }
+        sum += b.score;  // same sequential order in every lane
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (c[i].id == b.id) c[i].id = 0x7fffffff;
+    }
+    if (lane < tk) {
+        const float inv = 1.0f / (sum + 1e-12f);
+        eids[(size_t)t * tk + lane] = chosen_id;
+        wts[(size_t)t * tk + lane] = chosen_sc * inv * route_scale;
+    }
+}
+
+// Single workgroup: (token, expert) pairs grouped by expert in ascending
+// expert id, tokens ascending within an expert; the shared expert gets the
+// last slot with all M tokens.
+__global__ __launch_bounds__(256) void bucket_kernel(int M, int E, int tk, int use_shared,
+                                                     const int32_t* __restrict__ eids,
+                                                     int* __restrict__ meta, int* __restrict__ slot_eid,
+                                                     int* __restrict__ slot_M, int* __restrict__ slot_off,
+                                                     int* __restrict__ pair_tok, int* __restrict__ pair_of,
+                                                     int* __restrict__ pair_shared) {
     __shared__ unsigned long long hitmask[kMaxExperts];
     __shared__ int eoff[kMaxExperts];
     __shared__ int wave_tot[2][4];
     __shared__ int err;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (tid == 0) err = 0;
-
-    if (do_topk) {
-        for (int t = wave; t < M; t += 4) {
-            const float* row = logits + (size_t)t * E;
-            if (hash) {
-                int tok = ids ? ids[t] : -1;
-                if (lane == 0) {
-                    if (tok < 0 || tok >= vocab) {
-                        atomicOr(&err, 2);
-                        for (int k = 0; k < tk; ++k) {
-                            eids[(size_t)t * tk + k] = -1;
-                            wts[(size_t)t * tk + k] = 0.0f;
-                        }
-                    } else {
-                        float sc[kMaxTopK];
-                        float sum = 0.0f;
-                        for (int k = 0; k < tk; ++k) {
-                            int e = hash[(size_t)tok * tk + k];
-                            float x = (e >= 0 && e < E) ? row[e] : 0.0f;
-                            if (e < 0 || e >= E) atomicOr(&err, 1);
-                            if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
-                            sc[k] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
-                            sum += sc[k];
-                            eids[(size_t)t * tk + k] = e;
-                        }
-                        float inv = 1.0f / (sum + 1e-12f);
-                        for (int k = 0; k < tk; ++k) wts[(size_t)t * tk + k] = sc[k] * inv * route_scale;
-                    }
-                }
-                continue;
-            }
-            constexpr int PER = kMaxExperts / 64;
-            Cand c[PER];
-            int nper = (E + 63) / 64;
-#pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                int e = lane + 64 * i;
-                c[i].id = 0x7fffffff;
-                if (i < nper && e < E) {
-                    float x = row[e];
-                    if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
-                    float s = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
-                    c[i].score = s;
-                    c[i].sel = s + (bias ? bias[e] : 0.0f);
-                    c[i].id = e;
-                }
-            }
-            float chosen_sc[kMaxTopK];
-            int chosen_id[kMaxTopK];
-            for (int k = 0; k < tk; ++k) {
-                Cand b;
-                b.id = 0x7fffffff;
-                b.sel = 0.0f;
-                b.score = 0.0f;
-#pragma unroll
-                for (int i = 0; i < PER; ++i)
-                    if (cand_better(c[i], b)) b = c[i];
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) {
-                    Cand o;
-                    o.sel = __shfl_xor(b.sel, off, 64);
-                    o.score = __shfl_xor(b.score, off, 64);
-                    o.id = __shfl_xor(b.id, off, 64);
-                    if (cand_better(o, b)) b = o;
-                }
-                chosen_sc[k] = b.score;
-                chosen_id[k] = b.id;
-#pragma unroll
-                for (int i = 0; i < PER; ++i)
-                    if (c[i].id == b.id) c[i].id = 0x7fffffff;
-            }
-            if (lane == 0) {
-                float sum = 0.0f;
-                for (int k = 0; k < tk; ++k) sum += chosen_sc[k];
-                float inv = 1.0f / (sum + 1e-12f);
-                for (int k = 0; k < tk; ++k) {
-                    eids[(size_t)t * tk + k] = chosen_id[k];
-                    wts[(size_t)t * tk + k] = chosen_sc[k] * inv * route_scale;
-                }
-            }
-        }
-        __threadfence_block();
-    }
     for (int e = tid; e < E; e += 256) hitmask[e] = 0ull;
     __syncthreads();
     for (int i = tid; i < M * tk; i += 256) {
-        int t = i / tk;
-        int e = eids[i];
+        const int t = i / tk;
+        const int e = eids[i];
         if (e < 0 || e >= E)
             atomicOr(&err, 1);
         else
             atomicOr(&hitmask[e], 1ull << t);
     }
     __syncthreads();
-    // exclusive scans over experts of (active) and (count), 256 experts per pass
     int slot_base = 0, pair_base = 0;
     for (int e0 = 0; e0 < E; e0 += 256) {
-        int e = e0 + tid;
-        int cnt = (e < E) ? __popcll(hitmask[e]) : 0;
-        int act = cnt > 0;
+        const int e = e0 + tid;
+        const int cnt = (e < E) ? __popcll(hitmask[e]) : 0;
+        const int act = cnt > 0;
         int sa = act, sc = cnt;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            int ua = __shfl_up(sa, off, 64), uc = __shfl_up(sc, off, 64);
-            if (lane >= off) { sa += ua; sc += uc; }
+            const int ua = __shfl_up(sa, off, 64), uc = __shfl_up(sc, off, 64);
+            if (lane >= off) {
+                sa += ua;
+                sc += uc;
+            }
         }
-        if (lane == 63) { wave_tot[0][wave] = sa; wave_tot[1][wave] = sc; }
+        if (lane == 63) {
+            wave_tot[0][wave] = sa;
+            wave_tot[1][wave] = sc;
+        }
         __syncthreads();
         int pa = slot_base, pc = pair_base;
-        for (int w = 0; w < wave; ++w) { pa += wave_tot[0][w]; pc += wave_tot[1][w]; }
-        int ex_a = pa + sa - act, ex_c = pc + sc - cnt;
+        for (int w = 0; w < wave; ++w) {
+            pa += wave_tot[0][w];
+            pc += wave_tot[1][w];
+        }
+        const int ex_a = pa + sa - act, ex_c = pc + sc - cnt;
         if (act) {
             slot_eid[ex_a] = e;
             slot_M[ex_a] = cnt;
             slot_off[ex_a] = ex_c;
-            unsigned long long mk = hitmask[e];
-            int r = 0;
-            while (mk) {
-                int t = __ffsll((long long)mk) - 1;
-                pair_tok[ex_c + r] = t;
-                ++r;
-                mk &= mk - 1;
-            }
         }
         if (e < E) eoff[e] = ex_c;
         int tot_a = 0, tot_c = 0;
-        for (int w = 0; w < 4; ++w) { tot_a += wave_tot[0][w]; tot_c += wave_tot[1][w]; }
+        for (int w = 0; w < 4; ++w) {
+            tot_a += wave_tot[0][w];
+            tot_c += wave_tot[1][w];
+        }
         slot_base += tot_a;
         pair_base += tot_c;
         __syncthreads();
     }
     for (int i = tid; i < M * tk; i += 256) {
-        int t = i / tk;
-        int e = eids[i];
-        pair_of[i] = (e >= 0 && e < E) ? eoff[e] + __popcll(hitmask[e] & ((1ull << t) - 1ull)) : -1;
+        const int t = i / tk;
+        const int e = eids[i];
+        int p = -1;
+        if (e >= 0 && e < E) {
+            p = eoff[e] + __popcll(hitmask[e] & ((1ull << t) - 1ull));
+            pair_tok[p] = t;
+        }
+        pair_of[i] = p;
     }
     if (use_shared) {
         for (int t = tid; t < M; t += 256) {
@@ -283,42 +303,61 @@ __global__ __launch_bounds__(256) void route_bucket_kernel(
         meta[META_N_SLOTS] = slot_base + (use_shared ? 1 : 0);
         meta[META_N_ROUTED_PAIRS] = pair_base;
         meta[META_N_PAIRS] = pair_base + (use_shared ? M : 0);
-        meta[META_ERROR] = err;
+        meta[META_ERROR] = err | meta[META_TOPK_ERROR];
+        meta[META_TOPK_ERROR] = 0;
     }
 }
 
 void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, int M,
                          const float* logits, const int32_t* input_ids, int use_hash, int do_topk,
                          int use_shared, int32_t* eids, float* wts, const Scratch& s) {
-    hipLaunchKernelGGL(route_bucket_kernel, dim3(1), dim3(256), 0, st, M, g.E, g.tk, g.score_func,
-                       g.round_logits_bf16, g.route_scale, logits, L.router_bias,
-                       use_hash ? L.hash : nullptr, input_ids, g.vocab, do_topk, use_shared, eids, wts,
-                       s.meta, s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared);
+    if (do_topk)
+        hipLaunchKernelGGL(topk_kernel, dim3(M), dim3(64), 0, st, g.E, g.tk, g.score_func,
+                           g.round_logits_bf16, g.route_scale, logits, L.router_bias,
+                           use_hash ? L.hash : nullptr, input_ids, g.vocab, eids, wts, s.meta);
+    hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(256), 0, st, M, g.E, g.tk, use_shared, eids, s.meta,
+                       s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared);
 }
 
 // -------------------------------------------------------------- operand prep
 
-__device__ __forceinline__ float load_elem(const uint16_t* p, size_t i) {
-    return fst_bf16_to_f32(p[i]);
-}
-__device__ __forceinline__ float load_elem(const float* p, size_t i) { return p[i]; }
+// Element sources for the prep kernel: bf16 activations, or the SwiGLU of a
+// gate||up row (act[i] = silu(g[i]) * u[i], g = row[i], u = row[K + i]).
+struct SrcBf16 {
+    const uint16_t* p;
+    __device__ __forceinline__ float at(size_t row, int K, int i) const {
+        return fst_bf16_to_f32(p[row * K + i]);
+    }
+};
+struct SrcSwiGLU {
+    const float* p;
+    float lim;
+    __device__ __forceinline__ float at(size_t row, int K, int i) const {
+        float g = p[row * 2 * K + i], u = p[row * 2 * K + K + i];
+        if (lim > 0.0f) {
+            g = fminf(g, lim);
+            u = fminf(fmaxf(u, -lim), lim);
+        }
+        return (g / (1.0f + expf(-g))) * u;
+    }
+};
 
 // Per row: amax -> exponent s so that amax*2^-s lies in [2^9, 2^10); then the
 // k-interleaved fp16 operand (per super-block, lane group g, MFMA c: elements
-// 64g+4c+{0..3} and 64g+32+4c+{0..3}) and per-sub-block sums split hi+lo.
-template <typename T>
-__global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ x, const int* __restrict__ nrows_dev,
-                                                   int nrows_host, int K, _Float16* __restrict__ x16p,
+// 64g+4c+{0,2,1,3} and 64g+32+4c+{0,2,1,3}, the order q4k_bop produces the
+// weights in) and per-sub-block sums split hi+lo.
+template <typename Src>
+__global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restrict__ nrows_dev, int nrows_host,
+                                                   int K, _Float16* __restrict__ x16p,
                                                    uint4* __restrict__ sxp, int* __restrict__ xs) {
     const int row = blockIdx.x;
     const int nrows = nrows_dev ? nrows_dev[0] : nrows_host;
     if (row >= nrows) return;
     __shared__ float red[4];
     __shared__ int s_sh;
-    const T* xr = x + (size_t)row * K;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float m = 0.0f;
-    for (int i = tid; i < K; i += 256) m = fmaxf(m, fabsf(load_elem(xr, i)));
+    for (int i = tid; i < K; i += 256) m = fmaxf(m, fabsf(src.at(row, K, i)));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if (lane == 0) red[wave] = m;
@@ -340,12 +379,13 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ x, cons
     const int nchunk = K / 8;
     for (int q = tid; q < nchunk; q += 256) {
         int sb = q >> 5, gc = q & 31, g = gc >> 3, c = gc & 7;
-        size_t base = (size_t)sb * 256 + 64 * g + 4 * c;
+        int base = sb * 256 + 64 * g + 4 * c;
         h8_t v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            v[i] = (_Float16)ldexpf(load_elem(xr, base + i), -s);
-            v[4 + i] = (_Float16)ldexpf(load_elem(xr, base + 32 + i), -s);
+            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;  // nibble pair order of q4k_bop
+            v[i] = (_Float16)ldexpf(src.at(row, K, base + e), -s);
+            v[4 + i] = (_Float16)ldexpf(src.at(row, K, base + 32 + e), -s);
         }
         *reinterpret_cast<h8_t*>(dst + (size_t)q * 8) = v;
     }
@@ -354,7 +394,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ x, cons
     uint16_t* sx16 = reinterpret_cast<uint16_t*>(sxp + (size_t)row * (K / 256) * 4);
     for (int j = tid; j < nsub; j += 256) {
         float S = 0.0f;
-        for (int i = 0; i < 32; ++i) S += (float)(_Float16)ldexpf(load_elem(xr, (size_t)j * 32 + i), -s);
+        for (int i = 0; i < 32; ++i) S += (float)(_Float16)ldexpf(src.at(row, K, j * 32 + i), -s);
         _Float16 hi = (_Float16)S;
         _Float16 lo = (_Float16)(S - (float)hi);
         int sb = j >> 3, jj = j & 7, g = jj >> 1, odd = jj & 1;
@@ -367,29 +407,31 @@ __global__ __launch_bounds__(256) void prep_kernel(const T* __restrict__ x, cons
 
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p, uint4* sxp,
                       int* xs) {
-    hipLaunchKernelGGL(prep_kernel<uint16_t>, dim3(rows), dim3(256), 0, st, x, nullptr, rows, K, x16p,
-                       sxp, xs);
+    hipLaunchKernelGGL(prep_kernel<SrcBf16>, dim3(rows), dim3(256), 0, st, SrcBf16{x}, nullptr, rows, K,
+                       x16p, sxp, xs);
 }
-void launch_prep_act(hipStream_t st, const float* act, const int* meta, int max_rows, int K,
-                     _Float16* a16p, uint4* sxp, int* xs) {
-    hipLaunchKernelGGL(prep_kernel<float>, dim3(max_rows), dim3(256), 0, st, act, meta + META_N_PAIRS,
-                       max_rows, K, a16p, sxp, xs);
+void launch_prep_act(hipStream_t st, const float* gu, float swiglu_limit, const int* meta, int max_rows,
+                     int K, _Float16* a16p, uint4* sxp, int* xs) {
+    hipLaunchKernelGGL(prep_kernel<SrcSwiGLU>, dim3(max_rows), dim3(256), 0, st, SrcSwiGLU{gu, swiglu_limit},
+                       meta + META_N_PAIRS, max_rows, K, a16p, sxp, xs);
 }
 
-// ---------------------------------------------------------- Q4_K FFN kernel
+// ------------------------------------------------------- Q4_K linear kernel
 
-struct Q4kB {
-    h8_t w[8];  // sc*q as fp16, 8 MFMA B operands (one per 8-column chunk c)
-    h8_t m;     // {m_a, m_b, m_a, m_b, 0...}
+// Per-lane decode of one super-block row slice.  Lane (row r = lane&15, group
+// g = lane>>4) owns qs bytes [32g, 32g+32): low nibbles are sub-block 2g,
+// high nibbles 2g+1; B operand c holds elements 64g+4c+{0,2,1,3}, 64g+32+4c+{0,2,1,3}.
+typedef uint32_t u4v_t __attribute__((ext_vector_type(4)));
+
+struct Q4kScale {
+    h8_t SC8, NEG8;  // {sc_a x4, sc_b/16 x4}, {-1024 sc_a x4, -64 sc_b x4}
+    h8_t m;
     float d, dmin;
 };
 
-// Lane (row r = lane&15, group g = lane>>4) owns qs bytes [32g, 32g+32) of the
-// row's super-block: low nibbles are sub-block 2g, high nibbles 2g+1.
-__device__ __forceinline__ void q4k_build(const uint4 hdr, const uint4 qa, const uint4 qb, int g,
-                                          Q4kB& B) {
-    B.d = half_bits_to_f32(hdr.x & 0xffffu);
-    B.dmin = half_bits_to_f32(hdr.x >> 16);
+__device__ __forceinline__ void q4k_scales(const uint4 hdr, int g, Q4kScale& S) {
+    S.d = half_bits_to_f32(hdr.x & 0xffffu);
+    S.dmin = half_bits_to_f32(hdr.x >> 16);
     const uint32_t y = hdr.y, z = hdr.z, w = hdr.w;
     // get_scale_min_k4 for all 8 sub-blocks, byte-parallel
     const uint32_t sc_lo = y & 0x3F3F3F3Fu, m_lo = z & 0x3F3F3F3Fu;
@@ -403,116 +445,202 @@ __device__ __forceinline__ void q4k_build(const uint4 hdr, const uint4 qa, const
     const _Float16 mb = (_Float16)(float)((MM >> (sh + 8)) & 0xffu);
     const _Float16 fa = (_Float16)sca, na = (_Float16)(-1024.0f * sca);
     const _Float16 fb = (_Float16)(scb * 0.0625f), nb = (_Float16)(-64.0f * scb);
-    const h2_t SCA = {fa, fa}, NEGA = {na, na}, SCB = {fb, fb}, NEGB = {nb, nb};
-    const uint32_t D[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const uint32_t E0 = __builtin_amdgcn_perm(0u, D[c], 0x0C010C00u);  // [0,b1,0,b0]
-        const uint32_t E1 = __builtin_amdgcn_perm(0u, D[c], 0x0C030C02u);  // [0,b3,0,b2]
-        const h2_t l0 = __builtin_elementwise_fma(as_h2((E0 & 0x000F000Fu) | 0x64006400u), SCA, NEGA);
-        const h2_t l1 = __builtin_elementwise_fma(as_h2((E1 & 0x000F000Fu) | 0x64006400u), SCA, NEGA);
-        const h2_t u0 = __builtin_elementwise_fma(as_h2((E0 & 0x00F000F0u) | 0x64006400u), SCB, NEGB);
-        const h2_t u1 = __builtin_elementwise_fma(as_h2((E1 & 0x00F000F0u) | 0x64006400u), SCB, NEGB);
-        B.w[c] = h8_t{l0.x, l0.y, l1.x, l1.y, u0.x, u0.y, u1.x, u1.y};
-    }
+    S.SC8 = h8_t{fa, fa, fa, fa, fb, fb, fb, fb};
+    S.NEG8 = h8_t{na, na, na, na, nb, nb, nb, nb};
     const _Float16 z0 = (_Float16)0.0f;
-    B.m = h8_t{ma, mb, ma, mb, z0, z0, z0, z0};
+    S.m = h8_t{ma, mb, ma, mb, z0, z0, z0, z0};
 }
 
-// Grid: (max_slots * N/64) workgroups of 4 waves; wave w of tile T computes rows
-// T*64 + w*16 .. +15 of NPROJ projections for all tokens of its slot (expert).
-// MODE 0: gate/up, epilogue silu(g)*u.  MODE 1: down, epilogue scaling.
-template <int NPROJ, int NGRP, int MODE>
-__global__ __launch_bounds__(256) void q4k_ffn_kernel(
-    const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, size_t proj_stride,
-    int K, int N, const int* __restrict__ meta, const int* __restrict__ slot_eid,
-    const int* __restrict__ slot_M, const int* __restrict__ slot_off, const int* __restrict__ a_row,
-    const _Float16* __restrict__ A, const uint4* __restrict__ SX, const int* __restrict__ xs,
-    float* __restrict__ out, float swiglu_limit) {
-    const int tiles = N >> 6;
+// Exact fp16 sc*q for the 8 weights held in one dword D = [b3 b2 b1 b0] of
+// nibble bytes.  (x & m) | MAGIC (one v_and_or_b32) turns a nibble pair into
+// fp16 (1024 + q) (low nibbles) or (1024 + 16q) (high nibbles); one
+// v_pk_fma_f16 then gives (1024+q)*sc - 1024*sc = q*sc exactly (<= 945).
+// Slot order of the result: elements {0,2,1,3} of the low nibbles, then
+// {0,2,1,3} of the high nibbles (the activation operand is laid out to match).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
+    return r;
+}
+
+__device__ __forceinline__ h8_t q4k_bop(uint32_t D, const Q4kScale& S, uint32_t magic) {
+    const uint32_t D8 = D >> 8;
+    const u4v_t X = {and_or(D, 0x000F000Fu, magic), and_or(D8, 0x000F000Fu, magic),
+                     and_or(D, 0x00F000F0u, magic), and_or(D8, 0x00F000F0u, magic)};
+    return __builtin_elementwise_fma(__builtin_bit_cast(h8_t, X), S.SC8, S.NEG8);
+}
+
+struct WRaw {
+    uint4 h, a, b;
+};
+
+__device__ __forceinline__ uint4 ld_stream(const uint8_t* p) {
+    const u4v_t v = __builtin_nontemporal_load(reinterpret_cast<const u4v_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// One 2304-byte chunk = 16 rows x one super-block: [0,1024) nibble bytes
+// [32g, 32g+16) of row r at lane slot 16g+r, [1024,2048) bytes [32g+16,
+// 32g+32), [2048,2304) the 16-byte headers (d, dmin, scales) of rows 0..15.
+// Each of the three loads is one contiguous span across the wave.
+__device__ __forceinline__ WRaw load_wraw(const uint8_t* chunk, int lane) {
+    WRaw w;
+    w.a = ld_stream(chunk + 16 * lane);
+    w.b = ld_stream(chunk + 1024 + 16 * lane);
+    w.h = ld_stream(chunk + 2048 + 16 * (lane & 15));
+    return w;
+}
+
+// LDS activation stage: per token 36 uint4 (32 operand chunks, 4 min-term
+// chunks), padded to kTokStride to spread banks.
+constexpr int kTokStride = 37;
+
+// Y[pair][row] = 2^xs[a] * sum_k W[row][k] * A[a][k] for the rows of one
+// Q4_K matrix (N rows x K/256 super-blocks per row) of the slot's expert.
+// Grid: max_slots * N/64 workgroups of 4 waves; wave w of tile T owns rows
+// T*64 + 16w .. +15 and all tokens of its slot.  Weights stream through
+// registers two super-blocks ahead (ping-pong pair, loop unrolled by two);
+// the slot's activation operands are staged per super-block in a
+// double-buffered LDS ring shared by the 4 waves.
+#ifndef FST_Q4K_WAVES_PER_EU
+#define FST_Q4K_WAVES_PER_EU 3
+#endif
+#ifndef FST_Q4K_PF
+#define FST_Q4K_PF 2
+#endif
+// Y[pair][row] = 2^xs[a] * sum_k W[row][k] * A[a][k] for the rows of one
+// Q4_K matrix (N rows x K/256 super-blocks per row) of the slot's expert.
+// Grid: max_slots * N/(16*WAVES) workgroups; wave w of tile T owns rows
+// (T*WAVES + w)*16 .. +15 and up to TOKS tokens of its slot.
+//  - weights stream through a ring of PF+1 register sets (PF super-blocks
+//    ahead), the ring unrolled so each set keeps fixed registers;
+//  - the slot's activation operands are staged into LDS in macro-stages of MS
+//    super-blocks (double-buffered, prefetched one macro-stage ahead into
+//    registers), one workgroup barrier per macro-stage.
+template <int TOKS, int MS, int WAVES = 4, int PF = FST_Q4K_PF>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_Q4K_WAVES_PER_EU))) void q4k_linear_kernel(
+    const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
+    const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
+    const int* __restrict__ slot_off, const int* __restrict__ a_row, const _Float16* __restrict__ A,
+    const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out) {
+    constexpr int NGRP = (TOKS + 15) / 16;
+    constexpr int TS = TOKS * kTokStride;            // one super-block of one stage
+    constexpr int STAGE = MS * TS;                   // one macro-stage
+    constexpr int NCH = MS * TOKS * 36;              // 16-byte chunks per macro-stage
+    constexpr int NT = 64 * WAVES;                   // threads per workgroup
+    constexpr int NS = (NCH + NT - 1) / NT;          // staged chunks per thread
+    __shared__ uint4 lds[2 * STAGE];
+
+    const int tiles = N / (16 * WAVES);
     const int slot = blockIdx.x / tiles;
     const int tile = blockIdx.x - slot * tiles;
     if (slot >= meta[META_N_SLOTS]) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, g = lane >> 4;
-    const int Me = slot_M[slot], off = slot_off[slot];
-    const int row = tile * 64 + wave * 16 + r;
+    const int Me = min(slot_M[slot], TOKS), off = slot_off[slot];
+    const int row = (tile * WAVES + wave) * 16 + r;
     const int nsb = K >> 8;
-    const size_t rowbytes = (size_t)nsb * 144;
-    const uint8_t* wbase =
-        bank + (size_t)slot_eid[slot] * expert_stride + mat_offset + (size_t)row * rowbytes;
+    const int nms = (nsb + MS - 1) / MS;
+    // wave-tiled device layout (see repack_q4k_matrix): the wave's 16 rows are
+    // one contiguous run of nsb 2304-byte chunks read front to back
+    const uint8_t* wbase = bank + (size_t)slot_eid[slot] * expert_stride + mat_offset +
+                           (size_t)(tile * WAVES + wave) * nsb * 2304;
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
 
-    const h8_t* arow[NGRP];
-    const uint4* sxrow[NGRP];
-    bool aval[NGRP];
+    WRaw w[PF + 1];
 #pragma unroll
-    for (int q = 0; q < NGRP; ++q) {
-        const int tl = q * 16 + r;
-        aval[q] = tl < Me;
-        int ar = 0;
-        if (aval[q]) ar = a_row ? a_row[off + tl] : off + tl;
-        arow[q] = reinterpret_cast<const h8_t*>(A + (size_t)ar * K) + g * 8;
-        sxrow[q] = SX + (size_t)ar * nsb * 4 + g;
-    }
+    for (int j = 0; j < PF; ++j) w[j] = load_wraw(wbase + (size_t)min(j, nsb - 1) * 2304, lane);
 
-    f4_t acc[NPROJ][NGRP];
+    for (int i = tid; i < 2 * STAGE; i += NT) lds[i] = z4;
+    // staging map: chunk q of a macro-stage -> (super-block u, token tl, part)
+    const uint4* ssrc[NS];
+    int sdst[NS];
+    int sstep[NS];
+    int su[NS];
+    uint4 sv[NS];
 #pragma unroll
-    for (int p = 0; p < NPROJ; ++p)
-#pragma unroll
-        for (int q = 0; q < NGRP; ++q) acc[p][q] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-    uint4 nh[NPROJ], na[NPROJ], nb[NPROJ];
-#pragma unroll
-    for (int p = 0; p < NPROJ; ++p) {
-        const uint8_t* blk = wbase + p * proj_stride;
-        nh[p] = *reinterpret_cast<const uint4*>(blk);
-        na[p] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g);
-        nb[p] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * g);
-    }
-    const h8_t hz = h8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    for (int sb = 0; sb < nsb; ++sb) {
-        uint4 ch[NPROJ], ca[NPROJ], cb[NPROJ];
-#pragma unroll
-        for (int p = 0; p < NPROJ; ++p) { ch[p] = nh[p]; ca[p] = na[p]; cb[p] = nb[p]; }
-        if (sb + 1 < nsb) {
-#pragma unroll
-            for (int p = 0; p < NPROJ; ++p) {
-                const uint8_t* blk = wbase + p * proj_stride + (size_t)(sb + 1) * 144;
-                nh[p] = *reinterpret_cast<const uint4*>(blk);
-                na[p] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g);
-                nb[p] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * g);
+    for (int i = 0; i < NS; ++i) {
+        const int q = tid + NT * i;
+        const int u = q / (TOKS * 36), rem = q - u * (TOKS * 36);
+        const int tl = rem / 36, part = rem - tl * 36;
+        ssrc[i] = SX;
+        sdst[i] = -1;
+        sstep[i] = 0;
+        su[i] = u;
+        sv[i] = z4;
+        if (q < NCH && tl < Me) {
+            const int ar = a_row ? a_row[off + tl] : off + tl;
+            if (part < 32) {
+                ssrc[i] = reinterpret_cast<const uint4*>(A + (size_t)ar * K) + u * 32 + part;
+                sstep[i] = 32 * MS;
+            } else {
+                ssrc[i] = SX + (size_t)ar * nsb * 4 + u * 4 + (part - 32);
+                sstep[i] = 4 * MS;
             }
+            sdst[i] = u * TS + tl * kTokStride + part;
         }
-        h8_t a[NGRP][8], am[NGRP];
+    }
+    auto stage_load = [&](int m) {
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+            if (sdst[i] >= 0 && m * MS + su[i] < nsb) sv[i] = ssrc[i][(size_t)m * sstep[i]];
+    };
+    auto stage_store = [&](int m) {
+        uint4* dst = lds + (m & 1) * STAGE;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+            if (sdst[i] >= 0) dst[sdst[i]] = sv[i];
+    };
+    stage_load(0);
+    __syncthreads();
+    stage_store(0);
+    __syncthreads();
+
+    f4_t acc[NGRP];
+#pragma unroll
+    for (int q = 0; q < NGRP; ++q) acc[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+    const f4_t zf = f4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t magic = 0x64006400u;
+    const int ngrp_live = (Me + 15) >> 4;
+
+    // One super-block: consume `cur`, refill `nxt` (the set consumed one step
+    // earlier) with sb+PF, compute from the LDS macro-stage holding sb.
+    auto step = [&](int sb, const WRaw& cur, WRaw& nxt) {
+        const int m = sb / MS, u = sb - m * MS;
+        if (u == 0 && m + 1 < nms) stage_load(m + 1);
+        if (sb + PF < nsb) nxt = load_wraw(wbase + (size_t)(sb + PF) * 2304, lane);
+        const uint4* st = lds + (m & 1) * STAGE + u * TS + r * kTokStride;
+        Q4kScale S;
+        q4k_scales(cur.h, g, S);
+        const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
 #pragma unroll
         for (int q = 0; q < NGRP; ++q) {
-            if (q * 16 < Me) {
+            if (q > 0 && q >= ngrp_live) break;
+            const uint4* sq = st + q * 16 * kTokStride;
+            f4_t D = zf;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) a[q][c] = aval[q] ? arow[q][(size_t)sb * 32 + c] : hz;
-                am[q] = aval[q] ? __builtin_bit_cast(h8_t, sxrow[q][(size_t)sb * 4]) : hz;
+            for (int c = 0; c < 8; ++c) {
+                const h8_t a = __builtin_bit_cast(h8_t, sq[8 * g + c]);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, q4k_bop(Dw[c], S, magic), D, 0, 0, 0);
+            }
+            const h8_t am = __builtin_bit_cast(h8_t, sq[32 + g]);
+            const f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, S.m, zf, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[q][i] = fmaf(S.d, D[i], acc[q][i]);
+                acc[q][i] = fmaf(-S.dmin, Dm[i], acc[q][i]);
             }
         }
-#pragma unroll
-        for (int p = 0; p < NPROJ; ++p) {
-            Q4kB B;
-            q4k_build(ch[p], ca[p], cb[p], g, B);
-#pragma unroll
-            for (int q = 0; q < NGRP; ++q) {
-                if (q * 16 < Me) {
-                    f4_t D = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int c = 0; c < 8; ++c)
-                        D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q][c], B.w[c], D, 0, 0, 0);
-                    f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am[q], B.m,
-                                                                     f4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        acc[p][q][i] = fmaf(B.d, D[i], acc[p][q][i]);
-                        acc[p][q][i] = fmaf(-B.dmin, Dm[i], acc[p][q][i]);
-                    }
-                }
-            }
+        if (u == MS - 1 || sb == nsb - 1) {
+            if (m + 1 < nms) stage_store(m + 1);
+            __syncthreads();
         }
+    };
+    // ring of PF+1 register sets, unrolled so every set keeps fixed registers
+    for (int sb0 = 0; sb0 < nsb; sb0 += PF + 1) {
+#pragma unroll
+        for (int j = 0; j <= PF; ++j)
+            if (sb0 + j < nsb) step(sb0 + j, w[j], w[(j + PF) % (PF + 1)]);
     }
 
     // D layout: lane holds token rows 4g+i (i=0..3) of the group, column r.
@@ -525,54 +653,43 @@ __global__ __launch_bounds__(256) void q4k_ffn_kernel(
             if (tl >= Me) continue;
             const int pidx = off + tl;
             const int ar = a_row ? a_row[pidx] : pidx;
-            const int sh = xs[ar];
-            if (MODE == 0) {
-                float gv = ldexpf(acc[0][q][i], sh);
-                float uv = ldexpf(acc[NPROJ - 1][q][i], sh);
-                if (swiglu_limit > 0.0f) {
-                    gv = fminf(gv, swiglu_limit);
-                    uv = fminf(fmaxf(uv, -swiglu_limit), swiglu_limit);
-                }
-                out[(size_t)pidx * N + row] = (gv / (1.0f + expf(-gv))) * uv;
-            } else {
-                out[(size_t)pidx * N + row] = ldexpf(acc[0][q][i], sh);
-            }
+            out[(size_t)pidx * N + row] = ldexpf(acc[q][i], xs[ar]);
         }
     }
 }
 
-template <int NPROJ, int MODE>
-static void launch_q4k(hipStream_t st, int ngrp, dim3 grid, const uint8_t* bank, size_t stride,
-                       size_t mat_off, size_t proj_stride, int K, int N, const Scratch& s,
-                       const int* a_row, const _Float16* A, const uint4* SX, const int* xs, float* out,
-                       float lim) {
-#define FST_Q4K_LAUNCH(NG)                                                                            \
-    hipLaunchKernelGGL((q4k_ffn_kernel<NPROJ, NG, MODE>), grid, dim3(256), 0, st, bank, stride,       \
-                       mat_off, proj_stride, K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, \
-                       SX, xs, out, lim)
-    if (ngrp <= 1)
-        FST_Q4K_LAUNCH(1);
-    else if (ngrp == 2)
-        FST_Q4K_LAUNCH(2);
+// Token capacity of the launch (the call's M bounds every slot's M_e): 8, 16,
+// 32 or 64 tokens; smaller capacities stage more super-blocks per barrier.
+static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
+                              size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
+                              const _Float16* A, const uint4* SX, const int* xs, float* out) {
+    constexpr int W = 8;
+    const dim3 grid(slots * (unsigned)(N / (16 * W)));
+#define FST_Q4K_LAUNCH(T, MSV)                                                                         \
+    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W>), grid, dim3(64 * W), 0, st, bank, stride, mat_off,  \
+                       K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out)
+    if (M <= 8)
+        FST_Q4K_LAUNCH(8, 4);
+    else if (M <= 16)
+        FST_Q4K_LAUNCH(16, 2);
+    else if (M <= 32)
+        FST_Q4K_LAUNCH(32, 1);
     else
-        FST_Q4K_LAUNCH(4);
+        FST_Q4K_LAUNCH(64, 1);
 #undef FST_Q4K_LAUNCH
 }
 
-void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int ngrp,
-                        const Scratch& s) {
-    const size_t proj = (size_t)g.inter * (g.hd / 256) * 144;
-    dim3 grid((unsigned)s.max_slots * (g.inter / 64));
-    launch_q4k<2, 0>(st, ngrp, grid, L.bank, L.expert_stride, 0, proj, g.hd, g.inter, s, s.pair_tok,
-                     s.x16p, s.sxp, s.xs, s.act, g.swiglu_limit);
+// gate||up: the two [inter][hd/256] matrices are contiguous, so they are one
+// 2*inter-row matrix; the SwiGLU is applied by the following prep pass.
+void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
+    launch_q4k_linear(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
+                      s.pair_tok, s.x16p, s.sxp, s.xs, s.act);
 }
 
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int ngrp,
-                     const Scratch& s) {
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
     const size_t proj = (size_t)g.inter * (g.hd / 256) * 144;
-    dim3 grid((unsigned)s.max_slots * (g.hd / 64));
-    launch_q4k<1, 1>(st, ngrp, grid, L.bank, L.expert_stride, 2 * proj, 0, g.inter, g.hd, s, nullptr,
-                     s.a16p, s.sx2p, s.xs2, s.y, 0.0f);
+    launch_q4k_linear(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
+                      nullptr, s.a16p, s.sx2p, s.xs2, s.y);
 }
 
 // ------------------------------------------------------------------ combine
@@ -610,6 +727,20 @@ void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, co
     dim3 grid((g.hd + 255) / 256, M);
     hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, st, M, g.hd, g.tk, use_shared, s.y,
                        s.pair_of, s.pair_shared, wts, out, out_routed, out_shared);
+}
+
+// --------------------------------------------------------------------- copy
+
+__global__ __launch_bounds__(256) void copy_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                   size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+void launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes) {
+    const size_t n16 = bytes / 16;
+    const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 256 * 64);
+    hipLaunchKernelGGL(copy_kernel, dim3(blocks), dim3(256), 0, st, (uint4*)dst, (const uint4*)src, n16);
 }
 
 // ------------------------------------------------------------------ dequant

@@ -152,6 +152,9 @@ typedef struct fst_timings {
 } fst_timings;
 int fst_set_profiling(fst_ctx* ctx, int on);
 int fst_last_timings(fst_ctx* ctx, fst_timings* out);
+/* Plain streaming copy kernel (16-byte vector loads/stores) used to calibrate
+ * hardware byte counters against a known traffic volume.  Asynchronous. */
+int fst_device_copy(fst_ctx* ctx, void* d_dst, const void* d_src, size_t bytes);
 /* Number of distinct routed experts touched by the last MoE call (device -> host copy). */
 int fst_last_active_experts(fst_ctx* ctx, int* n_routed_active);
 
