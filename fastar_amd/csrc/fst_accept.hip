@@ -21,6 +21,9 @@ constexpr int kChunks = 64;
 typedef unsigned __int128 u128;
 
 struct AccWs {
+    int* row_done;            // [R] completion counters (zero between calls)
+    int* seq_done;            // [n_seq]
+    int* pred;                // [R] greedy argmax per row
     float* part_max;          // [R][kChunks]
     int* part_idx;            // [R][kChunks]
     unsigned long long* part_sum;  // [R][kChunks]
@@ -34,6 +37,9 @@ static AccWs carve(void* ws, int n_seq, int k) {
     const int R = n_seq * (k + 1) + n_seq * k;
     char* p = (char*)ws;
     AccWs w;
+    w.row_done = (int*)p; p += align256(sizeof(int) * R);
+    w.seq_done = (int*)p; p += align256(sizeof(int) * n_seq);
+    w.pred = (int*)p; p += align256(sizeof(int) * R);
     w.part_max = (float*)p; p += align256(sizeof(float) * R * kChunks);
     w.part_idx = (int*)p; p += align256(sizeof(int) * R * kChunks);
     w.part_sum = (unsigned long long*)p; p += align256(8ull * R * kChunks);
@@ -45,7 +51,8 @@ static AccWs carve(void* ws, int n_seq, int k) {
 size_t accept_ws_bytes(int n_seq, int k, int V) {
     (void)V;
     const int R = n_seq * (k + 1) + n_seq * k;
-    return align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
+    return align256(sizeof(int) * R) * 2 + align256(sizeof(int) * n_seq) +
+           align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
            align256(8ull * R * kChunks) + align256(16ull * n_seq * kChunks) + align256(64ull * n_seq) +
            256;
 }
@@ -441,14 +448,102 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
     }
 }
 
+// Greedy acceptance in one launch: every (row, chunk) workgroup reduces its
+// chunk; the last workgroup to finish a row reduces the row's 64 partials
+// (argmax with the reference's rules), and the last row to finish a sequence
+// resolves the longest matching prefix and the bonus token.  Counters are
+// re-armed to zero by the workgroup that consumes them.
+__global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict__ target, int k, int V,
+                                                         const int32_t* __restrict__ draft, AccWs w,
+                                                         int32_t* __restrict__ n_acc,
+                                                         int32_t* __restrict__ tokens) {
+    const int c = blockIdx.x, r = blockIdx.y;
+    const float* row = target + (size_t)r * V;
+    const int clen = (V + kChunks - 1) / kChunks;
+    const int b0 = c * clen, b1 = min(V, b0 + clen);
+    float best = 0.0f;
+    int bi = 0x7fffffff;
+    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) {
+        const float l = row[v];
+        if (l != l) continue;
+        if (bi == 0x7fffffff || l > best) { best = l; bi = v; }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ob = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (oi != 0x7fffffff && (bi == 0x7fffffff || ob > best || (ob == best && oi < bi))) {
+            best = ob;
+            bi = oi;
+        }
+    }
+    __shared__ float sm[4];
+    __shared__ int si[4];
+    __shared__ int s_last;
+    if (lane == 0) {
+        sm[wave] = best;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int q = 1; q < 4; ++q)
+            if (si[q] != 0x7fffffff && (bi == 0x7fffffff || sm[q] > best || (sm[q] == best && si[q] < bi))) {
+                best = sm[q];
+                bi = si[q];
+            }
+        st_coherent(&w.part_max[(size_t)r * kChunks + c], best);
+        st_coherent(&w.part_idx[(size_t)r * kChunks + c], bi == 0x7fffffff ? -1 : bi);
+        publish_wait();
+        s_last = signal_add(&w.row_done[r], 1) == kChunks - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x < 64) {
+        float m = ld_coherent(&w.part_max[(size_t)r * kChunks + lane]);
+        int i = ld_coherent(&w.part_idx[(size_t)r * kChunks + lane]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float om = __shfl_xor(m, off, 64);
+            const int oi = __shfl_xor(i, off, 64);
+            if (oi >= 0 && (i < 0 || om > m || (om == m && oi < i))) {
+                m = om;
+                i = oi;
+            }
+        }
+        int seq_last = 0;
+        const int s = r / (k + 1);
+        if (lane == 0) {
+            w.row_done[r] = 0;
+            const float x0 = row[0];
+            st_coherent(&w.pred[r], (x0 != x0 || i < 0) ? 0 : i);
+            publish_wait();
+            seq_last = signal_add(&w.seq_done[s], 1) == k;
+            if (seq_last) w.seq_done[s] = 0;
+        }
+        seq_last = __shfl(seq_last, 0, 64);
+        if (seq_last) {
+            // lane j holds row j's prediction and draft token j; the accepted
+            // length is the first mismatching lane (ballot), the bonus its prediction
+            const int pv = lane <= k ? __hip_atomic_load(&w.pred[s * (k + 1) + lane], __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0;
+            const int dv = lane < k ? draft[s * k + lane] : 0;
+            const unsigned long long match = __ballot(lane < k && pv == dv);
+            const int n = min(k, __ffsll((long long)~match) - 1);
+            const int bonus = __shfl(pv, n, 64);
+            if (lane <= k) tokens[s * (k + 1) + lane] = lane < n ? dv : (lane == n ? bonus : -1);
+            if (lane == 0) n_acc[s] = n;
+        }
+    }
+}
+
 void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k, int V,
                           const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* ws) {
     AccWs w = carve(ws, n_seq, k);
     const int R = n_seq * (k + 1);
-    hipLaunchKernelGGL(acc_stats_kernel, dim3(kChunks, R), dim3(256), 0, st, target, nullptr, R, V, 1.0f,
-                       w.part_max, w.part_idx);
-    hipLaunchKernelGGL(acc_greedy_final_kernel, dim3(n_seq), dim3(64), 0, st, target, k, V, w.part_max,
-                       w.part_idx, draft, n_acc, tokens);
+    hipLaunchKernelGGL(acc_greedy_kernel, dim3(kChunks, R), dim3(256), 0, st, target, k, V, draft, w, n_acc,
+                       tokens);
 }
 
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,

@@ -56,6 +56,7 @@ struct fst_ctx {
     // acceptance staging (grown on demand)
     void* acc_ws = nullptr;
     size_t acc_ws_cap = 0;
+    int acc_ws_nseq = -1, acc_ws_k = -1;  // shape whose counter layout the workspace holds
     float* acc_logits = nullptr;
     size_t acc_logits_cap = 0;
     int32_t* acc_io = nullptr;
@@ -169,6 +170,8 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         return fail(FST_EINVAL, "fst_create: only the Q4_K codec has a fused FFN path");
     if (c.hidden_dim <= 0 || c.hidden_dim % 512 || c.inter_dim <= 0 || c.inter_dim % 256)
         return fail(FST_EINVAL, "fst_create: hidden_dim must be a multiple of 512, inter_dim of 256");
+    if (c.hidden_dim > 8192 || c.inter_dim > 8192)
+        return fail(FST_EINVAL, "fst_create: hidden_dim and inter_dim must be <= 8192");
 
     if (c.n_experts <= 0 || c.n_experts > 1024)
         return fail(FST_EINVAL, "fst_create: n_experts must be in [1, 1024]");
@@ -237,8 +240,12 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.sxp, (size_t)T * (hd / 256) * 4)) || (rc = x->dalloc(&s.xs, T)) ||
         (rc = x->dalloc(&s.act, (size_t)P * 2 * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
-        (rc = x->dalloc(&s.y, (size_t)P * hd)))
+        (rc = x->dalloc(&s.y, (size_t)P * hd)) || (rc = x->dalloc(&s.tok_npairs, T)) ||
+        (rc = x->dalloc(&s.slot_done, S)) || (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 128))))
         return bail(rc);
+    if (hipMemsetAsync(s.slot_done, 0, sizeof(int) * S, x->st) != hipSuccess ||
+        hipMemsetAsync(s.tile_done, 0, sizeof(int) * T * (hd / 128), x->st) != hipSuccess)
+        return bail(fail(FST_EHIP, "hipMemsetAsync(counters) failed"));
     if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));
     x->ev.resize(17);
@@ -429,23 +436,20 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     hipStream_t st = ctx->st;
     ctx->mark_begin();
     if (do_router) {
-        fst::launch_router_logits(st, g, L, d_h, M, ctx->s.logits);
-        ctx->mark("router_logits");
+        fst::launch_router_prep(st, g, L, d_h, M, ctx->s.logits, ctx->s);
+        ctx->mark("router_prep");
     }
     fst::launch_route_bucket(st, g, L, M, ctx->s.logits, d_ids, use_hash, do_router, use_shared, d_eids, d_wts,
                              ctx->s);
     ctx->mark("route_bucket");
-    fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
-    ctx->mark("prep_x");
+    if (!do_router) {
+        fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
+        ctx->mark("prep_x");
+    }
     fst::launch_q4k_gate_up(st, g, L, M, ctx->s);
     ctx->mark("q4k_gate_up");
-    fst::launch_prep_act(st, ctx->s.act, c.swiglu_limit, ctx->s.meta, ctx->s.max_pairs, c.inter_dim,
-                         ctx->s.a16p, ctx->s.sx2p, ctx->s.xs2);
-    ctx->mark("prep_act");
-    fst::launch_q4k_down(st, g, L, M, ctx->s);
+    fst::launch_q4k_down(st, g, L, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared);
     ctx->mark("q4k_down");
-    fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared);
-    ctx->mark("combine");
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;
 }
@@ -555,13 +559,31 @@ int fst_shared_expert(fst_ctx* ctx, int lid, const uint16_t* h, uint16_t* out, i
 
 // ------------------------------------------------------------ acceptance
 
-static int grow(void** p, size_t* cap, size_t need) {
+// Grows a device buffer; a fresh buffer is zero-filled (the acceptance
+// workspace starts with its completion counters at zero).
+static int grow(hipStream_t st, void** p, size_t* cap, size_t need) {
     if (*cap >= need) return FST_OK;
-    if (*p) hipFree(*p);
+    if (*p) {
+        hipStreamSynchronize(st);
+        hipFree(*p);
+    }
     *p = nullptr;
     *cap = 0;
     if (hipMalloc(p, need) != hipSuccess) return fail(FST_ENOMEM, "hipMalloc(acceptance staging) failed");
+    if (hipMemsetAsync(*p, 0, need, st) != hipSuccess) return fail(FST_EHIP, "hipMemsetAsync failed");
     *cap = need;
+    return FST_OK;
+}
+
+// The acceptance workspace carries completion counters that the kernels leave
+// at zero; its layout depends on (n_seq, k), so a shape change re-zeroes it.
+static int accept_ws(fst_ctx* ctx, int n_seq, int k, int V) {
+    if (int rc = grow(ctx->st, &ctx->acc_ws, &ctx->acc_ws_cap, fst::accept_ws_bytes(n_seq, k, V))) return rc;
+    if (ctx->acc_ws_nseq != n_seq || ctx->acc_ws_k != k) {
+        FST_HIP_TRY(hipMemsetAsync(ctx->acc_ws, 0, ctx->acc_ws_cap, ctx->st));
+        ctx->acc_ws_nseq = n_seq;
+        ctx->acc_ws_k = k;
+    }
     return FST_OK;
 }
 
@@ -576,7 +598,7 @@ int fst_accept_greedy_dev(fst_ctx* ctx, const float* d_target, int n_seq, int k,
                           int32_t* d_n_acc, int32_t* d_tokens) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (int rc = check_accept_args(n_seq, k, V)) return rc;
-    if (int rc = grow(&ctx->acc_ws, &ctx->acc_ws_cap, fst::accept_ws_bytes(n_seq, k, V))) return rc;
+    if (int rc = accept_ws(ctx, n_seq, k, V)) return rc;
     ctx->mark_begin();
     fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens, ctx->acc_ws);
     ctx->mark("accept_greedy");
@@ -590,7 +612,7 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (int rc = check_accept_args(n_seq, k, V)) return rc;
     if (!(temperature > 0.0f)) return fail(FST_EINVAL, "temperature must be > 0");
-    if (int rc = grow(&ctx->acc_ws, &ctx->acc_ws_cap, fst::accept_ws_bytes(n_seq, k, V))) return rc;
+    if (int rc = accept_ws(ctx, n_seq, k, V)) return rc;
     const float inv_t = 1.0f / temperature;
     ctx->mark_begin();
     fst::launch_accept_stochastic(ctx->st, d_target, d_draft_logits, n_seq, k, V, d_draft, inv_t, seed, seq_base,
@@ -610,9 +632,9 @@ static int accept_host(fst_ctx* ctx, const float* target, const float* draft_log
     for (int i = 0; i < n_seq * k; ++i)
         if (draft[i] < 0 || draft[i] >= V) return fail(FST_EINVAL, "draft token out of range");
     const size_t nt = (size_t)n_seq * (k + 1) * V, nd = stochastic ? (size_t)n_seq * k * V : 0;
-    if (int rc = grow((void**)&ctx->acc_logits, &ctx->acc_logits_cap, (nt + nd) * sizeof(float) + 256)) return rc;
+    if (int rc = grow(ctx->st, (void**)&ctx->acc_logits, &ctx->acc_logits_cap, (nt + nd) * sizeof(float) + 256)) return rc;
     const size_t io = (size_t)n_seq * k + n_seq + (size_t)n_seq * (k + 1);
-    if (int rc = grow((void**)&ctx->acc_io, &ctx->acc_io_cap, io * 4 + 256)) return rc;
+    if (int rc = grow(ctx->st, (void**)&ctx->acc_io, &ctx->acc_io_cap, io * 4 + 256)) return rc;
     int32_t* d_draft = ctx->acc_io;
     int32_t* d_nacc = d_draft + (size_t)n_seq * k;
     int32_t* d_tok = d_nacc + n_seq;

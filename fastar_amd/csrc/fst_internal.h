@@ -26,6 +26,7 @@ enum MetaIdx {
     META_ERROR = 3,        // nonzero: invalid expert id seen
     META_N_ROUTED_PAIRS = 4,
     META_TOPK_ERROR = 5,   // set by the top-k kernel, folded into META_ERROR by bucketing
+    META_TOPK_DONE = 6,    // top-k workgroups finished (re-armed to 0 by the last one)
     META_WORDS = 8
 };
 
@@ -55,6 +56,9 @@ struct Scratch {
     uint4* sx2p;           // [P][inter/256][4]
     int* xs2;              // [P]
     float* y;              // [P][hd]
+    int* tok_npairs;       // [T] distinct (token, expert) pairs of each token incl. shared
+    int* slot_done;        // [S] gate/up workgroups finished per slot (re-armed to 0)
+    int* tile_done;        // [T][hd/128] down contributions finished per token row tile (re-armed)
 };
 
 // Device expert bank: n_layers x (n_experts + 1) packed experts.
@@ -73,6 +77,40 @@ struct Geometry {
     int vocab;
 };
 
+// ---- cross-workgroup hand-off inside one launch ----
+// On this multi-XCD GPU each XCD has its own L2; an agent-scope fence
+// (__threadfence) writes back and invalidates the whole L2, which is far too
+// expensive to issue per workgroup.  Data handed to another workgroup is
+// instead written with device-coherent stores (sc1), the writer waits for its
+// stores to complete, then signals with a relaxed device-scope atomic; the
+// reader uses device-coherent loads.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ int ld_coherent(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this thread's stores are complete (and keep the compiler from
+// moving memory operations across the point).
+__device__ __forceinline__ void publish_wait() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ int signal_add(int* c, int v) {
+    const int r = __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return r;
+}
+
 // ---- launchers (each enqueues on `st`) ----
 void launch_router_logits(hipStream_t st, const Geometry& g, const LayerView& L,
                           const uint16_t* h, int M, float* logits);
@@ -82,11 +120,18 @@ void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, 
                          const Scratch& s);
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p,
                       uint4* sxp, int* xs);
+// Router logits and the activation prep of the same rows in one launch.
+void launch_router_prep(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
+                        float* logits, const Scratch& s);
 void launch_prep_act(hipStream_t st, const float* gu, float swiglu_limit, const int* meta, int max_rows,
                      int K, _Float16* a16p, uint4* sxp, int* xs);
 // Weights must be in the wave-tiled device layout (repack_q4k_expert).
+// gate/up also runs each slot's SwiGLU prep (last workgroup of the slot);
+// down also runs the combine of each token row tile (last contribution).
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
+                     const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
+                     uint16_t* out_shared);
 // Host-side reorder of one packed Q4_K expert (gate|up|down, each [N][K/256]
 // blocks of 144 B) into the device layout the linear kernel streams.
 void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);

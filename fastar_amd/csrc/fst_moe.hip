@@ -39,17 +39,18 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t b) {
 
 // ---------------------------------------------------------------- router
 
-// One wave per (expert, pair of tokens): lane j owns the contiguous K/64
-// chunk j, sums it with a sequential fmaf chain, then the 64 partials are
-// combined by the halving tree p[j] += p[j+off] (off = 32..1) that lane 0
-// sees through shfl_down.  All loads of a wave are issued before the math.
+// Router logits: one wave per (expert, pair of tokens); lane j owns the
+// contiguous K/64 chunk j, sums it with a sequential fmaf chain, then the 64
+// partials are combined by the halving tree p[j] += p[j+off] (off = 32..1)
+// that lane 0 sees through shfl_down.  All loads of a wave are issued before
+// the math.  Workgroups past the router part each prepare one token row of
+// the expert operand (prep_row), so both consumers of h share one launch.
 template <int CH, int TPW>
-__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ w_nk,
-                                                            const uint16_t* __restrict__ h, int M,
-                                                            int K, int E, float* __restrict__ logits) {
+__device__ void router_block(const uint16_t* __restrict__ w_nk, const uint16_t* __restrict__ h, int M, int K,
+                             int E, int bx, int by, float* __restrict__ logits) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + wave;
-    const int t0 = blockIdx.y * TPW;
+    const int e = bx * 4 + wave;
+    const int t0 = by * TPW;
     if (e >= E) return;
     uint4 wq[CH / 8], xq[TPW][CH / 8];
     const uint4* wp = reinterpret_cast<const uint4*>(w_nk + (size_t)e * K + (size_t)lane * CH);
@@ -83,142 +84,64 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
     }
 }
 
-void launch_router_logits(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h,
-                          int M, float* logits) {
+template <int CH, int TPW>
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ w_nk,
+                                                            const uint16_t* __restrict__ h, int M, int K, int E,
+                                                            float* __restrict__ logits) {
+    router_block<CH, TPW>(w_nk, h, M, K, E, blockIdx.x, blockIdx.y, logits);
+}
+
+void launch_router_logits(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
+                          float* logits) {
     constexpr int TPW = 2;
-    dim3 grid((g.E + 3) / 4, (M + TPW - 1) / TPW);
+    const dim3 grid((g.E + 3) / 4, (M + TPW - 1) / TPW);
+#define FST_RL(CHV)                                                                                        \
+    hipLaunchKernelGGL((router_logits_kernel<CHV, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd, g.E, \
+                       logits)
     if (g.hd == 4096)
-        hipLaunchKernelGGL((router_logits_kernel<64, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
-                           g.E, logits);
+        FST_RL(64);
     else if (g.hd == 2048)
-        hipLaunchKernelGGL((router_logits_kernel<32, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
-                           g.E, logits);
+        FST_RL(32);
     else if (g.hd == 1024)
-        hipLaunchKernelGGL((router_logits_kernel<16, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
-                           g.E, logits);
+        FST_RL(16);
     else
-        hipLaunchKernelGGL((router_logits_kernel<8, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd,
-                           g.E, logits);
+        FST_RL(8);
+#undef FST_RL
 }
 
 // ------------------------------------------------------------ route + bucket
 
-struct Cand {
-    float sel, score;
-    int id;  // INT_MAX: empty
-};
-
-__device__ __forceinline__ bool cand_better(const Cand& a, const Cand& b) {
-    if (a.id == 0x7fffffff) return false;
-    if (b.id == 0x7fffffff) return true;
-    bool an = a.sel != a.sel, bn = b.sel != b.sel;
-    if (an != bn) return bn;  // a number beats NaN
-    if (!an && a.sel != b.sel) return a.sel > b.sel;
-    return a.id < b.id;
-}
-
 constexpr int kMaxExperts = 1024;
 
-// One wave per token: top-k and weights (src/fst_engine.cpp:974-1061
-// semantics; ties toward the lower expert id, NaN scores last), or the hash
-// table row for hash-routed layers (:1015-1021).
-__global__ __launch_bounds__(64) void topk_kernel(int E, int tk, int score_func, int round_bf16,
-                                                  float route_scale, const float* __restrict__ logits,
-                                                  const float* __restrict__ bias,
-                                                  const int32_t* __restrict__ hash,
-                                                  const int32_t* __restrict__ ids, int vocab,
-                                                  int32_t* __restrict__ eids, float* __restrict__ wts,
-                                                  int* __restrict__ meta) {
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float* row = logits + (size_t)t * E;
-    if (hash) {
-        if (lane == 0) {
-            const int tok = ids ? ids[t] : -1;
-            if (tok < 0 || tok >= vocab) {
-                atomicOr(&meta[META_TOPK_ERROR], 2);
-                for (int k = 0; k < tk; ++k) {
-                    eids[(size_t)t * tk + k] = -1;
-                    wts[(size_t)t * tk + k] = 0.0f;
-                }
-                return;
-            }
-            float sc[kMaxTopK];
-            float sum = 0.0f;
-            for (int k = 0; k < tk; ++k) {
-                const int e = hash[(size_t)tok * tk + k];
-                float x = (e >= 0 && e < E) ? row[e] : 0.0f;
-                if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
-                sc[k] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
-                sum += sc[k];
-                eids[(size_t)t * tk + k] = e;
-            }
-            const float inv = 1.0f / (sum + 1e-12f);
-            for (int k = 0; k < tk; ++k) wts[(size_t)t * tk + k] = sc[k] * inv * route_scale;
-        }
-        return;
-    }
-    constexpr int PER = kMaxExperts / 64;
-    Cand c[PER];
-    const int nper = (E + 63) / 64;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int e = lane + 64 * i;
-        c[i].id = 0x7fffffff;
-        c[i].sel = 0.0f;
-        c[i].score = 0.0f;
-        if (i < nper && e < E) {
-            float x = row[e];
-            if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
-            const float s = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
-            c[i].score = s;
-            c[i].sel = s + (bias ? bias[e] : 0.0f);
-            c[i].id = e;
-        }
-    }
-    float chosen_sc = 0.0f;
-    int chosen_id = 0;
-    float sum = 0.0f;
-    for (int k = 0; k < tk; ++k) {
-        Cand b;
-        b.id = 0x7fffffff;
-        b.sel = 0.0f;
-        b.score = 0.0f;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (i < nper && cand_better(c[i], b)) b = c[i];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            Cand o;
-            o.sel = __shfl_xor(b.sel, off, 64);
-            o.score = __shfl_xor(b.score, off, 64);
-            o.id = __shfl_xor(b.id, off, 64);
-            if (cand_better(o, b)) b = o;
-        }
-        if (lane == k) {
-            chosen_sc = b.score;
-            chosen_id = b.id;
-        }
-        sum += b.score;  // same sequential order in every lane
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (c[i].id == b.id) c[i].id = 0x7fffffff;
-    }
-    if (lane < tk) {
-        const float inv = 1.0f / (sum + 1e-12f);
-        eids[(size_t)t * tk + lane] = chosen_id;
-        wts[(size_t)t * tk + lane] = chosen_sc * inv * route_scale;
-    }
+// Total order used for top-k: larger score first, then lower expert id; NaN
+// scores rank below every number (and among themselves by id).  Encoded as a
+// 64-bit key: (order-preserving bits of the score) << 32 | (0xffffffff - id).
+// -0 is folded into +0 so that equal scores compare equal as in float math.
+__device__ __forceinline__ unsigned long long topk_key(float sel, int id) {
+    uint32_t u = fst_f32_bits(sel == 0.0f ? 0.0f : sel);
+    uint32_t o;
+    if (sel != sel)
+        o = 0u;
+    else
+        o = (u >> 31) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)o << 32) | (0xffffffffu - (uint32_t)id);
 }
 
-// Single workgroup: (token, expert) pairs grouped by expert in ascending
-// expert id, tokens ascending within an expert; the shared expert gets the
-// last slot with all M tokens.
-__global__ __launch_bounds__(256) void bucket_kernel(int M, int E, int tk, int use_shared,
-                                                     const int32_t* __restrict__ eids,
-                                                     int* __restrict__ meta, int* __restrict__ slot_eid,
-                                                     int* __restrict__ slot_M, int* __restrict__ slot_off,
-                                                     int* __restrict__ pair_tok, int* __restrict__ pair_of,
-                                                     int* __restrict__ pair_shared) {
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+    const unsigned lo = __shfl_xor((unsigned)v, m, 64), hi = __shfl_xor((unsigned)(v >> 32), m, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// (token, expert) pairs grouped per slot: the shared expert (if used) is slot
+// 0 with all M tokens (so its work starts first), then the routed experts in
+// ascending id, tokens ascending within an expert.  Also counts each token's
+// distinct pairs (the number of down contributions its combine waits for).
+// Run by one whole 256-thread workgroup.
+__device__ void bucket_block(int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids,
+                             int* __restrict__ meta, int* __restrict__ slot_eid, int* __restrict__ slot_M,
+                             int* __restrict__ slot_off, int* __restrict__ pair_tok,
+                             int* __restrict__ pair_of, int* __restrict__ pair_shared,
+                             int* __restrict__ tok_npairs) {
     __shared__ unsigned long long hitmask[kMaxExperts];
     __shared__ int eoff[kMaxExperts];
     __shared__ int wave_tot[2][4];
@@ -229,14 +152,15 @@ __global__ __launch_bounds__(256) void bucket_kernel(int M, int E, int tk, int u
     __syncthreads();
     for (int i = tid; i < M * tk; i += 256) {
         const int t = i / tk;
-        const int e = eids[i];
+        const int e = __hip_atomic_load(&eids[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (e < 0 || e >= E)
             atomicOr(&err, 1);
         else
             atomicOr(&hitmask[e], 1ull << t);
     }
     __syncthreads();
-    int slot_base = 0, pair_base = 0;
+    const int s0 = use_shared ? 1 : 0, p0 = use_shared ? M : 0;
+    int slot_base = s0, pair_base = p0;
     for (int e0 = 0; e0 < E; e0 += 256) {
         const int e = e0 + tid;
         const int cnt = (e < E) ? __popcll(hitmask[e]) : 0;
@@ -278,7 +202,7 @@ __global__ __launch_bounds__(256) void bucket_kernel(int M, int E, int tk, int u
     }
     for (int i = tid; i < M * tk; i += 256) {
         const int t = i / tk;
-        const int e = eids[i];
+        const int e = __hip_atomic_load(&eids[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         int p = -1;
         if (e >= 0 && e < E) {
             p = eoff[e] + __popcll(hitmask[e] & ((1ull << t) - 1ull));
@@ -286,37 +210,177 @@ __global__ __launch_bounds__(256) void bucket_kernel(int M, int E, int tk, int u
         }
         pair_of[i] = p;
     }
-    if (use_shared) {
-        for (int t = tid; t < M; t += 256) {
-            pair_tok[pair_base + t] = t;
-            pair_shared[t] = pair_base + t;
+    for (int t = tid; t < M; t += 256) {
+        int n = use_shared ? 1 : 0;
+        for (int j = 0; j < tk; ++j) {
+            const int e = __hip_atomic_load(&eids[t * tk + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (e < 0 || e >= E) continue;
+            bool dup = false;
+            for (int j2 = 0; j2 < j; ++j2)
+                dup |= __hip_atomic_load(&eids[t * tk + j2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == e;
+            n += dup ? 0 : 1;
         }
-        if (tid == 0) {
-            slot_eid[slot_base] = E;
-            slot_M[slot_base] = M;
-            slot_off[slot_base] = pair_base;
+        tok_npairs[t] = n;
+        if (use_shared) {
+            pair_tok[t] = t;
+            pair_shared[t] = t;
         }
+    }
+    if (use_shared && tid == 0) {
+        slot_eid[0] = E;
+        slot_M[0] = M;
+        slot_off[0] = 0;
     }
     __syncthreads();
     if (tid == 0) {
-        meta[META_N_ROUTED] = slot_base;
-        meta[META_N_SLOTS] = slot_base + (use_shared ? 1 : 0);
-        meta[META_N_ROUTED_PAIRS] = pair_base;
-        meta[META_N_PAIRS] = pair_base + (use_shared ? M : 0);
+        meta[META_N_ROUTED] = slot_base - s0;
+        meta[META_N_SLOTS] = slot_base;
+        meta[META_N_ROUTED_PAIRS] = pair_base - p0;
+        meta[META_N_PAIRS] = pair_base;
         meta[META_ERROR] = err | meta[META_TOPK_ERROR];
         meta[META_TOPK_ERROR] = 0;
     }
 }
 
+__global__ __launch_bounds__(256) void bucket_kernel(int M, int E, int tk, int use_shared,
+                                                     const int32_t* __restrict__ eids, int* __restrict__ meta,
+                                                     int* __restrict__ slot_eid, int* __restrict__ slot_M,
+                                                     int* __restrict__ slot_off, int* __restrict__ pair_tok,
+                                                     int* __restrict__ pair_of, int* __restrict__ pair_shared,
+                                                     int* __restrict__ tok_npairs) {
+    bucket_block(M, E, tk, use_shared, eids, meta, slot_eid, slot_M, slot_off, pair_tok, pair_of, pair_shared,
+                 tok_npairs);
+}
+
+// One workgroup per token: wave 0 selects the token's top-k (src/fst_engine.cpp
+// :974-1061 semantics with the order of topk_key) or reads its hash-table row
+// (:1015-1021) and writes eids/wts; the workgroup that finishes last then
+// groups all tokens' (token, expert) pairs (bucket_block) and re-arms the
+// completion counter.  PER = experts per lane.
+template <int PER>
+__global__ __launch_bounds__(256) void topk_bucket_kernel(
+    int M, int E, int tk, int score_func, int round_bf16, float route_scale, const float* __restrict__ logits,
+    const float* __restrict__ bias, const int32_t* __restrict__ hash, const int32_t* __restrict__ ids,
+    int vocab, int use_shared, int32_t* __restrict__ eids, float* __restrict__ wts, int* __restrict__ meta,
+    int* __restrict__ slot_eid, int* __restrict__ slot_M, int* __restrict__ slot_off,
+    int* __restrict__ pair_tok, int* __restrict__ pair_of, int* __restrict__ pair_shared,
+    int* __restrict__ tok_npairs) {
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const float* row = logits + (size_t)t * E;
+    if (tid < 64) {
+        if (hash) {
+            if (lane == 0) {
+                const int tok = ids ? ids[t] : -1;
+                if (tok < 0 || tok >= vocab) {
+                    atomicOr(&meta[META_TOPK_ERROR], 2);
+                    for (int k = 0; k < tk; ++k) {
+                        st_coherent(&eids[(size_t)t * tk + k], -1);
+                        st_coherent(&wts[(size_t)t * tk + k], 0.0f);
+                    }
+                } else {
+                    float sc[kMaxTopK];
+                    float sum = 0.0f;
+                    for (int k = 0; k < tk; ++k) {
+                        const int e = hash[(size_t)tok * tk + k];
+                        float x = (e >= 0 && e < E) ? row[e] : 0.0f;
+                        if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
+                        sc[k] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+                        sum += sc[k];
+                        st_coherent(&eids[(size_t)t * tk + k], e);
+                    }
+                    const float inv = 1.0f / (sum + 1e-12f);
+                    for (int k = 0; k < tk; ++k) st_coherent(&wts[(size_t)t * tk + k], sc[k] * inv * route_scale);
+                }
+            }
+        } else {
+            unsigned long long key[PER];
+            float sc[PER];
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int e = lane + 64 * i;
+                key[i] = 0ull;
+                sc[i] = 0.0f;
+                if (e < E) {
+                    float x = row[e];
+                    if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
+                    const float sv = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+                    sc[i] = sv;
+                    key[i] = topk_key(sv + (bias ? bias[e] : 0.0f), e);
+                }
+            }
+            float chosen_sc = 0.0f, sum = 0.0f;
+            int chosen_id = 0;
+            for (int k = 0; k < tk; ++k) {
+                unsigned long long b = key[0];
+#pragma unroll
+                for (int i = 1; i < PER; ++i) b = key[i] > b ? key[i] : b;
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) {
+                    const unsigned long long o = shfl_xor_u64(b, off);
+                    b = o > b ? o : b;
+                }
+                const int id = (int)(0xffffffffu - (uint32_t)b);
+                const int owner = id & 63, slot_i = id >> 6;
+                float mine = 0.0f;
+#pragma unroll
+                for (int i = 0; i < PER; ++i)
+                    if (i == slot_i) mine = sc[i];
+                const float s_win = __shfl(mine, owner, 64);
+                if (lane == owner) {
+#pragma unroll
+                    for (int i = 0; i < PER; ++i)
+                        if (i == slot_i) key[i] = 0ull;
+                }
+                if (lane == k) {
+                    chosen_sc = s_win;
+                    chosen_id = id;
+                }
+                sum += s_win;  // same sequential order in every lane
+            }
+            if (lane < tk) {
+                const float inv = 1.0f / (sum + 1e-12f);
+                st_coherent(&eids[(size_t)t * tk + lane], chosen_id);
+                st_coherent(&wts[(size_t)t * tk + lane], chosen_sc * inv * route_scale);
+            }
+        }
+    }
+    // completion: the last workgroup buckets every token
+    __shared__ int last;
+    publish_wait();
+    __syncthreads();
+    if (tid == 0) last = signal_add(&meta[META_TOPK_DONE], 1) == M - 1;
+    __syncthreads();
+    if (!last) return;
+    bucket_block(M, E, tk, use_shared, eids, meta, slot_eid, slot_M, slot_off, pair_tok, pair_of, pair_shared,
+                 tok_npairs);
+    if (tid == 0) meta[META_TOPK_DONE] = 0;
+}
+
 void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, int M,
                          const float* logits, const int32_t* input_ids, int use_hash, int do_topk,
                          int use_shared, int32_t* eids, float* wts, const Scratch& s) {
-    if (do_topk)
-        hipLaunchKernelGGL(topk_kernel, dim3(M), dim3(64), 0, st, g.E, g.tk, g.score_func,
-                           g.round_logits_bf16, g.route_scale, logits, L.router_bias,
-                           use_hash ? L.hash : nullptr, input_ids, g.vocab, eids, wts, s.meta);
-    hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(256), 0, st, M, g.E, g.tk, use_shared, eids, s.meta,
-                       s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared);
+    if (!do_topk) {
+        hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(256), 0, st, M, g.E, g.tk, use_shared, eids, s.meta,
+                           s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared, s.tok_npairs);
+        return;
+    }
+#define FST_TOPK(PERV)                                                                                     \
+    hipLaunchKernelGGL(topk_bucket_kernel<PERV>, dim3(M), dim3(256), 0, st, M, g.E, g.tk, g.score_func,      \
+                       g.round_logits_bf16, g.route_scale, logits, L.router_bias, use_hash ? L.hash : nullptr, \
+                       input_ids, g.vocab, use_shared, eids, wts, s.meta, s.slot_eid, s.slot_M, s.slot_off,   \
+                       s.pair_tok, s.pair_of, s.pair_shared, s.tok_npairs)
+    const int per = (g.E + 63) / 64;
+    if (per <= 1)
+        FST_TOPK(1);
+    else if (per <= 2)
+        FST_TOPK(2);
+    else if (per <= 4)
+        FST_TOPK(4);
+    else if (per <= 8)
+        FST_TOPK(8);
+    else
+        FST_TOPK(16);
+#undef FST_TOPK
 }
 
 // -------------------------------------------------------------- operand prep
@@ -346,24 +410,45 @@ struct SrcSwiGLU {
 // k-interleaved fp16 operand (per super-block, lane group g, MFMA c: elements
 // 64g+4c+{0,2,1,3} and 64g+32+4c+{0,2,1,3}, the order q4k_bop produces the
 // weights in) and per-sub-block sums split hi+lo.
-template <typename Src>
-__global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restrict__ nrows_dev, int nrows_host,
-                                                   int K, _Float16* __restrict__ x16p,
-                                                   uint4* __restrict__ sxp, int* __restrict__ xs) {
-    const int row = blockIdx.x;
-    const int nrows = nrows_dev ? nrows_dev[0] : nrows_host;
-    if (row >= nrows) return;
-    __shared__ float red[4];
+constexpr int kMaxPrepK = 8192;
+
+struct SrcSwiGLUCoherent {
+    const float* p;
+    float lim;
+    __device__ __forceinline__ float at(size_t row, int K, int i) const {
+        float g = ld_coherent(p + row * 2 * K + i), u = ld_coherent(p + row * 2 * K + K + i);
+        if (lim > 0.0f) {
+            g = fminf(g, lim);
+            u = fminf(fmaxf(u, -lim), lim);
+        }
+        return (g / (1.0f + expf(-g))) * u;
+    }
+};
+
+// One row by one workgroup of NT threads (xv: K floats of LDS): amax ->
+// exponent s so that amax*2^-s lies in [2^9, 2^10); then the k-interleaved
+// fp16 operand (per super-block, lane group g, MFMA c: elements
+// 64g+4c+{0,2,1,3} and 64g+32+4c+{0,2,1,3}, the order q4k_bop produces the
+// weights in) and the per-sub-block sums split hi+lo.
+template <int NT, typename Src>
+__device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __restrict__ x16p,
+                         uint4* __restrict__ sxp, int* __restrict__ xs) {
+    __shared__ float red[NT / 64];
     __shared__ int s_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float m = 0.0f;
-    for (int i = tid; i < K; i += 256) m = fmaxf(m, fabsf(src.at(row, K, i)));
+    for (int i = tid; i < K; i += NT) {
+        const float v = src.at(row, K, i);
+        xv[i] = v;
+        m = fmaxf(m, fabsf(v));
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if (lane == 0) red[wave] = m;
     __syncthreads();
     if (tid == 0) {
-        float a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        float a = red[0];
+        for (int w = 1; w < NT / 64; ++w) a = fmaxf(a, red[w]);
         int s = 0;
         if (a > 0.0f && a < INFINITY) {
             int e;
@@ -375,34 +460,89 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
     }
     __syncthreads();
     const int s = s_sh;
+    // fp16 values in place (exact power-of-two scaling, one rounding)
+    for (int i = tid; i < K; i += NT) xv[i] = (float)(_Float16)ldexpf(xv[i], -s);
+    __syncthreads();
     _Float16* dst = x16p + (size_t)row * K;
     const int nchunk = K / 8;
-    for (int q = tid; q < nchunk; q += 256) {
-        int sb = q >> 5, gc = q & 31, g = gc >> 3, c = gc & 7;
-        int base = sb * 256 + 64 * g + 4 * c;
+    for (int q = tid; q < nchunk; q += NT) {
+        const int sb = q >> 5, gc = q & 31, g = gc >> 3, c = gc & 7;
+        const int base = sb * 256 + 64 * g + 4 * c;
         h8_t v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;  // nibble pair order of q4k_bop
-            v[i] = (_Float16)ldexpf(src.at(row, K, base + e), -s);
-            v[4 + i] = (_Float16)ldexpf(src.at(row, K, base + 32 + e), -s);
+            v[i] = (_Float16)xv[base + e];
+            v[4 + i] = (_Float16)xv[base + 32 + e];
         }
         *reinterpret_cast<h8_t*>(dst + (size_t)q * 8) = v;
     }
-    // sub-block sums (32 consecutive elements, natural order, of the fp16 values)
+    // sub-block sums of the fp16 values (32 consecutive elements; the start of
+    // the fixed summation order is rotated by j to spread LDS banks)
     const int nsub = K / 32;
     uint16_t* sx16 = reinterpret_cast<uint16_t*>(sxp + (size_t)row * (K / 256) * 4);
-    for (int j = tid; j < nsub; j += 256) {
+    for (int j = tid; j < nsub; j += NT) {
         float S = 0.0f;
-        for (int i = 0; i < 32; ++i) S += (float)(_Float16)ldexpf(src.at(row, K, j * 32 + i), -s);
-        _Float16 hi = (_Float16)S;
-        _Float16 lo = (_Float16)(S - (float)hi);
-        int sb = j >> 3, jj = j & 7, g = jj >> 1, odd = jj & 1;
+        for (int i = 0; i < 32; ++i) S += xv[j * 32 + ((i + j) & 31)];
+        const _Float16 hi = (_Float16)S;
+        const _Float16 lo = (_Float16)(S - (float)hi);
+        const int sb = j >> 3, jj = j & 7, g = jj >> 1, odd = jj & 1;
         uint16_t* e = sx16 + ((size_t)sb * 4 + g) * 8;
         e[odd] = __builtin_bit_cast(uint16_t, hi);
         e[2 + odd] = __builtin_bit_cast(uint16_t, lo);
-        if (!odd) { e[4] = 0; e[5] = 0; e[6] = 0; e[7] = 0; }
+        if (!odd) {
+            e[4] = 0;
+            e[5] = 0;
+            e[6] = 0;
+            e[7] = 0;
+        }
     }
+    __syncthreads();
+}
+
+template <typename Src>
+__global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restrict__ nrows_dev, int nrows_host,
+                                                   int K, _Float16* __restrict__ x16p,
+                                                   uint4* __restrict__ sxp, int* __restrict__ xs) {
+    const int row = blockIdx.x;
+    const int nrows = nrows_dev ? nrows_dev[0] : nrows_host;
+    if (row >= nrows) return;
+    __shared__ float xv[kMaxPrepK];
+    prep_row<256>(src, row, K, xv, x16p, sxp, xs);
+}
+
+template <int CH, int TPW>
+__global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __restrict__ w_nk,
+                                                          const uint16_t* __restrict__ h, int M, int K, int E,
+                                                          float* __restrict__ logits, int nbx, int nrb,
+                                                          _Float16* __restrict__ x16p, uint4* __restrict__ sxp,
+                                                          int* __restrict__ xs) {
+    __shared__ float xv[kMaxPrepK];
+    const int b = blockIdx.x;
+    if (b >= nrb) {
+        prep_row<256>(SrcBf16{h}, b - nrb, K, xv, x16p, sxp, xs);
+        return;
+    }
+    router_block<CH, TPW>(w_nk, h, M, K, E, b % nbx, b / nbx, logits);
+}
+
+void launch_router_prep(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
+                        float* logits, const Scratch& s) {
+    constexpr int TPW = 2;
+    const int nbx = (g.E + 3) / 4, nby = (M + TPW - 1) / TPW, nrb = nbx * nby;
+    const dim3 grid(nrb + M);
+#define FST_RP(CHV)                                                                                       \
+    hipLaunchKernelGGL((router_prep_kernel<CHV, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd, g.E, \
+                       logits, nbx, nrb, s.x16p, s.sxp, s.xs)
+    if (g.hd == 4096)
+        FST_RP(64);
+    else if (g.hd == 2048)
+        FST_RP(32);
+    else if (g.hd == 1024)
+        FST_RP(16);
+    else
+        FST_RP(8);
+#undef FST_RP
 }
 
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p, uint4* sxp,
@@ -505,6 +645,29 @@ constexpr int kTokStride = 37;
 #ifndef FST_Q4K_WAVES_PER_EU
 #define FST_Q4K_WAVES_PER_EU 3
 #endif
+// What a linear-kernel launch does after its rows are written.
+struct EpiArgs {
+    int mode;               // 0: nothing; 1: SwiGLU prep of the slot; 2: combine of token row tiles
+    // mode 1: the last workgroup of a slot turns its pairs' gate||up rows into
+    // the down projection's operand
+    float swiglu_limit;
+    _Float16* a16p;
+    uint4* sx2p;
+    int* xs2;
+    int* slot_done;
+    // mode 2: the last contribution to a (token, 128-row tile) combines it
+    int tk, use_shared;
+    const int* pair_tok;
+    const int* pair_of;
+    const int* pair_shared;
+    const float* wts;
+    const int* tok_npairs;
+    int* tile_done;
+    uint16_t* out;
+    uint16_t* out_routed;
+    uint16_t* out_shared;
+};
+
 #ifndef FST_Q4K_PF
 #define FST_Q4K_PF 2
 #endif
@@ -522,7 +685,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
     const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
     const int* __restrict__ slot_off, const int* __restrict__ a_row, const _Float16* __restrict__ A,
-    const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out) {
+    const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out, EpiArgs ep) {
     constexpr int NGRP = (TOKS + 15) / 16;
     constexpr int TS = TOKS * kTokStride;            // one super-block of one stage
     constexpr int STAGE = MS * TS;                   // one macro-stage
@@ -653,7 +816,64 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
             if (tl >= Me) continue;
             const int pidx = off + tl;
             const int ar = a_row ? a_row[pidx] : pidx;
-            out[(size_t)pidx * N + row] = ldexpf(acc[q][i], xs[ar]);
+            const float v = ldexpf(acc[q][i], xs[ar]);
+            if (ep.mode == 0)
+                out[(size_t)pidx * N + row] = v;
+            else
+                st_coherent(&out[(size_t)pidx * N + row], v);
+        }
+    }
+    if (ep.mode == 0) return;
+
+    // ---- completion epilogues (counters are re-armed by their consumer) ----
+    __shared__ int s_flag[64];
+    __shared__ int s_nflag;
+    publish_wait();
+    __syncthreads();
+    float* xv = reinterpret_cast<float*>(lds);  // the staging ring is free now
+    if (ep.mode == 1) {
+        if (tid == 0) s_nflag = signal_add(&ep.slot_done[slot], 1) == tiles - 1;
+        __syncthreads();
+        if (!s_nflag) return;
+        if (tid == 0) ep.slot_done[slot] = 0;
+        const int inter = N / 2;
+        for (int tl = 0; tl < slot_M[slot]; ++tl)
+            prep_row<NT>(SrcSwiGLUCoherent{out, ep.swiglu_limit}, off + tl, inter, xv, ep.a16p, ep.sx2p, ep.xs2);
+        return;
+    }
+    // mode 2: one contribution per (pair, tile); the last one for a token combines its tile
+    if (tid == 0) s_nflag = 0;
+    __syncthreads();
+    const int nt128 = N / 128;
+    const int T128 = (tile * WAVES * 16) / 128;
+    for (int tl = tid; tl < slot_M[slot]; tl += NT) {
+        const int t = ep.pair_tok[off + tl];
+        const int old = signal_add(&ep.tile_done[t * nt128 + T128], 1);
+        if (old == ep.tok_npairs[t] - 1) {
+            ep.tile_done[t * nt128 + T128] = 0;
+            s_flag[atomicAdd(&s_nflag, 1)] = t;
+        }
+    }
+    __syncthreads();
+    const int nflag = s_nflag;
+    if (nflag == 0) return;
+    for (int f = 0; f < nflag; ++f) {
+        const int t = s_flag[f];
+        for (int i = tid; i < 128; i += NT) {
+            const int n = T128 * 128 + i;
+            float a = 0.0f;
+            for (int j = 0; j < ep.tk; ++j) {
+                const int p = ep.pair_of[t * ep.tk + j];
+                if (p < 0) continue;
+                a = a + ep.wts[t * ep.tk + j] * ld_coherent(out + (size_t)p * N + n);
+            }
+            if (ep.out_routed) ep.out_routed[(size_t)t * N + n] = fst_f32_to_bf16(a);
+            if (ep.use_shared) {
+                const float sv = ld_coherent(out + (size_t)ep.pair_shared[t] * N + n);
+                if (ep.out_shared) ep.out_shared[(size_t)t * N + n] = fst_f32_to_bf16(sv);
+                a = a + sv;
+            }
+            if (ep.out) ep.out[(size_t)t * N + n] = fst_f32_to_bf16(a);
         }
     }
 }
@@ -662,12 +882,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
 // 32 or 64 tokens; smaller capacities stage more super-blocks per barrier.
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
-                              const _Float16* A, const uint4* SX, const int* xs, float* out) {
+                              const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep) {
     constexpr int W = 8;
     const dim3 grid(slots * (unsigned)(N / (16 * W)));
 #define FST_Q4K_LAUNCH(T, MSV)                                                                         \
     hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W>), grid, dim3(64 * W), 0, st, bank, stride, mat_off,  \
-                       K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out)
+                       K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep)
     if (M <= 8)
         FST_Q4K_LAUNCH(8, 4);
     else if (M <= 16)
@@ -680,16 +900,42 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 }
 
 // gate||up: the two [inter][hd/256] matrices are contiguous, so they are one
-// 2*inter-row matrix; the SwiGLU is applied by the following prep pass.
+// 2*inter-row matrix; the last workgroup of each slot applies the SwiGLU and
+// prepares the down operand of the slot's pairs.
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
+    EpiArgs ep{};
+    ep.mode = 1;
+    ep.swiglu_limit = g.swiglu_limit;
+    ep.a16p = s.a16p;
+    ep.sx2p = s.sx2p;
+    ep.xs2 = s.xs2;
+    ep.slot_done = s.slot_done;
     launch_q4k_linear(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
-                      s.pair_tok, s.x16p, s.sxp, s.xs, s.act);
+                      s.pair_tok, s.x16p, s.sxp, s.xs, s.act, ep);
 }
 
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
+// down: the last contribution to each (token, 128-row tile) combines it:
+// out = bf16(sum_j w[t][j] y[pair(t,j)] + y[shared(t)]) in slot order
+// (src/fst_engine.cpp:4196-4201, :2851-2852), fp32 until one RNE rounding.
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
+                     const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
+                     uint16_t* out_shared) {
     const size_t proj = (size_t)g.inter * (g.hd / 256) * 144;
+    EpiArgs ep{};
+    ep.mode = 2;
+    ep.tk = g.tk;
+    ep.use_shared = use_shared;
+    ep.pair_tok = s.pair_tok;
+    ep.pair_of = s.pair_of;
+    ep.pair_shared = s.pair_shared;
+    ep.wts = wts;
+    ep.tok_npairs = s.tok_npairs;
+    ep.tile_done = s.tile_done;
+    ep.out = out;
+    ep.out_routed = out_routed;
+    ep.out_shared = out_shared;
     launch_q4k_linear(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
-                      nullptr, s.a16p, s.sx2p, s.xs2, s.y);
+                      nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
 }
 
 // ------------------------------------------------------------------ combine
