@@ -192,19 +192,6 @@ def test_router_ties_and_hash(fa, oracle, router_ctx):
 
 # ------------------------------------------------------------ MoE layer (C2)
 
-@pytest.fixture(scope="module")
-def c2_layer(fa):
-    note("create C2 ctx: 256 routed + 1 shared Q4_K experts")
-    ctx = fa.Context(n_experts=256, top_k=6, max_tokens=64)
-    seed = 2024
-    for e in range(257):
-        ctx.upload_expert(0, e, fa.synth_q4k_expert(seed, e))
-    w = fa.synth_normal_bf16(seed, 1000, (HD, 256), 0.0, 0.02)
-    ctx.upload_router_bf16(0, w)
-    yield ctx, seed, w
-    ctx.close()
-
-
 @pytest.mark.parametrize("M", [8, 32])
 def test_moe_layer_c2(fa, oracle, c2_layer, M):
     ctx, seed, w = c2_layer
