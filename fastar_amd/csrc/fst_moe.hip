@@ -680,7 +680,7 @@ struct EpiArgs {
 //  - the slot's activation operands are staged into LDS in macro-stages of MS
 //    super-blocks (double-buffered, prefetched one macro-stage ahead into
 //    registers), one workgroup barrier per macro-stage.
-template <int TOKS, int MS, int WAVES = 4, int PF = FST_Q4K_PF>
+template <int TOKS, int MS, int WAVES, int MODE, int PF = FST_Q4K_PF>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_Q4K_WAVES_PER_EU))) void q4k_linear_kernel(
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
     const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
@@ -817,13 +817,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
             const int pidx = off + tl;
             const int ar = a_row ? a_row[pidx] : pidx;
             const float v = ldexpf(acc[q][i], xs[ar]);
-            if (ep.mode == 0)
+            if constexpr (MODE == 0)
                 out[(size_t)pidx * N + row] = v;
             else
                 st_coherent(&out[(size_t)pidx * N + row], v);
         }
     }
-    if (ep.mode == 0) return;
+    if constexpr (MODE == 0) return;
 
     // ---- completion epilogues (counters are re-armed by their consumer) ----
     __shared__ int s_flag[64];
@@ -831,7 +831,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     publish_wait();
     __syncthreads();
     float* xv = reinterpret_cast<float*>(lds);  // the staging ring is free now
-    if (ep.mode == 1) {
+    if constexpr (MODE == 1) {
         if (tid == 0) s_nflag = signal_add(&ep.slot_done[slot], 1) == tiles - 1;
         __syncthreads();
         if (!s_nflag) return;
@@ -880,13 +880,14 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
 
 // Token capacity of the launch (the call's M bounds every slot's M_e): 8, 16,
 // 32 or 64 tokens; smaller capacities stage more super-blocks per barrier.
+template <int MODE>
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
                               const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep) {
     constexpr int W = 8;
     const dim3 grid(slots * (unsigned)(N / (16 * W)));
-#define FST_Q4K_LAUNCH(T, MSV)                                                                         \
-    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W>), grid, dim3(64 * W), 0, st, bank, stride, mat_off,  \
+#define FST_Q4K_LAUNCH(T, MSV)                                                                               \
+    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE>), grid, dim3(64 * W), 0, st, bank, stride, mat_off, \
                        K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep)
     if (M <= 8)
         FST_Q4K_LAUNCH(8, 4);
@@ -910,8 +911,8 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
     ep.sx2p = s.sx2p;
     ep.xs2 = s.xs2;
     ep.slot_done = s.slot_done;
-    launch_q4k_linear(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
-                      s.pair_tok, s.x16p, s.sxp, s.xs, s.act, ep);
+    launch_q4k_linear<1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
+                         s.pair_tok, s.x16p, s.sxp, s.xs, s.act, ep);
 }
 
 // down: the last contribution to each (token, 128-row tile) combines it:
@@ -934,8 +935,8 @@ void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int 
     ep.out = out;
     ep.out_routed = out_routed;
     ep.out_shared = out_shared;
-    launch_q4k_linear(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
-                      nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
+    launch_q4k_linear<2>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
+                         nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
 }
 
 // ------------------------------------------------------------------ combine

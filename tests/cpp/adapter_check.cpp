@@ -1,0 +1,82 @@
+// Drives the FSTEngine-shaped adapter (include/fst_engine_hip.h) the way the
+// reference's process_layer / generate_dspark call the engine members.
+//   adapter_check cpu : no GPU visible -> construction must throw runtime_error
+//   adapter_check gpu : small layer end to end, cross-checked between members
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "fst_engine_hip.h"
+
+static float bf(uint16_t v) {
+    uint32_t b = (uint32_t)v << 16;
+    float f;
+    std::memcpy(&f, &b, 4);
+    return f;
+}
+
+int main(int argc, char** argv) {
+    const bool gpu = argc > 1 && std::strcmp(argv[1], "gpu") == 0;
+    fst_config cfg;
+    fst_config_default(&cfg);
+    cfg.n_experts = 4;
+    cfg.top_k = 2;
+    cfg.max_tokens = 16;
+    if (!gpu) {
+        try {
+            fst_hip::FSTEngineHip eng(cfg);
+            std::printf("unexpected: engine constructed without a GPU\n");
+            return 1;
+        } catch (const std::runtime_error& e) {
+            std::printf("ADAPTER CPU OK: %s\n", e.what());
+            return std::strstr(e.what(), "fst_create") ? 0 : 1;
+        }
+    }
+    fst_hip::FSTEngineHip eng(cfg);
+    const int hd = cfg.hidden_dim, E = cfg.n_experts, tk = cfg.top_k, M = 4;
+    std::vector<uint8_t> expert(fst_expert_bytes(&cfg));
+    for (int e = 0; e <= E; ++e) {
+        fst_synth_q4k_expert(99, e, hd, cfg.inter_dim, 0.01f, expert.data());
+        eng.upload_expert(0, e, expert.data(), expert.size());
+    }
+    std::vector<float> rw((size_t)hd * E);
+    fst_synth_normal_f32(99, 7, rw.size(), 0.0f, 0.02f, rw.data());
+    std::vector<uint16_t> h((size_t)M * hd), routed(h.size()), shared(h.size()), fused(h.size());
+    fst_synth_normal_bf16(99, 8, h.size(), 0.0f, 1.0f, h.data());
+    std::vector<int> eids(M * tk), eids2(M * tk);
+    std::vector<float> wts(M * tk), wts2(M * tk);
+    // src/fst_engine.cpp:2826-2852 call order
+    eng.npu_router(eids.data(), wts.data(), h.data(), rw.data(), nullptr, M, E, tk, hd, 0, nullptr);
+    eng.process_expert_ffn(0, h.data(), routed.data(), M, eids.data(), tk, wts.data());
+    eng.process_shared_expert(0, h.data(), shared.data(), M);
+    eng.moe_layer(0, h.data(), fused.data(), M, nullptr, eids2.data(), wts2.data());
+    if (eids != eids2 || wts != wts2) {
+        std::printf("router mismatch between npu_router and moe_layer\n");
+        return 1;
+    }
+    double num = 0, den = 0;
+    for (size_t i = 0; i < h.size(); ++i) {
+        const double ref = (double)bf(routed[i]) + (double)bf(shared[i]);
+        num += (bf(fused[i]) - ref) * (bf(fused[i]) - ref);
+        den += ref * ref;
+    }
+    const double rel = std::sqrt(num / den);
+    // accept_block on planted logits: rows 0..2 match the draft, row 3 does not
+    const int k = 5, V = 1000;
+    std::vector<float> logits((size_t)(k + 1) * V, 0.0f);
+    std::vector<int> draft = {11, 22, 33, 44, 55};
+    for (int i = 0; i <= k; ++i) logits[(size_t)i * V + (i < 3 ? draft[i] : 700 + i)] = 5.0f;
+    std::vector<int> emitted;
+    const int n = eng.accept_block(logits.data(), k, V, draft.data(), &emitted);
+    const bool acc_ok = n == 3 && emitted.size() == 4 && emitted[0] == 11 && emitted[2] == 33 && emitted[3] == 703;
+    bool threw = false;
+    try {
+        eng.npu_router(eids.data(), wts.data(), h.data(), rw.data(), nullptr, M, E + 1, tk, hd, 0, nullptr);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    std::printf("ADAPTER GPU %s: combine rel=%.3e accept n=%d threw_on_bad_shape=%d\n",
+                (rel < 1e-2 && acc_ok && threw) ? "OK" : "FAIL", rel, n, (int)threw);
+    return (rel < 1e-2 && acc_ok && threw) ? 0 : 1;
+}
