@@ -168,8 +168,8 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     const fst_config& c = *cfg;
     if (c.codec != FST_CODEC_Q4K)
         return fail(FST_EINVAL, "fst_create: only the Q4_K codec has a fused FFN path");
-    if (c.hidden_dim <= 0 || c.hidden_dim % 512 || c.inter_dim <= 0 || c.inter_dim % 256)
-        return fail(FST_EINVAL, "fst_create: hidden_dim must be a multiple of 512, inter_dim of 256");
+    if (c.hidden_dim <= 0 || c.hidden_dim % 512 || c.inter_dim <= 0 || c.inter_dim % 512)
+        return fail(FST_EINVAL, "fst_create: hidden_dim and inter_dim must be multiples of 512");
     if (c.hidden_dim > 8192 || c.inter_dim > 8192)
         return fail(FST_EINVAL, "fst_create: hidden_dim and inter_dim must be <= 8192");
 
@@ -238,13 +238,12 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.pair_tok, P)) || (rc = x->dalloc(&s.pair_of, (size_t)T * tk)) ||
         (rc = x->dalloc(&s.pair_shared, T)) || (rc = x->dalloc(&s.x16p, (size_t)T * hd)) ||
         (rc = x->dalloc(&s.sxp, (size_t)T * (hd / 256) * 4)) || (rc = x->dalloc(&s.xs, T)) ||
-        (rc = x->dalloc(&s.act, (size_t)P * 2 * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
+        (rc = x->dalloc(&s.act, (size_t)P * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
         (rc = x->dalloc(&s.y, (size_t)P * hd)) || (rc = x->dalloc(&s.tok_npairs, T)) ||
-        (rc = x->dalloc(&s.slot_done, S)) || (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 128))))
+        (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 128))))
         return bail(rc);
-    if (hipMemsetAsync(s.slot_done, 0, sizeof(int) * S, x->st) != hipSuccess ||
-        hipMemsetAsync(s.tile_done, 0, sizeof(int) * T * (hd / 128), x->st) != hipSuccess)
+    if (hipMemsetAsync(s.tile_done, 0, sizeof(int) * T * (hd / 128), x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(counters) failed"));
     if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));
@@ -448,6 +447,9 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     }
     fst::launch_q4k_gate_up(st, g, L, M, ctx->s);
     ctx->mark("q4k_gate_up");
+    fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p, ctx->s.sx2p,
+                         ctx->s.xs2);
+    ctx->mark("prep_h");
     fst::launch_q4k_down(st, g, L, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared);
     ctx->mark("q4k_down");
     FST_HIP_TRY(hipGetLastError());

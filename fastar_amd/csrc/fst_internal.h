@@ -51,13 +51,12 @@ struct Scratch {
     _Float16* x16p;        // [T][hd]    k-interleaved, power-of-two prescaled
     uint4* sxp;            // [T][hd/256][4] sub-block sums (hi,lo) per lane group
     int* xs;               // [T] prescale exponent
-    float* act;            // [P][2*inter] raw gate||up projections
-    _Float16* a16p;        // [P][inter]
+    float* act;            // [P][inter] h = silu(gate) * up
+    _Float16* a16p;        // [P][inter] h as the down projection's operand
     uint4* sx2p;           // [P][inter/256][4]
     int* xs2;              // [P]
     float* y;              // [P][hd]
     int* tok_npairs;       // [T] distinct (token, expert) pairs of each token incl. shared
-    int* slot_done;        // [S] gate/up workgroups finished per slot (re-armed to 0)
     int* tile_done;        // [T][hd/128] down contributions finished per token row tile (re-armed)
 };
 
@@ -123,11 +122,12 @@ void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float
 // Router logits and the activation prep of the same rows in one launch.
 void launch_router_prep(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
                         float* logits, const Scratch& s);
-void launch_prep_act(hipStream_t st, const float* gu, float swiglu_limit, const int* meta, int max_rows,
-                     int K, _Float16* a16p, uint4* sxp, int* xs);
+// h rows -> the down projection's operand (one workgroup per pair).
+void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
+                     uint4* sxp, int* xs);
 // Weights must be in the wave-tiled device layout (repack_q4k_expert).
-// gate/up also runs each slot's SwiGLU prep (last workgroup of the slot);
-// down also runs the combine of each token row tile (last contribution).
+// gate/up writes h = silu(gate)*up; down runs the combine of each token row
+// tile (last contribution).
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
                      const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,

@@ -2,13 +2,15 @@
 //
 // One MoE layer call is a fixed chain of stream-ordered launches with no host
 // round trip:
-//   router_logits   h[M,K] . W_r  (canonical fp32 order, bit-exact vs the CPU oracle)
-//   route_bucket    top-k + weights, then (token, expert) pairs grouped per expert
-//   prep_bf16       activations -> power-of-two prescaled fp16 operand tiles
-//   q4k_ffn<gate|up> fused Q4_K decode + MFMA gate/up + SiLU*up  -> act[pair][inter]
-//   prep_act        act -> fp16 operand tiles
-//   q4k_ffn<down>   fused Q4_K decode + MFMA down                  -> y[pair][hidden]
-//   combine         out[t] = sum_j w[t][j] y[pair(t,j)] + y[shared(t)]  (fixed order)
+//   router_prep     h[M,K] . W_r (canonical fp32 order, bit-exact vs the CPU
+//                   oracle) and, in extra workgroups, h -> prescaled fp16 operand
+//   route_bucket    top-k + weights; the last workgroup groups (token, expert)
+//                   pairs per expert slot
+//   q4k_linear<1>   gate||up: fused Q4_K decode + MFMA; each workgroup pairs 64
+//                   gate rows with the same 64 up rows -> h = silu(g)*u
+//   prep_act        h -> prescaled fp16 operand (one workgroup per pair)
+//   q4k_linear<2>   down; the last contribution to each (token, 128-row tile)
+//                   combines it: out[t] = sum_j w[t][j] y[pair(t,j)] + y[shared(t)]
 //
 // The Q4_K contraction (reference semantics: kernels/fst_dequant_q4k_kernel.cc
 // w = d*sc*q - dmin*m, GEMM orientation A.B^T from scripts/fst_validate_gemms.py:174)
@@ -385,45 +387,31 @@ void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, 
 
 // -------------------------------------------------------------- operand prep
 
-// Element sources for the prep kernel: bf16 activations, or the SwiGLU of a
-// gate||up row (act[i] = silu(g[i]) * u[i], g = row[i], u = row[K + i]).
+// Element sources for the prep kernel: bf16 activations, or the fp32
+// h = silu(gate)*up rows written by the gate/up kernel.
 struct SrcBf16 {
     const uint16_t* p;
     __device__ __forceinline__ float at(size_t row, int K, int i) const {
         return fst_bf16_to_f32(p[row * K + i]);
     }
 };
-struct SrcSwiGLU {
+struct SrcF32 {
     const float* p;
-    float lim;
-    __device__ __forceinline__ float at(size_t row, int K, int i) const {
-        float g = p[row * 2 * K + i], u = p[row * 2 * K + K + i];
-        if (lim > 0.0f) {
-            g = fminf(g, lim);
-            u = fminf(fmaxf(u, -lim), lim);
-        }
-        return (g / (1.0f + expf(-g))) * u;
-    }
+    __device__ __forceinline__ float at(size_t row, int K, int i) const { return p[row * K + i]; }
 };
-
-// Per row: amax -> exponent s so that amax*2^-s lies in [2^9, 2^10); then the
-// k-interleaved fp16 operand (per super-block, lane group g, MFMA c: elements
-// 64g+4c+{0,2,1,3} and 64g+32+4c+{0,2,1,3}, the order q4k_bop produces the
-// weights in) and per-sub-block sums split hi+lo.
 constexpr int kMaxPrepK = 8192;
 
-struct SrcSwiGLUCoherent {
-    const float* p;
-    float lim;
-    __device__ __forceinline__ float at(size_t row, int K, int i) const {
-        float g = ld_coherent(p + row * 2 * K + i), u = ld_coherent(p + row * 2 * K + K + i);
-        if (lim > 0.0f) {
-            g = fminf(g, lim);
-            u = fminf(fmaxf(u, -lim), lim);
-        }
-        return (g / (1.0f + expf(-g))) * u;
+// Power-of-two prescale of a row whose largest finite |x| is a: the s with
+// a*2^-s in [2^9, 2^10) (0 for a zero, infinite or NaN maximum).
+__device__ __forceinline__ int prescale_exp(float a) {
+    int s = 0;
+    if (a > 0.0f && a < INFINITY) {
+        int e;
+        frexpf(a, &e);  // a = f*2^e, f in [0.5,1)
+        s = e - 10;
     }
-};
+    return s;
+}
 
 // One row by one workgroup of NT threads (xv: K floats of LDS): amax ->
 // exponent s so that amax*2^-s lies in [2^9, 2^10); then the k-interleaved
@@ -449,12 +437,7 @@ __device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __
     if (tid == 0) {
         float a = red[0];
         for (int w = 1; w < NT / 64; ++w) a = fmaxf(a, red[w]);
-        int s = 0;
-        if (a > 0.0f && a < INFINITY) {
-            int e;
-            frexpf(a, &e);  // a = f*2^e, f in [0.5,1)
-            s = e - 10;
-        }
+        const int s = prescale_exp(a);
         s_sh = s;
         xs[row] = s;
     }
@@ -550,10 +533,10 @@ void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float
     hipLaunchKernelGGL(prep_kernel<SrcBf16>, dim3(rows), dim3(256), 0, st, SrcBf16{x}, nullptr, rows, K,
                        x16p, sxp, xs);
 }
-void launch_prep_act(hipStream_t st, const float* gu, float swiglu_limit, const int* meta, int max_rows,
-                     int K, _Float16* a16p, uint4* sxp, int* xs) {
-    hipLaunchKernelGGL(prep_kernel<SrcSwiGLU>, dim3(max_rows), dim3(256), 0, st, SrcSwiGLU{gu, swiglu_limit},
-                       meta + META_N_PAIRS, max_rows, K, a16p, sxp, xs);
+void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
+                     uint4* sxp, int* xs) {
+    hipLaunchKernelGGL(prep_kernel<SrcF32>, dim3(max_rows), dim3(256), 0, st, SrcF32{h}, meta + META_N_PAIRS,
+                       max_rows, K, a16p, sxp, xs);
 }
 
 // ------------------------------------------------------- Q4_K linear kernel
@@ -645,17 +628,15 @@ constexpr int kTokStride = 37;
 #ifndef FST_Q4K_WAVES_PER_EU
 #define FST_Q4K_WAVES_PER_EU 3
 #endif
-// What a linear-kernel launch does after its rows are written.
+// What a linear-kernel launch does besides Y = W.A.
 struct EpiArgs {
-    int mode;               // 0: nothing; 1: SwiGLU prep of the slot; 2: combine of token row tiles
-    // mode 1: the last workgroup of a slot turns its pairs' gate||up rows into
-    // the down projection's operand
+    // mode 1 (gate||up): workgroup tile T holds gate rows [64T, 64T+64) in
+    // waves 0..3 and the matching up rows in waves 4..7; it writes
+    // h = silu(gate) * up (fp32) for its 64 rows
     float swiglu_limit;
-    _Float16* a16p;
-    uint4* sx2p;
-    int* xs2;
-    int* slot_done;
-    // mode 2: the last contribution to a (token, 128-row tile) combines it
+    float* h;
+    // mode 2 (down): the last contribution to a (token, 128-row tile)
+    // combines it
     int tk, use_shared;
     const int* pair_tok;
     const int* pair_of;
@@ -669,12 +650,12 @@ struct EpiArgs {
 };
 
 #ifndef FST_Q4K_PF
-#define FST_Q4K_PF 2
+#define FST_Q4K_PF 1
 #endif
 // Y[pair][row] = 2^xs[a] * sum_k W[row][k] * A[a][k] for the rows of one
 // Q4_K matrix (N rows x K/256 super-blocks per row) of the slot's expert.
-// Grid: max_slots * N/(16*WAVES) workgroups; wave w of tile T owns rows
-// (T*WAVES + w)*16 .. +15 and up to TOKS tokens of its slot.
+// Grid: max_slots * N/(16*WAVES) workgroups; each wave owns 16 rows and up to
+// TOKS tokens of its slot.
 //  - weights stream through a ring of PF+1 register sets (PF super-blocks
 //    ahead), the ring unrolled so each set keeps fixed registers;
 //  - the slot's activation operands are staged into LDS in macro-stages of MS
@@ -686,13 +667,14 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
     const int* __restrict__ slot_off, const int* __restrict__ a_row, const _Float16* __restrict__ A,
     const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out, EpiArgs ep) {
+    static_assert(MODE != 1 || WAVES % 2 == 0, "gate||up pairs waves");
     constexpr int NGRP = (TOKS + 15) / 16;
     constexpr int TS = TOKS * kTokStride;            // one super-block of one stage
     constexpr int STAGE = MS * TS;                   // one macro-stage
-    constexpr int NCH = MS * TOKS * 36;              // 16-byte chunks per macro-stage
     constexpr int NT = 64 * WAVES;                   // threads per workgroup
+    constexpr int NCH = MS * TOKS * 36;              // 16-byte chunks per macro-stage
     constexpr int NS = (NCH + NT - 1) / NT;          // staged chunks per thread
-    __shared__ uint4 lds[2 * STAGE];
+    __shared__ uint4 lds[2 * STAGE + 1];
 
     const int tiles = N / (16 * WAVES);
     const int slot = blockIdx.x / tiles;
@@ -701,58 +683,80 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, g = lane >> 4;
     const int Me = min(slot_M[slot], TOKS), off = slot_off[slot];
-    const int row = (tile * WAVES + wave) * 16 + r;
+    int wtile;  // 16-row tile of the matrix owned by this wave
+    if constexpr (MODE == 1) {
+        constexpr int HALF = WAVES / 2;
+        wtile = wave < HALF ? tile * HALF + wave : (N / 32) + tile * HALF + (wave - HALF);
+    } else {
+        wtile = tile * WAVES + wave;
+    }
+    const int row = wtile * 16 + r;
     const int nsb = K >> 8;
     const int nms = (nsb + MS - 1) / MS;
     // wave-tiled device layout (see repack_q4k_matrix): the wave's 16 rows are
     // one contiguous run of nsb 2304-byte chunks read front to back
-    const uint8_t* wbase = bank + (size_t)slot_eid[slot] * expert_stride + mat_offset +
-                           (size_t)(tile * WAVES + wave) * nsb * 2304;
+    const uint8_t* wbase =
+        bank + (size_t)slot_eid[slot] * expert_stride + mat_offset + (size_t)wtile * nsb * 2304;
     const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
 
-    WRaw w[PF + 1];
+    // Every global load below is unconditional, with clamped addresses, and
+    // every staging decision is a compile-time function of the unrolled
+    // position: the number of loads in flight is then the same on every path
+    // and the compiler waits only for the oldest super-block instead of
+    // draining the prefetch ring at each step.
+    constexpr int R = PF + 1;                        // weight register ring
+    constexpr int U = (MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R);  // lcm(MS, R)
+    static_assert(U % MS == 0 && U % R == 0, "unroll must cover whole stages and ring turns");
+    WRaw w[R];
 #pragma unroll
     for (int j = 0; j < PF; ++j) w[j] = load_wraw(wbase + (size_t)min(j, nsb - 1) * 2304, lane);
 
-    for (int i = tid; i < 2 * STAGE; i += NT) lds[i] = z4;
-    // staging map: chunk q of a macro-stage -> (super-block u, token tl, part)
-    const uint4* ssrc[NS];
+    for (int i = tid; i < 2 * STAGE + 1; i += NT) lds[i] = z4;
+    // staging map: chunk q of a macro-stage -> (super-block u, token tl, part);
+    // chunks past the slot's tokens read a valid address and land in the
+    // spare LDS slot 2*STAGE
+    const u4v_t* ssrc[NS];
     int sdst[NS];
     int sstep[NS];
     int su[NS];
-    uint4 sv[NS];
+    u4v_t sv[NS];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
         const int q = tid + NT * i;
         const int u = q / (TOKS * 36), rem = q - u * (TOKS * 36);
         const int tl = rem / 36, part = rem - tl * 36;
-        ssrc[i] = SX;
-        sdst[i] = -1;
+        ssrc[i] = reinterpret_cast<const u4v_t*>(SX);
+        sdst[i] = 2 * STAGE;
         sstep[i] = 0;
         su[i] = u;
-        sv[i] = z4;
         if (q < NCH && tl < Me) {
             const int ar = a_row ? a_row[off + tl] : off + tl;
             if (part < 32) {
-                ssrc[i] = reinterpret_cast<const uint4*>(A + (size_t)ar * K) + u * 32 + part;
+                ssrc[i] = reinterpret_cast<const u4v_t*>(A + (size_t)ar * K) + u * 32 + part;
                 sstep[i] = 32 * MS;
             } else {
-                ssrc[i] = SX + (size_t)ar * nsb * 4 + u * 4 + (part - 32);
+                ssrc[i] = reinterpret_cast<const u4v_t*>(SX + (size_t)ar * nsb * 4 + u * 4 + (part - 32));
                 sstep[i] = 4 * MS;
             }
             sdst[i] = u * TS + tl * kTokStride + part;
         }
     }
+    // past the last macro-stage, or past nsb inside a partial one, a chunk
+    // re-reads its first super-block (a valid address; the value is unused)
     auto stage_load = [&](int m) {
 #pragma unroll
-        for (int i = 0; i < NS; ++i)
-            if (sdst[i] >= 0 && m * MS + su[i] < nsb) sv[i] = ssrc[i][(size_t)m * sstep[i]];
+        for (int i = 0; i < NS; ++i) {
+            const bool live = m * MS + su[i] < nsb;
+            const size_t o = live ? (size_t)m * sstep[i] : 0;
+            sv[i] = ssrc[i][o];
+        }
     };
     auto stage_store = [&](int m) {
-        uint4* dst = lds + (m & 1) * STAGE;
+        const int base = (m & 1) * STAGE;
 #pragma unroll
-        for (int i = 0; i < NS; ++i)
-            if (sdst[i] >= 0) dst[sdst[i]] = sv[i];
+        for (int i = 0; i < NS; ++i) {
+            *reinterpret_cast<u4v_t*>(&lds[sdst[i] < 2 * STAGE ? base + sdst[i] : 2 * STAGE]) = sv[i];
+        }
     };
     stage_load(0);
     __syncthreads();
@@ -766,12 +770,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     const uint32_t magic = 0x64006400u;
     const int ngrp_live = (Me + 15) >> 4;
 
-    // One super-block: consume `cur`, refill `nxt` (the set consumed one step
-    // earlier) with sb+PF, compute from the LDS macro-stage holding sb.
-    auto step = [&](int sb, const WRaw& cur, WRaw& nxt) {
+    auto compute = [&](int sb, const WRaw& cur) {
         const int m = sb / MS, u = sb - m * MS;
-        if (u == 0 && m + 1 < nms) stage_load(m + 1);
-        if (sb + PF < nsb) nxt = load_wraw(wbase + (size_t)(sb + PF) * 2304, lane);
         const uint4* st = lds + (m & 1) * STAGE + u * TS + r * kTokStride;
         Q4kScale S;
         q4k_scales(cur.h, g, S);
@@ -794,19 +794,67 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
                 acc[q][i] = fmaf(-S.dmin, Dm[i], acc[q][i]);
             }
         }
-        if (u == MS - 1 || sb == nsb - 1) {
-            if (m + 1 < nms) stage_store(m + 1);
-            __syncthreads();
-        }
     };
-    // ring of PF+1 register sets, unrolled so every set keeps fixed registers
-    for (int sb0 = 0; sb0 < nsb; sb0 += PF + 1) {
+    // U super-blocks per iteration (the launcher guarantees nsb % U == 0):
+    // ring slot j % R, stage boundaries at j % MS, all known at compile time.
+    // Every iteration ends on a barrier.
+    for (int sb0 = 0; sb0 < nsb; sb0 += U) {
 #pragma unroll
-        for (int j = 0; j <= PF; ++j)
-            if (sb0 + j < nsb) step(sb0 + j, w[j], w[(j + PF) % (PF + 1)]);
+        for (int j = 0; j < U; ++j) {
+            const int sb = sb0 + j;
+            if (j % MS == 0) stage_load(sb / MS + 1);
+            w[(j + PF) % R] = load_wraw(wbase + (size_t)min(sb + PF, nsb - 1) * 2304, lane);
+            // keep the prefetches where they are issued (the scheduler would
+            // otherwise sink them next to their use to save registers)
+            __builtin_amdgcn_sched_barrier(0);
+            compute(sb, w[j % R]);
+            if (j % MS == MS - 1) {
+                stage_store(sb / MS + 1);
+                __syncthreads();
+            }
+        }
     }
 
     // D layout: lane holds token rows 4g+i (i=0..3) of the group, column r.
+    auto unscale = [&](int pidx) -> int { return xs[a_row ? a_row[pidx] : pidx]; };
+    if constexpr (MODE == 1) {
+        // gate waves hand their rows to the up waves through LDS (the staging
+        // ring is free: the loop ended on a barrier)
+        constexpr int HALF = WAVES / 2;
+        float* xg = reinterpret_cast<float*>(lds);
+        if (wave < HALF) {
+#pragma unroll
+            for (int q = 0; q < NGRP; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tl = q * 16 + 4 * g + i;
+                    xg[((wave * NGRP + q) * 4 + i) * 64 + lane] =
+                        tl < Me ? ldexpf(acc[q][i], unscale(off + tl)) : 0.0f;
+                }
+        }
+        __syncthreads();
+        if (wave < HALF) return;
+        const int inter = N / 2;
+        const int n = (tile * HALF + wave - HALF) * 16 + r;
+        const float lim = ep.swiglu_limit;
+#pragma unroll
+        for (int q = 0; q < NGRP; ++q) {
+            if (q * 16 >= Me) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tl = q * 16 + 4 * g + i;
+                if (tl >= Me) continue;
+                float gv = xg[(((wave - HALF) * NGRP + q) * 4 + i) * 64 + lane];
+                float uv = ldexpf(acc[q][i], unscale(off + tl));
+                if (lim > 0.0f) {
+                    gv = fminf(gv, lim);
+                    uv = fminf(fmaxf(uv, -lim), lim);
+                }
+                ep.h[(size_t)(off + tl) * inter + n] = (gv / (1.0f + expf(-gv))) * uv;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < NGRP; ++q) {
         if (q * 16 >= Me) continue;
@@ -815,8 +863,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
             const int tl = q * 16 + 4 * g + i;
             if (tl >= Me) continue;
             const int pidx = off + tl;
-            const int ar = a_row ? a_row[pidx] : pidx;
-            const float v = ldexpf(acc[q][i], xs[ar]);
+            const float v = ldexpf(acc[q][i], unscale(pidx));
             if constexpr (MODE == 0)
                 out[(size_t)pidx * N + row] = v;
             else
@@ -825,23 +872,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     }
     if constexpr (MODE == 0) return;
 
-    // ---- completion epilogues (counters are re-armed by their consumer) ----
+    // ---- mode 2: one contribution per (pair, tile); the last one for a token
+    // combines its tile (counters are re-armed by their consumer) ----
     __shared__ int s_flag[64];
     __shared__ int s_nflag;
     publish_wait();
     __syncthreads();
-    float* xv = reinterpret_cast<float*>(lds);  // the staging ring is free now
-    if constexpr (MODE == 1) {
-        if (tid == 0) s_nflag = signal_add(&ep.slot_done[slot], 1) == tiles - 1;
-        __syncthreads();
-        if (!s_nflag) return;
-        if (tid == 0) ep.slot_done[slot] = 0;
-        const int inter = N / 2;
-        for (int tl = 0; tl < slot_M[slot]; ++tl)
-            prep_row<NT>(SrcSwiGLUCoherent{out, ep.swiglu_limit}, off + tl, inter, xv, ep.a16p, ep.sx2p, ep.xs2);
-        return;
-    }
-    // mode 2: one contribution per (pair, tile); the last one for a token combines its tile
     if (tid == 0) s_nflag = 0;
     __syncthreads();
     const int nt128 = N / 128;
@@ -889,8 +925,11 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 #define FST_Q4K_LAUNCH(T, MSV)                                                                               \
     hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE>), grid, dim3(64 * W), 0, st, bank, stride, mat_off, \
                        K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep)
-    if (M <= 8)
+    // K is a multiple of 512 (checked at context creation): nsb is even
+    if (M <= 8 && (K >> 8) % 4 == 0)
         FST_Q4K_LAUNCH(8, 4);
+    else if (M <= 8)
+        FST_Q4K_LAUNCH(8, 2);
     else if (M <= 16)
         FST_Q4K_LAUNCH(16, 2);
     else if (M <= 32)
@@ -900,19 +939,14 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 #undef FST_Q4K_LAUNCH
 }
 
-// gate||up: the two [inter][hd/256] matrices are contiguous, so they are one
-// 2*inter-row matrix; the last workgroup of each slot applies the SwiGLU and
-// prepares the down operand of the slot's pairs.
+// gate||up: the two [inter][hd/256] matrices are contiguous; each workgroup
+// takes 64 gate rows and the same 64 up rows and writes h = silu(gate)*up.
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
     EpiArgs ep{};
-    ep.mode = 1;
     ep.swiglu_limit = g.swiglu_limit;
-    ep.a16p = s.a16p;
-    ep.sx2p = s.sx2p;
-    ep.xs2 = s.xs2;
-    ep.slot_done = s.slot_done;
+    ep.h = s.act;
     launch_q4k_linear<1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
-                         s.pair_tok, s.x16p, s.sxp, s.xs, s.act, ep);
+                         s.pair_tok, s.x16p, s.sxp, s.xs, nullptr, ep);
 }
 
 // down: the last contribution to each (token, 128-row tile) combines it:
@@ -923,7 +957,6 @@ void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int 
                      uint16_t* out_shared) {
     const size_t proj = (size_t)g.inter * (g.hd / 256) * 144;
     EpiArgs ep{};
-    ep.mode = 2;
     ep.tk = g.tk;
     ep.use_shared = use_shared;
     ep.pair_tok = s.pair_tok;
