@@ -226,6 +226,7 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     fst::Scratch& s = x->s;
     const int T = c.max_tokens, tk = c.top_k;
     s.max_tokens = T;
+    s.n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     s.max_pairs = T * tk + T;
     s.max_slots = std::min(E, T * tk) + 1;
     const int P = s.max_pairs, S = s.max_slots;

@@ -25,14 +25,13 @@ enum MetaIdx {
     META_N_PAIRS = 2,      // (token, expert) pairs incl. shared
     META_ERROR = 3,        // nonzero: invalid expert id seen
     META_N_ROUTED_PAIRS = 4,
-    META_TOPK_ERROR = 5,   // set by the top-k kernel, folded into META_ERROR by bucketing
-    META_TOPK_DONE = 6,    // top-k workgroups finished (re-armed to 0 by the last one)
     META_WORDS = 8
 };
 
 // Device scratch owned by a context, sized for max_tokens.
 struct Scratch {
     int max_tokens, max_pairs, max_slots;
+    int n_cu;              // compute units of the device (persistent grids)
     uint16_t* h;           // bf16 [T][hd] staging for host-pointer calls
     uint16_t* out;         // bf16 [T][hd]
     uint16_t* out_routed;  // bf16 [T][hd]

@@ -129,32 +129,30 @@ __device__ __forceinline__ unsigned long long topk_key(float sel, int id) {
     return ((unsigned long long)o << 32) | (0xffffffffu - (uint32_t)id);
 }
 
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-    const unsigned lo = __shfl_xor((unsigned)v, m, 64), hi = __shfl_xor((unsigned)(v >> 32), m, 64);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
 // (token, expert) pairs grouped per slot: the shared expert (if used) is slot
 // 0 with all M tokens (so its work starts first), then the routed experts in
 // ascending id, tokens ascending within an expert.  Also counts each token's
 // distinct pairs (the number of down contributions its combine waits for).
-// Run by one whole 256-thread workgroup.
-__device__ void bucket_block(int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids,
+// eids_s: the call's [M][tk] expert ids, already in LDS.  One workgroup of NT
+// threads.
+template <int NT>
+__device__ void bucket_block(int M, int E, int tk, int use_shared, const int* eids_s, int topk_err,
                              int* __restrict__ meta, int* __restrict__ slot_eid, int* __restrict__ slot_M,
                              int* __restrict__ slot_off, int* __restrict__ pair_tok,
                              int* __restrict__ pair_of, int* __restrict__ pair_shared,
                              int* __restrict__ tok_npairs) {
+    constexpr int NW = NT / 64;
     __shared__ unsigned long long hitmask[kMaxExperts];
     __shared__ int eoff[kMaxExperts];
-    __shared__ int wave_tot[2][4];
+    __shared__ int wave_tot[2][NW];
     __shared__ int err;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (tid == 0) err = 0;
-    for (int e = tid; e < E; e += 256) hitmask[e] = 0ull;
+    for (int e = tid; e < E; e += NT) hitmask[e] = 0ull;
     __syncthreads();
-    for (int i = tid; i < M * tk; i += 256) {
+    for (int i = tid; i < M * tk; i += NT) {
         const int t = i / tk;
-        const int e = __hip_atomic_load(&eids[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int e = eids_s[i];
         if (e < 0 || e >= E)
             atomicOr(&err, 1);
         else
@@ -163,7 +161,7 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int32_t
     __syncthreads();
     const int s0 = use_shared ? 1 : 0, p0 = use_shared ? M : 0;
     int slot_base = s0, pair_base = p0;
-    for (int e0 = 0; e0 < E; e0 += 256) {
+    for (int e0 = 0; e0 < E; e0 += NT) {
         const int e = e0 + tid;
         const int cnt = (e < E) ? __popcll(hitmask[e]) : 0;
         const int act = cnt > 0;
@@ -194,7 +192,7 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int32_t
         }
         if (e < E) eoff[e] = ex_c;
         int tot_a = 0, tot_c = 0;
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NW; ++w) {
             tot_a += wave_tot[0][w];
             tot_c += wave_tot[1][w];
         }
@@ -202,9 +200,9 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int32_t
         pair_base += tot_c;
         __syncthreads();
     }
-    for (int i = tid; i < M * tk; i += 256) {
+    for (int i = tid; i < M * tk; i += NT) {
         const int t = i / tk;
-        const int e = __hip_atomic_load(&eids[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int e = eids_s[i];
         int p = -1;
         if (e >= 0 && e < E) {
             p = eoff[e] + __popcll(hitmask[e] & ((1ull << t) - 1ull));
@@ -212,14 +210,13 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int32_t
         }
         pair_of[i] = p;
     }
-    for (int t = tid; t < M; t += 256) {
+    for (int t = tid; t < M; t += NT) {
         int n = use_shared ? 1 : 0;
         for (int j = 0; j < tk; ++j) {
-            const int e = __hip_atomic_load(&eids[t * tk + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int e = eids_s[t * tk + j];
             if (e < 0 || e >= E) continue;
             bool dup = false;
-            for (int j2 = 0; j2 < j; ++j2)
-                dup |= __hip_atomic_load(&eids[t * tk + j2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == e;
+            for (int j2 = 0; j2 < j; ++j2) dup |= eids_s[t * tk + j2] == e;
             n += dup ? 0 : 1;
         }
         tok_npairs[t] = n;
@@ -239,45 +236,58 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int32_t
         meta[META_N_SLOTS] = slot_base;
         meta[META_N_ROUTED_PAIRS] = pair_base - p0;
         meta[META_N_PAIRS] = pair_base;
-        meta[META_ERROR] = err | meta[META_TOPK_ERROR];
-        meta[META_TOPK_ERROR] = 0;
+        meta[META_ERROR] = err | topk_err;
     }
 }
 
-__global__ __launch_bounds__(256) void bucket_kernel(int M, int E, int tk, int use_shared,
-                                                     const int32_t* __restrict__ eids, int* __restrict__ meta,
-                                                     int* __restrict__ slot_eid, int* __restrict__ slot_M,
-                                                     int* __restrict__ slot_off, int* __restrict__ pair_tok,
-                                                     int* __restrict__ pair_of, int* __restrict__ pair_shared,
-                                                     int* __restrict__ tok_npairs) {
-    bucket_block(M, E, tk, use_shared, eids, meta, slot_eid, slot_M, slot_off, pair_tok, pair_of, pair_shared,
-                 tok_npairs);
+constexpr int kRouteThreads = 1024;
+
+// Caller-given routing: eids [M][tk] in global memory.
+__global__ __launch_bounds__(kRouteThreads) void bucket_kernel(
+    int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids, int* __restrict__ meta,
+    int* __restrict__ slot_eid, int* __restrict__ slot_M, int* __restrict__ slot_off, int* __restrict__ pair_tok,
+    int* __restrict__ pair_of, int* __restrict__ pair_shared, int* __restrict__ tok_npairs) {
+    __shared__ int s_eids[kMaxTokens * kMaxTopK];
+    for (int i = threadIdx.x; i < M * tk; i += kRouteThreads) s_eids[i] = eids[i];
+    __syncthreads();
+    bucket_block<kRouteThreads>(M, E, tk, use_shared, s_eids, 0, meta, slot_eid, slot_M, slot_off, pair_tok,
+                                pair_of, pair_shared, tok_npairs);
 }
 
-// One workgroup per token: wave 0 selects the token's top-k (src/fst_engine.cpp
-// :974-1061 semantics with the order of topk_key) or reads its hash-table row
-// (:1015-1021) and writes eids/wts; the workgroup that finishes last then
-// groups all tokens' (token, expert) pairs (bucket_block) and re-arms the
-// completion counter.  PER = experts per lane.
+// One workgroup: wave w selects the top-k of tokens w, w+16, ...
+// (src/fst_engine.cpp:974-1061 semantics with the order of topk_key) or reads
+// their hash-table rows (:1015-1021) and writes eids/wts; after one barrier
+// the same workgroup groups all tokens' (token, expert) pairs.  PER = experts
+// per lane.
 template <int PER>
-__global__ __launch_bounds__(256) void topk_bucket_kernel(
+__global__ __launch_bounds__(kRouteThreads) void topk_bucket_kernel(
     int M, int E, int tk, int score_func, int round_bf16, float route_scale, const float* __restrict__ logits,
     const float* __restrict__ bias, const int32_t* __restrict__ hash, const int32_t* __restrict__ ids,
     int vocab, int use_shared, int32_t* __restrict__ eids, float* __restrict__ wts, int* __restrict__ meta,
     int* __restrict__ slot_eid, int* __restrict__ slot_M, int* __restrict__ slot_off,
     int* __restrict__ pair_tok, int* __restrict__ pair_of, int* __restrict__ pair_shared,
     int* __restrict__ tok_npairs) {
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-    const float* row = logits + (size_t)t * E;
-    if (tid < 64) {
+    constexpr int NW = kRouteThreads / 64;
+    __shared__ int s_eids[kMaxTokens * kMaxTopK];
+    __shared__ int s_err;
+    __shared__ unsigned long long s_wkey[NW][kMaxTopK];
+    __shared__ float s_wsc[NW][kMaxTopK];
+    __shared__ float s_rank_sc[NW][kMaxTopK];
+    __shared__ int s_rank_id[NW][kMaxTopK];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if (tid == 0) s_err = 0;
+    __syncthreads();
+    for (int t = wave; t < M; t += NW) {
+        const float* row = logits + (size_t)t * E;
         if (hash) {
             if (lane == 0) {
                 const int tok = ids ? ids[t] : -1;
                 if (tok < 0 || tok >= vocab) {
-                    atomicOr(&meta[META_TOPK_ERROR], 2);
+                    atomicOr(&s_err, 2);
                     for (int k = 0; k < tk; ++k) {
-                        st_coherent(&eids[(size_t)t * tk + k], -1);
-                        st_coherent(&wts[(size_t)t * tk + k], 0.0f);
+                        s_eids[t * tk + k] = -1;
+                        eids[(size_t)t * tk + k] = -1;
+                        wts[(size_t)t * tk + k] = 0.0f;
                     }
                 } else {
                     float sc[kMaxTopK];
@@ -288,89 +298,117 @@ __global__ __launch_bounds__(256) void topk_bucket_kernel(
                         if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
                         sc[k] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
                         sum += sc[k];
-                        st_coherent(&eids[(size_t)t * tk + k], e);
+                        s_eids[t * tk + k] = e;
+                        eids[(size_t)t * tk + k] = e;
                     }
                     const float inv = 1.0f / (sum + 1e-12f);
-                    for (int k = 0; k < tk; ++k) st_coherent(&wts[(size_t)t * tk + k], sc[k] * inv * route_scale);
+                    for (int k = 0; k < tk; ++k) wts[(size_t)t * tk + k] = sc[k] * inv * route_scale;
                 }
             }
-        } else {
-            unsigned long long key[PER];
-            float sc[PER];
+            continue;
+        }
+        // Exact top-k by radix selection on the 32 order bits of topk_key
+        // (ballots, no 64-bit shuffles): T = the k-th largest order value,
+        // winners = {o > T} plus the lowest ids with o == T; then each winner
+        // is ranked among the winners by the full key (order desc, id asc).
+        uint32_t o[PER];
+        float sc[PER];
+        bool valid[PER];
 #pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                const int e = lane + 64 * i;
-                key[i] = 0ull;
-                sc[i] = 0.0f;
-                if (e < E) {
-                    float x = row[e];
-                    if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
-                    const float sv = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
-                    sc[i] = sv;
-                    key[i] = topk_key(sv + (bias ? bias[e] : 0.0f), e);
-                }
-            }
-            float chosen_sc = 0.0f, sum = 0.0f;
-            int chosen_id = 0;
-            for (int k = 0; k < tk; ++k) {
-                unsigned long long b = key[0];
-#pragma unroll
-                for (int i = 1; i < PER; ++i) b = key[i] > b ? key[i] : b;
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) {
-                    const unsigned long long o = shfl_xor_u64(b, off);
-                    b = o > b ? o : b;
-                }
-                const int id = (int)(0xffffffffu - (uint32_t)b);
-                const int owner = id & 63, slot_i = id >> 6;
-                float mine = 0.0f;
-#pragma unroll
-                for (int i = 0; i < PER; ++i)
-                    if (i == slot_i) mine = sc[i];
-                const float s_win = __shfl(mine, owner, 64);
-                if (lane == owner) {
-#pragma unroll
-                    for (int i = 0; i < PER; ++i)
-                        if (i == slot_i) key[i] = 0ull;
-                }
-                if (lane == k) {
-                    chosen_sc = s_win;
-                    chosen_id = id;
-                }
-                sum += s_win;  // same sequential order in every lane
-            }
-            if (lane < tk) {
-                const float inv = 1.0f / (sum + 1e-12f);
-                st_coherent(&eids[(size_t)t * tk + lane], chosen_id);
-                st_coherent(&wts[(size_t)t * tk + lane], chosen_sc * inv * route_scale);
+        for (int i = 0; i < PER; ++i) {
+            const int e = lane + 64 * i;
+            o[i] = 0u;
+            sc[i] = 0.0f;
+            valid[i] = e < E;
+            if (valid[i]) {
+                float x = row[e];
+                if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
+                const float sv = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+                sc[i] = sv;
+                o[i] = (uint32_t)(topk_key(sv + (bias ? bias[e] : 0.0f), e) >> 32);
             }
         }
+        auto count_ge = [&](uint32_t thr) -> int {
+            int c = 0;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) c += __popcll(__ballot(valid[i] && o[i] >= thr));
+            return c;
+        };
+        uint32_t T = 0u;
+        for (int bit = 31; bit >= 0; --bit) {
+            const uint32_t cand = T | (1u << bit);
+            if (count_ge(cand) >= tk) T = cand;
+        }
+        int need = tk;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) need -= __popcll(__ballot(valid[i] && o[i] > T));
+        // ties at T: lowest ids first (id = lane + 64 i)
+        bool win[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned long long tie = __ballot(valid[i] && o[i] == T);
+            const unsigned long long below = (lane == 0) ? 0ull : (tie & ((1ull << lane) - 1ull));
+            const int before = __popcll(below);
+            win[i] = valid[i] && (o[i] > T || (o[i] == T && before < need));
+            need -= min(need, __popcll(tie));
+        }
+        // compact the winners into LDS (ascending id), rank them, emit in rank order
+        unsigned long long* wkey = s_wkey[wave];
+        float* wsc = s_wsc[wave];
+        int base = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned long long m = __ballot(win[i]);
+            if (win[i]) {
+                const int pos = base + __popcll(lane == 0 ? 0ull : (m & ((1ull << lane) - 1ull)));
+                wkey[pos] = ((unsigned long long)o[i] << 32) | (0xffffffffu - (uint32_t)(lane + 64 * i));
+                wsc[pos] = sc[i];
+            }
+            base += __popcll(m);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < tk) {
+            const unsigned long long mk = wkey[lane];
+            int rank = 0;
+            for (int j = 0; j < tk; ++j) rank += wkey[j] > mk;
+            s_rank_sc[wave][rank] = wsc[lane];
+            s_rank_id[wave][rank] = (int)(0xffffffffu - (uint32_t)mk);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < tk) {
+            float sum = 0.0f;
+            for (int j = 0; j < tk; ++j) sum += s_rank_sc[wave][j];  // selection order, as the reference sums
+            const float inv = 1.0f / (sum + 1e-12f);
+            const int id = s_rank_id[wave][lane];
+            s_eids[t * tk + lane] = id;
+            eids[(size_t)t * tk + lane] = id;
+            wts[(size_t)t * tk + lane] = s_rank_sc[wave][lane] * inv * route_scale;
+        }
+        __builtin_amdgcn_wave_barrier();
     }
-    // completion: the last workgroup buckets every token
-    __shared__ int last;
-    publish_wait();
     __syncthreads();
-    if (tid == 0) last = signal_add(&meta[META_TOPK_DONE], 1) == M - 1;
-    __syncthreads();
-    if (!last) return;
-    bucket_block(M, E, tk, use_shared, eids, meta, slot_eid, slot_M, slot_off, pair_tok, pair_of, pair_shared,
-                 tok_npairs);
-    if (tid == 0) meta[META_TOPK_DONE] = 0;
+    bucket_block<kRouteThreads>(M, E, tk, use_shared, s_eids, s_err, meta, slot_eid, slot_M, slot_off, pair_tok,
+                                pair_of, pair_shared, tok_npairs);
 }
 
 void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, int M,
                          const float* logits, const int32_t* input_ids, int use_hash, int do_topk,
                          int use_shared, int32_t* eids, float* wts, const Scratch& s) {
     if (!do_topk) {
-        hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(256), 0, st, M, g.E, g.tk, use_shared, eids, s.meta,
-                           s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared, s.tok_npairs);
+        hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(kRouteThreads), 0, st, M, g.E, g.tk, use_shared, eids,
+                           s.meta, s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared,
+                           s.tok_npairs);
         return;
     }
 #define FST_TOPK(PERV)                                                                                     \
-    hipLaunchKernelGGL(topk_bucket_kernel<PERV>, dim3(M), dim3(256), 0, st, M, g.E, g.tk, g.score_func,      \
-                       g.round_logits_bf16, g.route_scale, logits, L.router_bias, use_hash ? L.hash : nullptr, \
-                       input_ids, g.vocab, use_shared, eids, wts, s.meta, s.slot_eid, s.slot_M, s.slot_off,   \
-                       s.pair_tok, s.pair_of, s.pair_shared, s.tok_npairs)
+    hipLaunchKernelGGL(topk_bucket_kernel<PERV>, dim3(1), dim3(kRouteThreads), 0, st, M, g.E, g.tk,        \
+                       g.score_func, g.round_logits_bf16, g.route_scale, logits, L.router_bias,            \
+                       use_hash ? L.hash : nullptr, input_ids, g.vocab, use_shared, eids, wts, s.meta,       \
+                       s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared, s.tok_npairs)
     const int per = (g.E + 63) / 64;
     if (per <= 1)
         FST_TOPK(1);
@@ -626,7 +664,7 @@ constexpr int kTokStride = 37;
 // the slot's activation operands are staged per super-block in a
 // double-buffered LDS ring shared by the 4 waves.
 #ifndef FST_Q4K_WAVES_PER_EU
-#define FST_Q4K_WAVES_PER_EU 3
+#define FST_Q4K_WAVES_PER_EU 4
 #endif
 // What a linear-kernel launch does besides Y = W.A.
 struct EpiArgs {
@@ -653,16 +691,18 @@ struct EpiArgs {
 #define FST_Q4K_PF 1
 #endif
 // Y[pair][row] = 2^xs[a] * sum_k W[row][k] * A[a][k] for the rows of one
-// Q4_K matrix (N rows x K/256 super-blocks per row) of the slot's expert.
-// Grid: max_slots * N/(16*WAVES) workgroups; each wave owns 16 rows and up to
-// TOKS tokens of its slot.
+// Q4_K matrix (N rows x K/256 super-blocks per row) of each slot's expert.
+// Work item t = (slot, tile) covers 16*WAVES rows: wave w owns 16 rows and up
+// to TOKS tokens of the slot.  The grid is persistent (a few workgroups per
+// CU) and walks t = blockIdx.x, +gridDim.x, ...; the first weights of the
+// next item are fetched while the current one finishes.
 //  - weights stream through a ring of PF+1 register sets (PF super-blocks
 //    ahead), the ring unrolled so each set keeps fixed registers;
 //  - the slot's activation operands are staged into LDS in macro-stages of MS
 //    super-blocks (double-buffered, prefetched one macro-stage ahead into
 //    registers), one workgroup barrier per macro-stage.
 template <int TOKS, int MS, int WAVES, int MODE, int PF = FST_Q4K_PF>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_Q4K_WAVES_PER_EU))) void q4k_linear_kernel(
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : 3))) void q4k_linear_kernel(
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
     const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
     const int* __restrict__ slot_off, const int* __restrict__ a_row, const _Float16* __restrict__ A,
@@ -674,75 +714,97 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     constexpr int NT = 64 * WAVES;                   // threads per workgroup
     constexpr int NCH = MS * TOKS * 36;              // 16-byte chunks per macro-stage
     constexpr int NS = (NCH + NT - 1) / NT;          // staged chunks per thread
+    constexpr int HALF = WAVES / 2;
+    constexpr int R = PF + 1;                        // weight register ring
+    constexpr int U = (MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R);  // lcm(MS, R)
+    static_assert(U % MS == 0 && U % R == 0, "unroll must cover whole stages and ring turns");
     __shared__ uint4 lds[2 * STAGE + 1];
+    __shared__ int s_flag[kMaxTokens];
+    __shared__ int s_nflag;
 
     const int tiles = N / (16 * WAVES);
-    const int slot = blockIdx.x / tiles;
-    const int tile = blockIdx.x - slot * tiles;
-    if (slot >= meta[META_N_SLOTS]) return;
+    const int total = meta[META_N_SLOTS] * tiles;
+    if ((int)blockIdx.x >= total) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, g = lane >> 4;
-    const int Me = min(slot_M[slot], TOKS), off = slot_off[slot];
-    int wtile;  // 16-row tile of the matrix owned by this wave
-    if constexpr (MODE == 1) {
-        constexpr int HALF = WAVES / 2;
-        wtile = wave < HALF ? tile * HALF + wave : (N / 32) + tile * HALF + (wave - HALF);
-    } else {
-        wtile = tile * WAVES + wave;
-    }
-    const int row = wtile * 16 + r;
     const int nsb = K >> 8;
-    const int nms = (nsb + MS - 1) / MS;
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+    const f4_t zf = f4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t magic = 0x64006400u;
+
+    // 16-row tile of the matrix owned by this wave in work item tt; MODE 1
+    // pairs gate rows [64T, 64T+64) (waves 0..3) with the same up rows
+    auto wave_tile = [&](int tile) -> int {
+        if constexpr (MODE == 1)
+            return wave < HALF ? tile * HALF + wave : (N / 32) + tile * HALF + (wave - HALF);
+        else
+            return tile * WAVES + wave;
+    };
     // wave-tiled device layout (see repack_q4k_matrix): the wave's 16 rows are
     // one contiguous run of nsb 2304-byte chunks read front to back
-    const uint8_t* wbase =
-        bank + (size_t)slot_eid[slot] * expert_stride + mat_offset + (size_t)wtile * nsb * 2304;
-    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+    auto wave_base = [&](int tt) -> const uint8_t* {
+        const int sl = tt / tiles;
+        return bank + (size_t)slot_eid[sl] * expert_stride + mat_offset +
+               (size_t)wave_tile(tt - sl * tiles) * nsb * 2304;
+    };
 
     // Every global load below is unconditional, with clamped addresses, and
     // every staging decision is a compile-time function of the unrolled
     // position: the number of loads in flight is then the same on every path
     // and the compiler waits only for the oldest super-block instead of
     // draining the prefetch ring at each step.
-    constexpr int R = PF + 1;                        // weight register ring
-    constexpr int U = (MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R);  // lcm(MS, R)
-    static_assert(U % MS == 0 && U % R == 0, "unroll must cover whole stages and ring turns");
+    const uint8_t* wbase = wave_base(blockIdx.x);
     WRaw w[R];
 #pragma unroll
-    for (int j = 0; j < PF; ++j) w[j] = load_wraw(wbase + (size_t)min(j, nsb - 1) * 2304, lane);
-
+    for (int j = 0; j < PF; ++j) w[j] = load_wraw(wbase + (size_t)j * 2304, lane);
     for (int i = tid; i < 2 * STAGE + 1; i += NT) lds[i] = z4;
-    // staging map: chunk q of a macro-stage -> (super-block u, token tl, part);
-    // chunks past the slot's tokens read a valid address and land in the
-    // spare LDS slot 2*STAGE
-    const u4v_t* ssrc[NS];
-    int sdst[NS];
-    int sstep[NS];
-    int su[NS];
-    u4v_t sv[NS];
+
+    // Staging map: chunk q = tid + NT*i of a macro-stage -> (super-block u,
+    // token tl, part).  Chunks past the slot's tokens read a valid address
+    // and land in the spare LDS slot 2*STAGE.  The next item's token rows are
+    // fetched when an item starts and its map is built (and its first stage
+    // loaded) during the current item's last macro-stage.
+    int su[NS], stl[NS], spart[NS];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
         const int q = tid + NT * i;
         const int u = q / (TOKS * 36), rem = q - u * (TOKS * 36);
-        const int tl = rem / 36, part = rem - tl * 36;
-        ssrc[i] = reinterpret_cast<const u4v_t*>(SX);
-        sdst[i] = 2 * STAGE;
-        sstep[i] = 0;
         su[i] = u;
-        if (q < NCH && tl < Me) {
-            const int ar = a_row ? a_row[off + tl] : off + tl;
-            if (part < 32) {
-                ssrc[i] = reinterpret_cast<const u4v_t*>(A + (size_t)ar * K) + u * 32 + part;
-                sstep[i] = 32 * MS;
-            } else {
-                ssrc[i] = reinterpret_cast<const u4v_t*>(SX + (size_t)ar * nsb * 4 + u * 4 + (part - 32));
-                sstep[i] = 4 * MS;
-            }
-            sdst[i] = u * TS + tl * kTokStride + part;
-        }
+        stl[i] = q < NCH ? rem / 36 : TOKS;
+        spart[i] = rem - (rem / 36) * 36;
     }
-    // past the last macro-stage, or past nsb inside a partial one, a chunk
-    // re-reads its first super-block (a valid address; the value is unused)
+    auto load_rows = [&](int tt, int* ar) {
+        const int sl = tt / tiles;
+        const int Mi = min(slot_M[sl], TOKS), offi = slot_off[sl];
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+            ar[i] = stl[i] < Mi ? (a_row ? a_row[offi + stl[i]] : offi + stl[i]) : -1;
+    };
+    const u4v_t* ssrc[NS];
+    int sdst[NS];
+    int sstep[NS];
+    u4v_t sv[NS];
+    auto build_map = [&](const int* ar) {
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            const int u = su[i], part = spart[i];
+            ssrc[i] = reinterpret_cast<const u4v_t*>(SX);
+            sdst[i] = 2 * STAGE;
+            sstep[i] = 0;
+            if (ar[i] >= 0) {
+                if (part < 32) {
+                    ssrc[i] = reinterpret_cast<const u4v_t*>(A + (size_t)ar[i] * K) + u * 32 + part;
+                    sstep[i] = 32 * MS;
+                } else {
+                    ssrc[i] = reinterpret_cast<const u4v_t*>(SX + (size_t)ar[i] * nsb * 4 + u * 4 + (part - 32));
+                    sstep[i] = 4 * MS;
+                }
+                sdst[i] = u * TS + stl[i] * kTokStride + part;
+            }
+        }
+    };
+    // past nsb inside a partial macro-stage a chunk re-reads its first
+    // super-block (a valid address; the value is unused)
     auto stage_load = [&](int m) {
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
@@ -754,180 +816,213 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(FST_
     auto stage_store = [&](int m) {
         const int base = (m & 1) * STAGE;
 #pragma unroll
-        for (int i = 0; i < NS; ++i) {
+        for (int i = 0; i < NS; ++i)
             *reinterpret_cast<u4v_t*>(&lds[sdst[i] < 2 * STAGE ? base + sdst[i] : 2 * STAGE]) = sv[i];
-        }
     };
-    stage_load(0);
-    __syncthreads();
-    stage_store(0);
-    __syncthreads();
-
-    f4_t acc[NGRP];
-#pragma unroll
-    for (int q = 0; q < NGRP; ++q) acc[q] = f4_t{0.f, 0.f, 0.f, 0.f};
-    const f4_t zf = f4_t{0.f, 0.f, 0.f, 0.f};
-    const uint32_t magic = 0x64006400u;
-    const int ngrp_live = (Me + 15) >> 4;
-
-    auto compute = [&](int sb, const WRaw& cur) {
-        const int m = sb / MS, u = sb - m * MS;
-        const uint4* st = lds + (m & 1) * STAGE + u * TS + r * kTokStride;
-        Q4kScale S;
-        q4k_scales(cur.h, g, S);
-        const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
-#pragma unroll
-        for (int q = 0; q < NGRP; ++q) {
-            if (q > 0 && q >= ngrp_live) break;
-            const uint4* sq = st + q * 16 * kTokStride;
-            f4_t D = zf;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const h8_t a = __builtin_bit_cast(h8_t, sq[8 * g + c]);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, q4k_bop(Dw[c], S, magic), D, 0, 0, 0);
-            }
-            const h8_t am = __builtin_bit_cast(h8_t, sq[32 + g]);
-            const f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, S.m, zf, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[q][i] = fmaf(S.d, D[i], acc[q][i]);
-                acc[q][i] = fmaf(-S.dmin, Dm[i], acc[q][i]);
-            }
-        }
-    };
-    // U super-blocks per iteration (the launcher guarantees nsb % U == 0):
-    // ring slot j % R, stage boundaries at j % MS, all known at compile time.
-    // Every iteration ends on a barrier.
-    for (int sb0 = 0; sb0 < nsb; sb0 += U) {
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-            const int sb = sb0 + j;
-            if (j % MS == 0) stage_load(sb / MS + 1);
-            w[(j + PF) % R] = load_wraw(wbase + (size_t)min(sb + PF, nsb - 1) * 2304, lane);
-            // keep the prefetches where they are issued (the scheduler would
-            // otherwise sink them next to their use to save registers)
-            __builtin_amdgcn_sched_barrier(0);
-            compute(sb, w[j % R]);
-            if (j % MS == MS - 1) {
-                stage_store(sb / MS + 1);
-                __syncthreads();
-            }
-        }
+    {
+        int ar0[NS];
+        load_rows(blockIdx.x, ar0);
+        build_map(ar0);
+        stage_load(0);
     }
+    const int nms = nsb / MS;
 
-    // D layout: lane holds token rows 4g+i (i=0..3) of the group, column r.
-    auto unscale = [&](int pidx) -> int { return xs[a_row ? a_row[pidx] : pidx]; };
-    if constexpr (MODE == 1) {
-        // gate waves hand their rows to the up waves through LDS (the staging
-        // ring is free: the loop ended on a barrier)
-        constexpr int HALF = WAVES / 2;
-        float* xg = reinterpret_cast<float*>(lds);
-        if (wave < HALF) {
+    for (int t = blockIdx.x; t < total; t += gridDim.x) {
+        const int slot = t / tiles;
+        const int tile = t - slot * tiles;
+        const int tn = t + (int)gridDim.x;
+        const uint8_t* nbase = tn < total ? wave_base(tn) : wbase;
+        const int Me = min(slot_M[slot], TOKS), off = slot_off[slot];
+        const int row = wave_tile(tile) * 16 + r;
+        int ar_next[NS];
+        load_rows(tn < total ? tn : t, ar_next);
+
+        __syncthreads();  // the previous item's readers of the LDS are done
+        stage_store(0);
+        __syncthreads();
+
+        f4_t acc[NGRP];
 #pragma unroll
-            for (int q = 0; q < NGRP; ++q)
+        for (int q = 0; q < NGRP; ++q) acc[q] = zf;
+        const int ngrp_live = (Me + 15) >> 4;
+
+        auto compute = [&](int sb, const WRaw& cur) {
+            const int m = sb / MS, u = sb - m * MS;
+            const uint4* st = lds + (m & 1) * STAGE + u * TS + r * kTokStride;
+            Q4kScale S;
+            q4k_scales(cur.h, g, S);
+            const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+#pragma unroll
+            for (int q = 0; q < NGRP; ++q) {
+                if (q > 0 && q >= ngrp_live) break;
+                const uint4* sq = st + q * 16 * kTokStride;
+                f4_t D = zf;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const h8_t a = __builtin_bit_cast(h8_t, sq[8 * g + c]);
+                    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, q4k_bop(Dw[c], S, magic), D, 0, 0, 0);
+                }
+                const h8_t am = __builtin_bit_cast(h8_t, sq[32 + g]);
+                const f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, S.m, zf, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int tl = q * 16 + 4 * g + i;
-                    xg[((wave * NGRP + q) * 4 + i) * 64 + lane] =
-                        tl < Me ? ldexpf(acc[q][i], unscale(off + tl)) : 0.0f;
+                    acc[q][i] = fmaf(S.d, D[i], acc[q][i]);
+                    acc[q][i] = fmaf(-S.dmin, Dm[i], acc[q][i]);
                 }
+            }
+        };
+        // U super-blocks per iteration (the launcher guarantees nsb % U == 0):
+        // ring slot j % R, stage boundaries at j % MS, all known at compile
+        // time.  The last PF prefetches are the next item's first chunks.
+        // Every iteration ends on a barrier.
+        for (int sb0 = 0; sb0 < nsb; sb0 += U) {
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int sb = sb0 + j;
+                if (j % MS == 0) {
+                    if (sb / MS + 1 < nms) {
+                        stage_load(sb / MS + 1);
+                    } else {
+                        build_map(ar_next);
+                        stage_load(0);
+                    }
+                }
+                const int pf = sb + PF;
+                w[(j + PF) % R] = load_wraw(pf < nsb ? wbase + (size_t)pf * 2304 : nbase + (size_t)(pf - nsb) * 2304,
+                                            lane);
+                // keep the prefetches where they are issued (the scheduler
+                // would otherwise sink them next to their use to save registers)
+                __builtin_amdgcn_sched_barrier(0);
+                compute(sb, w[j % R]);
+                if (j % MS == MS - 1) {
+                    if (sb / MS + 1 < nms) stage_store(sb / MS + 1);
+                    __syncthreads();
+                }
+            }
         }
-        __syncthreads();
-        if (wave < HALF) return;
-        const int inter = N / 2;
-        const int n = (tile * HALF + wave - HALF) * 16 + r;
-        const float lim = ep.swiglu_limit;
+        wbase = nbase;
+
+        // D layout: lane holds token rows 4g+i (i=0..3) of the group, column r.
+        auto unscale = [&](int pidx) -> int { return xs[a_row ? a_row[pidx] : pidx]; };
+        if constexpr (MODE == 1) {
+            // gate waves hand their rows to the up waves through LDS (the
+            // staging ring is free: the loop ended on a barrier)
+            float* xg = reinterpret_cast<float*>(lds);
+            if (wave < HALF) {
+#pragma unroll
+                for (int q = 0; q < NGRP; ++q)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tl = q * 16 + 4 * g + i;
+                        xg[((wave * NGRP + q) * 4 + i) * 64 + lane] =
+                            tl < Me ? ldexpf(acc[q][i], unscale(off + tl)) : 0.0f;
+                    }
+            }
+            __syncthreads();
+            if (wave >= HALF) {
+                const int inter = N / 2;
+                const int n = (tile * HALF + wave - HALF) * 16 + r;
+                const float lim = ep.swiglu_limit;
+#pragma unroll
+                for (int q = 0; q < NGRP; ++q) {
+                    if (q * 16 >= Me) break;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int tl = q * 16 + 4 * g + i;
+                        if (tl >= Me) continue;
+                        float gv = xg[(((wave - HALF) * NGRP + q) * 4 + i) * 64 + lane];
+                        float uv = ldexpf(acc[q][i], unscale(off + tl));
+                        if (lim > 0.0f) {
+                            gv = fminf(gv, lim);
+                            uv = fminf(fmaxf(uv, -lim), lim);
+                        }
+                        ep.h[(size_t)(off + tl) * inter + n] = (gv / (1.0f + expf(-gv))) * uv;
+                    }
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int q = 0; q < NGRP; ++q) {
-            if (q * 16 >= Me) break;
+            if (q * 16 >= Me) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tl = q * 16 + 4 * g + i;
                 if (tl >= Me) continue;
-                float gv = xg[(((wave - HALF) * NGRP + q) * 4 + i) * 64 + lane];
-                float uv = ldexpf(acc[q][i], unscale(off + tl));
-                if (lim > 0.0f) {
-                    gv = fminf(gv, lim);
-                    uv = fminf(fmaxf(uv, -lim), lim);
-                }
-                ep.h[(size_t)(off + tl) * inter + n] = (gv / (1.0f + expf(-gv))) * uv;
+                const int pidx = off + tl;
+                const float v = ldexpf(acc[q][i], unscale(pidx));
+                if constexpr (MODE == 0)
+                    out[(size_t)pidx * N + row] = v;
+                else
+                    st_coherent(&out[(size_t)pidx * N + row], v);
             }
         }
-        return;
-    }
-#pragma unroll
-    for (int q = 0; q < NGRP; ++q) {
-        if (q * 16 >= Me) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tl = q * 16 + 4 * g + i;
-            if (tl >= Me) continue;
-            const int pidx = off + tl;
-            const float v = ldexpf(acc[q][i], unscale(pidx));
-            if constexpr (MODE == 0)
-                out[(size_t)pidx * N + row] = v;
-            else
-                st_coherent(&out[(size_t)pidx * N + row], v);
-        }
-    }
-    if constexpr (MODE == 0) return;
+        if constexpr (MODE == 0) continue;
 
-    // ---- mode 2: one contribution per (pair, tile); the last one for a token
-    // combines its tile (counters are re-armed by their consumer) ----
-    __shared__ int s_flag[64];
-    __shared__ int s_nflag;
-    publish_wait();
-    __syncthreads();
-    if (tid == 0) s_nflag = 0;
-    __syncthreads();
-    const int nt128 = N / 128;
-    const int T128 = (tile * WAVES * 16) / 128;
-    for (int tl = tid; tl < slot_M[slot]; tl += NT) {
-        const int t = ep.pair_tok[off + tl];
-        const int old = signal_add(&ep.tile_done[t * nt128 + T128], 1);
-        if (old == ep.tok_npairs[t] - 1) {
-            ep.tile_done[t * nt128 + T128] = 0;
-            s_flag[atomicAdd(&s_nflag, 1)] = t;
+        // ---- mode 2: one contribution per (pair, tile); the last one for a
+        // token combines its tile (counters are re-armed by their consumer) ----
+        publish_wait();
+        __syncthreads();
+        if (tid == 0) s_nflag = 0;
+        __syncthreads();
+        const int nt128 = N / 128;
+        const int T128 = (tile * WAVES * 16) / 128;
+        for (int tl = tid; tl < slot_M[slot]; tl += NT) {
+            const int tok = ep.pair_tok[off + tl];
+            const int old = signal_add(&ep.tile_done[tok * nt128 + T128], 1);
+            if (old == ep.tok_npairs[tok] - 1) {
+                ep.tile_done[tok * nt128 + T128] = 0;
+                s_flag[atomicAdd(&s_nflag, 1)] = tok;
+            }
         }
-    }
-    __syncthreads();
-    const int nflag = s_nflag;
-    if (nflag == 0) return;
-    for (int f = 0; f < nflag; ++f) {
-        const int t = s_flag[f];
-        for (int i = tid; i < 128; i += NT) {
-            const int n = T128 * 128 + i;
-            float a = 0.0f;
-            for (int j = 0; j < ep.tk; ++j) {
-                const int p = ep.pair_of[t * ep.tk + j];
-                if (p < 0) continue;
-                a = a + ep.wts[t * ep.tk + j] * ld_coherent(out + (size_t)p * N + n);
+        __syncthreads();
+        const int nflag = s_nflag;
+        for (int f = 0; f < nflag; ++f) {
+            const int tok = s_flag[f];
+            for (int i = tid; i < 128; i += NT) {
+                const int n = T128 * 128 + i;
+                float a = 0.0f;
+                for (int j = 0; j < ep.tk; ++j) {
+                    const int p = ep.pair_of[tok * ep.tk + j];
+                    if (p < 0) continue;
+                    a = a + ep.wts[tok * ep.tk + j] * ld_coherent(out + (size_t)p * N + n);
+                }
+                if (ep.out_routed) ep.out_routed[(size_t)tok * N + n] = fst_f32_to_bf16(a);
+                if (ep.use_shared) {
+                    const float sv2 = ld_coherent(out + (size_t)ep.pair_shared[tok] * N + n);
+                    if (ep.out_shared) ep.out_shared[(size_t)tok * N + n] = fst_f32_to_bf16(sv2);
+                    a = a + sv2;
+                }
+                if (ep.out) ep.out[(size_t)tok * N + n] = fst_f32_to_bf16(a);
             }
-            if (ep.out_routed) ep.out_routed[(size_t)t * N + n] = fst_f32_to_bf16(a);
-            if (ep.use_shared) {
-                const float sv = ld_coherent(out + (size_t)ep.pair_shared[t] * N + n);
-                if (ep.out_shared) ep.out_shared[(size_t)t * N + n] = fst_f32_to_bf16(sv);
-                a = a + sv;
-            }
-            if (ep.out) ep.out[(size_t)t * N + n] = fst_f32_to_bf16(a);
         }
     }
 }
 
 // Token capacity of the launch (the call's M bounds every slot's M_e): 8, 16,
 // 32 or 64 tokens; smaller capacities stage more super-blocks per barrier.
+#ifndef FST_Q4K_WG_PER_CU
+#define FST_Q4K_WG_PER_CU 2
+#endif
 template <int MODE>
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
                               const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep) {
     constexpr int W = 8;
-    const dim3 grid(slots * (unsigned)(N / (16 * W)));
+    // persistent grid: FST_Q4K_WG_PER_CU workgroups per CU at most
+    const unsigned items = slots * (unsigned)(N / (16 * W));
+    // (token capacities above 8 run at 3 waves per SIMD: one 8-wave workgroup per CU)
+    const unsigned wg_per_cu = M <= 8 ? FST_Q4K_WG_PER_CU : 1;
+    const dim3 grid(std::min(items, (unsigned)s.n_cu * wg_per_cu));
 #define FST_Q4K_LAUNCH(T, MSV)                                                                               \
     hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE>), grid, dim3(64 * W), 0, st, bank, stride, mat_off, \
                        K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep)
     // K is a multiple of 512 (checked at context creation): nsb is even
-    if (M <= 8 && (K >> 8) % 4 == 0)
-        FST_Q4K_LAUNCH(8, 4);
+#ifndef FST_MS8
+#define FST_MS8 2
+#endif
+    if (M <= 8 && (K >> 8) % FST_MS8 == 0)
+        FST_Q4K_LAUNCH(8, FST_MS8);
     else if (M <= 8)
         FST_Q4K_LAUNCH(8, 2);
     else if (M <= 16)
