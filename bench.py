@@ -39,8 +39,8 @@ def log(*a):
 def setup(fa):
     ctx = fa.Context(n_experts=E, top_k=TK, max_tokens=64)
     t0 = time.time()
-    for e in range(E + 1):
-        ctx.upload_expert(0, e, fa.synth_q4k_expert(SEED, e))
+    # generated in HBM; byte-identical to fa.synth_q4k_expert(SEED, e), which the CPU baseline uses
+    ctx.synth_experts(SEED, 0, 0, E + 1, 0)
     w = fa.synth_normal_bf16(SEED, 1000, (HD, E), 0.0, 0.02)
     ctx.upload_router_bf16(0, w)
     log("uploaded %d experts (%.2f GB) in %.1fs" % (E + 1, (E + 1) * EXPERT_BYTES / 1e9, time.time() - t0))

@@ -81,6 +81,16 @@ _SIGS = {
     "fst_last_timings": (C.c_int, [P, P]),
     "fst_last_active_experts": (C.c_int, [P, P]),
     "fst_device_copy": (C.c_int, [P, P, P, SZ]),
+    "fst_upload_norm": (C.c_int, [P, C.c_int, P]),
+    "fst_lm_head_bytes": (SZ, [P]),
+    "fst_upload_lm_head": (C.c_int, [P, P, SZ]),
+    "fst_rmsnorm_dev": (C.c_int, [P, C.c_int, P, P, C.c_int, P, P]),
+    "fst_lm_head_dev": (C.c_int, [P, P, C.c_int, P]),
+    "fst_verify_forward_dev": (C.c_int, [P, P, C.c_int, P, P]),
+    "fst_verify_forward": (C.c_int, [P, P, C.c_int, P, P]),
+    "fst_synth_experts_dev": (C.c_int, [P, U64, C.c_int, C.c_int, C.c_int, U64, C.c_float]),
+    "fst_synth_lm_head_dev": (C.c_int, [P, U64, U64, C.c_float]),
+    "fst_synth_q4k_blocks": (C.c_int, [U64, U64, SZ, C.c_float, P]),
     "fst_synth_q4k_expert": (C.c_int, [U64, U64, C.c_int, C.c_int, C.c_float, P]),
     "fst_synth_mxfp4_expert": (C.c_int, [U64, U64, C.c_int, C.c_int, C.c_int, C.c_int, P]),
     "fst_synth_normal_bf16": (C.c_int, [U64, U64, SZ, C.c_float, C.c_float, P]),
@@ -144,6 +154,16 @@ def synth_q4k_expert(seed, expert_id, hd=4096, inter=2048, d_sigma=0.01):
     out = np.empty(3 * hd * inter // 256 * 144, dtype=np.uint8)
     _check(lib().fst_synth_q4k_expert(seed, expert_id, hd, inter, d_sigma, _ptr(out)))
     return out
+
+
+def synth_q4k_blocks(seed, matrix_id, nblocks, d_sigma=0.01):
+    out = np.empty(nblocks * 144, dtype=np.uint8)
+    _check(lib().fst_synth_q4k_blocks(seed, matrix_id, nblocks, d_sigma, _ptr(out)))
+    return out
+
+
+def lm_head_bytes(cfg):
+    return lib().fst_lm_head_bytes(C.byref(cfg))
 
 
 def synth_mxfp4_expert(seed, expert_id, hd=4096, inter=2048, e_lo=108, e_hi=128):
@@ -284,6 +304,30 @@ class Context:
         _check(lib().fst_accept_stochastic(self.h, _ptr(target), _ptr(dl), n_seq, k, V, _ptr(draft),
                                            temperature, seed, seq_base, _ptr(n_acc), _ptr(tok)))
         return n_acc, tok
+
+    # verify forward (norms, residual stream, LM head)
+    def upload_norm(self, lid, w_bf16):
+        w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+        _check(lib().fst_upload_norm(self.h, lid, _ptr(w)))
+
+    def upload_lm_head(self, packed):
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        _check(lib().fst_upload_lm_head(self.h, _ptr(packed), packed.nbytes))
+
+    def synth_experts(self, seed, lid, e_first, e_count, id_base, d_sigma=0.01):
+        _check(lib().fst_synth_experts_dev(self.h, seed, lid, e_first, e_count, id_base, d_sigma))
+
+    def synth_lm_head(self, seed, matrix_id, d_sigma=0.01):
+        _check(lib().fst_synth_lm_head_dev(self.h, seed, matrix_id, d_sigma))
+
+    def verify_forward(self, h, input_ids=None):
+        """h: [M][hidden] bf16 (updated copy returned); returns (logits [M][vocab], h_out)."""
+        h = np.array(h, dtype=np.uint16, copy=True, order="C")
+        M = h.shape[0]
+        logits = np.empty((M, self.cfg.vocab_size), np.float32)
+        ids = None if input_ids is None else np.ascontiguousarray(input_ids, dtype=np.int32)
+        _check(lib().fst_verify_forward(self.h, _ptr(h), M, _ptr(ids), _ptr(logits)))
+        return logits, h
 
     def dequant(self, codec, blocks):
         blocks = np.ascontiguousarray(blocks, dtype=np.uint8)

@@ -50,6 +50,12 @@ struct fst_ctx {
     float* bias = nullptr;                   // [L][E]
     std::vector<char> has_router, has_bias;
     std::vector<int32_t*> hash;              // [L] (lid < n_hash_layers)
+    uint16_t* norms = nullptr;               // [L+1][hd] bf16 (moe norms, then the final norm)
+    std::vector<char> has_norm;              // [L+1]
+    uint8_t* lm_head = nullptr;              // [vocab][hd/256] Q4_K, device layout
+    int* lm_tab = nullptr;                   // one-slot table for the dense LM-head call
+    uint16_t* mn = nullptr;                  // [T][hd] normed layer input
+    bool nested = false;                     // inside verify_forward: no per-kernel marks
     fst::Scratch s{};
     std::vector<void*> allocs;
     std::vector<uint8_t> staging;            // host repack buffer for expert uploads
@@ -73,6 +79,7 @@ struct fst_ctx {
         for (void* p : allocs) hipFree(p);
         for (int32_t* p : hash)
             if (p) hipFree(p);
+        if (lm_head) hipFree(lm_head);
         if (acc_ws) hipFree(acc_ws);
         if (acc_logits) hipFree(acc_logits);
         if (acc_io) hipFree(acc_io);
@@ -104,13 +111,14 @@ struct fst_ctx {
 
     // profiling marks: mark(name) after a launch closes the interval opened by the previous mark
     void mark_begin() {
+        if (nested) return;
         n_ev = 0;
         if (!profiling) return;
         hipEventRecord(ev[0], st);
         n_ev = 1;
     }
-    void mark(const char* name) {
-        if (!profiling || n_ev >= (int)ev.size()) return;
+    void mark(const char* name, bool outer = false) {
+        if ((nested && !outer) || !profiling || n_ev >= (int)ev.size()) return;
         hipEventRecord(ev[n_ev], st);
         ev_names[n_ev] = name;
         ++n_ev;
@@ -222,6 +230,10 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     x->has_router.assign(L, 0);
     x->has_bias.assign(L, 0);
     x->hash.assign(L, nullptr);
+    if ((rc = x->dalloc(&x->norms, (size_t)(L + 1) * hd))) return bail(rc);
+    x->has_norm.assign(L + 1, 0);
+    if ((rc = x->dalloc(&x->lm_tab, fst::META_WORDS + 4))) return bail(rc);
+    if ((rc = x->dalloc(&x->mn, (size_t)c.max_tokens * hd))) return bail(rc);
 
     fst::Scratch& s = x->s;
     const int T = c.max_tokens, tk = c.top_k;
@@ -699,6 +711,183 @@ int fst_dequant(fst_ctx* ctx, int codec, const void* blocks, size_t nblocks, flo
         rc = fail(FST_EHIP, "dequant download failed");
     if (hipStreamSynchronize(ctx->st) != hipSuccess && !rc) rc = fail(FST_EHIP, "dequant sync failed");
     cleanup();
+    return rc;
+}
+
+
+// ------------------------------------------------ verify forward (C5 path)
+
+static constexpr float kNormEps = 1e-6f;  // rms_cpu default and the NPU rmsnorm (src/fst_engine.cpp:89)
+
+int fst_upload_norm(fst_ctx* ctx, int lid, const uint16_t* w) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (lid < 0 || lid > ctx->cfg.n_layers) return fail(FST_EINVAL, "norm id must be in [0, n_layers]");
+    if (!w) return fail(FST_EINVAL, "null norm weights");
+    const int hd = ctx->cfg.hidden_dim;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->norms + (size_t)lid * hd, w, (size_t)hd * 2, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    ctx->has_norm[lid] = 1;
+    return FST_OK;
+}
+
+size_t fst_lm_head_bytes(const fst_config* c) {
+    if (!c || c->hidden_dim <= 0 || c->vocab_size <= 0) return 0;
+    return (size_t)c->vocab_size * (c->hidden_dim / 256) * 144;
+}
+
+static int lm_head_alloc(fst_ctx* ctx) {
+    const fst_config& c = ctx->cfg;
+    if (c.vocab_size % 128) return fail(FST_EINVAL, "vocab_size must be a multiple of 128 for the LM head");
+    if (!ctx->lm_head) {
+        void* p = nullptr;
+        if (hipMalloc(&p, fst_lm_head_bytes(&c)) != hipSuccess) return fail(FST_ENOMEM, "hipMalloc(lm_head) failed");
+        ctx->lm_head = static_cast<uint8_t*>(p);
+    }
+    return FST_OK;
+}
+
+int fst_upload_lm_head(fst_ctx* ctx, const void* packed, size_t bytes) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    const size_t need = fst_lm_head_bytes(&ctx->cfg);
+    if (!packed || bytes != need)
+        return fail(FST_EINVAL, "LM head size mismatch: got " + std::to_string(bytes) + ", expected " +
+                                    std::to_string(need));
+    if (int rc = lm_head_alloc(ctx)) return rc;
+    std::vector<uint8_t> tiled(bytes);
+    fst::repack_q4k_matrix(static_cast<const uint8_t*>(packed), tiled.data(), ctx->cfg.vocab_size,
+                           ctx->cfg.hidden_dim);
+    FST_HIP_TRY(hipMemcpyAsync(ctx->lm_head, tiled.data(), bytes, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
+}
+
+int fst_synth_experts_dev(fst_ctx* ctx, uint64_t seed, int lid, int e_first, int e_count, uint64_t id_base,
+                          float d_sigma) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    const fst_config& c = ctx->cfg;
+    if (e_first < 0 || e_count < 0 || e_first + e_count > c.n_experts + 1)
+        return fail(FST_EINVAL, "expert range out of [0, n_experts]");
+    if (e_first + e_count == c.n_experts + 1 && !c.has_shared) return fail(FST_EINVAL, "config has no shared expert");
+    const int hd = c.hidden_dim, inter = c.inter_dim;
+    const uint64_t gate_blocks = (uint64_t)inter * (hd / 256);
+    const size_t proj = gate_blocks * 144;
+    for (int e = e_first; e < e_first + e_count; ++e) {
+        uint8_t* dst = ctx->bank + ((size_t)lid * (c.n_experts + 1) + e) * ctx->expert_stride;
+        const uint64_t id = id_base + (uint64_t)e;
+        fst::launch_synth_q4k_tiled(ctx->st, seed, id, 0, inter, hd, d_sigma, dst);
+        fst::launch_synth_q4k_tiled(ctx->st, seed, id, gate_blocks, inter, hd, d_sigma, dst + proj);
+        fst::launch_synth_q4k_tiled(ctx->st, seed, id, 2 * gate_blocks, hd, inter, d_sigma, dst + 2 * proj);
+    }
+    FST_HIP_TRY(hipGetLastError());
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    for (int e = e_first; e < e_first + e_count; ++e)
+        if (!ctx->uploaded[lid][e]) {
+            ctx->uploaded[lid][e] = 1;
+            ctx->n_uploaded[lid]++;
+        }
+    return FST_OK;
+}
+
+int fst_synth_lm_head_dev(fst_ctx* ctx, uint64_t seed, uint64_t id, float d_sigma) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (int rc = lm_head_alloc(ctx)) return rc;
+    fst::launch_synth_q4k_tiled(ctx->st, seed, id, 0, ctx->cfg.vocab_size, ctx->cfg.hidden_dim, d_sigma,
+                                ctx->lm_head);
+    FST_HIP_TRY(hipGetLastError());
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
+}
+
+int fst_rmsnorm_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, const uint16_t* d_y, int M, uint16_t* d_h_out,
+                    uint16_t* d_normed) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (lid < 0 || lid > ctx->cfg.n_layers) return fail(FST_EINVAL, "norm id must be in [0, n_layers]");
+    if (!ctx->has_norm[lid]) return fail(FST_ENOTREADY, "norm weights not uploaded");
+    if (!d_h || !d_normed) return fail(FST_EINVAL, "null device buffer");
+    if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    const int hd = ctx->cfg.hidden_dim;
+    fst::launch_resid_norm(ctx->st, d_h, d_y, ctx->norms + (size_t)lid * hd, M, hd, kNormEps, d_h_out, d_normed,
+                           nullptr, nullptr);
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+// final norm (optionally after adding d_y to the residual d_h) + LM head
+static int final_head(fst_ctx* ctx, uint16_t* d_h, const uint16_t* d_y, int M, float* d_logits) {
+    const fst_config& c = ctx->cfg;
+    if (!ctx->lm_head) return fail(FST_ENOTREADY, "LM head not uploaded");
+    if (!ctx->has_norm[c.n_layers]) return fail(FST_ENOTREADY, "final norm weights not uploaded");
+    const int hd = c.hidden_dim;
+    fst::launch_resid_norm(ctx->st, d_h, d_y, ctx->norms + (size_t)c.n_layers * hd, M, hd, kNormEps,
+                           d_y ? d_h : nullptr, nullptr, &ctx->s, ctx->lm_tab);
+    fst::launch_q4k_dense(ctx->st, ctx->lm_head, M, hd, c.vocab_size, ctx->s, ctx->lm_tab, d_logits);
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_lm_head_dev(fst_ctx* ctx, const uint16_t* d_h, int M, float* d_logits) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!d_h || !d_logits) return fail(FST_EINVAL, "null device buffer");
+    if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    ctx->mark_begin();
+    if (int rc = final_head(ctx, const_cast<uint16_t*>(d_h), nullptr, M, d_logits)) return rc;
+    ctx->mark("lm_head");
+    return FST_OK;
+}
+
+int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_input_ids, float* d_logits) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!d_h || !d_logits) return fail(FST_EINVAL, "null device buffer");
+    const fst_config& c = ctx->cfg;
+    if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    for (int l = 0; l < c.n_layers; ++l)
+        if (!ctx->has_norm[l]) return fail(FST_ENOTREADY, "norm weights of layer " + std::to_string(l) + " not uploaded");
+    const int hd = c.hidden_dim;
+    ctx->mark_begin();
+    ctx->nested = true;
+    int rc = FST_OK;
+    for (int l = 0; l < c.n_layers && rc == FST_OK; ++l) {
+        // h += y (previous layer), mn = RMSNorm_l(h); y = MoE_l(mn)
+        fst::launch_resid_norm(ctx->st, d_h, l > 0 ? ctx->s.out : nullptr, ctx->norms + (size_t)l * hd, M, hd,
+                               kNormEps, l > 0 ? d_h : nullptr, ctx->mn, nullptr, nullptr);
+        rc = run_moe(ctx, l, ctx->mn, M, d_input_ids, 1, ctx->s.eids, ctx->s.wts, c.top_k, 1, c.has_shared,
+                     ctx->s.out, nullptr, nullptr);
+    }
+    ctx->nested = false;
+    if (rc) return rc;
+    ctx->mark("layers", true);
+    if ((rc = final_head(ctx, d_h, ctx->s.out, M, d_logits))) return rc;
+    ctx->mark("lm_head", true);
+    return FST_OK;
+}
+
+int fst_verify_forward(fst_ctx* ctx, uint16_t* h, int M, const int32_t* input_ids, float* logits) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!h || !logits) return fail(FST_EINVAL, "null host buffer");
+    const fst_config& c = ctx->cfg;
+    if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    const int hd = c.hidden_dim;
+    const size_t nlog = (size_t)M * c.vocab_size;
+    float* d_logits = nullptr;
+    FST_HIP_TRY(hipMalloc(&d_logits, nlog * sizeof(float)));
+    int rc = FST_OK;
+    do {
+        if (hipMemcpyAsync(ctx->s.h, h, (size_t)M * hd * 2, hipMemcpyHostToDevice, ctx->st) != hipSuccess ||
+            (input_ids &&
+             hipMemcpyAsync(ctx->s.ids, input_ids, M * 4, hipMemcpyHostToDevice, ctx->st) != hipSuccess)) {
+            rc = fail(FST_EHIP, "host-to-device copy failed");
+            break;
+        }
+        if ((rc = fst_verify_forward_dev(ctx, ctx->s.h, M, input_ids ? ctx->s.ids : nullptr, d_logits))) break;
+        if (hipMemcpyAsync(logits, d_logits, nlog * sizeof(float), hipMemcpyDeviceToHost, ctx->st) != hipSuccess ||
+            hipMemcpyAsync(h, ctx->s.h, (size_t)M * hd * 2, hipMemcpyDeviceToHost, ctx->st) != hipSuccess) {
+            rc = fail(FST_EHIP, "device-to-host copy failed");
+            break;
+        }
+        rc = check_meta_error(ctx);
+    } while (0);
+    hipStreamSynchronize(ctx->st);
+    hipFree(d_logits);
     return rc;
 }
 

@@ -121,6 +121,14 @@ void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float
 // Router logits and the activation prep of the same rows in one launch.
 void launch_router_prep(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
                         float* logits, const Scratch& s);
+// Residual add + RMSNorm per token row (see resid_norm_kernel); optional
+// outputs: h_out (x), normed (bf16), the fp16 operand in prep->x16p/sxp/xs,
+// and a one-slot table for launch_q4k_dense in slot_tab (META_WORDS + 3 ints).
+void launch_resid_norm(hipStream_t st, const uint16_t* h, const uint16_t* y, const uint16_t* w, int M, int d,
+                       float eps, uint16_t* h_out, uint16_t* normed, const Scratch* prep, int* slot_tab);
+// logits[M][N] = x . W^T for one resident Q4_K matrix W (device layout).
+void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, const Scratch& s, int* slot_tab,
+                      float* out);
 // h rows -> the down projection's operand (one workgroup per pair).
 void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
                      uint4* sxp, int* xs);
@@ -134,6 +142,11 @@ void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int 
 // Host-side reorder of one packed Q4_K expert (gate|up|down, each [N][K/256]
 // blocks of 144 B) into the device layout the linear kernel streams.
 void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);
+void repack_q4k_matrix(const uint8_t* src, uint8_t* dst, int N, int K);
+// Synthetic Q4_K matrix [N][K/256] (blocks b0.. of generator stream `id`)
+// written in the device layout at dst.
+void launch_synth_q4k_tiled(hipStream_t st, uint64_t seed, uint64_t id, uint64_t b0, int N, int K, float sigma,
+                            uint8_t* dst);
 void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
                     const float* wts, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 void launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);

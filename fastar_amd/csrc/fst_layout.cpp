@@ -40,6 +40,19 @@ static void repack_matrix(const uint8_t* src, uint8_t* dst, int N, int K) {
         }
 }
 
+// Large matrices (the LM head) are split over row tiles between threads.
+void repack_q4k_matrix(const uint8_t* src, uint8_t* dst, int N, int K) {
+    const int tiles = N / 16, nt = 8;
+    const size_t tile_src = (size_t)16 * (K / 256) * 144;
+    std::vector<std::thread> th;
+    for (int i = 0; i < nt; ++i) {
+        const int t0 = tiles * i / nt, t1 = tiles * (i + 1) / nt;
+        if (t0 >= t1) continue;
+        th.emplace_back([=] { repack_matrix(src + t0 * tile_src, dst + t0 * tile_src, (t1 - t0) * 16, K); });
+    }
+    for (auto& t : th) t.join();
+}
+
 void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter) {
     const size_t proj = (size_t)inter * (hd / 256) * 144;
     std::thread a([&] { repack_matrix(src, dst, inter, hd); });

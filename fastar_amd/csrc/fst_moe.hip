@@ -571,6 +571,85 @@ void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float
     hipLaunchKernelGGL(prep_kernel<SrcBf16>, dim3(rows), dim3(256), 0, st, SrcBf16{x}, nullptr, rows, K,
                        x16p, sxp, xs);
 }
+// ---------------------------------------------------- residual + RMSNorm
+
+// Element source reading a row already held in LDS.
+struct SrcRow {
+    const float* p;
+    __device__ __forceinline__ float at(size_t, int, int i) const { return p[i]; }
+};
+
+// One workgroup per token row (process_layer's non-HC residual and norm,
+// src/fst_engine.cpp:2913-2917 and :2738-2741; rms_cpu :89-90):
+//   x   = y ? bf16(h + y) : h          (the previous sublayer's residual add)
+//   ss  = sum_j x_j^2 in double, canonical order: lane p of 64 sums the
+//         contiguous chunk p sequentially, then p[j] += p[j+off], off = 32..1
+//   r   = (float)(1 / sqrt(ss/d + eps))
+//   out = bf16((x * r) * w)            (fp32 products, no contraction, RNE)
+// x is written back to h_out (when given); out goes to normed (when given)
+// and, when x16p is given, straight into the linear kernel's fp16 operand
+// (prep_row).  Block 0 also writes a one-slot table for a dense linear call
+// over the M rows (when slot_tab is given: meta, slot_eid, slot_M, slot_off).
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restrict__ h,
+                                                         const uint16_t* __restrict__ y,
+                                                         const uint16_t* __restrict__ w, int M, int d,
+                                                         float eps, uint16_t* __restrict__ h_out,
+                                                         uint16_t* __restrict__ normed, _Float16* __restrict__ x16p,
+                                                         uint4* __restrict__ sxp, int* __restrict__ xs,
+                                                         int* __restrict__ slot_tab) {
+    __shared__ float xrow[kMaxPrepK];
+    __shared__ float nrow[kMaxPrepK];
+    __shared__ double part[64];
+    __shared__ float s_r;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (slot_tab && t == 0 && tid == 0) {
+        slot_tab[META_N_SLOTS] = 1;
+        slot_tab[META_WORDS + 0] = 0;  // slot_eid
+        slot_tab[META_WORDS + 1] = M;  // slot_M
+        slot_tab[META_WORDS + 2] = 0;  // slot_off
+    }
+    for (int j = tid; j < d; j += 256) {
+        float x = fst_bf16_to_f32(h[(size_t)t * d + j]);
+        if (y) x = fst_bf16_to_f32(fst_f32_to_bf16(x + fst_bf16_to_f32(y[(size_t)t * d + j])));
+        xrow[j] = x;
+        if (h_out) h_out[(size_t)t * d + j] = fst_f32_to_bf16(x);
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int C = d / 64;
+        double a = 0.0;
+        for (int i = 0; i < C; ++i) {
+            const double v = (double)xrow[tid * C + i];
+            a = a + v * v;
+        }
+        part[tid] = a;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int off = 32; off >= 1; off >>= 1)
+            for (int j = 0; j < off; ++j) part[j] = part[j] + part[j + off];
+        s_r = (float)(1.0 / sqrt(part[0] / (double)d + (double)eps));
+    }
+    __syncthreads();
+    const float r = s_r;
+    for (int j = tid; j < d; j += 256) {
+        const uint16_t o = fst_f32_to_bf16((xrow[j] * r) * fst_bf16_to_f32(w[j]));
+        nrow[j] = fst_bf16_to_f32(o);
+        if (normed) normed[(size_t)t * d + j] = o;
+    }
+    __syncthreads();
+    if (x16p) prep_row<256>(SrcRow{nrow}, t, d, xrow, x16p, sxp, xs);
+}
+#pragma clang fp contract(on)
+
+void launch_resid_norm(hipStream_t st, const uint16_t* h, const uint16_t* y, const uint16_t* w, int M, int d,
+                       float eps, uint16_t* h_out, uint16_t* normed, const Scratch* prep, int* slot_tab) {
+    hipLaunchKernelGGL(resid_norm_kernel, dim3(M), dim3(256), 0, st, h, y, w, M, d, eps, h_out, normed,
+                       prep ? prep->x16p : nullptr, prep ? prep->sxp : nullptr, prep ? prep->xs : nullptr,
+                       slot_tab);
+}
+
 void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
                      uint4* sxp, int* xs) {
     hipLaunchKernelGGL(prep_kernel<SrcF32>, dim3(max_rows), dim3(256), 0, st, SrcF32{h}, meta + META_N_PAIRS,
@@ -1065,6 +1144,18 @@ void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int 
     ep.out_shared = out_shared;
     launch_q4k_linear<2>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
                          nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
+}
+
+// Dense Q4_K linear over M rows (the LM head): logits[m][n] = sum_k W[n][k] x[m][k],
+// operand prepared by launch_resid_norm with `prep` and `slot_tab`.
+void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, const Scratch& s, int* slot_tab,
+                      float* out) {
+    Scratch t = s;
+    t.meta = slot_tab;
+    t.slot_eid = slot_tab + META_WORDS;
+    t.slot_M = slot_tab + META_WORDS + 1;
+    t.slot_off = slot_tab + META_WORDS + 2;
+    launch_q4k_linear<0>(st, M, 1u, W, 0, 0, K, N, t, nullptr, s.x16p, s.sxp, s.xs, out, EpiArgs{});
 }
 
 // ------------------------------------------------------------------ combine

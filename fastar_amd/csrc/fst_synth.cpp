@@ -11,6 +11,7 @@
 
 #include "../../include/fst_exact_math.h"
 #include "../../include/fst_hip.h"
+#include "fst_synth_gen.h"
 
 namespace {
 
@@ -21,37 +22,6 @@ inline fst_philox_ctr philox(uint64_t seed, uint64_t a, uint64_t b) {
     c.v[2] = (uint32_t)b;
     c.v[3] = (uint32_t)(b >> 32);
     return fst_philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
-}
-
-// binary32 -> binary16 bits, round to nearest even (subnormals and overflow handled).
-uint16_t f32_to_f16(float f) {
-    uint32_t x = fst_f32_bits(f);
-    uint32_t sign = (x >> 16) & 0x8000u;
-    uint32_t ax = x & 0x7fffffffu;
-    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
-    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);  // rounds to >= 65520 -> inf
-    if (ax < 0x33000000u) return (uint16_t)sign;               // < 2^-25 -> 0
-    int e = (int)(ax >> 23) - 127;
-    uint32_t m = (ax & 0x7fffffu) | 0x800000u;
-    if (e < -14) {
-        // subnormal: value = m * 2^(e-23); target unit 2^-24
-        int shift = -14 - e + 13;  // bits to drop from the 24-bit significand to units of 2^-24
-        uint32_t q = m >> shift;
-        uint32_t rem = m & ((1u << shift) - 1u);
-        uint32_t half = 1u << (shift - 1);
-        if (rem > half || (rem == half && (q & 1u))) ++q;
-        return (uint16_t)(sign | q);
-    }
-    uint32_t q = m >> 13;
-    uint32_t rem = m & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;
-    uint32_t he = (uint32_t)(e + 15);
-    if (q == 0x800u) {
-        q = 0x400u;
-        ++he;
-    }
-    if (he >= 31) return (uint16_t)(sign | 0x7c00u);
-    return (uint16_t)(sign | (he << 10) | (q & 0x3ffu));
 }
 
 void normal_pair(fst_philox_ctr r, double* z0, double* z1) {
@@ -81,7 +51,6 @@ void parallel_for(size_t n, F f) {
     for (auto& t : th) t.join();
 }
 
-constexpr uint64_t kTagQ4k = 0x51344bull << 40;
 constexpr uint64_t kTagMx = 0x4d5846ull << 40;
 
 }  // namespace
@@ -90,27 +59,13 @@ extern "C" {
 
 int fst_synth_q4k_expert(uint64_t seed, uint64_t expert_id, int hd, int inter, float d_sigma, uint8_t* out) {
     if (!out || hd <= 0 || inter <= 0 || hd % 256 || inter % 256) return FST_EINVAL;
-    const size_t nblk = 3 * (size_t)hd * inter / 256;
-    parallel_for(nblk, [&](size_t b0, size_t b1) {
-        for (size_t b = b0; b < b1; ++b) {
-            uint8_t* blk = out + b * 144;
-            const uint64_t lane = kTagQ4k ^ (expert_id << 8);
-            // 140 random bytes: scales[12] then qs[128]
-            uint8_t rnd[144];
-            for (int j = 0; j < 9; ++j) {
-                fst_philox_ctr r = philox(seed, b, lane | (uint64_t)j);
-                std::memcpy(rnd + 16 * j, r.v, 16);
-            }
-            double z0, z1;
-            normal_pair(philox(seed, b, lane | 9u), &z0, &z1);
-            const uint16_t d = f32_to_f16((float)std::fabs(z0 * d_sigma));
-            const uint16_t dmin = f32_to_f16((float)std::fabs(z1 * d_sigma));
-            blk[0] = (uint8_t)d;
-            blk[1] = (uint8_t)(d >> 8);
-            blk[2] = (uint8_t)dmin;
-            blk[3] = (uint8_t)(dmin >> 8);
-            std::memcpy(blk + 4, rnd, 140);
-        }
+    return fst_synth_q4k_blocks(seed, expert_id, 3 * (size_t)hd * inter / 256, d_sigma, out);
+}
+
+int fst_synth_q4k_blocks(uint64_t seed, uint64_t id, size_t nblocks, float d_sigma, uint8_t* out) {
+    if (!out) return FST_EINVAL;
+    parallel_for(nblocks, [&](size_t b0, size_t b1) {
+        for (size_t b = b0; b < b1; ++b) fst_synth_q4k_block(seed, id, b, d_sigma, out + b * 144);
     });
     return FST_OK;
 }

@@ -158,10 +158,45 @@ int fst_device_copy(fst_ctx* ctx, void* d_dst, const void* d_src, size_t bytes);
 /* Number of distinct routed experts touched by the last MoE call (device -> host copy). */
 int fst_last_active_experts(fst_ctx* ctx, int* n_routed_active);
 
-/* ---- synthetic inputs (host-only; deterministic from a seed) ---- */
-/* One Q4_K expert: uniform nibbles and 6-bit scales/mins, d,dmin ~ |N(0, sigma)| in fp16. */
+/* ---- verify forward: residual stream, norms, LM head ----
+ * The non-HC layer of process_layer (src/fst_engine.cpp:2738-2741 RMSNorm with
+ * moe_norm, :2826-2852 MoE, :2913-2917 residual h = bf16(h + ffn_out)) and
+ * apply_final_norm_and_lm_head (:2115-2160; final norm, Q4_K LM head
+ * [vocab][hidden/256] blocks instead of the reference's bf16 head).
+ * RMSNorm: eps 1e-6, sum of squares in double in a fixed order, out =
+ * bf16((x * r) * w) (see resid_norm_kernel). */
+/* lid in [0, n_layers): the layer's moe_norm; lid == n_layers: the final norm. */
+int fst_upload_norm(fst_ctx* ctx, int lid, const uint16_t* w_bf16);
+/* Bytes of a packed Q4_K LM head: vocab_size * hidden_dim/256 * 144. */
+size_t fst_lm_head_bytes(const fst_config* cfg);
+/* vocab_size must be a multiple of 128. */
+int fst_upload_lm_head(fst_ctx* ctx, const void* packed, size_t bytes);
+/* d_h_out (nullable) = d_y ? bf16(d_h + d_y) : d_h;  d_normed = RMSNorm_lid(that). */
+int fst_rmsnorm_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, const uint16_t* d_y, int M, uint16_t* d_h_out,
+                    uint16_t* d_normed);
+/* d_logits[M][vocab] fp32 = LMHead(RMSNorm_final(d_h)). */
+int fst_lm_head_dev(fst_ctx* ctx, const uint16_t* d_h, int M, float* d_logits);
+/* For l in 0..n_layers-1: h = h + MoE_l(RMSNorm_l(h)); then logits =
+ * LMHead(RMSNorm_final(h)).  d_h [M][hidden] bf16 is updated in place. */
+int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_input_ids, float* d_logits);
+int fst_verify_forward(fst_ctx* ctx, uint16_t* h, int M, const int32_t* input_ids, float* logits);
+
+/* ---- synthetic inputs (deterministic from a seed) ---- */
+/* One Q4_K expert (gate|up|down in the packed ABI layout): uniform nibbles and
+ * 6-bit scales/mins, d,dmin = fp16(|z|*sigma) with z ~ N(0,1) (Irwin-Hall). */
 int fst_synth_q4k_expert(uint64_t seed, uint64_t expert_id, int hd, int inter, float d_sigma,
                          uint8_t* out);
+/* nblocks consecutive 144-byte Q4_K blocks of matrix `id` (the expert above is
+ * id = expert_id, 3*hd*inter/256 blocks). */
+int fst_synth_q4k_blocks(uint64_t seed, uint64_t id, size_t nblocks, float d_sigma, uint8_t* out);
+/* The same bytes generated on the device straight into the resident layout:
+ * experts e_first..e_first+e_count-1 of layer lid (e == n_experts: shared)
+ * from generator id id_base + e (= fst_synth_q4k_expert(seed, id_base + e)),
+ * and the LM head from generator id `id` (= fst_synth_q4k_blocks(seed, id,
+ * vocab*hidden/256)).  Synchronous. */
+int fst_synth_experts_dev(fst_ctx* ctx, uint64_t seed, int lid, int e_first, int e_count, uint64_t id_base,
+                          float d_sigma);
+int fst_synth_lm_head_dev(fst_ctx* ctx, uint64_t seed, uint64_t id, float d_sigma);
 int fst_synth_mxfp4_expert(uint64_t seed, uint64_t expert_id, int hd, int inter, int e_lo,
                            int e_hi, uint8_t* out);
 /* n values ~ N(mean, std) rounded to bf16 / kept fp32. */

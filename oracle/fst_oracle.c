@@ -439,11 +439,53 @@ int fo_accept_stochastic(const float* target, const float* draft_logits, int k, 
 /* src/fst_engine.cpp:89-91 (rms_cpu): r = 1/sqrt(mean(x^2)+eps), out =
  * bf16(x*r*w); this build rounds RNE and accumulates the mean in double. */
 void fo_rmsnorm(const float* x, const uint16_t* w, int M, int d, float eps, uint16_t* out) {
+    /* src/fst_engine.cpp:89-90 (rms_cpu) with RNE output and a fixed order
+     * for the sum of squares: in double, 64 partials over contiguous d/64
+     * chunks summed sequentially, then p[j] += p[j+off] for off = 32..1. */
+    const int C = d / 64;
     for (int m = 0; m < M; ++m) {
-        double ss = 0.0;
-        for (int j = 0; j < d; ++j) ss += (double)x[(size_t)m * d + j] * x[(size_t)m * d + j];
-        float r = (float)(1.0 / sqrt(ss / d + eps));
+        const float* xr = x + (size_t)m * d;
+        double p[64];
+        for (int j = 0; j < 64; ++j) {
+            double a = 0.0;
+            for (int i = 0; i < C; ++i) {
+                const double v = (double)xr[j * C + i];
+                a = a + v * v;
+            }
+            p[j] = a;
+        }
+        for (int off = 32; off >= 1; off >>= 1)
+            for (int j = 0; j < off; ++j) p[j] = p[j] + p[j + off];
+        const float r = (float)(1.0 / sqrt(p[0] / (double)d + (double)eps));
         for (int j = 0; j < d; ++j)
-            out[(size_t)m * d + j] = fst_f32_to_bf16(x[(size_t)m * d + j] * r * fst_bf16_to_f32(w[j]));
+            out[(size_t)m * d + j] = fst_f32_to_bf16((xr[j] * r) * fst_bf16_to_f32(w[j]));
     }
+}
+
+/* Dense Q4_K linear (the LM head, src/fst_engine.cpp:2115-2160 with a Q4_K
+ * head): y[m][n] = sum_k W[n][k] x[m][k], W dequantised per
+ * kernels/fst_dequant_q4k_kernel.cc, double accumulation.  blocks: [N][K/256]. */
+int fo_q4k_linear(const uint8_t* blocks, int N, int K, const uint16_t* x, int M, float* y) {
+    if (K % 256) return 1;
+    float* xf = (float*)malloc(sizeof(float) * (size_t)M * K);
+    if (!xf) return 2;
+    for (size_t i = 0; i < (size_t)M * K; ++i) xf[i] = fst_bf16_to_f32(x[i]);
+    const size_t row_bytes = (size_t)(K / 256) * 144;
+#pragma omp parallel num_threads(FO_NT)
+    {
+        float* wr = (float*)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+        for (int n = 0; n < N; ++n) {
+            fo_q4k_dequant(blocks + (size_t)n * row_bytes, (size_t)(K / 256), wr);
+            for (int m = 0; m < M; ++m) {
+                const float* xr = xf + (size_t)m * K;
+                double acc = 0.0;
+                for (int k = 0; k < K; ++k) acc += (double)xr[k] * (double)wr[k];
+                y[(size_t)m * N + n] = (float)acc;
+            }
+        }
+        free(wr);
+    }
+    free(xf);
+    return 0;
 }

@@ -52,8 +52,12 @@ int fo_accept_stochastic(const float* target, const float* draft_logits, int k, 
                          const int32_t* draft, float temperature, uint64_t seed, uint64_t seq,
                          int32_t* n_acc, int32_t* tokens);
 
-/* RMSNorm (src/fst_engine.cpp:89-91 with RNE): out = bf16(x * rsqrt(mean(x^2)+eps) * w). */
+/* RMSNorm (src/fst_engine.cpp:89-91 with RNE): out = bf16((x * r) * w),
+ * r = (float)(1/sqrt(ss/d + eps)), ss in double in the fixed order of fst_oracle.c. */
 void fo_rmsnorm(const float* x, const uint16_t* w, int M, int d, float eps, uint16_t* out);
+
+/* Dense Q4_K linear (LM head): y[M][N] = x[M][K] . W^T, W = blocks [N][K/256]. */
+int fo_q4k_linear(const uint8_t* blocks, int N, int K, const uint16_t* x, int M, float* y);
 
 /* exact-math passthroughs for pinning tests */
 float fo_expf(float x);

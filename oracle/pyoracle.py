@@ -44,6 +44,7 @@ def lib():
         "fo_accept_greedy": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
         "fo_accept_stochastic": (C.c_int, [P, P, C.c_int, C.c_int, P, C.c_float, C.c_uint64, C.c_uint64, P, P]),
         "fo_rmsnorm": (None, [P, P, C.c_int, C.c_int, C.c_float, P]),
+        "fo_q4k_linear": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, P]),
         "fo_expf": (C.c_float, [C.c_float]),
         "fo_logf": (C.c_float, [C.c_float]),
         "fo_sigmoidf": (C.c_float, [C.c_float]),
@@ -175,6 +176,26 @@ def rmsnorm(x, w, eps=1e-6):
     out = np.empty((M, d), np.uint16)
     lib().fo_rmsnorm(_p(x), _p(np.ascontiguousarray(w, np.uint16)), M, d, eps, _p(out))
     return out
+
+
+def q4k_linear(blocks, x, N, K):
+    """y[M][N] = x . W^T for a packed Q4_K matrix W [N][K/256] (LM head)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    M = x.shape[0]
+    y = np.empty((M, N), np.float32)
+    rc = lib().fo_q4k_linear(_p(np.ascontiguousarray(blocks, np.uint8)), N, K, _p(x), M, _p(y))
+    if rc:
+        raise ValueError("fo_q4k_linear failed (%d)" % rc)
+    return y
+
+
+def resid_norm(h, y, w, eps=1e-6):
+    """Residual add then RMSNorm: x = bf16(h + y) (or h), returns (x bf16, RMSNorm(x) bf16)."""
+    from fastar_amd import bf16_to_f32, f32_to_bf16  # bit helpers only (numpy)
+    x = np.ascontiguousarray(h, np.uint16)
+    if y is not None:
+        x = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(np.ascontiguousarray(y, np.uint16))).reshape(x.shape)
+    return x, rmsnorm(bf16_to_f32(x).reshape(x.shape), w, eps)
 
 
 def philox(ctr, key):

@@ -43,8 +43,8 @@ def c2_layer(fa):
     a bf16 router ~N(0, 0.02), all generated from C2_SEED."""
     print("[gpu-test] create C2 ctx: 256 routed + 1 shared Q4_K experts", flush=True)
     ctx = fa.Context(n_experts=256, top_k=6, max_tokens=64)
-    for e in range(257):
-        ctx.upload_expert(0, e, fa.synth_q4k_expert(C2_SEED, e))
+    # generated on the device; byte-identical to fa.synth_q4k_expert(C2_SEED, e)
+    ctx.synth_experts(C2_SEED, 0, 0, 257, 0)
     w = fa.synth_normal_bf16(C2_SEED, 1000, (HD, 256), 0.0, 0.02)
     ctx.upload_router_bf16(0, w)
     yield ctx, C2_SEED, w

@@ -1,0 +1,205 @@
+"""GPU tests of the verify forward (BASELINE C5): residual + RMSNorm, the
+dense Q4_K LM head, the layer stack and per-sequence acceptance, through the
+C-ABI, against the CPU oracle.  Also checks that device-generated synthetic
+weights are byte-identical to the host generator's."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from tests.helpers import bf16_to_f32, f32_to_bf16, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+HD, INTER = 4096, 2048
+
+
+def _log(*a):
+    print("[gpu-test]", *a, flush=True)
+
+
+def _dev(ctx, arr):
+    return ctx.to_device(np.ascontiguousarray(arr))
+
+
+def _rmsnorm_dev(fa, ctx, lid, h, y=None):
+    M = h.shape[0]
+    dh = _dev(ctx, h)
+    dy = _dev(ctx, y) if y is not None else None
+    dho = ctx.dev_alloc(h.nbytes)
+    dn = ctx.dev_alloc(h.nbytes)
+    fa._check(fa.lib().fst_rmsnorm_dev(ctx.h, lid, dh, dy, M, dho, dn))
+    ctx.sync()
+    x = ctx.to_host(dho, h.shape, np.uint16) if y is not None else h
+    n = ctx.to_host(dn, h.shape, np.uint16)
+    for p in (dh, dy, dho, dn):
+        if p:
+            ctx.dev_free(p)
+    return x, n
+
+
+def _lm_head_dev(fa, ctx, h):
+    M = h.shape[0]
+    dh = _dev(ctx, h)
+    dl = ctx.dev_alloc(M * ctx.cfg.vocab_size * 4)
+    fa._check(fa.lib().fst_lm_head_dev(ctx.h, dh, M, dl))
+    ctx.sync()
+    out = ctx.to_host(dl, (M, ctx.cfg.vocab_size), np.float32)
+    ctx.dev_free(dh)
+    ctx.dev_free(dl)
+    return out
+
+
+def test_device_synth_matches_host(fa):
+    """fst_synth_experts_dev / fst_synth_lm_head_dev write the same bytes as the
+    host generator: an expert uploaded from host bytes and its device-generated
+    twin give bit-identical FFN outputs, and so do the two LM heads."""
+    _log("device synth vs host synth")
+    V = 1280
+    with fa.Context(n_experts=4, top_k=1, max_tokens=16, vocab_size=V) as ctx:
+        ctx.upload_expert(0, 0, fa.synth_q4k_expert(41, 100))
+        ctx.synth_experts(41, 0, 1, 1, 99)  # expert 1 <- generator id 100
+        ctx.synth_experts(41, 0, 2, 3, 0)  # the rest of the layer (2, 3, shared)
+        rng = np.random.default_rng(1)
+        h = f32_to_bf16(rng.normal(0, 1, (8, HD)).astype(np.float32)).reshape(8, HD)
+        w = np.ones((8, 1), np.float32)
+        a = ctx.expert_ffn(0, h, np.zeros((8, 1), np.int32), w)
+        b = ctx.expert_ffn(0, h, np.ones((8, 1), np.int32), w)
+        assert np.array_equal(a, b)
+        ctx.upload_norm(1, f32_to_bf16(np.ones(HD, np.float32)))
+        ctx.upload_lm_head(fa.synth_q4k_blocks(41, 500, V * HD // 256))
+        la = _lm_head_dev(fa, ctx, h)
+        ctx.synth_lm_head(41, 500)
+        lb = _lm_head_dev(fa, ctx, h)
+        assert np.array_equal(la, lb)
+
+
+def test_rmsnorm_dev_bit_exact(fa, oracle):
+    _log("rmsnorm_dev vs oracle")
+    rng = np.random.default_rng(2)
+    with fa.Context(n_experts=4, top_k=1, max_tokens=64, n_layers=2) as ctx:
+        for lid in range(3):
+            w = f32_to_bf16(rng.normal(1, 0.1, HD).astype(np.float32))
+            ctx.upload_norm(lid, w)
+            for M in (1, 7, 32, 64):
+                h = f32_to_bf16(rng.normal(0, 2, (M, HD)).astype(np.float32)).reshape(M, HD)
+                y = f32_to_bf16(rng.normal(0, 0.5, (M, HD)).astype(np.float32)).reshape(M, HD)
+                x_ref, n_ref = oracle.resid_norm(h, y, w)
+                x, n = _rmsnorm_dev(fa, ctx, lid, h, y)
+                assert np.array_equal(x, x_ref)
+                assert np.array_equal(n, n_ref)
+                _, n0 = _rmsnorm_dev(fa, ctx, lid, h)
+                assert np.array_equal(n0, oracle.rmsnorm(bf16_to_f32(h).reshape(M, HD), w))
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_lm_head_vs_oracle(fa, oracle, M):
+    """Final norm + Q4_K LM head vs the oracle (fp64 accumulation)."""
+    _log("lm_head M=%d" % M)
+    V = 2560
+    rng = np.random.default_rng(3 + M)
+    blocks = fa.synth_q4k_blocks(43, 7, V * HD // 256)
+    w = f32_to_bf16(rng.normal(1, 0.1, HD).astype(np.float32))
+    with fa.Context(n_experts=4, top_k=1, max_tokens=64, n_layers=1, vocab_size=V) as ctx:
+        ctx.upload_norm(1, w)
+        ctx.upload_lm_head(blocks)
+        h = f32_to_bf16(rng.normal(0, 1, (M, HD)).astype(np.float32)).reshape(M, HD)
+        got = _lm_head_dev(fa, ctx, h)
+    ref = oracle.q4k_linear(blocks, oracle.rmsnorm(bf16_to_f32(h).reshape(M, HD), w), V, HD)
+    for m in range(M):
+        assert rel_l2(got[m], ref[m]) < 1e-2
+
+
+def _layer_stack_ctx(fa, L, E, tk, V, seed):
+    ctx = fa.Context(n_experts=E, top_k=tk, max_tokens=64, n_layers=L, vocab_size=V)
+    routers, norms = [], []
+    for l in range(L):
+        ctx.synth_experts(seed, l, 0, E + 1, l * 1000)
+        w = fa.synth_normal_bf16(seed, 1000 + l, (HD, E), 0.0, 0.02)
+        ctx.upload_router_bf16(l, w)
+        routers.append(w)
+    for l in range(L + 1):
+        n = fa.synth_normal_bf16(seed, 2000 + l, (HD,), 1.0, 0.1)
+        ctx.upload_norm(l, n)
+        norms.append(n)
+    ctx.synth_lm_head(seed, 999999)
+    return ctx, routers, norms
+
+
+def test_verify_forward_matches_composition_and_oracle(fa, oracle):
+    """fst_verify_forward equals the composition of its public pieces
+    (rmsnorm_dev, moe_layer, lm_head_dev) bit for bit, and every piece of that
+    composition matches the oracle on the GPU's own inputs: norms bit-exact,
+    routing bit-exact, MoE outputs and logits within 1e-2 relative L2."""
+    L, E, tk, V, M, seed = 2, 8, 2, 1280, 16, 61
+    _log("verify_forward L=%d E=%d M=%d" % (L, E, M))
+    ctx, routers, norms = _layer_stack_ctx(fa, L, E, tk, V, seed)
+    with ctx:
+        h0 = fa.synth_normal_bf16(seed, 3000, (M, HD))
+        logits, h_fin = ctx.verify_forward(h0)
+
+        h, y = h0, None
+        for l in range(L):
+            x, mn = _rmsnorm_dev(fa, ctx, l, h, y)
+            x_ref, mn_ref = oracle.resid_norm(h, y, norms[l])
+            assert np.array_equal(x, x_ref) and np.array_equal(mn, mn_ref)
+            out, eids, wts = ctx.moe_layer(l, mn)
+            e_ref, w_ref, _ = oracle.router(mn, routers[l], None, tk)
+            assert np.array_equal(eids, e_ref) and np.array_equal(wts, w_ref)
+            yr = np.zeros((M, tk, HD), np.float32)
+            for j in range(tk):
+                for m in range(M):
+                    yr[m, j] = oracle.expert_ffn(0, fa.synth_q4k_expert(seed, l * 1000 + int(e_ref[m, j])),
+                                                 mn[m:m + 1])[0]
+            ys = oracle.expert_ffn(0, fa.synth_q4k_expert(seed, l * 1000 + E), mn)
+            _, comb = oracle.combine(yr, ys, w_ref)
+            assert rel_l2(bf16_to_f32(out), comb) < 1e-2
+            h, y = x, out
+        x, _ = _rmsnorm_dev(fa, ctx, L, h, y)
+        assert np.array_equal(x, h_fin)
+        manual = _lm_head_dev(fa, ctx, x)
+        assert np.array_equal(manual, logits)
+        blocks = fa.synth_q4k_blocks(seed, 999999, V * HD // 256)
+        ref = oracle.q4k_linear(blocks, oracle.rmsnorm(bf16_to_f32(x).reshape(M, HD), norms[L]), V, HD)
+        assert rel_l2(logits, ref) < 1e-2
+
+
+def test_c5_full_verify_step(fa, oracle):
+    """BASELINE C5 at full size: 4 sequences x block 8 (M = 32), 8 layers of
+    256 routed + 1 shared Q4_K experts (29 GB resident), RMSNorm eps 1e-6 with
+    weights ~N(1, 0.1), Q4_K LM head 4096 -> 129,280, then greedy and
+    stochastic acceptance per sequence.  Acceptance is bit-exact vs the oracle
+    on the GPU's logits; logits of 512 vocabulary rows are checked against the
+    oracle from the GPU's final residual."""
+    L, E, tk, V, n_seq, k, seed = 8, 256, 6, 129280, 4, 7, 5
+    M = n_seq * (k + 1)
+    _log("C5: building 8 layers x 257 experts + LM head on device")
+    ctx, routers, norms = _layer_stack_ctx(fa, L, E, tk, V, seed)
+    with ctx:
+        h0 = fa.synth_normal_bf16(seed, 3000, (M, HD))
+        _log("C5: verify forward")
+        logits, h_fin = ctx.verify_forward(h0)
+        assert np.isfinite(logits).all()
+        tgt = logits.reshape(n_seq, k + 1, V)
+        # plant accepted prefixes 0, 3, 7 and one random draft
+        draft = np.zeros((n_seq, k), np.int32)
+        for s, n_plant in enumerate([0, 3, 7, None]):
+            am = tgt[s].argmax(1)
+            draft[s] = (am[:k] + 1) % V
+            if n_plant is not None:
+                draft[s, :n_plant] = am[:n_plant]
+        n_acc, tok = ctx.accept_greedy(tgt, draft)
+        for s in range(n_seq):
+            rn, rt = oracle.accept_greedy(tgt[s], draft[s])
+            assert n_acc[s] == rn and np.array_equal(tok[s, :rn + 1], rt[:rn + 1])
+        assert list(n_acc[:3]) == [0, 3, 7]
+        dl = fa.synth_normal_f32(seed, 4000, (n_seq, k, V), 0.0, 2.0)
+        n_acc2, tok2 = ctx.accept_stochastic(tgt, dl, draft, 1.0, seed, 0)
+        for s in range(n_seq):
+            rn, rt = oracle.accept_stochastic(tgt[s], dl[s], draft[s], 1.0, seed, s)
+            assert n_acc2[s] == rn and np.array_equal(tok2[s, :rn + 1], rt[:rn + 1])
+        rows = np.sort(np.random.default_rng(9).choice(V, 512, replace=False))
+        blocks = fa.synth_q4k_blocks(seed, 999999, V * HD // 256).reshape(V, HD // 256 * 144)
+        hn = oracle.rmsnorm(bf16_to_f32(h_fin).reshape(M, HD), norms[L])
+        ref = oracle.q4k_linear(np.ascontiguousarray(blocks[rows]), hn, len(rows), HD)
+        assert rel_l2(logits[:, rows], ref) < 1e-2
