@@ -116,6 +116,144 @@ def cpu_baseline(hs, w, threads, min_seconds=10.0, max_steps=16):
     return tokens / secs, secs, steps, nexp / steps
 
 
+# ------------------------------------------------------------ other configs
+# BASELINE configs other than C2 are parity-test cases; these modes measure
+# them for the record (one JSON line each, not the driver's headline).
+
+def timed(ctx, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    ctx.sync()
+    return (time.perf_counter() - t0) / steps
+
+
+def bench_c1(fa, args):
+    """C1: one Q4_K expert FFN at M = 1, back to back over 64 distinct resident
+    experts (906 MB > the 256 MB Infinity Cache); per-expert time."""
+    L = fa.lib()
+    NE = 64
+    ctx = fa.Context(n_experts=NE, top_k=1, max_tokens=64)
+    ctx.synth_experts(SEED, 0, 0, NE + 1, 0)
+    h = fa.synth_normal_bf16(SEED, 3000, (1, HD))
+    dh = ctx.to_device(h)
+    de = ctx.to_device(np.arange(NE, dtype=np.int32))
+    dw = ctx.to_device(np.ones(NE, np.float32))
+    do = ctx.dev_alloc(HD * 2)
+
+    def one(i):
+        fa._check(L.fst_moe_ffn_dev(ctx.h, 0, dh, 1, de + 4 * (i % NE), dw, 0, do, None, None))
+    t = timed(ctx, one, args.steps, args.warmup)
+    ctx.set_profiling(True)
+    one(0)
+    kern = {k: round(v * 1e3, 2) for k, v in ctx.last_timings()}
+    ctx.set_profiling(False)
+    ctx.close()
+    return {"metric": "C1 single-expert Q4_K SwiGLU FFN latency at M=1", "value": round(t * 1e6, 2),
+            "unit": "us/expert", "higher_is_better": False,
+            "packed_weight_GBps": round(EXPERT_BYTES / t / 1e9, 1), "kernel_us": kern,
+            "config": {"workload": "C1: 64 distinct resident experts, one fst_moe_ffn_dev call each, M=1"}}
+
+
+def bench_c3(fa, args):
+    """C3: greedy and stochastic acceptance, k = 7, V = 129,280, one sequence."""
+    L = fa.lib()
+    ctx = fa.Context(n_experts=8, top_k=1, max_tokens=64)
+    tgt = fa.synth_normal_f32(SEED, 4000, (1, K_DRAFT + 1, VOCAB), 0.0, 2.0)
+    dl = fa.synth_normal_f32(SEED, 4001, (1, K_DRAFT, VOCAB), 0.0, 2.0)
+    draft = np.array([[int(np.argmax(tgt[0, i])) if i < 3 else i for i in range(K_DRAFT)]], np.int32)
+    dt, dd, dr = ctx.to_device(tgt), ctx.to_device(dl), ctx.to_device(draft)
+    dn, dk = ctx.dev_alloc(4), ctx.dev_alloc(4 * (K_DRAFT + 1))
+    g = timed(ctx, lambda i: fa._check(L.fst_accept_greedy_dev(ctx.h, dt, 1, K_DRAFT, VOCAB, dr, dn, dk)),
+              args.steps, args.warmup)
+    st = timed(ctx, lambda i: fa._check(L.fst_accept_stochastic_dev(ctx.h, dt, dd, 1, K_DRAFT, VOCAB, dr, 1.0,
+                                                                    SEED, i, dn, dk)), args.steps, args.warmup)
+    ctx.close()
+    return {"metric": "C3 acceptance latency (k=7, V=129280)", "value": round(g * 1e6, 2), "unit": "us",
+            "higher_is_better": False, "greedy_us": round(g * 1e6, 2), "stochastic_us": round(st * 1e6, 2),
+            "config": {"workload": "C3: target + draft logits fp32 [8,129280] ~N(0,4) resident, T=1.0"}}
+
+
+def bench_c4(fa, args):
+    """C4: Zipf(1.1)-routed verify at blocks 16 and 32 (caller-given routing),
+    256 routed + 1 shared experts resident."""
+    L = fa.lib()
+    ctx = fa.Context(n_experts=E, top_k=TK, max_tokens=64)
+    ctx.synth_experts(SEED, 0, 0, E + 1, 0)
+    out = {}
+    for M in (16, 32):
+        rng = np.random.default_rng(300 + M)
+        p = 1.0 / np.arange(1, E + 1) ** 1.1
+        p /= p.sum()
+        perm = rng.permutation(E)
+        batches = []
+        for b in range(N_BATCH):
+            eids = np.stack([perm[rng.choice(E, TK, replace=False, p=p)] for _ in range(M)]).astype(np.int32)
+            w = rng.random((M, TK)).astype(np.float32) + 0.05
+            batches.append((eids, (w / w.sum(1, keepdims=True)).astype(np.float32)))
+        distinct = float(np.mean([len(set(e.ravel().tolist())) for e, _ in batches]))
+        de = [ctx.to_device(e) for e, _ in batches]
+        dw = [ctx.to_device(w) for _, w in batches]
+        dh = ctx.to_device(fa.synth_normal_bf16(SEED, 5000 + M, (M, HD)))
+        do = ctx.dev_alloc(M * HD * 2)
+        t = timed(ctx, lambda i: fa._check(L.fst_moe_ffn_dev(ctx.h, 0, dh, M, de[i % N_BATCH], dw[i % N_BATCH], 1,
+                                                             do, None, None)), args.steps, args.warmup)
+        byts = (distinct + 1) * EXPERT_BYTES
+        out["M%d" % M] = {"tokens_per_s": round(M / t, 1), "us_per_step": round(t * 1e6, 2),
+                          "mean_distinct_routed": round(distinct, 2),
+                          "packed_weight_GBps": round(byts / t / 1e9, 1)}
+    ctx.close()
+    return {"metric": "C4 Zipf-routed MoE verify throughput", "value": out["M32"]["tokens_per_s"],
+            "unit": "tokens/s", "higher_is_better": True, "blocks": out,
+            "config": {"workload": "C4: Zipf(1.1) routing over 256 experts, top-6 + shared, M=16 and 32"}}
+
+
+def bench_c5(fa, args):
+    """C5: 4 sequences x block 8 (M = 32): 8 MoE layers (RMSNorm + router +
+    256 routed / 1 shared Q4_K experts each, 29 GB resident) + final norm +
+    Q4_K LM head 4096 -> 129,280 + greedy acceptance per sequence."""
+    L = fa.lib()
+    NL, n_seq = 8, 4
+    M = n_seq * (K_DRAFT + 1)
+    ctx = fa.Context(n_experts=E, top_k=TK, max_tokens=64, n_layers=NL, vocab_size=VOCAB)
+    t0 = time.time()
+    for l in range(NL):
+        ctx.synth_experts(SEED, l, 0, E + 1, l * 1000)
+        ctx.upload_router_bf16(l, fa.synth_normal_bf16(SEED, 1000 + l, (HD, E), 0.0, 0.02))
+    for l in range(NL + 1):
+        ctx.upload_norm(l, fa.synth_normal_bf16(SEED, 2000 + l, (HD,), 1.0, 0.1))
+    ctx.synth_lm_head(SEED, 999999)
+    log("C5 weights resident in %.1fs" % (time.time() - t0))
+    hs = [fa.synth_normal_bf16(SEED, 3000 + b, (M, HD)) for b in range(N_BATCH)]
+    dsrc = [ctx.to_device(h) for h in hs]
+    dh = ctx.dev_alloc(M * HD * 2)
+    dl = ctx.dev_alloc(M * VOCAB * 4)
+    dr = ctx.to_device(np.zeros((n_seq, K_DRAFT), np.int32))
+    dn, dk = ctx.dev_alloc(4 * n_seq), ctx.dev_alloc(4 * n_seq * (K_DRAFT + 1))
+
+    def step(i):
+        fa._check(L.fst_device_copy(ctx.h, dh, dsrc[i % N_BATCH], M * HD * 2))
+        fa._check(L.fst_verify_forward_dev(ctx.h, dh, M, None, dl))
+        fa._check(L.fst_accept_greedy_dev(ctx.h, dl, n_seq, K_DRAFT, VOCAB, dr, dn, dk))
+    t = timed(ctx, step, args.steps, args.warmup)
+    ctx.set_profiling(True)
+    fa._check(L.fst_device_copy(ctx.h, dh, dsrc[0], M * HD * 2))
+    fa._check(L.fst_verify_forward_dev(ctx.h, dh, M, None, dl))
+    parts = {k: round(v * 1e3, 1) for k, v in ctx.last_timings()}
+    ctx.set_profiling(False)
+    ctx.close()
+    lm_bytes = VOCAB * (HD // 256) * 144
+    return {"metric": "C5 verified tokens/s for a full verify step (4 seq x block 8, 8 layers + LM head)",
+            "value": round(M / t, 1), "unit": "tokens/s", "higher_is_better": True,
+            "ms_per_step": round(t * 1e3, 4), "parts_us": parts,
+            "lm_head_GBps": round(lm_bytes / (parts.get("lm_head", 1e9) * 1e-6) / 1e9, 1),
+            "config": {"workload": "C5: M=32, 8 layers x (RMSNorm + router + 256+1 Q4_K experts), "
+                                   "Q4_K LM head 4096->129280, greedy acceptance x4"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -125,6 +263,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="also run N launches of the plain copy kernel (512 MiB) for PMC calibration")
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="c2 (default) is the headline; the others print their own record line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; the verify path is not sharded across GPUs "
@@ -132,6 +272,12 @@ def main():
         sys.exit(2)
 
     import fastar_amd as fa
+    if args.config != "c2":
+        fn = {"c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config]
+        res = fn(fa, args)
+        res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "data": "synthetic"})
+        print(json.dumps(res), flush=True)
+        return
     L = fa.lib()
     ctx, w, hs, logits, draft, bufs = setup(fa)
 
@@ -219,7 +365,7 @@ def main():
             "parallelism": "1 GPU",
         },
         "roofline": {
-            "kernel": "q4k_linear gate+up (fused Q4_K decode, fp16 MFMA; last workgroup per expert runs SwiGLU prep)",
+            "kernel": "q4k_linear gate+up (fused Q4_K decode, fp16 MFMA; each workgroup pairs 64 gate with 64 up rows and writes silu(g)*u)",
             "bound": "hbm",
             "achieved": round(gu_achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -7,6 +7,9 @@
 //   process_expert_ffn    include/fst_engine.h:318   src/fst_engine.cpp:4068-4371
 //   process_shared_expert include/fst_engine.h:319   src/fst_engine.cpp:4373-4489
 //   accept/reject         src/fst_engine.cpp:6021-6063 (inline in generate_dspark)
+//   apply_final_norm_and_lm_head include/fst_engine.h:276 src/fst_engine.cpp:2115-2160
+//   process_layer (FFN half, non-HC residual) include/fst_engine.h:308
+//                         src/fst_engine.cpp:2734-2917
 //
 // FSTEngineHip keeps those member signatures, argument meanings and buffer
 // layouts (bf16_t = uint16_t host buffers, row-major [M][hidden], token-major
@@ -97,6 +100,35 @@ public:
         check(fst_accept_greedy(ctx_, target_logits, 1, k, V, draft, &n_acc, tok.data()), "fst_accept_greedy");
         if (emitted) emitted->assign(tok.begin(), tok.begin() + n_acc + 1);
         return n_acc;
+    }
+
+    // include/fst_engine.h:276: logits[M][vocab] = LMHead(RMSNorm_final(hidden_state)).
+    // The final norm weights go in with upload_norm(n_layers, w), the Q4_K head
+    // with upload_lm_head.  hidden_state is the plain [M][hidden] residual
+    // (the HC collapse of the reference's 4-stream residual is not on this path).
+    void apply_final_norm_and_lm_head(bf16_t* hidden_state, int M, float* logits) {
+        const size_t hbytes = (size_t)M * cfg_.hidden_dim * sizeof(bf16_t);
+        const size_t lbytes = (size_t)M * cfg_.vocab_size * sizeof(float);
+        void* dh = fst_device_alloc(ctx_, hbytes);
+        void* dl = fst_device_alloc(ctx_, lbytes);
+        int rc = (dh && dl) ? FST_OK : FST_ENOMEM;
+        if (rc == FST_OK) rc = fst_copy_to_device(ctx_, dh, hidden_state, hbytes);
+        if (rc == FST_OK) rc = fst_lm_head_dev(ctx_, static_cast<const uint16_t*>(dh), M, static_cast<float*>(dl));
+        if (rc == FST_OK) rc = fst_copy_to_host(ctx_, logits, dl, lbytes);
+        fst_device_free(ctx_, dh);
+        fst_device_free(ctx_, dl);
+        check(rc, "apply_final_norm_and_lm_head");
+    }
+
+    // The FFN half of process_layer without HC (src/fst_engine.cpp:2738-2741,
+    // :2826-2852, :2913-2917) for every layer, then the final norm and head:
+    // h = h + MoE_l(RMSNorm_l(h)) for l < n_layers; logits = LMHead(RMSNorm(h)).
+    void verify_forward(bf16_t* h, int M, const int* input_ids, float* logits) {
+        check(fst_verify_forward(ctx_, h, M, input_ids, logits), "fst_verify_forward");
+    }
+    void upload_norm(int lid, const bf16_t* w) { check(fst_upload_norm(ctx_, lid, w), "fst_upload_norm"); }
+    void upload_lm_head(const void* packed, size_t bytes) {
+        check(fst_upload_lm_head(ctx_, packed, bytes), "fst_upload_lm_head");
     }
 
     // Rejection-sampling variant (no counterpart in the reference, which only

@@ -76,7 +76,39 @@ int main(int argc, char** argv) {
     } catch (const std::runtime_error&) {
         threw = true;
     }
-    std::printf("ADAPTER GPU %s: combine rel=%.3e accept n=%d threw_on_bad_shape=%d\n",
-                (rel < 1e-2 && acc_ok && threw) ? "OK" : "FAIL", rel, n, (int)threw);
-    return (rel < 1e-2 && acc_ok && threw) ? 0 : 1;
+    // apply_final_norm_and_lm_head (include/fst_engine.h:276) on a small head:
+    // one logit row recomputed here from the GPU dequant of the same blocks
+    // and a double-precision RMSNorm must agree to 1e-2
+    double head_rel = 1.0;
+    {
+        fst_config c2 = cfg;
+        c2.vocab_size = 256;
+        fst_hip::FSTEngineHip head(c2);
+        std::vector<uint16_t> nw(hd);
+        fst_synth_normal_bf16(99, 9, nw.size(), 1.0f, 0.1f, nw.data());
+        head.upload_norm(c2.n_layers, nw.data());
+        std::vector<uint8_t> lm(fst_lm_head_bytes(&c2));
+        fst_synth_q4k_blocks(99, 12345, lm.size() / 144, 0.01f, lm.data());
+        head.upload_lm_head(lm.data(), lm.size());
+        std::vector<float> lg((size_t)M * c2.vocab_size);
+        head.apply_final_norm_and_lm_head(h.data(), M, lg.data());
+        std::vector<float> wf(lm.size() / 144 * 256);
+        if (fst_dequant(head.handle(), FST_CODEC_Q4K, lm.data(), lm.size() / 144, wf.data(), nullptr) != FST_OK)
+            return 1;
+        double ss = 0;
+        for (int j = 0; j < hd; ++j) ss += (double)bf(h[j]) * bf(h[j]);
+        const double r = 1.0 / std::sqrt(ss / hd + 1e-6);
+        double hn = 0, hd2 = 0;
+        for (int v = 0; v < c2.vocab_size; ++v) {
+            double acc = 0;
+            for (int j = 0; j < hd; ++j) acc += bf(h[j]) * r * bf(nw[j]) * wf[(size_t)v * hd + j];
+            hn += (lg[v] - acc) * (lg[v] - acc);
+            hd2 += acc * acc;
+        }
+        head_rel = std::sqrt(hn / hd2);
+    }
+    const bool ok = rel < 1e-2 && acc_ok && threw && head_rel < 1e-2;
+    std::printf("ADAPTER GPU %s: combine rel=%.3e accept n=%d threw_on_bad_shape=%d lm_head rel=%.3e\n",
+                ok ? "OK" : "FAIL", rel, n, (int)threw, head_rel);
+    return ok ? 0 : 1;
 }
