@@ -218,20 +218,28 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
 
 // dec layout per sequence: [0] n_acc, [1] sampling target row, [2] mode
 // (0: residual vs draft row, 1: sample from target row), [3] U', [4] Sp, [5] Sq,
-// [6] draft row, [7] packed (row max bits of target | any) unused.
-__global__ __launch_bounds__(64) void acc_decide_kernel(
+// [6] draft row, [7] unused.
+// One workgroup per sequence; wave w decides positions w, w+NW, ... in
+// parallel (each decision is independent given the logits and uniforms).
+constexpr int kDecideWaves = 8;
+__global__ __launch_bounds__(64 * kDecideWaves) void acc_decide_kernel(
     const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
     float inv_t, const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base,
     const float* __restrict__ part_max, const int* __restrict__ part_idx,
     const unsigned long long* __restrict__ part_sum, unsigned long long* __restrict__ dec,
     int32_t* __restrict__ n_acc, int32_t* __restrict__ tokens) {
-    const int s = blockIdx.x, lane = threadIdx.x;
+    const int s = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n_tgt = n_seq * (k + 1);
     __shared__ int accept[64];
     __shared__ unsigned long long Sp_s[65], Sq_s[64];
-    for (int i = 0; i < k; ++i) {
-        const int rt = s * (k + 1) + i, rd = n_tgt + s * k + i;
+    for (int i = wave; i <= k; i += kDecideWaves) {
+        const int rt = s * (k + 1) + i;
         const unsigned long long Sp = wave_sum_u64(part_sum[(size_t)rt * kChunks + lane]);
+        if (i == k) {
+            if (lane == 0) Sp_s[k] = Sp;
+            continue;
+        }
+        const int rd = n_tgt + s * k + i;
         const unsigned long long Sq = wave_sum_u64(part_sum[(size_t)rd * kChunks + lane]);
         float mp, mq;
         int ap, aq;
@@ -253,13 +261,8 @@ __global__ __launch_bounds__(64) void acc_decide_kernel(
             Sq_s[i] = Sq;
         }
     }
-    {
-        const int rt = s * (k + 1) + k;
-        const unsigned long long Sp = wave_sum_u64(part_sum[(size_t)rt * kChunks + lane]);
-        if (lane == 0) Sp_s[k] = Sp;
-    }
     __syncthreads();
-    if (lane == 0) {
+    if (threadIdx.x == 0) {
         int n = 0;
         while (n < k && accept[n]) ++n;
         unsigned long long* d = dec + (size_t)s * 8;
@@ -353,54 +356,72 @@ __global__ __launch_bounds__(256) void acc_res_chunks_kernel(
     }
 }
 
-// Inverse-CDF pick: first v with prefix > target, where target = (U' * total) >> 24.
+__device__ __forceinline__ u128 shfl_u128(u128 v, int src) {
+    const uint64_t lo = (uint64_t)v, hi = (uint64_t)(v >> 64);
+    const uint32_t a = __shfl((uint32_t)lo, src, 64), b = __shfl((uint32_t)(lo >> 32), src, 64);
+    const uint32_t c = __shfl((uint32_t)hi, src, 64), d = __shfl((uint32_t)(hi >> 32), src, 64);
+    return ((u128)(((uint64_t)d << 32) | c) << 64) | (u128)(((uint64_t)b << 32) | a);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave (exact, unsigned 128-bit).
+__device__ __forceinline__ u128 wave_incl_scan_u128(u128 v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const u128 o = shfl_u128(v, max(lane - off, 0));
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+// Inverse-CDF pick: the first v whose inclusive prefix exceeds
+// target = (U' * total) >> 24.  Chunk sums are scanned by one wave (lane c
+// = chunk c), then the chosen chunk by the whole workgroup (thread t owns a
+// contiguous run), and only the owning thread walks its few elements.
 __global__ __launch_bounds__(256) void acc_sample_kernel(
     const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
     float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
     const unsigned long long* __restrict__ part_sum, unsigned long long* __restrict__ dec,
     const unsigned long long* __restrict__ part_res, int32_t* __restrict__ tokens) {
-    const int s = blockIdx.x, tid = threadIdx.x;
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ RowCtx rc;
     __shared__ u128 s_target, s_before;
     __shared__ int s_chunk;
-    __shared__ u128 tsum[256];
+    __shared__ u128 wtot[4];
+    __shared__ int s_owner;
+    __shared__ u128 s_run;
     __shared__ int s_tok;
     unsigned long long* d = dec + (size_t)s * 8;
     if (tid < 64) load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
     __syncthreads();
-    if (tid == 0) {
+    if (tid < 64) {
         const unsigned long long U2 = d[3];
-        u128 tot = 0;
-        u128 cs[kChunks];
-        for (int c = 0; c < kChunks; ++c) {
-            const unsigned long long* o = part_res + ((size_t)s * kChunks + c) * 2;
-            cs[c] = ((u128)o[1] << 64) | (u128)o[0];
-            tot += cs[c];
-        }
-        if (rc.mode == 0 && tot == 0) {
+        const unsigned long long* o = part_res + ((size_t)s * kChunks + lane) * 2;
+        u128 cs = ((u128)o[1] << 64) | (u128)o[0];
+        u128 pre = wave_incl_scan_u128(cs);
+        u128 tot = shfl_u128(pre, 63);
+        int mode = rc.mode;
+        if (mode == 0 && tot == 0) {
             // residual is identically zero: sample from the target row instead
-            rc.mode = 1;
-            tot = 0;
-            const int rt = (int)d[1];
-            for (int c = 0; c < kChunks; ++c) {
-                cs[c] = part_sum[(size_t)rt * kChunks + c];
-                tot += cs[c];
-            }
+            mode = 1;
+            cs = (u128)part_sum[(size_t)((int)d[1]) * kChunks + lane];
+            pre = wave_incl_scan_u128(cs);
+            tot = shfl_u128(pre, 63);
         }
-        s_chunk = -1;
-        s_tok = 0;
+        int chunk = -1;
+        u128 tg = 0;
         if (tot != 0) {
-            const u128 tg = ((u128)U2 * tot) >> 24;
-            u128 run = 0;
-            for (int c = 0; c < kChunks; ++c) {
-                if (run + cs[c] > tg) {
-                    s_chunk = c;
-                    s_before = run;
-                    break;
-                }
-                run += cs[c];
-            }
+            tg = ((u128)U2 * tot) >> 24;
+            const unsigned long long hit = __ballot(pre > tg);
+            chunk = hit ? __ffsll((long long)hit) - 1 : -1;
+        }
+        const u128 before = chunk > 0 ? shfl_u128(pre, chunk - 1) : (u128)0;
+        if (lane == 0) {
+            rc.mode = mode;
+            s_chunk = chunk;
             s_target = tg;
+            s_before = before;
+            s_tok = 0;
         }
     }
     __syncthreads();
@@ -408,65 +429,79 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
     if (c >= 0) {
         const int clen = (V + kChunks - 1) / kChunks;
         const int b0 = c * clen, b1 = min(V, b0 + clen);
-        // thread tid owns the contiguous run [b0 + tid*per, ...)
         const int per = (clen + 255) / 256;
         const int v0 = b0 + tid * per, v1 = min(b1, v0 + per);
         u128 acc = 0;
         for (int v = v0; v < v1; ++v)
             acc += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
-        tsum[tid] = acc;
+        const u128 pre = wave_incl_scan_u128(acc);
+        if (lane == 63) wtot[wave] = pre;
+        if (tid == 0) s_owner = 0x7fffffff;
         __syncthreads();
-        if (tid == 0) {
-            u128 run = s_before;
-            int owner = -1;
-            for (int i = 0; i < 256; ++i) {
-                if (run + tsum[i] > s_target) { owner = i; break; }
-                run += tsum[i];
-            }
-            tsum[0] = run;
-            s_tok = owner;
-        }
+        u128 base = s_before;
+        for (int w2 = 0; w2 < wave; ++w2) base += wtot[w2];
+        const unsigned long long hit = __ballot(base + pre > s_target);
+        if (hit && lane == __ffsll((long long)hit) - 1) atomicMin(&s_owner, tid);
         __syncthreads();
-        if (tid == s_tok) {
-            u128 run = tsum[0];
+        if (tid == s_owner) s_run = base + pre - acc;  // prefix before this thread's run
+        __syncthreads();
+        if (tid == s_owner) {
+            u128 run = s_run;
             int tok = v1 - 1;
             for (int v = v0; v < v1; ++v) {
                 run += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq,
                                  rc.mode);
-                if (run > s_target) { tok = v; break; }
+                if (run > s_target) {
+                    tok = v;
+                    break;
+                }
             }
             s_tok = tok;
         }
         __syncthreads();
-        if (tid == 0) {
-            const int n = (int)d[0];
-            tokens[s * (k + 1) + n] = s_tok >= 0 ? s_tok : 0;
-        }
+        if (tid == 0) tokens[s * (k + 1) + (int)d[0]] = s_owner == 0x7fffffff ? 0 : s_tok;
     } else if (tid == 0) {
-        const int n = (int)d[0];
-        tokens[s * (k + 1) + n] = 0;
+        tokens[s * (k + 1) + (int)d[0]] = 0;
     }
 }
 
 // Greedy acceptance in one launch: every (row, chunk) workgroup reduces its
-// chunk; the last workgroup to finish a row reduces the row's 64 partials
+// chunk; the last workgroup to finish a row reduces the row's CH partials
 // (argmax with the reference's rules), and the last row to finish a sequence
 // resolves the longest matching prefix and the bonus token.  Counters are
-// re-armed to zero by the workgroup that consumes them.
+// re-armed to zero by the workgroup that consumes them.  CH is small on
+// purpose: increments of one device-scope counter serialise at the memory
+// side (a few hundred ns each), so a row waits on CH of them.
+template <int CH>
 __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict__ target, int k, int V,
                                                          const int32_t* __restrict__ draft, AccWs w,
                                                          int32_t* __restrict__ n_acc,
                                                          int32_t* __restrict__ tokens) {
+    static_assert(CH <= 64, "one lane per chunk partial");
     const int c = blockIdx.x, r = blockIdx.y;
     const float* row = target + (size_t)r * V;
-    const int clen = (V + kChunks - 1) / kChunks;
-    const int b0 = c * clen, b1 = min(V, b0 + clen);
+    const int clen = ((V + CH - 1) / CH + 3) & ~3;  // multiple of 4 elements
+    const int b0 = min(V, c * clen), b1 = min(V, b0 + clen);
     float best = 0.0f;
     int bi = 0x7fffffff;
-    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) {
-        const float l = row[v];
-        if (l != l) continue;
-        if (bi == 0x7fffffff || l > best) { best = l; bi = v; }
+    auto take = [&](float l, int v) {
+        if (l != l) return;
+        if (bi == 0x7fffffff || l > best) {
+            best = l;
+            bi = v;
+        }
+    };
+    if ((V & 3) == 0) {
+        // 16-byte loads: thread t takes elements b0 + 4(t + 256 j) .. +3, in index order
+        for (int v = b0 + 4 * (int)threadIdx.x; v < b1; v += 1024) {
+            const float4 q = *reinterpret_cast<const float4*>(row + v);
+            take(q.x, v);
+            take(q.y, v + 1);
+            take(q.z, v + 2);
+            take(q.w, v + 3);
+        }
+    } else {
+        for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) take(row[v], v);
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -495,13 +530,17 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
         st_coherent(&w.part_max[(size_t)r * kChunks + c], best);
         st_coherent(&w.part_idx[(size_t)r * kChunks + c], bi == 0x7fffffff ? -1 : bi);
         publish_wait();
-        s_last = signal_add(&w.row_done[r], 1) == kChunks - 1;
+        s_last = signal_add(&w.row_done[r], 1) == CH - 1;
     }
     __syncthreads();
     if (!s_last) return;
     if (threadIdx.x < 64) {
-        float m = ld_coherent(&w.part_max[(size_t)r * kChunks + lane]);
-        int i = ld_coherent(&w.part_idx[(size_t)r * kChunks + lane]);
+        float m = 0.0f;
+        int i = -1;
+        if (lane < CH) {
+            m = ld_coherent(&w.part_max[(size_t)r * kChunks + lane]);
+            i = ld_coherent(&w.part_idx[(size_t)r * kChunks + lane]);
+        }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
             const float om = __shfl_xor(m, off, 64);
@@ -538,11 +577,15 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
     }
 }
 
+#ifndef FST_GREEDY_CHUNKS
+#define FST_GREEDY_CHUNKS 16
+#endif
 void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k, int V,
                           const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* ws) {
     AccWs w = carve(ws, n_seq, k);
     const int R = n_seq * (k + 1);
-    hipLaunchKernelGGL(acc_greedy_kernel, dim3(kChunks, R), dim3(256), 0, st, target, k, V, draft, w, n_acc,
+    constexpr int CH = FST_GREEDY_CHUNKS;
+    hipLaunchKernelGGL(acc_greedy_kernel<CH>, dim3(CH, R), dim3(256), 0, st, target, k, V, draft, w, n_acc,
                        tokens);
 }
 
@@ -557,7 +600,7 @@ void launch_accept_stochastic(hipStream_t st, const float* target, const float* 
                        inv_t, w.part_max, w.part_idx);
     hipLaunchKernelGGL(acc_sums_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
                        inv_t, w.part_max, w.part_idx, w.part_sum);
-    hipLaunchKernelGGL(acc_decide_kernel, dim3(n_seq), dim3(64), 0, st, target, draft_logits, n_seq, k, V,
+    hipLaunchKernelGGL(acc_decide_kernel, dim3(n_seq), dim3(64 * kDecideWaves), 0, st, target, draft_logits, n_seq, k, V,
                        inv_t, draft, seed, seq_base, w.part_max, w.part_idx, w.part_sum, w.dec, n_acc,
                        tokens);
     hipLaunchKernelGGL(acc_res_chunks_kernel, dim3(kChunks, n_seq), dim3(256), 0, st, target, draft_logits,
