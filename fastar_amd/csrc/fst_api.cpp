@@ -254,9 +254,9 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.act, (size_t)P * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
         (rc = x->dalloc(&s.y, (size_t)P * hd)) || (rc = x->dalloc(&s.tok_npairs, T)) ||
-        (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 128))))
+        (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 16))))
         return bail(rc);
-    if (hipMemsetAsync(s.tile_done, 0, sizeof(int) * T * (hd / 128), x->st) != hipSuccess)
+    if (hipMemsetAsync(s.tile_done, 0, sizeof(int) * T * (hd / 16), x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(counters) failed"));
     if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));

@@ -56,7 +56,7 @@ struct Scratch {
     int* xs2;              // [P]
     float* y;              // [P][hd]
     int* tok_npairs;       // [T] distinct (token, expert) pairs of each token incl. shared
-    int* tile_done;        // [T][hd/128] down contributions finished per token row tile (re-armed)
+    int* tile_done;        // [T][hd/16] (used: hd / rows per item) down contributions finished per token row tile (re-armed)
 };
 
 // Device expert bank: n_layers x (n_experts + 1) packed experts.

@@ -460,7 +460,6 @@ template <int NT, typename Src>
 __device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __restrict__ x16p,
                          uint4* __restrict__ sxp, int* __restrict__ xs) {
     __shared__ float red[NT / 64];
-    __shared__ int s_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float m = 0.0f;
     for (int i = tid; i < K; i += NT) {
@@ -472,50 +471,45 @@ __device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if (lane == 0) red[wave] = m;
     __syncthreads();
-    if (tid == 0) {
-        float a = red[0];
-        for (int w = 1; w < NT / 64; ++w) a = fmaxf(a, red[w]);
-        const int s = prescale_exp(a);
-        s_sh = s;
-        xs[row] = s;
-    }
-    __syncthreads();
-    const int s = s_sh;
-    // fp16 values in place (exact power-of-two scaling, one rounding)
-    for (int i = tid; i < K; i += NT) xv[i] = (float)(_Float16)ldexpf(xv[i], -s);
-    __syncthreads();
-    _Float16* dst = x16p + (size_t)row * K;
-    const int nchunk = K / 8;
-    for (int q = tid; q < nchunk; q += NT) {
-        const int sb = q >> 5, gc = q & 31, g = gc >> 3, c = gc & 7;
-        const int base = sb * 256 + 64 * g + 4 * c;
-        h8_t v;
+    float a = red[0];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;  // nibble pair order of q4k_bop
-            v[i] = (_Float16)xv[base + e];
-            v[4 + i] = (_Float16)xv[base + 32 + e];
-        }
+    for (int w = 1; w < NT / 64; ++w) a = fmaxf(a, red[w]);
+    const int s = prescale_exp(a);
+    if (tid == 0) xs[row] = s;
+    // One pass over the operand chunks: chunk q = 32 sb + 8g + c holds the
+    // fp16 values (exact power-of-two scaling, one rounding) of elements
+    // 64g+4c+{0,2,1,3} and 64g+32+4c+{0,2,1,3} of super-block sb; the 8
+    // lanes of one (sb, g) then reduce the two sub-block sums (hi+lo split).
+    // K/8 is a multiple of 8, so each 8-lane group runs the same iterations.
+    _Float16* dst = x16p + (size_t)row * K;
+    uint4* sx = sxp + (size_t)row * (K / 256) * 4;
+    for (int q = tid; q < K / 8; q += NT) {
+        const int sb = q >> 5, g = (q >> 3) & 3, c = q & 7;
+        const int base = sb * 256 + 64 * g + 4 * c;
+        const float4 lo4 = *reinterpret_cast<const float4*>(xv + base);
+        const float4 hi4 = *reinterpret_cast<const float4*>(xv + base + 32);
+        h8_t v;
+        v[0] = (_Float16)ldexpf(lo4.x, -s);
+        v[1] = (_Float16)ldexpf(lo4.z, -s);
+        v[2] = (_Float16)ldexpf(lo4.y, -s);
+        v[3] = (_Float16)ldexpf(lo4.w, -s);
+        v[4] = (_Float16)ldexpf(hi4.x, -s);
+        v[5] = (_Float16)ldexpf(hi4.z, -s);
+        v[6] = (_Float16)ldexpf(hi4.y, -s);
+        v[7] = (_Float16)ldexpf(hi4.w, -s);
         *reinterpret_cast<h8_t*>(dst + (size_t)q * 8) = v;
-    }
-    // sub-block sums of the fp16 values (32 consecutive elements; the start of
-    // the fixed summation order is rotated by j to spread LDS banks)
-    const int nsub = K / 32;
-    uint16_t* sx16 = reinterpret_cast<uint16_t*>(sxp + (size_t)row * (K / 256) * 4);
-    for (int j = tid; j < nsub; j += NT) {
-        float S = 0.0f;
-        for (int i = 0; i < 32; ++i) S += xv[j * 32 + ((i + j) & 31)];
-        const _Float16 hi = (_Float16)S;
-        const _Float16 lo = (_Float16)(S - (float)hi);
-        const int sb = j >> 3, jj = j & 7, g = jj >> 1, odd = jj & 1;
-        uint16_t* e = sx16 + ((size_t)sb * 4 + g) * 8;
-        e[odd] = __builtin_bit_cast(uint16_t, hi);
-        e[2 + odd] = __builtin_bit_cast(uint16_t, lo);
-        if (!odd) {
-            e[4] = 0;
-            e[5] = 0;
-            e[6] = 0;
-            e[7] = 0;
+        float s0 = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+        float s1 = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            s0 += __shfl_xor(s0, o, 64);
+            s1 += __shfl_xor(s1, o, 64);
+        }
+        if (c == 0) {
+            const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
+            const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
+            const _Float16 z = (_Float16)0.0f;
+            *reinterpret_cast<h8_t*>(sx + sb * 4 + g) = h8_t{h0, h1, l0, l1, z, z, z, z};
         }
     }
     __syncthreads();
@@ -745,6 +739,9 @@ constexpr int kTokStride = 37;
 #ifndef FST_Q4K_WAVES_PER_EU
 #define FST_Q4K_WAVES_PER_EU 4
 #endif
+#ifndef FST_Q4K_WPE_MID
+#define FST_Q4K_WPE_MID 4
+#endif
 // What a linear-kernel launch does besides Y = W.A.
 struct EpiArgs {
     // mode 1 (gate||up): workgroup tile T holds gate rows [64T, 64T+64) in
@@ -781,7 +778,7 @@ struct EpiArgs {
 //    super-blocks (double-buffered, prefetched one macro-stage ahead into
 //    registers), one workgroup barrier per macro-stage.
 template <int TOKS, int MS, int WAVES, int MODE, int PF = FST_Q4K_PF>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : 3))) void q4k_linear_kernel(
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : (TOKS <= 32 ? FST_Q4K_WPE_MID : 3)))) void q4k_linear_kernel(
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
     const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
     const int* __restrict__ slot_off, const int* __restrict__ a_row, const _Float16* __restrict__ A,
@@ -931,21 +928,28 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
             Q4kScale S;
             q4k_scales(cur.h, g, S);
             const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+            // each decoded weight operand feeds every live 16-token group
+            f4_t D[NGRP];
+#pragma unroll
+            for (int q = 0; q < NGRP; ++q) D[q] = zf;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const h8_t b = q4k_bop(Dw[c], S, magic);
+#pragma unroll
+                for (int q = 0; q < NGRP; ++q) {
+                    if (q > 0 && q >= ngrp_live) break;
+                    const h8_t a = __builtin_bit_cast(h8_t, st[q * 16 * kTokStride + 8 * g + c]);
+                    D[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, D[q], 0, 0, 0);
+                }
+            }
 #pragma unroll
             for (int q = 0; q < NGRP; ++q) {
                 if (q > 0 && q >= ngrp_live) break;
-                const uint4* sq = st + q * 16 * kTokStride;
-                f4_t D = zf;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const h8_t a = __builtin_bit_cast(h8_t, sq[8 * g + c]);
-                    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, q4k_bop(Dw[c], S, magic), D, 0, 0, 0);
-                }
-                const h8_t am = __builtin_bit_cast(h8_t, sq[32 + g]);
+                const h8_t am = __builtin_bit_cast(h8_t, st[q * 16 * kTokStride + 32 + g]);
                 const f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, S.m, zf, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    acc[q][i] = fmaf(S.d, D[i], acc[q][i]);
+                    acc[q][i] = fmaf(S.d, D[q][i], acc[q][i]);
                     acc[q][i] = fmaf(-S.dmin, Dm[i], acc[q][i]);
                 }
             }
@@ -1044,8 +1048,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         __syncthreads();
         if (tid == 0) s_nflag = 0;
         __syncthreads();
-        const int nt128 = N / 128;
-        const int T128 = (tile * WAVES * 16) / 128;
+        constexpr int TR = 16 * WAVES;  // rows per work item
+        const int nt128 = N / TR;
+        const int T128 = tile;
         for (int tl = tid; tl < slot_M[slot]; tl += NT) {
             const int tok = ep.pair_tok[off + tl];
             const int old = signal_add(&ep.tile_done[tok * nt128 + T128], 1);
@@ -1058,8 +1063,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         const int nflag = s_nflag;
         for (int f = 0; f < nflag; ++f) {
             const int tok = s_flag[f];
-            for (int i = tid; i < 128; i += NT) {
-                const int n = T128 * 128 + i;
+            for (int i = tid; i < TR; i += NT) {
+                const int n = T128 * TR + i;
                 float a = 0.0f;
                 for (int j = 0; j < ep.tk; ++j) {
                     const int p = ep.pair_of[tok * ep.tk + j];
@@ -1087,21 +1092,29 @@ template <int MODE>
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
                               const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep) {
-    constexpr int W = 8;
+#ifndef FST_Q4K_W
+#define FST_Q4K_W 8
+#endif
+    constexpr int W = FST_Q4K_W;
     // persistent grid: FST_Q4K_WG_PER_CU workgroups per CU at most
     const unsigned items = slots * (unsigned)(N / (16 * W));
     // (token capacities above 8 run at 3 waves per SIMD: one 8-wave workgroup per CU)
-    const unsigned wg_per_cu = M <= 8 ? FST_Q4K_WG_PER_CU : 1;
+    const unsigned wg_per_cu =
+        (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1)) * (8 / W);
     const dim3 grid(std::min(items, (unsigned)s.n_cu * wg_per_cu));
 #define FST_Q4K_LAUNCH(T, MSV)                                                                               \
     hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE>), grid, dim3(64 * W), 0, st, bank, stride, mat_off, \
                        K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep)
     // K is a multiple of 512 (checked at context creation): nsb is even
 #ifndef FST_MS8
-#define FST_MS8 2
+#define FST_MS8 1
 #endif
-    if (M <= 8 && (K >> 8) % FST_MS8 == 0)
-        FST_Q4K_LAUNCH(8, FST_MS8);
+#ifndef FST_MS8_DN
+#define FST_MS8_DN 2
+#endif
+    constexpr int ms8 = MODE == 2 ? FST_MS8_DN : FST_MS8;
+    if (M <= 8 && (K >> 8) % ms8 == 0)
+        FST_Q4K_LAUNCH(8, ms8);
     else if (M <= 8)
         FST_Q4K_LAUNCH(8, 2);
     else if (M <= 16)
