@@ -211,6 +211,39 @@ def bench_c4(fa, args):
             "config": {"workload": "C4: Zipf(1.1) routing over 256 experts, top-6 + shared, M=16 and 32"}}
 
 
+def bench_c2mx(fa, args):
+    """C2 with MXFP4 experts (the engine's live format): 256 routed + 1 shared
+    MXFP4 experts (13,369,344 B each) resident, same router and block size."""
+    L = fa.lib()
+    ctx = fa.Context(n_experts=E, top_k=TK, max_tokens=64, codec=fa.CODEC_MXFP4)
+    ctx.synth_experts(SEED, 0, 0, E + 1, 0)
+    ctx.upload_router_bf16(0, fa.synth_normal_bf16(SEED, 1000, (HD, E), 0.0, 0.02))
+    hs = fa.synth_normal_bf16(SEED, 3000, (N_BATCH, M, HD))
+    dh = ctx.to_device(hs)
+    do, de, dw = ctx.dev_alloc(M * HD * 2), ctx.dev_alloc(M * TK * 4), ctx.dev_alloc(M * TK * 4)
+    t = timed(ctx, lambda i: fa._check(L.fst_moe_layer_dev(ctx.h, 0, dh + (i % N_BATCH) * M * HD * 2, M, None, do,
+                                                            de, dw)), args.steps, args.warmup)
+    ctx.set_profiling(True)
+    acts = []
+    per = {}
+    for i in range(N_BATCH):
+        fa._check(L.fst_moe_layer_dev(ctx.h, 0, dh + i * M * HD * 2, M, None, do, de, dw))
+        acts.append(ctx.last_active_experts())
+        for k, v in ctx.last_timings():
+            per.setdefault(k, []).append(v)
+    ctx.set_profiling(False)
+    ctx.close()
+    mx_expert = 3 * INTER * (HD // 32) * 17
+    byts = (np.mean(acts) + 1) * mx_expert
+    kern = {k: round(float(np.mean(v)) * 1e3, 2) for k, v in per.items()}
+    gu = (np.mean(acts) + 1) * 2 * mx_expert / 3 / (kern["q4k_gate_up"] * 1e-6) / 1e9
+    return {"metric": "verified tokens/s for block-8 MoE-layer verify, MXFP4 experts", "value": round(M / t, 1),
+            "unit": "tokens/s", "higher_is_better": True, "us_per_step": round(t * 1e6, 2),
+            "packed_weight_GBps_step": round(byts / t / 1e9, 1), "gate_up_GBps": round(gu, 1),
+            "kernel_us": kern, "mean_distinct_routed": round(float(np.mean(acts)), 2),
+            "config": {"workload": "C2 shape with MXFP4 experts (no acceptance in the step)"}}
+
+
 def bench_c5(fa, args):
     """C5: 4 sequences x block 8 (M = 32): 8 MoE layers (RMSNorm + router +
     256 routed / 1 shared Q4_K experts each, 29 GB resident) + final norm +
@@ -263,7 +296,7 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="also run N launches of the plain copy kernel (512 MiB) for PMC calibration")
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c2mx", "c3", "c4", "c5"],
                     help="c2 (default) is the headline; the others print their own record line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -273,7 +306,7 @@ def main():
 
     import fastar_amd as fa
     if args.config != "c2":
-        fn = {"c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config]
+        fn = {"c1": bench_c1, "c2mx": bench_c2mx, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config]
         res = fn(fa, args)
         res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "data": "synthetic"})
         print(json.dumps(res), flush=True)

@@ -174,8 +174,8 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     if (!cfg || !out) return fail(FST_EINVAL, "fst_create: null argument");
     *out = nullptr;
     const fst_config& c = *cfg;
-    if (c.codec != FST_CODEC_Q4K)
-        return fail(FST_EINVAL, "fst_create: only the Q4_K codec has a fused FFN path");
+    if (c.codec != FST_CODEC_Q4K && c.codec != FST_CODEC_MXFP4)
+        return fail(FST_EINVAL, "fst_create: codec must be FST_CODEC_Q4K or FST_CODEC_MXFP4");
     if (c.hidden_dim <= 0 || c.hidden_dim % 512 || c.inter_dim <= 0 || c.inter_dim % 512)
         return fail(FST_EINVAL, "fst_create: hidden_dim and inter_dim must be multiples of 512");
     if (c.hidden_dim > 8192 || c.inter_dim > 8192)
@@ -358,8 +358,12 @@ int fst_upload_expert(fst_ctx* ctx, int lid, int eid, const void* packed, size_t
                                     std::to_string(ctx->expert_bytes));
     uint8_t* dst = ctx->bank + ((size_t)lid * (ctx->cfg.n_experts + 1) + eid) * ctx->expert_stride;
     ctx->staging.resize(bytes);
-    fst::repack_q4k_expert(static_cast<const uint8_t*>(packed), ctx->staging.data(), ctx->cfg.hidden_dim,
-                           ctx->cfg.inter_dim);
+    if (ctx->cfg.codec == FST_CODEC_MXFP4)
+        fst::repack_mx_expert(static_cast<const uint8_t*>(packed), ctx->staging.data(), ctx->cfg.hidden_dim,
+                              ctx->cfg.inter_dim);
+    else
+        fst::repack_q4k_expert(static_cast<const uint8_t*>(packed), ctx->staging.data(), ctx->cfg.hidden_dim,
+                               ctx->cfg.inter_dim);
     FST_HIP_TRY(hipMemcpyAsync(dst, ctx->staging.data(), bytes, hipMemcpyHostToDevice, ctx->st));
     FST_HIP_TRY(hipStreamSynchronize(ctx->st));
     if (!ctx->uploaded[lid][eid]) {
@@ -447,22 +451,28 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     const int use_hash = do_router && lid < c.n_hash_layers && L.hash && d_ids;
     hipStream_t st = ctx->st;
     ctx->mark_begin();
+    const bool mx = c.codec == FST_CODEC_MXFP4;  // bf16 operands: no fp16 operand prep
     if (do_router) {
-        fst::launch_router_prep(st, g, L, d_h, M, ctx->s.logits, ctx->s);
+        if (mx)
+            fst::launch_router_logits(st, g, L, d_h, M, ctx->s.logits);
+        else
+            fst::launch_router_prep(st, g, L, d_h, M, ctx->s.logits, ctx->s);
         ctx->mark("router_prep");
     }
     fst::launch_route_bucket(st, g, L, M, ctx->s.logits, d_ids, use_hash, do_router, use_shared, d_eids, d_wts,
                              ctx->s);
     ctx->mark("route_bucket");
-    if (!do_router) {
+    if (!do_router && !mx) {
         fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
         ctx->mark("prep_x");
     }
-    fst::launch_q4k_gate_up(st, g, L, M, ctx->s);
+    fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h);
     ctx->mark("q4k_gate_up");
-    fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p, ctx->s.sx2p,
-                         ctx->s.xs2);
-    ctx->mark("prep_h");
+    if (!mx) {
+        fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p,
+                             ctx->s.sx2p, ctx->s.xs2);
+        ctx->mark("prep_h");
+    }
     fst::launch_q4k_down(st, g, L, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared);
     ctx->mark("q4k_down");
     FST_HIP_TRY(hipGetLastError());
@@ -774,6 +784,15 @@ int fst_synth_experts_dev(fst_ctx* ctx, uint64_t seed, int lid, int e_first, int
     for (int e = e_first; e < e_first + e_count; ++e) {
         uint8_t* dst = ctx->bank + ((size_t)lid * (c.n_experts + 1) + e) * ctx->expert_stride;
         const uint64_t id = id_base + (uint64_t)e;
+        if (c.codec == FST_CODEC_MXFP4) {
+            // d_sigma is unused; scales e in [108, 128) as fst_synth_mxfp4_expert's defaults
+            const uint64_t mb = (uint64_t)inter * (hd / 32);
+            const size_t mp = mb * 17;
+            fst::launch_synth_mx_tiled(ctx->st, seed, id, 0, inter, hd, 108, 128, dst);
+            fst::launch_synth_mx_tiled(ctx->st, seed, id, mb, inter, hd, 108, 128, dst + mp);
+            fst::launch_synth_mx_tiled(ctx->st, seed, id, 2 * mb, hd, inter, 108, 128, dst + 2 * mp);
+            continue;
+        }
         fst::launch_synth_q4k_tiled(ctx->st, seed, id, 0, inter, hd, d_sigma, dst);
         fst::launch_synth_q4k_tiled(ctx->st, seed, id, gate_blocks, inter, hd, d_sigma, dst + proj);
         fst::launch_synth_q4k_tiled(ctx->st, seed, id, 2 * gate_blocks, hd, inter, d_sigma, dst + 2 * proj);

@@ -135,7 +135,8 @@ void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_ro
 // Weights must be in the wave-tiled device layout (repack_q4k_expert).
 // gate/up writes h = silu(gate)*up; down runs the combine of each token row
 // tile (last contribution).
-void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
+void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                        const uint16_t* h_in);
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
                      const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
                      uint16_t* out_shared);
@@ -143,10 +144,14 @@ void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int 
 // blocks of 144 B) into the device layout the linear kernel streams.
 void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);
 void repack_q4k_matrix(const uint8_t* src, uint8_t* dst, int N, int K);
+// The same for an MXFP4 expert (2176-byte chunks of 16 rows x 256 weights).
+void repack_mx_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);
 // Synthetic Q4_K matrix [N][K/256] (blocks b0.. of generator stream `id`)
 // written in the device layout at dst.
 void launch_synth_q4k_tiled(hipStream_t st, uint64_t seed, uint64_t id, uint64_t b0, int N, int K, float sigma,
                             uint8_t* dst);
+void launch_synth_mx_tiled(hipStream_t st, uint64_t seed, uint64_t id, uint64_t b0, int N, int K, int e_lo,
+                           int e_hi, uint8_t* dst);
 void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
                     const float* wts, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 void launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);

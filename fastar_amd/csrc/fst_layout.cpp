@@ -62,4 +62,41 @@ void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter) {
     b.join();
 }
 
+// MXFP4 (17-byte blocks of 32 weights: e8m0 scale byte, then 16 bytes with
+// elements 2i / 2i+1 in the low / high nibble of byte i) in the same spirit:
+//
+//   matrix = [N/16 row tiles][K/256] chunks of 2176 bytes; chunk (t, sb)
+//   holds the 8 blocks of K range [256 sb, 256 sb + 256) of rows 16t..16t+15:
+//     [0,    1024)  lane L = 16g + r: the 16 nibble bytes of block 2g   of row r
+//     [1024, 2048)  lane L = 16g + r: the 16 nibble bytes of block 2g+1 of row r
+//     [2048, 2176)  row r: the 8 scale bytes of its blocks 0..7
+//
+// so lane (g, r) holds the 64 consecutive weights [64g, 64g+64) of the
+// super-block range, and the expert keeps exactly its packed size.
+static void repack_mx_matrix(const uint8_t* src, uint8_t* dst, int N, int K) {
+    const int nsb = K / 256, bpr = K / 32;
+    for (int t = 0; t < N / 16; ++t)
+        for (int sb = 0; sb < nsb; ++sb) {
+            uint8_t* chunk = dst + ((size_t)t * nsb + sb) * 2176;
+            for (int r = 0; r < 16; ++r) {
+                const uint8_t* row = src + (size_t)(t * 16 + r) * bpr * 17;
+                for (int j = 0; j < 8; ++j) {
+                    const uint8_t* b = row + (size_t)(sb * 8 + j) * 17;
+                    chunk[2048 + 8 * r + j] = b[0];
+                    const int g = j >> 1, L = 16 * g + r;
+                    std::memcpy(chunk + (j & 1) * 1024 + 16 * L, b + 1, 16);
+                }
+            }
+        }
+}
+
+void repack_mx_expert(const uint8_t* src, uint8_t* dst, int hd, int inter) {
+    const size_t proj = (size_t)inter * (hd / 32) * 17;
+    std::thread a([&] { repack_mx_matrix(src, dst, inter, hd); });
+    std::thread b([&] { repack_mx_matrix(src + proj, dst + proj, inter, hd); });
+    repack_mx_matrix(src + 2 * proj, dst + 2 * proj, hd, inter);
+    a.join();
+    b.join();
+}
+
 }  // namespace fst

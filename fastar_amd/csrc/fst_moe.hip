@@ -663,7 +663,7 @@ struct Q4kScale {
     float d, dmin;
 };
 
-__device__ __forceinline__ void q4k_scales(const uint4 hdr, int g, Q4kScale& S) {
+__device__ __forceinline__ void q4k_scales(const u4v_t hdr, int g, Q4kScale& S) {
     S.d = half_bits_to_f32(hdr.x & 0xffffu);
     S.dmin = half_bits_to_f32(hdr.x >> 16);
     const uint32_t y = hdr.y, z = hdr.z, w = hdr.w;
@@ -704,13 +704,14 @@ __device__ __forceinline__ h8_t q4k_bop(uint32_t D, const Q4kScale& S, uint32_t 
     return __builtin_elementwise_fma(__builtin_bit_cast(h8_t, X), S.SC8, S.NEG8);
 }
 
+// (ext-vector members: HIP's uint4 struct copies defeat scalar replacement
+// and put the register ring in scratch)
 struct WRaw {
-    uint4 h, a, b;
+    u4v_t h, a, b;
 };
 
-__device__ __forceinline__ uint4 ld_stream(const uint8_t* p) {
-    const u4v_t v = __builtin_nontemporal_load(reinterpret_cast<const u4v_t*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
+__device__ __forceinline__ u4v_t ld_stream(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u4v_t*>(p));
 }
 
 // One 2304-byte chunk = 16 rows x one super-block: [0,1024) nibble bytes
@@ -725,8 +726,29 @@ __device__ __forceinline__ WRaw load_wraw(const uint8_t* chunk, int lane) {
     return w;
 }
 
+// MXFP4 chunk (fst_layout.cpp): 2176 bytes = [0,1024) block 2g of row r at
+// lane slot 16g+r, [1024,2048) block 2g+1, [2048,2176) the 8 scale bytes of
+// each row (h.x, h.y of the lane's row).
+__device__ __forceinline__ WRaw load_wraw_mx(const uint8_t* chunk, int lane) {
+    WRaw w;
+    w.a = ld_stream(chunk + 16 * lane);
+    w.b = ld_stream(chunk + 1024 + 16 * lane);
+    typedef uint32_t u2v_t __attribute__((ext_vector_type(2)));
+    const u2v_t hv = __builtin_nontemporal_load(reinterpret_cast<const u2v_t*>(chunk + 2048 + 8 * (lane & 15)));
+    w.h = u4v_t{hv.x, hv.y, 0u, 0u};
+    return w;
+}
+
+// e8m0 block scale as float: 2^(e-127); the reference kernel maps e = 0 and
+// e = 255 to 0 (kernels/fst_dequant_v4_vectorized_kernel.cc:280-351).
+__device__ __forceinline__ float e8m0_scale(uint32_t e) {
+    return (e == 0u || e == 255u) ? 0.0f : __uint_as_float(e << 23);
+}
+
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+
 // LDS activation stage: per token 36 uint4 (32 operand chunks, 4 min-term
-// chunks), padded to kTokStride to spread banks.
+// chunks; MXFP4 uses the 32 operand chunks only), padded to kTokStride.
 constexpr int kTokStride = 37;
 
 // Y[pair][row] = 2^xs[a] * sum_k W[row][k] * A[a][k] for the rows of one
@@ -749,6 +771,7 @@ struct EpiArgs {
     // h = silu(gate) * up (fp32) for its 64 rows
     float swiglu_limit;
     float* h;
+    uint16_t* h16;  // MXFP4 path: h rounded to bf16 (the down operand as is)
     // mode 2 (down): the last contribution to a (token, 128-row tile)
     // combines it
     int tk, use_shared;
@@ -777,18 +800,21 @@ struct EpiArgs {
 //  - the slot's activation operands are staged into LDS in macro-stages of MS
 //    super-blocks (double-buffered, prefetched one macro-stage ahead into
 //    registers), one workgroup barrier per macro-stage.
-template <int TOKS, int MS, int WAVES, int MODE, int PF = FST_Q4K_PF>
+template <int TOKS, int MS, int WAVES, int MODE, int CODEC = 0, int PF = FST_Q4K_PF>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : (TOKS <= 32 ? FST_Q4K_WPE_MID : 3)))) void q4k_linear_kernel(
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
     const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
     const int* __restrict__ slot_off, const int* __restrict__ a_row, const _Float16* __restrict__ A,
     const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out, EpiArgs ep) {
     static_assert(MODE != 1 || WAVES % 2 == 0, "gate||up pairs waves");
+    constexpr bool MX = CODEC == 1;                  // MXFP4 weights, bf16 operand, bf16 MFMA
+    constexpr int CHUNK = MX ? 2176 : 2304;          // bytes per (16 rows x 256 weights)
+    constexpr int PARTS = MX ? 32 : 36;              // staged 16-byte chunks per token per super-block
     constexpr int NGRP = (TOKS + 15) / 16;
     constexpr int TS = TOKS * kTokStride;            // one super-block of one stage
     constexpr int STAGE = MS * TS;                   // one macro-stage
     constexpr int NT = 64 * WAVES;                   // threads per workgroup
-    constexpr int NCH = MS * TOKS * 36;              // 16-byte chunks per macro-stage
+    constexpr int NCH = MS * TOKS * PARTS;           // 16-byte chunks per macro-stage
     constexpr int NS = (NCH + NT - 1) / NT;          // staged chunks per thread
     constexpr int HALF = WAVES / 2;
     constexpr int R = PF + 1;                        // weight register ring
@@ -821,7 +847,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     auto wave_base = [&](int tt) -> const uint8_t* {
         const int sl = tt / tiles;
         return bank + (size_t)slot_eid[sl] * expert_stride + mat_offset +
-               (size_t)wave_tile(tt - sl * tiles) * nsb * 2304;
+               (size_t)wave_tile(tt - sl * tiles) * nsb * CHUNK;
+    };
+    auto load_w = [&](const uint8_t* chunk) -> WRaw {
+        if constexpr (MX)
+            return load_wraw_mx(chunk, lane);
+        else
+            return load_wraw(chunk, lane);
     };
 
     // Every global load below is unconditional, with clamped addresses, and
@@ -832,7 +864,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     const uint8_t* wbase = wave_base(blockIdx.x);
     WRaw w[R];
 #pragma unroll
-    for (int j = 0; j < PF; ++j) w[j] = load_wraw(wbase + (size_t)j * 2304, lane);
+    for (int j = 0; j < PF; ++j) w[j] = load_w(wbase + (size_t)j * CHUNK);
     for (int i = tid; i < 2 * STAGE + 1; i += NT) lds[i] = z4;
 
     // Staging map: chunk q = tid + NT*i of a macro-stage -> (super-block u,
@@ -844,10 +876,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
         const int q = tid + NT * i;
-        const int u = q / (TOKS * 36), rem = q - u * (TOKS * 36);
+        const int u = q / (TOKS * PARTS), rem = q - u * (TOKS * PARTS);
         su[i] = u;
-        stl[i] = q < NCH ? rem / 36 : TOKS;
-        spart[i] = rem - (rem / 36) * 36;
+        stl[i] = q < NCH ? rem / PARTS : TOKS;
+        spart[i] = rem - (rem / PARTS) * PARTS;
     }
     auto load_rows = [&](int tt, int* ar) {
         const int sl = tt / tiles;
@@ -864,7 +896,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int u = su[i], part = spart[i];
-            ssrc[i] = reinterpret_cast<const u4v_t*>(SX);
+            ssrc[i] = reinterpret_cast<const u4v_t*>(MX ? (const void*)A : (const void*)SX);
             sdst[i] = 2 * STAGE;
             sstep[i] = 0;
             if (ar[i] >= 0) {
@@ -925,9 +957,32 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         auto compute = [&](int sb, const WRaw& cur) {
             const int m = sb / MS, u = sb - m * MS;
             const uint4* st = lds + (m & 1) * STAGE + u * TS + r * kTokStride;
+            const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+            if constexpr (MX) {
+                // lane (g, r): blocks 2g (cur.a) and 2g+1 (cur.b) of row r; the
+                // hardware FP4 (E2M1) conversion applies the block scale exactly
+                const uint32_t sw = g < 2 ? cur.h.x : cur.h.y;
+                const float s0 = e8m0_scale((sw >> ((g & 1) * 16)) & 0xffu);
+                const float s1 = e8m0_scale((sw >> ((g & 1) * 16 + 8)) & 0xffu);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const float sc = c < 4 ? s0 : s1;
+                    const auto v0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 0);
+                    const auto v1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 1);
+                    const auto v2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 2);
+                    const auto v3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 3);
+                    const bf8_t b = {v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
+#pragma unroll
+                    for (int q = 0; q < NGRP; ++q) {
+                        if (q > 0 && q >= ngrp_live) break;
+                        const bf8_t a = __builtin_bit_cast(bf8_t, st[q * 16 * kTokStride + 8 * g + c]);
+                        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[q], 0, 0, 0);
+                    }
+                }
+                return;
+            } else {
             Q4kScale S;
             q4k_scales(cur.h, g, S);
-            const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
             // each decoded weight operand feeds every live 16-token group
             f4_t D[NGRP];
 #pragma unroll
@@ -953,6 +1008,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                     acc[q][i] = fmaf(-S.dmin, Dm[i], acc[q][i]);
                 }
             }
+            }
         };
         // U super-blocks per iteration (the launcher guarantees nsb % U == 0):
         // ring slot j % R, stage boundaries at j % MS, all known at compile
@@ -971,8 +1027,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                     }
                 }
                 const int pf = sb + PF;
-                w[(j + PF) % R] = load_wraw(pf < nsb ? wbase + (size_t)pf * 2304 : nbase + (size_t)(pf - nsb) * 2304,
-                                            lane);
+                w[(j + PF) % R] = load_w(pf < nsb ? wbase + (size_t)pf * CHUNK : nbase + (size_t)(pf - nsb) * CHUNK);
                 // keep the prefetches where they are issued (the scheduler
                 // would otherwise sink them next to their use to save registers)
                 __builtin_amdgcn_sched_barrier(0);
@@ -986,7 +1041,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         wbase = nbase;
 
         // D layout: lane holds token rows 4g+i (i=0..3) of the group, column r.
-        auto unscale = [&](int pidx) -> int { return xs[a_row ? a_row[pidx] : pidx]; };
+        auto unscale = [&](int pidx) -> int {
+            if constexpr (MX)
+                return 0;
+            else
+                return xs[a_row ? a_row[pidx] : pidx];
+        };
         if constexpr (MODE == 1) {
             // gate waves hand their rows to the up waves through LDS (the
             // staging ring is free: the loop ended on a barrier)
@@ -1019,7 +1079,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                             gv = fminf(gv, lim);
                             uv = fminf(fmaxf(uv, -lim), lim);
                         }
-                        ep.h[(size_t)(off + tl) * inter + n] = (gv / (1.0f + expf(-gv))) * uv;
+                        const float hv = (gv / (1.0f + expf(-gv))) * uv;
+                        if constexpr (MX)
+                            ep.h16[(size_t)(off + tl) * inter + n] = fst_f32_to_bf16(hv);
+                        else
+                            ep.h[(size_t)(off + tl) * inter + n] = hv;
                     }
                 }
             }
@@ -1088,7 +1152,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
 #ifndef FST_Q4K_WG_PER_CU
 #define FST_Q4K_WG_PER_CU 2
 #endif
-template <int MODE>
+template <int MODE, int CODEC = 0>
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
                               const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep) {
@@ -1103,7 +1167,8 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
         (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1)) * (8 / W);
     const dim3 grid(std::min(items, (unsigned)s.n_cu * wg_per_cu));
 #define FST_Q4K_LAUNCH(T, MSV)                                                                               \
-    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE>), grid, dim3(64 * W), 0, st, bank, stride, mat_off, \
+    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE, CODEC>), grid, dim3(64 * W), 0, st, bank, stride,  \
+                       mat_off, \
                        K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep)
     // K is a multiple of 512 (checked at context creation): nsb is even
 #ifndef FST_MS8
@@ -1126,14 +1191,22 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 #undef FST_Q4K_LAUNCH
 }
 
-// gate||up: the two [inter][hd/256] matrices are contiguous; each workgroup
-// takes 64 gate rows and the same 64 up rows and writes h = silu(gate)*up.
-void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
+// gate||up: the two [inter][hd/K-block] matrices are contiguous; each
+// workgroup takes 64 gate rows and the same 64 up rows and writes
+// h = silu(gate)*up (fp32 for Q4_K, bf16 for MXFP4).  The Q4_K operand is the
+// prescaled fp16 one (router_prep); MXFP4 stages the bf16 rows of h_in as is.
+void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                        const uint16_t* h_in) {
     EpiArgs ep{};
     ep.swiglu_limit = g.swiglu_limit;
     ep.h = s.act;
-    launch_q4k_linear<1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
-                         s.pair_tok, s.x16p, s.sxp, s.xs, nullptr, ep);
+    ep.h16 = reinterpret_cast<uint16_t*>(s.a16p);
+    if (g.codec == 1)
+        launch_q4k_linear<1, 1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
+                                s.pair_tok, reinterpret_cast<const _Float16*>(h_in), nullptr, nullptr, nullptr, ep);
+    else
+        launch_q4k_linear<1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
+                             s.pair_tok, s.x16p, s.sxp, s.xs, nullptr, ep);
 }
 
 // down: the last contribution to each (token, 128-row tile) combines it:
@@ -1142,7 +1215,7 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
                      const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
                      uint16_t* out_shared) {
-    const size_t proj = (size_t)g.inter * (g.hd / 256) * 144;
+    const size_t proj = g.codec == 1 ? (size_t)g.inter * (g.hd / 32) * 17 : (size_t)g.inter * (g.hd / 256) * 144;
     EpiArgs ep{};
     ep.tk = g.tk;
     ep.use_shared = use_shared;
@@ -1155,8 +1228,12 @@ void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int 
     ep.out = out;
     ep.out_routed = out_routed;
     ep.out_shared = out_shared;
-    launch_q4k_linear<2>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
-                         nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
+    if (g.codec == 1)
+        launch_q4k_linear<2, 1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd,
+                                s, nullptr, s.a16p, nullptr, nullptr, s.y, ep);
+    else
+        launch_q4k_linear<2>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
+                             nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
 }
 
 // Dense Q4_K linear over M rows (the LM head): logits[m][n] = sum_k W[n][k] x[m][k],

@@ -51,7 +51,6 @@ void parallel_for(size_t n, F f) {
     for (auto& t : th) t.join();
 }
 
-constexpr uint64_t kTagMx = 0x4d5846ull << 40;
 
 }  // namespace
 
@@ -76,14 +75,7 @@ int fst_synth_mxfp4_expert(uint64_t seed, uint64_t expert_id, int hd, int inter,
         return FST_EINVAL;
     const size_t nblk = 3 * (size_t)hd * inter / 32;
     parallel_for(nblk, [&](size_t b0, size_t b1) {
-        for (size_t b = b0; b < b1; ++b) {
-            uint8_t* blk = out + b * 17;
-            const uint64_t lane = kTagMx ^ (expert_id << 8);
-            fst_philox_ctr r0 = philox(seed, b, lane);
-            fst_philox_ctr r1 = philox(seed, b, lane | 1u);
-            blk[0] = (uint8_t)(e_lo + (int)(r1.v[0] % (uint32_t)(e_hi - e_lo)));
-            std::memcpy(blk + 1, r0.v, 16);
-        }
+        for (size_t b = b0; b < b1; ++b) fst_synth_mx_block(seed, expert_id, b, e_lo, e_hi, out + b * 17);
     });
     return FST_OK;
 }

@@ -47,4 +47,31 @@ void launch_synth_q4k_tiled(hipStream_t st, uint64_t seed, uint64_t id, uint64_t
                        N, K / 256, sigma, dst);
 }
 
+// MXFP4: one thread per 17-byte block of one [N][K/32] matrix (blocks b0..
+// of stream `id`), written in the MXFP4 device layout (fst_layout.cpp).
+__global__ __launch_bounds__(256) void synth_mx_tiled_kernel(uint64_t seed, uint64_t id, uint64_t b0, int N,
+                                                             int bpr, int e_lo, int e_hi, uint8_t* __restrict__ dst) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)N * bpr) return;
+    const int n = (int)(i / bpr), kb = (int)(i - (size_t)n * bpr);
+    uint8_t blk[17];
+    fst_synth_mx_block(seed, id, b0 + i, e_lo, e_hi, blk);
+    const int nsb = bpr / 8, sb = kb >> 3, j = kb & 7, r = n & 15;
+    uint8_t* chunk = dst + ((size_t)(n >> 4) * nsb + sb) * 2176;
+    chunk[2048 + 8 * r + j] = blk[0];
+    uint8_t* q = chunk + (j & 1) * 1024 + 16 * (16 * (j >> 1) + r);
+    uint32_t w[4];
+    for (int k = 0; k < 4; ++k)
+        w[k] = (uint32_t)blk[1 + 4 * k] | ((uint32_t)blk[2 + 4 * k] << 8) | ((uint32_t)blk[3 + 4 * k] << 16) |
+               ((uint32_t)blk[4 + 4 * k] << 24);
+    *reinterpret_cast<uint4*>(q) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+void launch_synth_mx_tiled(hipStream_t st, uint64_t seed, uint64_t id, uint64_t b0, int N, int K, int e_lo,
+                           int e_hi, uint8_t* dst) {
+    const size_t nblk = (size_t)N * (K / 32);
+    hipLaunchKernelGGL(synth_mx_tiled_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, st, seed, id, b0,
+                       N, K / 32, e_lo, e_hi, dst);
+}
+
 }  // namespace fst

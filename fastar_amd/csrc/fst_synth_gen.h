@@ -84,3 +84,17 @@ FST_HD void fst_synth_q4k_block(uint64_t seed, uint64_t id, uint64_t b, float d_
     blk[2] = (uint8_t)dmin;
     blk[3] = (uint8_t)(dmin >> 8);
 }
+
+constexpr uint64_t kFstSynthTagMx = 0x4d5846ull << 40;
+
+// One 17-byte MXFP4 block b of expert `id`: scale byte e_lo + (word % (e_hi -
+// e_lo)) from counter (b, tag ^ id<<8 | 1), then the 16 nibble bytes = the
+// Philox words of counter (b, tag ^ id<<8).
+FST_HD void fst_synth_mx_block(uint64_t seed, uint64_t id, uint64_t b, int e_lo, int e_hi, uint8_t* blk) {
+    const uint64_t lane = kFstSynthTagMx ^ (id << 8);
+    const fst_philox_ctr r0 = fst_synth_philox(seed, b, lane);
+    const fst_philox_ctr r1 = fst_synth_philox(seed, b, lane | 1u);
+    blk[0] = (uint8_t)(e_lo + (int)(r1.v[0] % (uint32_t)(e_hi - e_lo)));
+    for (int w = 0; w < 4; ++w)
+        for (int k = 0; k < 4; ++k) blk[1 + 4 * w + k] = (uint8_t)(r0.v[w] >> (8 * k));
+}

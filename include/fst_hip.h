@@ -193,7 +193,9 @@ int fst_synth_q4k_blocks(uint64_t seed, uint64_t id, size_t nblocks, float d_sig
  * experts e_first..e_first+e_count-1 of layer lid (e == n_experts: shared)
  * from generator id id_base + e (= fst_synth_q4k_expert(seed, id_base + e)),
  * and the LM head from generator id `id` (= fst_synth_q4k_blocks(seed, id,
- * vocab*hidden/256)).  Synchronous. */
+ * vocab*hidden/256)).  For an MXFP4 context the experts are those of
+ * fst_synth_mxfp4_expert(seed, id_base + e, ..., e_lo = 108, e_hi = 128)
+ * (d_sigma unused).  Synchronous. */
 int fst_synth_experts_dev(fst_ctx* ctx, uint64_t seed, int lid, int e_first, int e_count, uint64_t id_base,
                           float d_sigma);
 int fst_synth_lm_head_dev(fst_ctx* ctx, uint64_t seed, uint64_t id, float d_sigma);
