@@ -663,26 +663,37 @@ struct Q4kScale {
     float d, dmin;
 };
 
-__device__ __forceinline__ void q4k_scales(const u4v_t hdr, int g, Q4kScale& S) {
+// perm selector placing bytes 2(g&1) and 2(g&1)+1 of a dword into the low
+// byte of each 16-bit half (v_perm_b32: 0..3 pick source bytes, 0x0C gives 0)
+__device__ __forceinline__ uint32_t q4k_scale_sel(int g) {
+    const uint32_t a = 2u * (uint32_t)(g & 1);
+    return 0x0C000C00u | ((a + 1u) << 16) | a;
+}
+
+// The two 6-bit fields of lane group g as an exact fp16 pair: (x & 63) | fp16
+// 1024 (one v_and_or_b32 on the spread bytes), minus 1024 (one v_pk_add_f16).
+__device__ __forceinline__ h2_t q4k_field_pair(uint32_t bytes, uint32_t sel) {
+    const uint32_t spread = __builtin_amdgcn_perm(0u, bytes, sel);
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(spread), "v"(0x003F003Fu), "v"(0x64006400u));
+    return as_h2(r) - h2_t{(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+__device__ __forceinline__ void q4k_scales(const u4v_t hdr, int g, uint32_t sel, Q4kScale& S) {
     S.d = half_bits_to_f32(hdr.x & 0xffffu);
     S.dmin = half_bits_to_f32(hdr.x >> 16);
     const uint32_t y = hdr.y, z = hdr.z, w = hdr.w;
-    // get_scale_min_k4 for all 8 sub-blocks, byte-parallel
-    const uint32_t sc_lo = y & 0x3F3F3F3Fu, m_lo = z & 0x3F3F3F3Fu;
-    const uint32_t sc_hi = (w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u);
-    const uint32_t m_hi = ((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u);
-    const uint32_t SC = g < 2 ? sc_lo : sc_hi;
-    const uint32_t MM = g < 2 ? m_lo : m_hi;
-    const int sh = (g & 1) * 16;
-    const float sca = (float)((SC >> sh) & 0xffu), scb = (float)((SC >> (sh + 8)) & 0xffu);
-    const _Float16 ma = (_Float16)(float)((MM >> sh) & 0xffu);
-    const _Float16 mb = (_Float16)(float)((MM >> (sh + 8)) & 0xffu);
-    const _Float16 fa = (_Float16)sca, na = (_Float16)(-1024.0f * sca);
-    const _Float16 fb = (_Float16)(scb * 0.0625f), nb = (_Float16)(-64.0f * scb);
-    S.SC8 = h8_t{fa, fa, fa, fa, fb, fb, fb, fb};
-    S.NEG8 = h8_t{na, na, na, na, nb, nb, nb, nb};
+    // get_scale_min_k4 byte-parallel: sub-blocks 0..3 in the low 6 bits of
+    // q[0..3] / q[4..7]; 4..7 from q[8..11] nibbles and the top bits of q[0..7]
+    const uint32_t SC = g < 2 ? y : ((w & 0x0F0F0F0Fu) | ((y >> 2) & 0x30303030u));
+    const uint32_t MM = g < 2 ? z : (((w >> 4) & 0x0F0F0F0Fu) | ((z >> 2) & 0x30303030u));
+    const h2_t sc = q4k_field_pair(SC, sel), mm = q4k_field_pair(MM, sel);
+    const h2_t f = sc * h2_t{(_Float16)1.0f, (_Float16)0.0625f};          // sc_a, sc_b/16
+    const h2_t n = sc * h2_t{(_Float16)-1024.0f, (_Float16)-64.0f};       // -1024 sc_a, -64 sc_b
+    S.SC8 = h8_t{f.x, f.x, f.x, f.x, f.y, f.y, f.y, f.y};
+    S.NEG8 = h8_t{n.x, n.x, n.x, n.x, n.y, n.y, n.y, n.y};
     const _Float16 z0 = (_Float16)0.0f;
-    S.m = h8_t{ma, mb, ma, mb, z0, z0, z0, z0};
+    S.m = h8_t{mm.x, mm.y, mm.x, mm.y, z0, z0, z0, z0};
 }
 
 // Exact fp16 sc*q for the 8 weights held in one dword D = [b3 b2 b1 b0] of
@@ -833,6 +844,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
     const f4_t zf = f4_t{0.f, 0.f, 0.f, 0.f};
     const uint32_t magic = 0x64006400u;
+    const uint32_t ssel = q4k_scale_sel(g);
 
     // 16-row tile of the matrix owned by this wave in work item tt; MODE 1
     // pairs gate rows [64T, 64T+64) (waves 0..3) with the same up rows
@@ -982,7 +994,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                 return;
             } else {
             Q4kScale S;
-            q4k_scales(cur.h, g, S);
+            q4k_scales(cur.h, g, ssel, S);
             // each decoded weight operand feeds every live 16-token group
             f4_t D[NGRP];
 #pragma unroll
