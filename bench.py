@@ -81,7 +81,7 @@ def step(fa, ctx, bufs, i):
                                       bufs["tok"]))
 
 
-def cpu_baseline(hs, w, threads, min_seconds=10.0, max_steps=16):
+def cpu_baseline(hs, w, threads, min_seconds=10.0, max_steps=64):
     """CPU oracle on whole verify steps (router + every routed expert touched +
     shared expert + combine, fp64-accumulated, `threads` OpenMP threads), over
     successive hidden batches until at least `min_seconds` of CPU work."""
