@@ -88,6 +88,11 @@ _SIGS = {
     "fst_lm_head_dev": (C.c_int, [P, P, C.c_int, P]),
     "fst_verify_forward_dev": (C.c_int, [P, P, C.c_int, P, P]),
     "fst_verify_forward": (C.c_int, [P, P, C.c_int, P, P]),
+    "fst_upload_hc": (C.c_int, [P, C.c_int, P, P, P]),
+    "fst_upload_hc_head": (C.c_int, [P, P, C.c_float, P]),
+    "fst_hc_pre_dev": (C.c_int, [P, C.c_int, P, C.c_int, P, P, P]),
+    "fst_hc_post_dev": (C.c_int, [P, P, P, P, P, C.c_int]),
+    "fst_hc_head_dev": (C.c_int, [P, P, C.c_int, P]),
     "fst_synth_experts_dev": (C.c_int, [P, U64, C.c_int, C.c_int, C.c_int, U64, C.c_float]),
     "fst_synth_lm_head_dev": (C.c_int, [P, U64, U64, C.c_float]),
     "fst_synth_q4k_blocks": (C.c_int, [U64, U64, SZ, C.c_float, P]),
@@ -320,8 +325,64 @@ class Context:
     def synth_lm_head(self, seed, matrix_id, d_sigma=0.01):
         _check(lib().fst_synth_lm_head_dev(self.h, seed, matrix_id, d_sigma))
 
+    # Hyper-Connections (4 residual streams)
+    def upload_hc(self, lid, fn_bf16, scale, base):
+        """fn: bf16 [24][4*hidden]; scale f32[3]; base f32[24]."""
+        fn = np.ascontiguousarray(fn_bf16, dtype=np.uint16)
+        sc = np.ascontiguousarray(scale, dtype=np.float32)
+        b = np.ascontiguousarray(base, dtype=np.float32)
+        _check(lib().fst_upload_hc(self.h, lid, _ptr(fn), _ptr(sc), _ptr(b)))
+
+    def upload_hc_head(self, fn_bf16, scale, base=None):
+        fn = np.ascontiguousarray(fn_bf16, dtype=np.uint16)
+        b = None if base is None else np.ascontiguousarray(base, dtype=np.float32)
+        _check(lib().fst_upload_hc_head(self.h, _ptr(fn), float(scale), _ptr(b)))
+
+    def hc_pre(self, lid, h_hc):
+        """h_hc [M][4][hidden] bf16 -> (cur [M][hidden] bf16, post [M][4], comb [M][16])."""
+        h_hc = np.ascontiguousarray(h_hc, dtype=np.uint16)
+        M, d = h_hc.shape[0], h_hc.shape[2]
+        dh = self.to_device(h_hc)
+        dc, dp, dm = self.dev_alloc(M * d * 2), self.dev_alloc(M * 16), self.dev_alloc(M * 64)
+        try:
+            _check(lib().fst_hc_pre_dev(self.h, lid, dh, M, dc, dp, dm))
+            self.sync()
+            return (self.to_host(dc, (M, d), np.uint16), self.to_host(dp, (M, 4), np.float32),
+                    self.to_host(dm, (M, 16), np.float32))
+        finally:
+            for p in (dh, dc, dp, dm):
+                self.dev_free(p)
+
+    def hc_post(self, block_out, h_hc, post, comb):
+        """Returns the updated [M][4][hidden] streams."""
+        h_hc = np.ascontiguousarray(h_hc, dtype=np.uint16)
+        M = h_hc.shape[0]
+        ptrs = [self.to_device(np.ascontiguousarray(block_out, dtype=np.uint16)), self.to_device(h_hc),
+                self.to_device(np.ascontiguousarray(post, dtype=np.float32)),
+                self.to_device(np.ascontiguousarray(comb, dtype=np.float32))]
+        try:
+            _check(lib().fst_hc_post_dev(self.h, ptrs[0], ptrs[1], ptrs[2], ptrs[3], M))
+            self.sync()
+            return self.to_host(ptrs[1], h_hc.shape, np.uint16)
+        finally:
+            for p in ptrs:
+                self.dev_free(p)
+
+    def hc_head(self, h_hc):
+        h_hc = np.ascontiguousarray(h_hc, dtype=np.uint16)
+        M, d = h_hc.shape[0], h_hc.shape[2]
+        dh, do = self.to_device(h_hc), self.dev_alloc(M * d * 2)
+        try:
+            _check(lib().fst_hc_head_dev(self.h, dh, M, do))
+            self.sync()
+            return self.to_host(do, (M, d), np.uint16)
+        finally:
+            self.dev_free(dh)
+            self.dev_free(do)
+
     def verify_forward(self, h, input_ids=None):
-        """h: [M][hidden] bf16 (updated copy returned); returns (logits [M][vocab], h_out)."""
+        """h: [M][hidden] bf16, or [M][4][hidden] once HC is uploaded (updated
+        copy returned); returns (logits [M][vocab], h_out)."""
         h = np.array(h, dtype=np.uint16, copy=True, order="C")
         M = h.shape[0]
         logits = np.empty((M, self.cfg.vocab_size), np.float32)

@@ -55,6 +55,18 @@ struct fst_ctx {
     uint8_t* lm_head = nullptr;              // [vocab][hd/256] Q4_K, device layout
     int* lm_tab = nullptr;                   // one-slot table for the dense LM-head call
     uint16_t* mn = nullptr;                  // [T][hd] normed layer input
+    // Hyper-Connections (4-stream residual)
+    uint16_t* hc_fn = nullptr;               // [L][24][4 hd] bf16 (checkpoint layout)
+    float* hc_sb = nullptr;                  // [L][3 + 24] scale, base
+    std::vector<char> has_hc;                // [L]
+    uint16_t* hc_head_fn = nullptr;          // [4][4 hd]
+    float* hc_head_base = nullptr;           // [4]
+    float hc_head_scale = 1.0f;
+    bool has_hc_head = false;
+    uint16_t* hc_cur = nullptr;              // [T][hd]
+    float* hc_post = nullptr;                // [T][4]
+    float* hc_comb = nullptr;                // [T][16]
+    uint16_t* hc_h = nullptr;                // [T][4][hd] host-call staging
     bool nested = false;                     // inside verify_forward: no per-kernel marks
     fst::Scratch s{};
     std::vector<void*> allocs;
@@ -234,6 +246,13 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     x->has_norm.assign(L + 1, 0);
     if ((rc = x->dalloc(&x->lm_tab, fst::META_WORDS + 4))) return bail(rc);
     if ((rc = x->dalloc(&x->mn, (size_t)c.max_tokens * hd))) return bail(rc);
+    if ((rc = x->dalloc(&x->hc_fn, (size_t)L * 24 * 4 * hd)) || (rc = x->dalloc(&x->hc_sb, (size_t)L * 27)) ||
+        (rc = x->dalloc(&x->hc_head_fn, (size_t)4 * 4 * hd)) || (rc = x->dalloc(&x->hc_head_base, 4)) ||
+        (rc = x->dalloc(&x->hc_cur, (size_t)c.max_tokens * hd)) || (rc = x->dalloc(&x->hc_post, (size_t)c.max_tokens * 4)) ||
+        (rc = x->dalloc(&x->hc_comb, (size_t)c.max_tokens * 16)) ||
+        (rc = x->dalloc(&x->hc_h, (size_t)c.max_tokens * 4 * hd)))
+        return bail(rc);
+    x->has_hc.assign(L, 0);
 
     fst::Scratch& s = x->s;
     const int T = c.max_tokens, tk = c.top_k;
@@ -854,6 +873,77 @@ int fst_lm_head_dev(fst_ctx* ctx, const uint16_t* d_h, int M, float* d_logits) {
     return FST_OK;
 }
 
+// HC mode: the FFN control of every layer and the output head are uploaded.
+static bool hc_ready(fst_ctx* ctx) {
+    if (!ctx->has_hc_head) return false;
+    for (int l = 0; l < ctx->cfg.n_layers; ++l)
+        if (!ctx->has_hc[l]) return false;
+    return true;
+}
+
+int fst_upload_hc(fst_ctx* ctx, int lid, const uint16_t* fn, const float* scale, const float* base) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    if (!fn || !scale || !base) return fail(FST_EINVAL, "null HC tensor");
+    if (ctx->cfg.hidden_dim > 8192) return fail(FST_EINVAL, "HC needs hidden_dim <= 8192");
+    const size_t n = (size_t)24 * 4 * ctx->cfg.hidden_dim;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->hc_fn + (size_t)lid * n, fn, n * 2, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipMemcpyAsync(ctx->hc_sb + (size_t)lid * 27, scale, 3 * sizeof(float), hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipMemcpyAsync(ctx->hc_sb + (size_t)lid * 27 + 3, base, 24 * sizeof(float), hipMemcpyHostToDevice,
+                               ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    ctx->has_hc[lid] = 1;
+    return FST_OK;
+}
+
+int fst_upload_hc_head(fst_ctx* ctx, const uint16_t* fn, float scale, const float* base) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!fn) return fail(FST_EINVAL, "null HC head tensor");
+    if (ctx->cfg.hidden_dim > 8192) return fail(FST_EINVAL, "HC needs hidden_dim <= 8192");
+    const size_t n = (size_t)4 * 4 * ctx->cfg.hidden_dim;
+    float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (base) std::memcpy(b, base, sizeof(b));
+    FST_HIP_TRY(hipMemcpyAsync(ctx->hc_head_fn, fn, n * 2, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipMemcpyAsync(ctx->hc_head_base, b, sizeof(b), hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    ctx->hc_head_scale = scale;
+    ctx->has_hc_head = true;
+    return FST_OK;
+}
+
+int fst_hc_pre_dev(fst_ctx* ctx, int lid, const uint16_t* d_h_hc, int M, uint16_t* d_cur, float* d_post,
+                   float* d_comb) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    if (!ctx->has_hc[lid]) return fail(FST_ENOTREADY, "HC tensors of the layer not uploaded");
+    if (!d_h_hc || !d_cur || !d_post || !d_comb) return fail(FST_EINVAL, "null device buffer");
+    if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    const int hd = ctx->cfg.hidden_dim;
+    fst::launch_hc_pre(ctx->st, d_h_hc, ctx->hc_fn + (size_t)lid * 24 * 4 * hd, ctx->hc_sb + (size_t)lid * 27,
+                       ctx->hc_sb + (size_t)lid * 27 + 3, M, hd, d_cur, d_post, d_comb);
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_hc_post_dev(fst_ctx* ctx, const uint16_t* d_block_out, uint16_t* d_h_hc, const float* d_post,
+                    const float* d_comb, int M) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!d_block_out || !d_h_hc || !d_post || !d_comb) return fail(FST_EINVAL, "null device buffer");
+    if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    fst::launch_hc_post(ctx->st, d_block_out, d_h_hc, d_post, d_comb, M, ctx->cfg.hidden_dim);
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_hc_head_dev(fst_ctx* ctx, const uint16_t* d_h_hc, int M, uint16_t* d_plain) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!ctx->has_hc_head) return fail(FST_ENOTREADY, "HC head tensors not uploaded");
+    if (!d_h_hc || !d_plain) return fail(FST_EINVAL, "null device buffer");
+    if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    fst::launch_hc_head(ctx->st, d_h_hc, ctx->hc_head_fn, ctx->hc_head_scale, ctx->hc_head_base, M,
+                        ctx->cfg.hidden_dim, d_plain);
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
 int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_input_ids, float* d_logits) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (!d_h || !d_logits) return fail(FST_EINVAL, "null device buffer");
@@ -862,20 +952,36 @@ int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_
     for (int l = 0; l < c.n_layers; ++l)
         if (!ctx->has_norm[l]) return fail(FST_ENOTREADY, "norm weights of layer " + std::to_string(l) + " not uploaded");
     const int hd = c.hidden_dim;
+    const bool hc = hc_ready(ctx);
     ctx->mark_begin();
     ctx->nested = true;
     int rc = FST_OK;
     for (int l = 0; l < c.n_layers && rc == FST_OK; ++l) {
-        // h += y (previous layer), mn = RMSNorm_l(h); y = MoE_l(mn)
-        fst::launch_resid_norm(ctx->st, d_h, l > 0 ? ctx->s.out : nullptr, ctx->norms + (size_t)l * hd, M, hd,
-                               kNormEps, l > 0 ? d_h : nullptr, ctx->mn, nullptr, nullptr);
+        if (hc) {
+            // cur = hc_pre(h); mn = RMSNorm_l(cur); y = MoE_l(mn); h = hc_post(y, h)
+            fst::launch_hc_pre(ctx->st, d_h, ctx->hc_fn + (size_t)l * 24 * 4 * hd, ctx->hc_sb + (size_t)l * 27,
+                               ctx->hc_sb + (size_t)l * 27 + 3, M, hd, ctx->hc_cur, ctx->hc_post, ctx->hc_comb);
+            fst::launch_resid_norm(ctx->st, ctx->hc_cur, nullptr, ctx->norms + (size_t)l * hd, M, hd, kNormEps,
+                                   nullptr, ctx->mn, nullptr, nullptr);
+        } else {
+            // h += y (previous layer), mn = RMSNorm_l(h); y = MoE_l(mn)
+            fst::launch_resid_norm(ctx->st, d_h, l > 0 ? ctx->s.out : nullptr, ctx->norms + (size_t)l * hd, M, hd,
+                                   kNormEps, l > 0 ? d_h : nullptr, ctx->mn, nullptr, nullptr);
+        }
         rc = run_moe(ctx, l, ctx->mn, M, d_input_ids, 1, ctx->s.eids, ctx->s.wts, c.top_k, 1, c.has_shared,
                      ctx->s.out, nullptr, nullptr);
+        if (hc && rc == FST_OK) fst::launch_hc_post(ctx->st, ctx->s.out, d_h, ctx->hc_post, ctx->hc_comb, M, hd);
     }
     ctx->nested = false;
     if (rc) return rc;
     ctx->mark("layers", true);
-    if ((rc = final_head(ctx, d_h, ctx->s.out, M, d_logits))) return rc;
+    if (hc) {
+        fst::launch_hc_head(ctx->st, d_h, ctx->hc_head_fn, ctx->hc_head_scale, ctx->hc_head_base, M, hd, ctx->hc_cur);
+        rc = final_head(ctx, ctx->hc_cur, nullptr, M, d_logits);
+    } else {
+        rc = final_head(ctx, d_h, ctx->s.out, M, d_logits);
+    }
+    if (rc) return rc;
     ctx->mark("lm_head", true);
     return FST_OK;
 }
@@ -886,20 +992,23 @@ int fst_verify_forward(fst_ctx* ctx, uint16_t* h, int M, const int32_t* input_id
     const fst_config& c = ctx->cfg;
     if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
     const int hd = c.hidden_dim;
+    const bool hc = hc_ready(ctx);
+    const size_t hbytes = (size_t)M * (hc ? 4 : 1) * hd * 2;
+    uint16_t* d_res = hc ? ctx->hc_h : ctx->s.h;
     const size_t nlog = (size_t)M * c.vocab_size;
     float* d_logits = nullptr;
     FST_HIP_TRY(hipMalloc(&d_logits, nlog * sizeof(float)));
     int rc = FST_OK;
     do {
-        if (hipMemcpyAsync(ctx->s.h, h, (size_t)M * hd * 2, hipMemcpyHostToDevice, ctx->st) != hipSuccess ||
+        if (hipMemcpyAsync(d_res, h, hbytes, hipMemcpyHostToDevice, ctx->st) != hipSuccess ||
             (input_ids &&
              hipMemcpyAsync(ctx->s.ids, input_ids, M * 4, hipMemcpyHostToDevice, ctx->st) != hipSuccess)) {
             rc = fail(FST_EHIP, "host-to-device copy failed");
             break;
         }
-        if ((rc = fst_verify_forward_dev(ctx, ctx->s.h, M, input_ids ? ctx->s.ids : nullptr, d_logits))) break;
+        if ((rc = fst_verify_forward_dev(ctx, d_res, M, input_ids ? ctx->s.ids : nullptr, d_logits))) break;
         if (hipMemcpyAsync(logits, d_logits, nlog * sizeof(float), hipMemcpyDeviceToHost, ctx->st) != hipSuccess ||
-            hipMemcpyAsync(h, ctx->s.h, (size_t)M * hd * 2, hipMemcpyDeviceToHost, ctx->st) != hipSuccess) {
+            hipMemcpyAsync(h, d_res, hbytes, hipMemcpyDeviceToHost, ctx->st) != hipSuccess) {
             rc = fail(FST_EHIP, "device-to-host copy failed");
             break;
         }

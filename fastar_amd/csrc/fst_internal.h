@@ -129,6 +129,13 @@ void launch_resid_norm(hipStream_t st, const uint16_t* h, const uint16_t* y, con
 // logits[M][N] = x . W^T for one resident Q4_K matrix W (device layout).
 void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, const Scratch& s, int* slot_tab,
                       float* out);
+// Hyper-Connections (4 residual streams of width d; see fst_hc.hip).
+void launch_hc_pre(hipStream_t st, const uint16_t* h_hc, const uint16_t* fnT, const float* scale, const float* base,
+                   int M, int d, uint16_t* cur, float* post, float* comb);
+void launch_hc_post(hipStream_t st, const uint16_t* bo, uint16_t* h_hc, const float* post, const float* comb, int M,
+                    int d);
+void launch_hc_head(hipStream_t st, const uint16_t* h_hc, const uint16_t* fnT, float scale, const float* base, int M,
+                    int d, uint16_t* plain);
 // h rows -> the down projection's operand (one workgroup per pair).
 void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
                      uint4* sxp, int* xs);

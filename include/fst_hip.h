@@ -181,6 +181,25 @@ int fst_lm_head_dev(fst_ctx* ctx, const uint16_t* d_h, int M, float* d_logits);
 int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_input_ids, float* d_logits);
 int fst_verify_forward(fst_ctx* ctx, uint16_t* h, int M, const int32_t* input_ids, float* logits);
 
+/* ---- Hyper-Connections: 4 residual streams of width hidden_dim ----
+ * hc_pre / hc_post / output_hc_head (src/fst_engine.cpp:2286-2459) with the
+ * control matvec of npu_gemm_hc (:694-742); fixed orders as in fst_hc.hip.
+ * fn is the checkpoint's bf16 [24][4*hidden] (TID_HC_FFN_FN) with scale f32[3]
+ * and base f32[24]; the head fn is bf16 [4][4*hidden] (TID_HC_HEAD_FN), scale
+ * and base f32[4] (nullable: zeros).  When every layer's HC and the head are
+ * uploaded, fst_verify_forward[_dev] runs in HC mode: h is [M][4][hidden],
+ * each layer is h = hc_post(MoE(RMSNorm(hc_pre(h))), h), and the head input
+ * is output_hc_head(h). */
+int fst_upload_hc(fst_ctx* ctx, int lid, const uint16_t* fn, const float* scale, const float* base);
+int fst_upload_hc_head(fst_ctx* ctx, const uint16_t* fn, float scale, const float* base);
+/* d_cur [M][hidden] bf16, d_post [M][4], d_comb [M][16] (comb[dst + 4*src]). */
+int fst_hc_pre_dev(fst_ctx* ctx, int lid, const uint16_t* d_h_hc, int M, uint16_t* d_cur, float* d_post,
+                   float* d_comb);
+/* In place on d_h_hc [M][4][hidden]. */
+int fst_hc_post_dev(fst_ctx* ctx, const uint16_t* d_block_out, uint16_t* d_h_hc, const float* d_post,
+                    const float* d_comb, int M);
+int fst_hc_head_dev(fst_ctx* ctx, const uint16_t* d_h_hc, int M, uint16_t* d_plain);
+
 /* ---- synthetic inputs (deterministic from a seed) ---- */
 /* One Q4_K expert (gate|up|down in the packed ABI layout): uniform nibbles and
  * 6-bit scales/mins, d,dmin = fp16(|z|*sigma) with z ~ N(0,1) (Irwin-Hall). */

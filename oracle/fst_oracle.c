@@ -489,3 +489,173 @@ int fo_q4k_linear(const uint8_t* blocks, int N, int K, const uint16_t* x, int M,
     free(xf);
     return 0;
 }
+
+/* ------------------------------------------------- Hyper-Connections (HC) */
+
+/* src/fst_engine.cpp:2286-2459 (hc_split_sinkhorn, hc_rmsnorm_no_weight,
+ * hc_pre, hc_post, output_hc_head) and :694-742 (npu_gemm_hc) for N = 4
+ * streams of width d, with fixed orders where the reference leaves them to
+ * the NPU or to libm:
+ *  - sum of squares over the 4d values: double, 64 partials over contiguous
+ *    chunks, then p[j] += p[j+off] (off = 32..1); inv = 1/sqrtf((float)(ss/n) + eps);
+ *  - the control matvec mix[n] = flat . fn[n]: per 1024-wide K chunk, 16
+ *    partials of 64 consecutive products (sequential fmaf), a halving tree,
+ *    the chunk sum rounded to bf16 (the NPU tile output), chunk sums added
+ *    in order in float, the total rounded to bf16;
+ *  - exp is fst_expf; bf16 rounding is RNE; no contraction. */
+static float fo_hc_inv_rms(const float* v, int n, float eps) {
+    const int C = n / 64;
+    double p[64];
+    for (int j = 0; j < 64; ++j) {
+        double a = 0.0;
+        for (int i = 0; i < C; ++i) {
+            const double x = (double)v[j * C + i];
+            a = a + x * x;
+        }
+        p[j] = a;
+    }
+    for (int off = 32; off >= 1; off >>= 1)
+        for (int j = 0; j < off; ++j) p[j] = p[j] + p[j + off];
+    return 1.0f / sqrtf((float)(p[0] / (double)n) + eps);
+}
+
+void fo_hc_mix(const uint16_t* flat_bf, const uint16_t* fnT, int K, int nout, float* mix) {
+    for (int n = 0; n < nout; ++n) {
+        const uint16_t* w = fnT + (size_t)n * K;
+        float acc = 0.0f;
+        for (int c0 = 0; c0 < K; c0 += 1024) {
+            float p[16];
+            for (int l = 0; l < 16; ++l) {
+                float a = 0.0f;
+                for (int i = 0; i < 64; ++i) {
+                    const int k = c0 + l * 64 + i;
+                    a = fmaf(fst_bf16_to_f32(flat_bf[k]), fst_bf16_to_f32(w[k]), a);
+                }
+                p[l] = a;
+            }
+            for (int off = 8; off >= 1; off >>= 1)
+                for (int l = 0; l < off; ++l) p[l] = p[l] + p[l + off];
+            acc = acc + fst_bf16_to_f32(fst_f32_to_bf16(p[0]));
+        }
+        mix[n] = fst_bf16_to_f32(fst_f32_to_bf16(acc));
+    }
+}
+
+void fo_hc_split(const float* mix, const float* scale, const float* base, int n, int iters, float eps,
+                 float* split) {
+    const float pre_scale = scale[0], post_scale = scale[1], comb_scale = scale[2];
+    for (int i = 0; i < n; ++i) {
+        const float z = mix[i] * pre_scale + base[i];
+        split[i] = 1.0f / (1.0f + fst_expf(-z)) + eps;
+    }
+    for (int i = 0; i < n; ++i) {
+        const int off = n + i;
+        const float z = mix[off] * post_scale + base[off];
+        split[off] = 2.0f / (1.0f + fst_expf(-z));
+    }
+    float c[16];
+    for (int dst = 0; dst < n; ++dst) {
+        float row_max = -1e30f;
+        for (int src = 0; src < n; ++src) {
+            const int idx = src + dst * n;
+            const float v = mix[2 * n + idx] * comb_scale + base[2 * n + idx];
+            c[idx] = v;
+            if (v > row_max) row_max = v;
+        }
+        float row_sum = 0.0f;
+        for (int src = 0; src < n; ++src) {
+            const int idx = src + dst * n;
+            c[idx] = fst_expf(c[idx] - row_max);
+            row_sum += c[idx];
+        }
+        const float inv = 1.0f / row_sum;
+        for (int src = 0; src < n; ++src) c[src + dst * n] = c[src + dst * n] * inv + eps;
+    }
+    for (int src = 0; src < n; ++src) {
+        float sum = 0.0f;
+        for (int dst = 0; dst < n; ++dst) sum += c[src + dst * n];
+        const float inv = 1.0f / (sum + eps);
+        for (int dst = 0; dst < n; ++dst) c[src + dst * n] *= inv;
+    }
+    for (int it = 1; it < iters; ++it) {
+        for (int dst = 0; dst < n; ++dst) {
+            float sum = 0.0f;
+            for (int src = 0; src < n; ++src) sum += c[src + dst * n];
+            const float inv = 1.0f / (sum + eps);
+            for (int src = 0; src < n; ++src) c[src + dst * n] *= inv;
+        }
+        for (int src = 0; src < n; ++src) {
+            float sum = 0.0f;
+            for (int dst = 0; dst < n; ++dst) sum += c[src + dst * n];
+            const float inv = 1.0f / (sum + eps);
+            for (int dst = 0; dst < n; ++dst) c[src + dst * n] *= inv;
+        }
+    }
+    for (int i = 0; i < n * n; ++i) split[2 * n + i] = c[i];
+}
+
+static void fo_hc_flat(const uint16_t* r, int n, float eps, uint16_t* flat_bf) {
+    float* v = (float*)malloc(sizeof(float) * (size_t)n);
+    if (!v) return;
+    for (int i = 0; i < n; ++i) v[i] = fst_bf16_to_f32(r[i]);
+    const float inv = fo_hc_inv_rms(v, n, eps);
+    for (int i = 0; i < n; ++i) flat_bf[i] = fst_f32_to_bf16(v[i] * inv);
+    free(v);
+}
+
+void fo_hc_pre(const uint16_t* h_hc, const uint16_t* fnT, const float* scale, const float* base, int M, int d,
+               int iters, float eps, uint16_t* cur, float* post, float* comb) {
+    const int N = 4, K = N * d, NM = 2 * N + N * N;
+    uint16_t* flat = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)K);
+    for (int m = 0; m < M; ++m) {
+        const uint16_t* r = h_hc + (size_t)m * K;
+        fo_hc_flat(r, K, eps, flat);
+        float mix[24], split[24];
+        fo_hc_mix(flat, fnT, K, NM, mix);
+        fo_hc_split(mix, scale, base, N, iters, eps, split);
+        for (int i = 0; i < N; ++i) post[(size_t)m * N + i] = split[N + i];
+        for (int i = 0; i < N * N; ++i) comb[(size_t)m * N * N + i] = split[2 * N + i];
+        for (int j = 0; j < d; ++j) {
+            float acc = 0.0f;
+            for (int h = 0; h < N; ++h) acc = acc + split[h] * fst_bf16_to_f32(r[(size_t)h * d + j]);
+            cur[(size_t)m * d + j] = fst_f32_to_bf16(acc);
+        }
+    }
+    free(flat);
+}
+
+void fo_hc_post(const uint16_t* bo, const uint16_t* h_hc, const float* post, const float* comb, int M, int d,
+                uint16_t* out_hc) {
+    const int N = 4;
+    for (int m = 0; m < M; ++m)
+        for (int dst = 0; dst < N; ++dst)
+            for (int j = 0; j < d; ++j) {
+                float acc = fst_bf16_to_f32(bo[(size_t)m * d + j]) * post[(size_t)m * N + dst];
+                for (int src = 0; src < N; ++src)
+                    acc = acc + comb[(size_t)m * N * N + dst + src * N] *
+                                    fst_bf16_to_f32(h_hc[(size_t)m * N * d + (size_t)src * d + j]);
+                out_hc[(size_t)m * N * d + (size_t)dst * d + j] = fst_f32_to_bf16(acc);
+            }
+}
+
+void fo_hc_head(const uint16_t* h_hc, const uint16_t* fnT, float scale, const float* base, int M, int d, float eps,
+                uint16_t* plain) {
+    const int N = 4, K = N * d;
+    uint16_t* flat = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)K);
+    for (int m = 0; m < M; ++m) {
+        const uint16_t* r = h_hc + (size_t)m * K;
+        fo_hc_flat(r, K, eps, flat);
+        float mix[4], w[4];
+        fo_hc_mix(flat, fnT, K, N, mix);
+        for (int h = 0; h < N; ++h) {
+            const float z = mix[h] * scale + (base ? base[h] : 0.0f);
+            w[h] = 1.0f / (1.0f + fst_expf(-z)) + eps;
+        }
+        for (int j = 0; j < d; ++j) {
+            float acc = 0.0f;
+            for (int h = 0; h < N; ++h) acc = acc + w[h] * fst_bf16_to_f32(r[(size_t)h * d + j]);
+            plain[(size_t)m * d + j] = fst_f32_to_bf16(acc);
+        }
+    }
+    free(flat);
+}

@@ -59,6 +59,19 @@ void fo_rmsnorm(const float* x, const uint16_t* w, int M, int d, float eps, uint
 /* Dense Q4_K linear (LM head): y[M][N] = x[M][K] . W^T, W = blocks [N][K/256]. */
 int fo_q4k_linear(const uint8_t* blocks, int N, int K, const uint16_t* x, int M, float* y);
 
+/* Hyper-Connections with 4 streams of width d (residual h_hc [M][4][d] bf16).
+ * fnT: the control matrices transposed to [outputs][4d] bf16 (24 outputs for
+ * pre/post/comb, 4 for the head).  iters = Sinkhorn iterations (20), eps 1e-6. */
+void fo_hc_mix(const uint16_t* flat_bf, const uint16_t* fnT, int K, int nout, float* mix);
+void fo_hc_split(const float* mix, const float* scale, const float* base, int n, int iters, float eps,
+                 float* split);
+void fo_hc_pre(const uint16_t* h_hc, const uint16_t* fnT, const float* scale, const float* base, int M, int d,
+               int iters, float eps, uint16_t* cur, float* post, float* comb);
+void fo_hc_post(const uint16_t* bo, const uint16_t* h_hc, const float* post, const float* comb, int M, int d,
+                uint16_t* out_hc);
+void fo_hc_head(const uint16_t* h_hc, const uint16_t* fnT, float scale, const float* base, int M, int d, float eps,
+                uint16_t* plain);
+
 /* exact-math passthroughs for pinning tests */
 float fo_expf(float x);
 float fo_logf(float x);

@@ -45,6 +45,11 @@ def lib():
         "fo_accept_stochastic": (C.c_int, [P, P, C.c_int, C.c_int, P, C.c_float, C.c_uint64, C.c_uint64, P, P]),
         "fo_rmsnorm": (None, [P, P, C.c_int, C.c_int, C.c_float, P]),
         "fo_q4k_linear": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, P]),
+        "fo_hc_mix": (None, [P, P, C.c_int, C.c_int, P]),
+        "fo_hc_split": (None, [P, P, P, C.c_int, C.c_int, C.c_float, P]),
+        "fo_hc_pre": (None, [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_float, P, P, P]),
+        "fo_hc_post": (None, [P, P, P, P, C.c_int, C.c_int, P]),
+        "fo_hc_head": (None, [P, P, C.c_float, P, C.c_int, C.c_int, C.c_float, P]),
         "fo_expf": (C.c_float, [C.c_float]),
         "fo_logf": (C.c_float, [C.c_float]),
         "fo_sigmoidf": (C.c_float, [C.c_float]),
@@ -196,6 +201,54 @@ def resid_norm(h, y, w, eps=1e-6):
     if y is not None:
         x = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(np.ascontiguousarray(y, np.uint16))).reshape(x.shape)
     return x, rmsnorm(bf16_to_f32(x).reshape(x.shape), w, eps)
+
+
+HC_ITERS, HC_EPS = 20, 1e-6
+
+
+def hc_mix(flat_bf, fnT):
+    fnT = np.ascontiguousarray(fnT, np.uint16)
+    nout, K = fnT.shape
+    mix = np.empty(nout, np.float32)
+    lib().fo_hc_mix(_p(np.ascontiguousarray(flat_bf, np.uint16)), _p(fnT), K, nout, _p(mix))
+    return mix
+
+
+def hc_split(mix, scale, base, n=4, iters=HC_ITERS, eps=HC_EPS):
+    out = np.empty(2 * n + n * n, np.float32)
+    lib().fo_hc_split(_p(np.ascontiguousarray(mix, np.float32)), _p(np.ascontiguousarray(scale, np.float32)),
+                      _p(np.ascontiguousarray(base, np.float32)), n, iters, eps, _p(out))
+    return out
+
+
+def hc_pre(h_hc, fnT, scale, base, iters=HC_ITERS, eps=HC_EPS):
+    """h_hc [M][4][d] bf16, fnT [24][4d] bf16 -> (cur [M][d] bf16, post [M][4], comb [M][16])."""
+    h_hc = np.ascontiguousarray(h_hc, np.uint16)
+    M, _, d = h_hc.shape
+    cur = np.empty((M, d), np.uint16)
+    post = np.empty((M, 4), np.float32)
+    comb = np.empty((M, 16), np.float32)
+    lib().fo_hc_pre(_p(h_hc), _p(np.ascontiguousarray(fnT, np.uint16)), _p(np.ascontiguousarray(scale, np.float32)),
+                    _p(np.ascontiguousarray(base, np.float32)), M, d, iters, eps, _p(cur), _p(post), _p(comb))
+    return cur, post, comb
+
+
+def hc_post(bo, h_hc, post, comb):
+    h_hc = np.ascontiguousarray(h_hc, np.uint16)
+    M, _, d = h_hc.shape
+    out = np.empty_like(h_hc)
+    lib().fo_hc_post(_p(np.ascontiguousarray(bo, np.uint16)), _p(h_hc), _p(np.ascontiguousarray(post, np.float32)),
+                     _p(np.ascontiguousarray(comb, np.float32)), M, d, _p(out))
+    return out
+
+
+def hc_head(h_hc, fnT, scale, base, eps=HC_EPS):
+    h_hc = np.ascontiguousarray(h_hc, np.uint16)
+    M, _, d = h_hc.shape
+    out = np.empty((M, d), np.uint16)
+    b = None if base is None else np.ascontiguousarray(base, np.float32)
+    lib().fo_hc_head(_p(h_hc), _p(np.ascontiguousarray(fnT, np.uint16)), float(scale), _p(b), M, d, eps, _p(out))
+    return out
 
 
 def philox(ctr, key):
