@@ -111,3 +111,37 @@ def test_hc_head_uniform_weights(oracle):
     for k in range(4):
         acc = acc + w * bf16_to_f32(h[:, k])
     assert np.array_equal(out, f32_to_bf16(acc).reshape(M, d))
+
+
+def test_hc_post_vs_float64_detects_transposed_comb(oracle):
+    """out[dst] = bo post[dst] + sum_src comb[dst + 4 src] r[src]
+    (src/fst_engine.cpp:2394-2414); using comb transposed must not match."""
+    rng = np.random.default_rng(26)
+    d, M = 1024, 3
+    h = _bf16(rng, (M, 4, d))
+    bo = _bf16(rng, (M, d))
+    post = rng.uniform(0, 2, (M, 4)).astype(np.float32)
+    comb = rng.uniform(0, 1, (M, 16)).astype(np.float32)
+    out = bf16_to_f32(oracle.hc_post(bo, h, post, comb)).reshape(M, 4, d).astype(np.float64)
+    r = bf16_to_f32(h).reshape(M, 4, d).astype(np.float64)
+    b = bf16_to_f32(bo).reshape(M, d).astype(np.float64)
+    c = comb.reshape(M, 4, 4).astype(np.float64)  # [m][src][dst]
+    ref = b[:, None, :] * post[:, :, None] + np.einsum("msd,msj->mdj", c, r)
+    assert rel_l2(out, ref) < 5e-3
+    bad = b[:, None, :] * post[:, :, None] + np.einsum("mds,msj->mdj", c, r)
+    assert rel_l2(out, bad) > 0.1
+
+
+def test_hc_head_vs_float64(oracle):
+    rng = np.random.default_rng(27)
+    d, M = 4096, 2
+    h = _bf16(rng, (M, 4, d))
+    fnT = _bf16(rng, (4, 4 * d), 0.0, 0.02)
+    base = rng.normal(0, 1, 4).astype(np.float32)
+    out = bf16_to_f32(oracle.hc_head(h, fnT, 0.7, base)).reshape(M, d)
+    for m in range(M):
+        r = bf16_to_f32(h[m]).astype(np.float64)
+        flat = r.ravel() / np.sqrt((r.ravel() ** 2).mean() + 1e-6)
+        z = bf16_to_f32(fnT).astype(np.float64) @ flat * 0.7 + base
+        w = 1.0 / (1.0 + np.exp(-z)) + 1e-6
+        assert rel_l2(out[m], (w[:, None] * r).sum(0)) < 2e-2
