@@ -88,6 +88,8 @@ _SIGS = {
     "fst_lm_head_dev": (C.c_int, [P, P, C.c_int, P]),
     "fst_verify_forward_dev": (C.c_int, [P, P, C.c_int, P, P]),
     "fst_verify_forward": (C.c_int, [P, P, C.c_int, P, P]),
+    "fst_upload_shared_bf16": (C.c_int, [P, C.c_int, P, P, P]),
+    "fst_upload_lm_head_bf16": (C.c_int, [P, P]),
     "fst_upload_hc": (C.c_int, [P, C.c_int, P, P, P]),
     "fst_upload_hc_head": (C.c_int, [P, P, C.c_float, P]),
     "fst_hc_pre_dev": (C.c_int, [P, C.c_int, P, C.c_int, P, P, P]),
@@ -324,6 +326,15 @@ class Context:
 
     def synth_lm_head(self, seed, matrix_id, d_sigma=0.01):
         _check(lib().fst_synth_lm_head_dev(self.h, seed, matrix_id, d_sigma))
+
+    def upload_shared_bf16(self, lid, gate, up, down):
+        """bf16 shared expert: gate, up [inter][hidden], down [hidden][inter]."""
+        g, u, d = (np.ascontiguousarray(t, dtype=np.uint16) for t in (gate, up, down))
+        _check(lib().fst_upload_shared_bf16(self.h, lid, _ptr(g), _ptr(u), _ptr(d)))
+
+    def upload_lm_head_bf16(self, w):
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        _check(lib().fst_upload_lm_head_bf16(self.h, _ptr(w)))
 
     # Hyper-Connections (4 residual streams)
     def upload_hc(self, lid, fn_bf16, scale, base):

@@ -53,6 +53,9 @@ struct fst_ctx {
     uint16_t* norms = nullptr;               // [L+1][hd] bf16 (moe norms, then the final norm)
     std::vector<char> has_norm;              // [L+1]
     uint8_t* lm_head = nullptr;              // [vocab][hd/256] Q4_K, device layout
+    uint16_t* lm_head16 = nullptr;           // [vocab][hd] bf16 (checkpoint layout)
+    int lm_kind = 0;                         // LM head in use: 0 none, 1 Q4_K, 2 bf16
+    std::vector<uint16_t*> shared16;         // [L] bf16 shared expert: gate [inter][hd], up, down [hd][inter]
     int* lm_tab = nullptr;                   // one-slot table for the dense LM-head call
     uint16_t* mn = nullptr;                  // [T][hd] normed layer input
     // Hyper-Connections (4-stream residual)
@@ -92,6 +95,9 @@ struct fst_ctx {
         for (int32_t* p : hash)
             if (p) hipFree(p);
         if (lm_head) hipFree(lm_head);
+        if (lm_head16) hipFree(lm_head16);
+        for (uint16_t* p : shared16)
+            if (p) hipFree(p);
         if (acc_ws) hipFree(acc_ws);
         if (acc_logits) hipFree(acc_logits);
         if (acc_io) hipFree(acc_io);
@@ -253,6 +259,7 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&x->hc_h, (size_t)c.max_tokens * 4 * hd)))
         return bail(rc);
     x->has_hc.assign(L, 0);
+    x->shared16.assign(L, nullptr);
 
     fst::Scratch& s = x->s;
     const int T = c.max_tokens, tk = c.top_k;
@@ -273,7 +280,8 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.act, (size_t)P * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
         (rc = x->dalloc(&s.y, (size_t)P * hd)) || (rc = x->dalloc(&s.tok_npairs, T)) ||
-        (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 16))))
+        (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 16))) ||
+        (rc = x->dalloc(&s.sh_h16, (size_t)T * c.inter_dim)) || (rc = x->dalloc(&s.ys, (size_t)T * hd)))
         return bail(rc);
     if (hipMemsetAsync(s.tile_done, 0, sizeof(int) * T * (hd / 16), x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(counters) failed"));
@@ -459,7 +467,8 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     if (use_shared && !c.has_shared) return fail(FST_EINVAL, "config has no shared expert");
     if (use_routed && ctx->n_uploaded[lid] - (ctx->uploaded[lid][c.n_experts] ? 1 : 0) < c.n_experts)
         return fail(FST_ENOTREADY, "not all routed experts of layer " + std::to_string(lid) + " are uploaded");
-    if (use_shared && !ctx->uploaded[lid][c.n_experts])
+    const bool sh16 = use_shared && ctx->shared16[lid];  // bf16 shared expert: its own launches
+    if (use_shared && !sh16 && !ctx->uploaded[lid][c.n_experts])
         return fail(FST_ENOTREADY, "shared expert of layer " + std::to_string(lid) + " is not uploaded");
     if (do_router && !ctx->has_router[lid])
         return fail(FST_ENOTREADY, "router of layer " + std::to_string(lid) + " is not uploaded");
@@ -478,8 +487,23 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
             fst::launch_router_prep(st, g, L, d_h, M, ctx->s.logits, ctx->s);
         ctx->mark("router_prep");
     }
-    fst::launch_route_bucket(st, g, L, M, ctx->s.logits, d_ids, use_hash, do_router, use_shared, d_eids, d_wts,
-                             ctx->s);
+    if (sh16) {
+        // process_shared_expert (src/fst_engine.cpp:4373-4489) over bf16 weights; its fp32
+        // output joins the combine of the routed down projection (or is the result)
+        const int hd = c.hidden_dim, inter = c.inter_dim;
+        const uint16_t* W = ctx->shared16[lid];
+        fst::launch_bf16_gate_up(st, W, hd, inter, d_h, M, c.swiglu_limit, ctx->s.sh_h16);
+        fst::launch_bf16_linear(st, W + (size_t)2 * inter * hd, inter, hd, ctx->s.sh_h16, M,
+                                use_routed ? ctx->s.ys : nullptr, use_routed ? nullptr : d_out,
+                                use_routed ? nullptr : d_out_shared);
+        ctx->mark("shared_bf16");
+        if (!use_routed) {
+            FST_HIP_TRY(hipGetLastError());
+            return FST_OK;
+        }
+    }
+    fst::launch_route_bucket(st, g, L, M, ctx->s.logits, d_ids, use_hash, do_router, use_shared && !sh16, d_eids,
+                             d_wts, ctx->s);
     ctx->mark("route_bucket");
     if (!do_router && !mx) {
         fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
@@ -492,7 +516,8 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
                              ctx->s.sx2p, ctx->s.xs2);
         ctx->mark("prep_h");
     }
-    fst::launch_q4k_down(st, g, L, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared);
+    fst::launch_q4k_down(st, g, L, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared,
+                         sh16 ? ctx->s.ys : nullptr);
     ctx->mark("q4k_down");
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;
@@ -787,6 +812,43 @@ int fst_upload_lm_head(fst_ctx* ctx, const void* packed, size_t bytes) {
                            ctx->cfg.hidden_dim);
     FST_HIP_TRY(hipMemcpyAsync(ctx->lm_head, tiled.data(), bytes, hipMemcpyHostToDevice, ctx->st));
     FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    ctx->lm_kind = 1;
+    return FST_OK;
+}
+
+int fst_upload_lm_head_bf16(fst_ctx* ctx, const uint16_t* w) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!w) return fail(FST_EINVAL, "null LM head");
+    const fst_config& c = ctx->cfg;
+    if (c.vocab_size % 128) return fail(FST_EINVAL, "vocab_size must be a multiple of 128 for the LM head");
+    const size_t bytes = (size_t)c.vocab_size * c.hidden_dim * 2;
+    if (!ctx->lm_head16) {
+        void* p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) return fail(FST_ENOMEM, "hipMalloc(lm_head bf16) failed");
+        ctx->lm_head16 = static_cast<uint16_t*>(p);
+    }
+    FST_HIP_TRY(hipMemcpyAsync(ctx->lm_head16, w, bytes, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    ctx->lm_kind = 2;
+    return FST_OK;
+}
+
+int fst_upload_shared_bf16(fst_ctx* ctx, int lid, const uint16_t* gate, const uint16_t* up, const uint16_t* down) {
+    if (int rc = check_lid(ctx, lid)) return rc;
+    const fst_config& c = ctx->cfg;
+    if (!c.has_shared) return fail(FST_EINVAL, "config has no shared expert");
+    if (!gate || !up || !down) return fail(FST_EINVAL, "null shared-expert matrix");
+    const size_t n = (size_t)c.inter_dim * c.hidden_dim;
+    if (!ctx->shared16[lid]) {
+        void* p = nullptr;
+        if (hipMalloc(&p, 3 * n * 2) != hipSuccess) return fail(FST_ENOMEM, "hipMalloc(shared expert bf16) failed");
+        ctx->shared16[lid] = static_cast<uint16_t*>(p);
+    }
+    uint16_t* d = ctx->shared16[lid];
+    FST_HIP_TRY(hipMemcpyAsync(d, gate, n * 2, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipMemcpyAsync(d + n, up, n * 2, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipMemcpyAsync(d + 2 * n, down, n * 2, hipMemcpyHostToDevice, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
     return FST_OK;
 }
 
@@ -853,9 +915,17 @@ int fst_rmsnorm_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, const uint16_t* 
 // final norm (optionally after adding d_y to the residual d_h) + LM head
 static int final_head(fst_ctx* ctx, uint16_t* d_h, const uint16_t* d_y, int M, float* d_logits) {
     const fst_config& c = ctx->cfg;
-    if (!ctx->lm_head) return fail(FST_ENOTREADY, "LM head not uploaded");
+    if (!ctx->lm_kind) return fail(FST_ENOTREADY, "LM head not uploaded");
     if (!ctx->has_norm[c.n_layers]) return fail(FST_ENOTREADY, "final norm weights not uploaded");
     const int hd = c.hidden_dim;
+    if (ctx->lm_kind == 2) {
+        // bf16 head as the reference keeps it: normed rows in bf16, then Y = W x
+        fst::launch_resid_norm(ctx->st, d_h, d_y, ctx->norms + (size_t)c.n_layers * hd, M, hd, kNormEps,
+                               d_y ? d_h : nullptr, ctx->mn, nullptr, nullptr);
+        fst::launch_bf16_linear(ctx->st, ctx->lm_head16, hd, c.vocab_size, ctx->mn, M, d_logits, nullptr, nullptr);
+        FST_HIP_TRY(hipGetLastError());
+        return FST_OK;
+    }
     fst::launch_resid_norm(ctx->st, d_h, d_y, ctx->norms + (size_t)c.n_layers * hd, M, hd, kNormEps,
                            d_y ? d_h : nullptr, nullptr, &ctx->s, ctx->lm_tab);
     fst::launch_q4k_dense(ctx->st, ctx->lm_head, M, hd, c.vocab_size, ctx->s, ctx->lm_tab, d_logits);

@@ -56,6 +56,8 @@ struct Scratch {
     int* xs2;              // [P]
     float* y;              // [P][hd]
     int* tok_npairs;       // [T] distinct (token, expert) pairs of each token incl. shared
+    uint16_t* sh_h16;      // [T][inter] bf16 shared-expert h (bf16 shared expert)
+    float* ys;             // [T][hd] fp32 shared-expert output (bf16 shared expert)
     int* tile_done;        // [T][hd/16] (used: hd / rows per item) down contributions finished per token row tile (re-armed)
 };
 
@@ -129,6 +131,12 @@ void launch_resid_norm(hipStream_t st, const uint16_t* h, const uint16_t* y, con
 // logits[M][N] = x . W^T for one resident Q4_K matrix W (device layout).
 void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, const Scratch& s, int* slot_tab,
                       float* out);
+// Linear layers over plain bf16 [N][K] weights (fst_dense.hip).
+int bf16_linear_rows_per_wg(int K, int gate_up);
+void launch_bf16_linear(hipStream_t st, const uint16_t* W, int K, int N, const uint16_t* x, int M, float* y32,
+                        uint16_t* y16a, uint16_t* y16b);
+void launch_bf16_gate_up(hipStream_t st, const uint16_t* W, int K, int inter, const uint16_t* x, int M,
+                         float swiglu_limit, uint16_t* h);
 // Hyper-Connections (4 residual streams of width d; see fst_hc.hip).
 void launch_hc_pre(hipStream_t st, const uint16_t* h_hc, const uint16_t* fnT, const float* scale, const float* base,
                    int M, int d, uint16_t* cur, float* post, float* comb);
@@ -146,7 +154,7 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
                         const uint16_t* h_in);
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
                      const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
-                     uint16_t* out_shared);
+                     uint16_t* out_shared, const float* ys);
 // Host-side reorder of one packed Q4_K expert (gate|up|down, each [N][K/256]
 // blocks of 144 B) into the device layout the linear kernel streams.
 void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);

@@ -795,6 +795,7 @@ struct EpiArgs {
     uint16_t* out;
     uint16_t* out_routed;
     uint16_t* out_shared;
+    const float* ys;  // shared expert computed beforehand ([T][hd] fp32), or null
 };
 
 #ifndef FST_Q4K_PF
@@ -1149,7 +1150,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                 }
                 if (ep.out_routed) ep.out_routed[(size_t)tok * N + n] = fst_f32_to_bf16(a);
                 if (ep.use_shared) {
-                    const float sv2 = ld_coherent(out + (size_t)ep.pair_shared[tok] * N + n);
+                    const float sv2 = ep.ys ? ep.ys[(size_t)tok * N + n]
+                                            : ld_coherent(out + (size_t)ep.pair_shared[tok] * N + n);
                     if (ep.out_shared) ep.out_shared[(size_t)tok * N + n] = fst_f32_to_bf16(sv2);
                     a = a + sv2;
                 }
@@ -1226,7 +1228,7 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
 // (src/fst_engine.cpp:4196-4201, :2851-2852), fp32 until one RNE rounding.
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
                      const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
-                     uint16_t* out_shared) {
+                     uint16_t* out_shared, const float* ys) {
     const size_t proj = g.codec == 1 ? (size_t)g.inter * (g.hd / 32) * 17 : (size_t)g.inter * (g.hd / 256) * 144;
     EpiArgs ep{};
     ep.tk = g.tk;
@@ -1240,6 +1242,7 @@ void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int 
     ep.out = out;
     ep.out_routed = out_routed;
     ep.out_shared = out_shared;
+    ep.ys = ys;
     if (g.codec == 1)
         launch_q4k_linear<2, 1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd,
                                 s, nullptr, s.a16p, nullptr, nullptr, s.y, ep);

@@ -97,6 +97,12 @@ int fst_upload_router_bf16(fst_ctx* ctx, int lid, const uint16_t* w_kn, const fl
 int fst_upload_router_f32(fst_ctx* ctx, int lid, const float* w_kn, const float* bias);
 /* tid2eid hash table [vocab][top_k] for lid < n_hash_layers (src/fst_engine.cpp:1015-1021). */
 int fst_upload_hash_table(fst_ctx* ctx, int lid, const int32_t* tid2eid);
+/* The shared expert in bf16, as the reference keeps it (TID_SHARED_GATE/UP/DOWN,
+ * process_shared_expert src/fst_engine.cpp:4373-4489): gate, up [inter][hidden]
+ * and down [hidden][inter], row-major.  Once uploaded, the layer's shared expert
+ * runs from these matrices (bf16 MFMA, h rounded to bf16) instead of expert
+ * slot n_experts of the codec bank. */
+int fst_upload_shared_bf16(fst_ctx* ctx, int lid, const uint16_t* gate, const uint16_t* up, const uint16_t* down);
 /* Device address of a resident expert (for in-place generation/inspection). */
 void* fst_expert_device_ptr(fst_ctx* ctx, int lid, int eid);
 
@@ -171,6 +177,10 @@ int fst_upload_norm(fst_ctx* ctx, int lid, const uint16_t* w_bf16);
 size_t fst_lm_head_bytes(const fst_config* cfg);
 /* vocab_size must be a multiple of 128. */
 int fst_upload_lm_head(fst_ctx* ctx, const void* packed, size_t bytes);
+/* The reference's own bf16 head [vocab][hidden] (TID_LM_HEAD, row-major as
+ * stored; src/fst_engine.cpp:2115-2160).  The head uploaded last is the one
+ * fst_lm_head_dev / fst_verify_forward use. */
+int fst_upload_lm_head_bf16(fst_ctx* ctx, const uint16_t* w);
 /* d_h_out (nullable) = d_y ? bf16(d_h + d_y) : d_h;  d_normed = RMSNorm_lid(that). */
 int fst_rmsnorm_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, const uint16_t* d_y, int M, uint16_t* d_h_out,
                     uint16_t* d_normed);
