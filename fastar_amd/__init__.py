@@ -89,6 +89,18 @@ _SIGS = {
     "fst_verify_forward_dev": (C.c_int, [P, P, C.c_int, P, P]),
     "fst_verify_forward": (C.c_int, [P, P, C.c_int, P, P]),
     "fst_upload_shared_bf16": (C.c_int, [P, C.c_int, P, P, P]),
+    "fst_get_config": (C.c_int, [P, P]),
+    "fst_bank_open": (C.c_int, [C.c_char_p, P]),
+    "fst_bank_close": (None, [P]),
+    "fst_bank_get_header": (C.c_int, [P, P]),
+    "fst_bank_n_tensors": (C.c_int, [P]),
+    "fst_bank_tensor_at": (C.c_int, [P, C.c_int, P]),
+    "fst_bank_find": (C.c_int, [P, C.c_uint32, C.c_int, P]),
+    "fst_bank_read_tensor": (C.c_int, [P, P, P, SZ]),
+    "fst_bank_read_expert": (C.c_int, [P, C.c_int, C.c_int, P, SZ]),
+    "fst_bank_config": (C.c_int, [P, P]),
+    "fst_bank_load_layer": (C.c_int, [P, P, C.c_int, C.c_int]),
+    "fst_bank_load_head": (C.c_int, [P, P, C.c_int]),
     "fst_upload_lm_head_bf16": (C.c_int, [P, P]),
     "fst_upload_hc": (C.c_int, [P, C.c_int, P, P, P]),
     "fst_upload_hc_head": (C.c_int, [P, P, C.c_float, P]),
@@ -447,3 +459,91 @@ class Context:
 
     def sync(self):
         _check(lib().fst_sync(self.h))
+
+    # .fst model file
+    def load_bank_layer(self, bank, lid, flags=None):
+        _check(lib().fst_bank_load_layer(self.h, bank.h, lid, BANK_LAYER_ALL if flags is None else flags))
+
+    def load_bank_head(self, bank, flags=None):
+        _check(lib().fst_bank_load_head(self.h, bank.h, BANK_HEAD_ALL if flags is None else flags))
+
+    def config(self):
+        c = fst_config()
+        _check(lib().fst_get_config(self.h, C.byref(c)))
+        return c
+
+
+# ---------------------------------------------------------------- .fst files
+
+(BANK_EXPERTS, BANK_ROUTER, BANK_NORM, BANK_SHARED, BANK_HC, BANK_HASH) = (1, 2, 4, 8, 16, 32)
+BANK_LAYER_ALL, BANK_BIAS_AS_FP16 = 63, 256
+BANK_HEAD_NORM, BANK_HEAD_LM, BANK_HEAD_HC, BANK_HEAD_ALL = 1, 2, 4, 7
+
+
+class fst_bank_header(C.Structure):
+    _fields_ = ([("magic", C.c_char * 4)] +
+                [(n, C.c_uint32) for n in ("version", "hidden_dim", "n_layers", "n_experts", "top_k", "n_q_heads",
+                                           "n_kv_heads", "head_dim", "inter_dim", "n_shared", "reserved0")] +
+                [("vocab_size", C.c_uint64), ("rms_eps", C.c_float), ("rope_freq_base", C.c_float)] +
+                [(n, C.c_uint64) for n in ("shared_dir_offset", "shared_dir_count", "expert_bank_offset",
+                                           "expert_block_bytes", "expert_block_stride", "expert_count", "dspark",
+                                           "dspark_noise_token_id")])
+
+
+class fst_bank_tensor(C.Structure):
+    _fields_ = [("tid", C.c_uint32), ("lid", C.c_uint16), ("sid", C.c_uint16), ("qtype", C.c_uint16),
+                ("ndim", C.c_uint16), ("shape", C.c_uint64 * 3), ("offset", C.c_uint64), ("size", C.c_uint64)]
+
+
+class Bank:
+    """An opened .fst model file (fst_bank_open); needs no GPU."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        _check(lib().fst_bank_open(str(path).encode(), C.byref(h)))
+        self.h = h
+        self.header = fst_bank_header()
+        _check(lib().fst_bank_get_header(self.h, C.byref(self.header)))
+
+    def close(self):
+        if self.h:
+            lib().fst_bank_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def tensors(self):
+        out = []
+        for i in range(lib().fst_bank_n_tensors(self.h)):
+            t = fst_bank_tensor()
+            _check(lib().fst_bank_tensor_at(self.h, i, C.byref(t)))
+            out.append(t)
+        return out
+
+    def find(self, tid, lid=-1):
+        t = fst_bank_tensor()
+        _check(lib().fst_bank_find(self.h, tid, lid, C.byref(t)))
+        return t
+
+    def read_tensor(self, t):
+        out = np.empty(t.size, np.uint8)
+        _check(lib().fst_bank_read_tensor(self.h, C.byref(t), _ptr(out), out.nbytes))
+        return out
+
+    def read_expert(self, lid, eid):
+        out = np.empty(self.header.expert_block_bytes, np.uint8)
+        _check(lib().fst_bank_read_expert(self.h, lid, eid, _ptr(out), out.nbytes))
+        return out
+
+    def config(self, **kw):
+        c = fst_config()
+        _check(lib().fst_bank_config(self.h, C.byref(c)))
+        for k, v in kw.items():
+            if not hasattr(c, k):
+                raise TypeError("unknown config field %s" % k)
+            setattr(c, k, v)
+        return c

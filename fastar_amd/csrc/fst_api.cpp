@@ -155,6 +155,10 @@ struct fst_ctx {
     }
 };
 
+namespace fst {
+int set_error(int code, const char* msg) { return fail(code, msg); }
+}  // namespace fst
+
 extern "C" {
 
 void fst_config_default(fst_config* c) {
@@ -297,6 +301,12 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
 }
 
 void fst_destroy(fst_ctx* ctx) { delete ctx; }
+
+int fst_get_config(const fst_ctx* ctx, fst_config* out) {
+    if (!ctx || !out) return fail(FST_EINVAL, "null argument");
+    *out = ctx->cfg;
+    return FST_OK;
+}
 void* fst_stream(fst_ctx* ctx) { return ctx ? (void*)ctx->st : nullptr; }
 
 int fst_sync(fst_ctx* ctx) {

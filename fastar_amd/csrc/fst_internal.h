@@ -7,6 +7,9 @@
 
 namespace fst {
 
+// Records the message returned by fst_last_error() and returns code.
+int set_error(int code, const char* msg);
+
 // Q4_K super-block: 256 weights in 144 bytes (fp16 d, fp16 dmin, 12 bytes of
 // packed 6-bit scales/mins, 128 bytes of nibbles).
 constexpr int kQ4kBlockElems = 256;

@@ -78,6 +78,8 @@ int fst_abi_version(void);
 size_t fst_expert_bytes(const fst_config* cfg);
 
 int fst_create(const fst_config* cfg, fst_ctx** out);
+/* The configuration the context was created with. */
+int fst_get_config(const fst_ctx* ctx, fst_config* out);
 void fst_destroy(fst_ctx* ctx);
 void* fst_stream(fst_ctx* ctx);       /* hipStream_t of the context */
 int fst_sync(fst_ctx* ctx);
@@ -234,6 +236,78 @@ int fst_synth_mxfp4_expert(uint64_t seed, uint64_t expert_id, int hd, int inter,
 int fst_synth_normal_bf16(uint64_t seed, uint64_t stream, size_t n, float mean, float std,
                           uint16_t* out);
 int fst_synth_normal_f32(uint64_t seed, uint64_t stream, size_t n, float mean, float std, float* out);
+
+/* ---- on-disk .fst model file (expert bank + shared tensors) ----
+ * Reader for the file written by scripts/fst_converter.py (convert_to_fst,
+ * :718-776) and read by ExpertPager (src/expert_pager.cpp:88-130, :265-290)
+ * and FSTEngine::load_shared_weights (src/fst_engine.cpp:1500-1760).
+ * Layout (little-endian): a 128-byte header (fst_bank_header fields in file
+ * order, HEADER_FMT "<4sIIIIIIIIIIIQffQQQQQQQQ", :169), a directory of 64-byte
+ * tensor entries (SHARED_ENTRY_FMT "<IHHHHIQQQQQQ"), page-aligned tensor data,
+ * and the expert bank: expert (l, e) at expert_bank_offset +
+ * (l * n_experts + e) * expert_block_stride, expert_block_bytes long, dense
+ * MXFP4 gate|up|down (17-byte blocks; the fst_upload_expert MXFP4 layout).
+ * The bank functions need no GPU. */
+typedef struct fst_bank fst_bank;
+typedef struct fst_bank_header {
+    char magic[4];                 /* "FST\0" */
+    uint32_t version, hidden_dim, n_layers, n_experts, top_k, n_q_heads, n_kv_heads, head_dim, inter_dim,
+        n_shared, reserved0;
+    uint64_t vocab_size;
+    float rms_eps, rope_freq_base;
+    uint64_t shared_dir_offset, shared_dir_count, expert_bank_offset, expert_block_bytes, expert_block_stride,
+        expert_count;
+    uint64_t dspark; /* block_size | markov_rank << 16 */
+    uint64_t dspark_noise_token_id;
+} fst_bank_header;
+typedef struct fst_bank_tensor {
+    uint32_t tid;                  /* TID_* of scripts/fst_converter.py:116-160 */
+    uint16_t lid;                  /* layer, 0xFFFF = global */
+    uint16_t sid, qtype, ndim;     /* qtype: 1 Q8_0, 2 BF16, 3 F32 */
+    uint64_t shape[3];             /* padded with 1 */
+    uint64_t offset, size;         /* bytes in the file */
+} fst_bank_tensor;
+enum {
+    FST_TID_OUTPUT_NORM = 1, FST_TID_LM_HEAD = 2, FST_TID_INPUT_NORM = 3, FST_TID_POST_ATTN_NORM = 4,
+    FST_TID_ROUTER = 9, FST_TID_ROUTER_BIAS = 10, FST_TID_SHARED_GATE = 11, FST_TID_SHARED_UP = 12,
+    FST_TID_SHARED_DOWN = 13, FST_TID_HC_FFN_FN = 26, FST_TID_HC_FFN_SCALE = 27, FST_TID_HC_FFN_BASE = 28,
+    FST_TID_HC_HEAD_FN = 29, FST_TID_HC_HEAD_SCALE = 30, FST_TID_HC_HEAD_BASE = 31
+};
+/* Opens and validates the file: magic, directory and every tensor and expert
+ * inside the file. */
+int fst_bank_open(const char* path, fst_bank** out);
+void fst_bank_close(fst_bank* b);
+int fst_bank_get_header(const fst_bank* b, fst_bank_header* out);
+int fst_bank_n_tensors(const fst_bank* b);
+int fst_bank_tensor_at(const fst_bank* b, int i, fst_bank_tensor* out);
+/* The entry with this tid and layer (lid = -1: the first entry with the tid);
+ * FST_ENOTREADY if absent. */
+int fst_bank_find(const fst_bank* b, uint32_t tid, int lid, fst_bank_tensor* out);
+/* Raw bytes of a tensor (bytes == t->size). */
+int fst_bank_read_tensor(const fst_bank* b, const fst_bank_tensor* t, void* dst, size_t bytes);
+/* Expert (lid, eid) as stored (bytes == expert_block_bytes); ExpertPager::load_from_disk. */
+int fst_bank_read_expert(const fst_bank* b, int lid, int eid, void* dst, size_t bytes);
+/* A context configuration for the file: geometry from the header, MXFP4
+ * codec, and the engine's fixed DeepSeek-V4 router settings
+ * (src/fst_engine.cpp:1506-1526, include/fst_engine.h:138-144): sqrt(softplus)
+ * scores, route_scale 1.5, 3 hash layers, bf16-rounded logits, no SwiGLU clamp
+ * (the NPU FFN applies none). */
+int fst_bank_config(const fst_bank* b, fst_config* cfg);
+enum {
+    FST_BANK_EXPERTS = 1,   /* routed experts -> fst_upload_expert */
+    FST_BANK_ROUTER = 2,    /* TID 9 [E][hidden] (+ TID 10 bias) -> router */
+    FST_BANK_NORM = 4,      /* TID 4 moe norm (absent: ones, as the engine) */
+    FST_BANK_SHARED = 8,    /* TID 11-13 -> fst_upload_shared_bf16 */
+    FST_BANK_HC = 16,       /* TID 26-28 -> fst_upload_hc (when present) */
+    FST_BANK_HASH = 32,     /* <path>.tid2eid sidecar rows of the layer (when present, lid < n_hash_layers) */
+    FST_BANK_LAYER_ALL = 63,
+    FST_BANK_BIAS_AS_FP16 = 256  /* read a 2-byte bias as fp16, as the engine does (:1626-1630) */
+};
+/* Loads layer lid of the file into the context (flags above). */
+int fst_bank_load_layer(fst_ctx* ctx, const fst_bank* b, int lid, int flags);
+enum { FST_BANK_HEAD_NORM = 1, FST_BANK_HEAD_LM = 2, FST_BANK_HEAD_HC = 4, FST_BANK_HEAD_ALL = 7 };
+/* Output norm (TID 1), bf16 LM head (TID 2), HC head (TID 29-31, when present). */
+int fst_bank_load_head(fst_ctx* ctx, const fst_bank* b, int flags);
 
 #ifdef __cplusplus
 }
