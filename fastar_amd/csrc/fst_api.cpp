@@ -283,12 +283,9 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.sxp, (size_t)T * (hd / 256) * 4)) || (rc = x->dalloc(&s.xs, T)) ||
         (rc = x->dalloc(&s.act, (size_t)P * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
-        (rc = x->dalloc(&s.y, (size_t)P * hd)) || (rc = x->dalloc(&s.tok_npairs, T)) ||
-        (rc = x->dalloc(&s.tile_done, (size_t)T * (hd / 16))) ||
+        (rc = x->dalloc(&s.y, (size_t)P * hd)) ||
         (rc = x->dalloc(&s.sh_h16, (size_t)T * c.inter_dim)) || (rc = x->dalloc(&s.ys, (size_t)T * hd)))
         return bail(rc);
-    if (hipMemsetAsync(s.tile_done, 0, sizeof(int) * T * (hd / 16), x->st) != hipSuccess)
-        return bail(fail(FST_EHIP, "hipMemsetAsync(counters) failed"));
     if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));
     x->ev.resize(17);
@@ -491,11 +488,10 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     ctx->mark_begin();
     const bool mx = c.codec == FST_CODEC_MXFP4;  // bf16 operands: no fp16 operand prep
     if (do_router) {
-        if (mx)
-            fst::launch_router_logits(st, g, L, d_h, M, ctx->s.logits);
-        else
-            fst::launch_router_prep(st, g, L, d_h, M, ctx->s.logits, ctx->s);
-        ctx->mark("router_prep");
+        // logits, operand prep (Q4_K) and top-k + bucketing in one launch
+        fst::launch_route(st, g, L, d_h, M, mx ? 0 : 1, d_ids, use_hash, use_shared && !sh16, d_eids, d_wts,
+                          ctx->s);
+        ctx->mark("route");
     }
     if (sh16) {
         // process_shared_expert (src/fst_engine.cpp:4373-4489) over bf16 weights; its fp32
@@ -512,12 +508,13 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
             return FST_OK;
         }
     }
-    fst::launch_route_bucket(st, g, L, M, ctx->s.logits, d_ids, use_hash, do_router, use_shared && !sh16, d_eids,
-                             d_wts, ctx->s);
-    ctx->mark("route_bucket");
-    if (!do_router && !mx) {
-        fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
-        ctx->mark("prep_x");
+    if (!do_router) {
+        fst::launch_bucket(st, g, M, use_shared && !sh16, d_eids, ctx->s);
+        ctx->mark("bucket");
+        if (!mx) {
+            fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
+            ctx->mark("prep_x");
+        }
     }
     fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h);
     ctx->mark("q4k_gate_up");
@@ -526,9 +523,11 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
                              ctx->s.sx2p, ctx->s.xs2);
         ctx->mark("prep_h");
     }
-    fst::launch_q4k_down(st, g, L, M, use_shared, ctx->s, d_wts, d_out, d_out_routed, d_out_shared,
-                         sh16 ? ctx->s.ys : nullptr);
+    fst::launch_q4k_down(st, g, L, M, ctx->s);
     ctx->mark("q4k_down");
+    fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out, d_out_routed,
+                        d_out_shared);
+    ctx->mark("combine");
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;
 }
@@ -590,11 +589,9 @@ int fst_router(fst_ctx* ctx, int lid, const uint16_t* h, int M, const int32_t* i
     FST_HIP_TRY(hipMemcpyAsync(ctx->s.h, h, (size_t)M * c.hidden_dim * 2, hipMemcpyHostToDevice, ctx->st));
     if (input_ids) FST_HIP_TRY(hipMemcpyAsync(ctx->s.ids, input_ids, M * 4, hipMemcpyHostToDevice, ctx->st));
     ctx->mark_begin();
-    fst::launch_router_logits(ctx->st, ctx->geo, L, ctx->s.h, M, ctx->s.logits);
-    ctx->mark("router_logits");
-    fst::launch_route_bucket(ctx->st, ctx->geo, L, M, ctx->s.logits, input_ids ? ctx->s.ids : nullptr, use_hash,
-                             1, 0, ctx->s.eids, ctx->s.wts, ctx->s);
-    ctx->mark("route_bucket");
+    fst::launch_route(ctx->st, ctx->geo, L, ctx->s.h, M, 0, input_ids ? ctx->s.ids : nullptr, use_hash, 0,
+                      ctx->s.eids, ctx->s.wts, ctx->s);
+    ctx->mark("route");
     FST_HIP_TRY(hipGetLastError());
     FST_HIP_TRY(hipMemcpyAsync(eids, ctx->s.eids, (size_t)M * c.top_k * 4, hipMemcpyDeviceToHost, ctx->st));
     FST_HIP_TRY(hipMemcpyAsync(wts, ctx->s.wts, (size_t)M * c.top_k * 4, hipMemcpyDeviceToHost, ctx->st));
@@ -905,6 +902,7 @@ int fst_synth_lm_head_dev(fst_ctx* ctx, uint64_t seed, uint64_t id, float d_sigm
                                 ctx->lm_head);
     FST_HIP_TRY(hipGetLastError());
     FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    ctx->lm_kind = 1;
     return FST_OK;
 }
 

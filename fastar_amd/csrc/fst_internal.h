@@ -58,10 +58,8 @@ struct Scratch {
     uint4* sx2p;           // [P][inter/256][4]
     int* xs2;              // [P]
     float* y;              // [P][hd]
-    int* tok_npairs;       // [T] distinct (token, expert) pairs of each token incl. shared
     uint16_t* sh_h16;      // [T][inter] bf16 shared-expert h (bf16 shared expert)
     float* ys;             // [T][hd] fp32 shared-expert output (bf16 shared expert)
-    int* tile_done;        // [T][hd/16] (used: hd / rows per item) down contributions finished per token row tile (re-armed)
 };
 
 // Device expert bank: n_layers x (n_experts + 1) packed experts.
@@ -115,17 +113,16 @@ __device__ __forceinline__ int signal_add(int* c, int v) {
 }
 
 // ---- launchers (each enqueues on `st`) ----
-void launch_router_logits(hipStream_t st, const Geometry& g, const LayerView& L,
-                          const uint16_t* h, int M, float* logits);
-void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, int M,
-                         const float* logits, const int32_t* input_ids, int use_hash,
-                         int do_topk, int use_shared, int32_t* eids, float* wts,
-                         const Scratch& s);
+// Router logits with the fp16 operand prep of h (prep, Q4_K), then top-k (or
+// hash rows) and the bucketing of the call (two launches).
+void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M, int prep,
+                  const int32_t* input_ids, int use_hash, int use_shared, int32_t* eids, float* wts,
+                  const Scratch& s);
+// Bucketing of caller-given routing eids [M][tk].
+void launch_bucket(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
+                   const Scratch& s);
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p,
                       uint4* sxp, int* xs);
-// Router logits and the activation prep of the same rows in one launch.
-void launch_router_prep(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
-                        float* logits, const Scratch& s);
 // Residual add + RMSNorm per token row (see resid_norm_kernel); optional
 // outputs: h_out (x), normed (bf16), the fp16 operand in prep->x16p/sxp/xs,
 // and a one-slot table for launch_q4k_dense in slot_tab (META_WORDS + 3 ints).
@@ -151,13 +148,11 @@ void launch_hc_head(hipStream_t st, const uint16_t* h_hc, const uint16_t* fnT, f
 void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
                      uint4* sxp, int* xs);
 // Weights must be in the wave-tiled device layout (repack_q4k_expert).
-// gate/up writes h = silu(gate)*up; down runs the combine of each token row
-// tile (last contribution).
+// gate/up writes h = silu(gate)*up; down writes y[pair] (fp32), combined by
+// launch_combine.
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
                         const uint16_t* h_in);
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
-                     const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
-                     uint16_t* out_shared, const float* ys);
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
 // Host-side reorder of one packed Q4_K expert (gate|up|down, each [N][K/256]
 // blocks of 144 B) into the device layout the linear kernel streams.
 void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);
@@ -170,8 +165,9 @@ void launch_synth_q4k_tiled(hipStream_t st, uint64_t seed, uint64_t id, uint64_t
                             uint8_t* dst);
 void launch_synth_mx_tiled(hipStream_t st, uint64_t seed, uint64_t id, uint64_t b0, int N, int K, int e_lo,
                            int e_hi, uint8_t* dst);
+// out = bf16(sum_j w_j y[pair(t,j)] + shared) per token (see combine_kernel).
 void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
-                    const float* wts, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
+                    const float* wts, const float* ys, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 void launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);
 void launch_dequant(hipStream_t st, int codec, const uint8_t* blocks, size_t nblocks,
                     float* out_f32, uint16_t* out_bf16);

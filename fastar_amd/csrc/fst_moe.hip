@@ -86,34 +86,34 @@ __device__ void router_block(const uint16_t* __restrict__ w_nk, const uint16_t* 
     }
 }
 
-template <int CH, int TPW>
-__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ w_nk,
-                                                            const uint16_t* __restrict__ h, int M, int K, int E,
-                                                            float* __restrict__ logits) {
-    router_block<CH, TPW>(w_nk, h, M, K, E, blockIdx.x, blockIdx.y, logits);
-}
-
-void launch_router_logits(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
-                          float* logits) {
-    constexpr int TPW = 2;
-    const dim3 grid((g.E + 3) / 4, (M + TPW - 1) / TPW);
-#define FST_RL(CHV)                                                                                        \
-    hipLaunchKernelGGL((router_logits_kernel<CHV, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd, g.E, \
-                       logits)
-    if (g.hd == 4096)
-        FST_RL(64);
-    else if (g.hd == 2048)
-        FST_RL(32);
-    else if (g.hd == 1024)
-        FST_RL(16);
-    else
-        FST_RL(8);
-#undef FST_RL
-}
-
 // ------------------------------------------------------------ route + bucket
 
 constexpr int kMaxExperts = 1024;
+
+// Wave-wide max / min of a uint32 held by every lane (all 64 lanes active):
+// DPP within each row of 16 lanes, then the four row results.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    x = max(x, dpp<0xb1>(x));   // quad_perm [1,0,3,2]
+    x = max(x, dpp<0x4e>(x));   // quad_perm [2,3,0,1]
+    x = max(x, dpp<0x124>(x));  // row_ror 4
+    x = max(x, dpp<0x128>(x));  // row_ror 8
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+    x = min(x, dpp<0xb1>(x));
+    x = min(x, dpp<0x4e>(x));
+    x = min(x, dpp<0x124>(x));
+    x = min(x, dpp<0x128>(x));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return min(min(a, b), min(c, d));
+}
 
 // Total order used for top-k: larger score first, then lower expert id; NaN
 // scores rank below every number (and among themselves by id).  Encoded as a
@@ -139,8 +139,7 @@ template <int NT>
 __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* eids_s, int topk_err,
                              int* __restrict__ meta, int* __restrict__ slot_eid, int* __restrict__ slot_M,
                              int* __restrict__ slot_off, int* __restrict__ pair_tok,
-                             int* __restrict__ pair_of, int* __restrict__ pair_shared,
-                             int* __restrict__ tok_npairs) {
+                             int* __restrict__ pair_of, int* __restrict__ pair_shared) {
     constexpr int NW = NT / 64;
     __shared__ unsigned long long hitmask[kMaxExperts];
     __shared__ int eoff[kMaxExperts];
@@ -210,21 +209,11 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
         }
         pair_of[i] = p;
     }
-    for (int t = tid; t < M; t += NT) {
-        int n = use_shared ? 1 : 0;
-        for (int j = 0; j < tk; ++j) {
-            const int e = eids_s[t * tk + j];
-            if (e < 0 || e >= E) continue;
-            bool dup = false;
-            for (int j2 = 0; j2 < j; ++j2) dup |= eids_s[t * tk + j2] == e;
-            n += dup ? 0 : 1;
-        }
-        tok_npairs[t] = n;
-        if (use_shared) {
+    if (use_shared)
+        for (int t = tid; t < M; t += NT) {
             pair_tok[t] = t;
             pair_shared[t] = t;
         }
-    }
     if (use_shared && tid == 0) {
         slot_eid[0] = E;
         slot_M[0] = M;
@@ -246,32 +235,53 @@ constexpr int kRouteThreads = 1024;
 __global__ __launch_bounds__(kRouteThreads) void bucket_kernel(
     int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids, int* __restrict__ meta,
     int* __restrict__ slot_eid, int* __restrict__ slot_M, int* __restrict__ slot_off, int* __restrict__ pair_tok,
-    int* __restrict__ pair_of, int* __restrict__ pair_shared, int* __restrict__ tok_npairs) {
+    int* __restrict__ pair_of, int* __restrict__ pair_shared) {
     __shared__ int s_eids[kMaxTokens * kMaxTopK];
     for (int i = threadIdx.x; i < M * tk; i += kRouteThreads) s_eids[i] = eids[i];
     __syncthreads();
     bucket_block<kRouteThreads>(M, E, tk, use_shared, s_eids, 0, meta, slot_eid, slot_M, slot_off, pair_tok,
-                                pair_of, pair_shared, tok_npairs);
+                                pair_of, pair_shared);
 }
 
-// One workgroup: wave w selects the top-k of tokens w, w+16, ...
-// (src/fst_engine.cpp:974-1061 semantics with the order of topk_key) or reads
-// their hash-table rows (:1015-1021) and writes eids/wts; after one barrier
-// the same workgroup groups all tokens' (token, expert) pairs.  PER = experts
-// per lane.
-template <int PER>
-__global__ __launch_bounds__(kRouteThreads) void topk_bucket_kernel(
-    int M, int E, int tk, int score_func, int round_bf16, float route_scale, const float* __restrict__ logits,
-    const float* __restrict__ bias, const int32_t* __restrict__ hash, const int32_t* __restrict__ ids,
-    int vocab, int use_shared, int32_t* __restrict__ eids, float* __restrict__ wts, int* __restrict__ meta,
-    int* __restrict__ slot_eid, int* __restrict__ slot_M, int* __restrict__ slot_off,
-    int* __restrict__ pair_tok, int* __restrict__ pair_of, int* __restrict__ pair_shared,
-    int* __restrict__ tok_npairs) {
-    constexpr int NW = kRouteThreads / 64;
+// Arguments of the routing step (top-k or hash rows, then bucketing).
+struct RouteArgs {
+    int M, E, tk, score_func, round_bf16;
+    float route_scale;
+    const float* logits;
+    const float* bias;
+    const int32_t* hash;
+    const int32_t* ids;
+    int vocab, use_shared;
+    int32_t* eids;
+    float* wts;
+    int* meta;
+    int* slot_eid;
+    int* slot_M;
+    int* slot_off;
+    int* pair_tok;
+    int* pair_of;
+    int* pair_shared;
+};
+
+// One workgroup of NT threads: wave w selects the top-k of tokens w, w+NT/64,
+// ... (src/fst_engine.cpp:974-1061 semantics with the order of topk_key) or
+// reads their hash-table rows (:1015-1021) and writes eids/wts; after one
+// barrier the same workgroup groups all tokens' (token, expert) pairs.  PER =
+// experts per lane.
+template <int PER, int NT>
+__device__ void topk_bucket_block(const RouteArgs& ra) {
+    const int M = ra.M, E = ra.E, tk = ra.tk, score_func = ra.score_func, round_bf16 = ra.round_bf16;
+    const float route_scale = ra.route_scale;
+    const float* __restrict__ logits = ra.logits;
+    const float* __restrict__ bias = ra.bias;
+    const int32_t* __restrict__ hash = ra.hash;
+    const int32_t* __restrict__ ids = ra.ids;
+    const int vocab = ra.vocab;
+    int32_t* __restrict__ eids = ra.eids;
+    float* __restrict__ wts = ra.wts;
+    constexpr int NW = NT / 64;
     __shared__ int s_eids[kMaxTokens * kMaxTopK];
     __shared__ int s_err;
-    __shared__ unsigned long long s_wkey[NW][kMaxTopK];
-    __shared__ float s_wsc[NW][kMaxTopK];
     __shared__ float s_rank_sc[NW][kMaxTopK];
     __shared__ int s_rank_id[NW][kMaxTopK];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -307,20 +317,22 @@ __global__ __launch_bounds__(kRouteThreads) void topk_bucket_kernel(
             }
             continue;
         }
-        // Exact top-k by radix selection on the 32 order bits of topk_key
-        // (ballots, no 64-bit shuffles): T = the k-th largest order value,
-        // winners = {o > T} plus the lowest ids with o == T; then each winner
-        // is ranked among the winners by the full key (order desc, id asc).
+        // Exact top-k by extraction in rank order (order bits of topk_key
+        // descending, then id ascending): each round the wave takes the best
+        // head over its lanes (a lane's head is its best remaining expert;
+        // id = lane + 64 i, so a lane's candidates ascend in id) with a DPP
+        // max, breaks an exact tie by the lowest id, and the winning lane
+        // retires that expert.
         uint32_t o[PER];
         float sc[PER];
-        bool valid[PER];
+        bool live[PER];
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int e = lane + 64 * i;
             o[i] = 0u;
             sc[i] = 0.0f;
-            valid[i] = e < E;
-            if (valid[i]) {
+            live[i] = e < E;
+            if (live[i]) {
                 float x = row[e];
                 if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
                 const float sv = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
@@ -328,53 +340,34 @@ __global__ __launch_bounds__(kRouteThreads) void topk_bucket_kernel(
                 o[i] = (uint32_t)(topk_key(sv + (bias ? bias[e] : 0.0f), e) >> 32);
             }
         }
-        auto count_ge = [&](uint32_t thr) -> int {
-            int c = 0;
+        for (int r = 0; r < tk; ++r) {
+            uint32_t ho = 0u, hid = 0xffffffffu;
+            float hsc = 0.0f;
+            int hi = -1;
 #pragma unroll
-            for (int i = 0; i < PER; ++i) c += __popcll(__ballot(valid[i] && o[i] >= thr));
-            return c;
-        };
-        uint32_t T = 0u;
-        for (int bit = 31; bit >= 0; --bit) {
-            const uint32_t cand = T | (1u << bit);
-            if (count_ge(cand) >= tk) T = cand;
-        }
-        int need = tk;
+            for (int i = 0; i < PER; ++i)
+                if (live[i] && (hi < 0 || o[i] > ho)) {
+                    ho = o[i];
+                    hid = (uint32_t)(lane + 64 * i);
+                    hsc = sc[i];
+                    hi = i;
+                }
+            const uint32_t mo = wave_max_u32(hi >= 0 ? ho : 0u);
+            const unsigned long long tie = __ballot(hi >= 0 && ho == mo);
+            const uint32_t wid = __popcll(tie) == 1
+                                     ? (uint32_t)__builtin_amdgcn_readlane((int)hid, __ffsll((long long)tie) - 1)
+                                     : wave_min_u32((tie >> lane) & 1ull ? hid : 0xffffffffu);
+            const int wl = (int)(wid & 63u);
+            const float wsc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, hsc), wl));
+            if (lane == wl) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) need -= __popcll(__ballot(valid[i] && o[i] > T));
-        // ties at T: lowest ids first (id = lane + 64 i)
-        bool win[PER];
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const unsigned long long tie = __ballot(valid[i] && o[i] == T);
-            const unsigned long long below = (lane == 0) ? 0ull : (tie & ((1ull << lane) - 1ull));
-            const int before = __popcll(below);
-            win[i] = valid[i] && (o[i] > T || (o[i] == T && before < need));
-            need -= min(need, __popcll(tie));
-        }
-        // compact the winners into LDS (ascending id), rank them, emit in rank order
-        unsigned long long* wkey = s_wkey[wave];
-        float* wsc = s_wsc[wave];
-        int base = 0;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const unsigned long long m = __ballot(win[i]);
-            if (win[i]) {
-                const int pos = base + __popcll(lane == 0 ? 0ull : (m & ((1ull << lane) - 1ull)));
-                wkey[pos] = ((unsigned long long)o[i] << 32) | (0xffffffffu - (uint32_t)(lane + 64 * i));
-                wsc[pos] = sc[i];
+                for (int i = 0; i < PER; ++i)
+                    if (i == hi) live[i] = false;
             }
-            base += __popcll(m);
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane < tk) {
-            const unsigned long long mk = wkey[lane];
-            int rank = 0;
-            for (int j = 0; j < tk; ++j) rank += wkey[j] > mk;
-            s_rank_sc[wave][rank] = wsc[lane];
-            s_rank_id[wave][rank] = (int)(0xffffffffu - (uint32_t)mk);
+            if (lane == 0) {
+                s_rank_id[wave][r] = (int)wid;
+                s_rank_sc[wave][r] = wsc;
+            }
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -391,36 +384,30 @@ __global__ __launch_bounds__(kRouteThreads) void topk_bucket_kernel(
         __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    bucket_block<kRouteThreads>(M, E, tk, use_shared, s_eids, s_err, meta, slot_eid, slot_M, slot_off, pair_tok,
-                                pair_of, pair_shared, tok_npairs);
+    bucket_block<NT>(M, E, tk, ra.use_shared, s_eids, s_err, ra.meta, ra.slot_eid, ra.slot_M, ra.slot_off,
+                     ra.pair_tok, ra.pair_of, ra.pair_shared);
 }
 
-void launch_route_bucket(hipStream_t st, const Geometry& g, const LayerView& L, int M,
-                         const float* logits, const int32_t* input_ids, int use_hash, int do_topk,
-                         int use_shared, int32_t* eids, float* wts, const Scratch& s) {
-    if (!do_topk) {
-        hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(kRouteThreads), 0, st, M, g.E, g.tk, use_shared, eids,
-                           s.meta, s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared,
-                           s.tok_npairs);
-        return;
-    }
-#define FST_TOPK(PERV)                                                                                     \
-    hipLaunchKernelGGL(topk_bucket_kernel<PERV>, dim3(1), dim3(kRouteThreads), 0, st, M, g.E, g.tk,        \
-                       g.score_func, g.round_logits_bf16, g.route_scale, logits, L.router_bias,            \
-                       use_hash ? L.hash : nullptr, input_ids, g.vocab, use_shared, eids, wts, s.meta,       \
-                       s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared, s.tok_npairs)
-    const int per = (g.E + 63) / 64;
-    if (per <= 1)
-        FST_TOPK(1);
-    else if (per <= 2)
-        FST_TOPK(2);
-    else if (per <= 4)
-        FST_TOPK(4);
-    else if (per <= 8)
-        FST_TOPK(8);
-    else
-        FST_TOPK(16);
-#undef FST_TOPK
+template <int PER>
+__global__ __launch_bounds__(kRouteThreads) void topk_bucket_kernel(RouteArgs ra) {
+    topk_bucket_block<PER, kRouteThreads>(ra);
+}
+
+static RouteArgs route_args(const Geometry& g, const LayerView& L, int M, const float* logits,
+                            const int32_t* input_ids, int use_hash, int use_shared, int32_t* eids, float* wts,
+                            const Scratch& s) {
+    return RouteArgs{M,          g.E,         g.tk,       g.score_func,
+                     g.round_logits_bf16, g.route_scale, logits, L.router_bias,
+                     use_hash ? L.hash : nullptr, input_ids, g.vocab, use_shared,
+                     eids,       wts,         s.meta,     s.slot_eid,
+                     s.slot_M,   s.slot_off,  s.pair_tok, s.pair_of,
+                     s.pair_shared};
+}
+
+void launch_bucket(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
+                   const Scratch& s) {
+    hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(kRouteThreads), 0, st, M, g.E, g.tk, use_shared, eids, s.meta,
+                       s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared);
 }
 
 // -------------------------------------------------------------- operand prep
@@ -526,6 +513,18 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
     prep_row<256>(src, row, K, xv, x16p, sxp, xs);
 }
 
+// The routing front of a layer call in one launch: workgroups [0, nrb) compute
+// the router logits (router_block), workgroups [nrb, nrb + nprep) prepare the
+// expert operand of each token row (prep_row; Q4_K only), and the router
+// workgroup that finishes last runs the top-k and bucketing of the call
+// (topk_bucket_block) on the logits the others published with device-coherent
+// stores.  `done` counts finished router workgroups; the last one re-arms it.
+// Router logits (workgroups [0, nrb), router_block) and the fp16 expert
+// operand of each token row (workgroups [nrb, nrb + nprep), prep_row; Q4_K
+// only) in one launch; the top-k and bucketing of the call follow in
+// topk_bucket_kernel.  (A single launch whose last router workgroup runs the
+// top-k was measured slower: the hand-off through device-coherent stores and
+// a contended completion counter costs more than the kernel boundary.)
 template <int CH, int TPW>
 __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __restrict__ w_nk,
                                                           const uint16_t* __restrict__ h, int M, int K, int E,
@@ -541,14 +540,15 @@ __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __rest
     router_block<CH, TPW>(w_nk, h, M, K, E, b % nbx, b / nbx, logits);
 }
 
-void launch_router_prep(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M,
-                        float* logits, const Scratch& s) {
+void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M, int prep,
+                  const int32_t* input_ids, int use_hash, int use_shared, int32_t* eids, float* wts,
+                  const Scratch& s) {
     constexpr int TPW = 2;
     const int nbx = (g.E + 3) / 4, nby = (M + TPW - 1) / TPW, nrb = nbx * nby;
-    const dim3 grid(nrb + M);
+    const dim3 grid(nrb + (prep ? M : 0));
 #define FST_RP(CHV)                                                                                       \
     hipLaunchKernelGGL((router_prep_kernel<CHV, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd, g.E, \
-                       logits, nbx, nrb, s.x16p, s.sxp, s.xs)
+                       s.logits, nbx, nrb, s.x16p, s.sxp, s.xs)
     if (g.hd == 4096)
         FST_RP(64);
     else if (g.hd == 2048)
@@ -558,6 +558,20 @@ void launch_router_prep(hipStream_t st, const Geometry& g, const LayerView& L, c
     else
         FST_RP(8);
 #undef FST_RP
+    const RouteArgs ra = route_args(g, L, M, s.logits, input_ids, use_hash, use_shared, eids, wts, s);
+    const int per = (g.E + 63) / 64;
+#define FST_TOPK(PERV) hipLaunchKernelGGL(topk_bucket_kernel<PERV>, dim3(1), dim3(kRouteThreads), 0, st, ra)
+    if (per <= 1)
+        FST_TOPK(1);
+    else if (per <= 2)
+        FST_TOPK(2);
+    else if (per <= 4)
+        FST_TOPK(4);
+    else if (per <= 8)
+        FST_TOPK(8);
+    else
+        FST_TOPK(16);
+#undef FST_TOPK
 }
 
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p, uint4* sxp,
@@ -775,27 +789,14 @@ constexpr int kTokStride = 37;
 #ifndef FST_Q4K_WPE_MID
 #define FST_Q4K_WPE_MID 4
 #endif
-// What a linear-kernel launch does besides Y = W.A.
+// What a linear-kernel launch does besides Y = W.A (mode 1, gate||up:
+// workgroup tile T holds gate rows [64T, 64T+64) in waves 0..3 and the
+// matching up rows in waves 4..7; it writes h = silu(gate) * up for its 64
+// rows, fp32 for Q4_K, bf16 for MXFP4 (the down operand as is)).
 struct EpiArgs {
-    // mode 1 (gate||up): workgroup tile T holds gate rows [64T, 64T+64) in
-    // waves 0..3 and the matching up rows in waves 4..7; it writes
-    // h = silu(gate) * up (fp32) for its 64 rows
     float swiglu_limit;
     float* h;
-    uint16_t* h16;  // MXFP4 path: h rounded to bf16 (the down operand as is)
-    // mode 2 (down): the last contribution to a (token, 128-row tile)
-    // combines it
-    int tk, use_shared;
-    const int* pair_tok;
-    const int* pair_of;
-    const int* pair_shared;
-    const float* wts;
-    const int* tok_npairs;
-    int* tile_done;
-    uint16_t* out;
-    uint16_t* out_routed;
-    uint16_t* out_shared;
-    const float* ys;  // shared expert computed beforehand ([T][hd] fp32), or null
+    uint16_t* h16;
 };
 
 #ifndef FST_Q4K_PF
@@ -833,8 +834,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     constexpr int U = (MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R);  // lcm(MS, R)
     static_assert(U % MS == 0 && U % R == 0, "unroll must cover whole stages and ring turns");
     __shared__ uint4 lds[2 * STAGE + 1];
-    __shared__ int s_flag[kMaxTokens];
-    __shared__ int s_nflag;
 
     const int tiles = N / (16 * WAVES);
     const int total = meta[META_N_SLOTS] * tiles;
@@ -1110,52 +1109,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                 const int tl = q * 16 + 4 * g + i;
                 if (tl >= Me) continue;
                 const int pidx = off + tl;
-                const float v = ldexpf(acc[q][i], unscale(pidx));
-                if constexpr (MODE == 0)
-                    out[(size_t)pidx * N + row] = v;
-                else
-                    st_coherent(&out[(size_t)pidx * N + row], v);
-            }
-        }
-        if constexpr (MODE == 0) continue;
-
-        // ---- mode 2: one contribution per (pair, tile); the last one for a
-        // token combines its tile (counters are re-armed by their consumer) ----
-        publish_wait();
-        __syncthreads();
-        if (tid == 0) s_nflag = 0;
-        __syncthreads();
-        constexpr int TR = 16 * WAVES;  // rows per work item
-        const int nt128 = N / TR;
-        const int T128 = tile;
-        for (int tl = tid; tl < slot_M[slot]; tl += NT) {
-            const int tok = ep.pair_tok[off + tl];
-            const int old = signal_add(&ep.tile_done[tok * nt128 + T128], 1);
-            if (old == ep.tok_npairs[tok] - 1) {
-                ep.tile_done[tok * nt128 + T128] = 0;
-                s_flag[atomicAdd(&s_nflag, 1)] = tok;
-            }
-        }
-        __syncthreads();
-        const int nflag = s_nflag;
-        for (int f = 0; f < nflag; ++f) {
-            const int tok = s_flag[f];
-            for (int i = tid; i < TR; i += NT) {
-                const int n = T128 * TR + i;
-                float a = 0.0f;
-                for (int j = 0; j < ep.tk; ++j) {
-                    const int p = ep.pair_of[tok * ep.tk + j];
-                    if (p < 0) continue;
-                    a = a + ep.wts[tok * ep.tk + j] * ld_coherent(out + (size_t)p * N + n);
-                }
-                if (ep.out_routed) ep.out_routed[(size_t)tok * N + n] = fst_f32_to_bf16(a);
-                if (ep.use_shared) {
-                    const float sv2 = ep.ys ? ep.ys[(size_t)tok * N + n]
-                                            : ld_coherent(out + (size_t)ep.pair_shared[tok] * N + n);
-                    if (ep.out_shared) ep.out_shared[(size_t)tok * N + n] = fst_f32_to_bf16(sv2);
-                    a = a + sv2;
-                }
-                if (ep.out) ep.out[(size_t)tok * N + n] = fst_f32_to_bf16(a);
+                out[(size_t)pidx * N + row] = ldexpf(acc[q][i], unscale(pidx));
             }
         }
     }
@@ -1223,32 +1177,15 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
                              s.pair_tok, s.x16p, s.sxp, s.xs, nullptr, ep);
 }
 
-// down: the last contribution to each (token, 128-row tile) combines it:
-// out = bf16(sum_j w[t][j] y[pair(t,j)] + y[shared(t)]) in slot order
-// (src/fst_engine.cpp:4196-4201, :2851-2852), fp32 until one RNE rounding.
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, int use_shared,
-                     const Scratch& s, const float* wts, uint16_t* out, uint16_t* out_routed,
-                     uint16_t* out_shared, const float* ys) {
+// down: y[pair][n] (fp32) for every (token, expert) pair of the call.
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
     const size_t proj = g.codec == 1 ? (size_t)g.inter * (g.hd / 32) * 17 : (size_t)g.inter * (g.hd / 256) * 144;
-    EpiArgs ep{};
-    ep.tk = g.tk;
-    ep.use_shared = use_shared;
-    ep.pair_tok = s.pair_tok;
-    ep.pair_of = s.pair_of;
-    ep.pair_shared = s.pair_shared;
-    ep.wts = wts;
-    ep.tok_npairs = s.tok_npairs;
-    ep.tile_done = s.tile_done;
-    ep.out = out;
-    ep.out_routed = out_routed;
-    ep.out_shared = out_shared;
-    ep.ys = ys;
     if (g.codec == 1)
         launch_q4k_linear<2, 1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd,
-                                s, nullptr, s.a16p, nullptr, nullptr, s.y, ep);
+                                s, nullptr, s.a16p, nullptr, nullptr, s.y, EpiArgs{});
     else
         launch_q4k_linear<2>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
-                             nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
+                             nullptr, s.a16p, s.sx2p, s.xs2, s.y, EpiArgs{});
 }
 
 // Dense Q4_K linear over M rows (the LM head): logits[m][n] = sum_k W[n][k] x[m][k],
@@ -1265,39 +1202,62 @@ void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, con
 
 // ------------------------------------------------------------------ combine
 
-// src/fst_engine.cpp:4196-4201 and :2851-2852: fp32 accumulation in slot
-// order j = 0..tk-1, then + shared, one bf16 rounding (RNE).
+// src/fst_engine.cpp:4196-4201 and :2851-2852: out = bf16(sum_j w[t][j] y[pair(t,j)]
+// + y_shared[t]), fp32 accumulation in slot order j = 0..tk-1, then the shared
+// term (weight 1.0), one RNE rounding.  The shared term is its pair's row of y,
+// or row t of ys when the shared expert ran from bf16 weights.  One thread per
+// 4 consecutive columns of one token.
 __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int use_shared,
                                                       const float* __restrict__ y,
                                                       const int* __restrict__ pair_of,
                                                       const int* __restrict__ pair_shared,
+                                                      const float* __restrict__ ys,
                                                       const float* __restrict__ wts,
                                                       uint16_t* __restrict__ out,
                                                       uint16_t* __restrict__ out_routed,
                                                       uint16_t* __restrict__ out_shared) {
     const int t = blockIdx.y;
-    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (t >= M || n >= hd) return;
-    float acc = 0.0f;
+    int p[kMaxTopK];
+    float w[kMaxTopK];
     for (int j = 0; j < tk; ++j) {
-        const int p = pair_of[t * tk + j];
-        if (p < 0) continue;
-        acc = acc + wts[t * tk + j] * y[(size_t)p * hd + n];
+        p[j] = pair_of[t * tk + j];
+        w[j] = wts[t * tk + j];
     }
-    if (out_routed) out_routed[(size_t)t * hd + n] = fst_f32_to_bf16(acc);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < tk; ++j) {
+        if (p[j] < 0) continue;
+        const float4 v = *reinterpret_cast<const float4*>(y + (size_t)p[j] * hd + n);
+        a.x = a.x + w[j] * v.x;
+        a.y = a.y + w[j] * v.y;
+        a.z = a.z + w[j] * v.z;
+        a.w = a.w + w[j] * v.w;
+    }
+    auto put = [&](uint16_t* o, const float4& v) {
+        if (!o) return;
+        const uint32_t lo = fst_f32_to_bf16(v.x) | ((uint32_t)fst_f32_to_bf16(v.y) << 16);
+        const uint32_t hi = fst_f32_to_bf16(v.z) | ((uint32_t)fst_f32_to_bf16(v.w) << 16);
+        *reinterpret_cast<uint2*>(o + (size_t)t * hd + n) = make_uint2(lo, hi);
+    };
+    put(out_routed, a);
     if (use_shared) {
-        const float sv = y[(size_t)pair_shared[t] * hd + n];
-        if (out_shared) out_shared[(size_t)t * hd + n] = fst_f32_to_bf16(sv);
-        acc = acc + sv;
+        const float* src = ys ? ys + (size_t)t * hd : y + (size_t)pair_shared[t] * hd;
+        const float4 v = *reinterpret_cast<const float4*>(src + n);
+        put(out_shared, v);
+        a.x = a.x + v.x;
+        a.y = a.y + v.y;
+        a.z = a.z + v.z;
+        a.w = a.w + v.w;
     }
-    if (out) out[(size_t)t * hd + n] = fst_f32_to_bf16(acc);
+    put(out, a);
 }
 
 void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
-                    const float* wts, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared) {
-    dim3 grid((g.hd + 255) / 256, M);
-    hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, st, M, g.hd, g.tk, use_shared, s.y,
-                       s.pair_of, s.pair_shared, wts, out, out_routed, out_shared);
+                    const float* wts, const float* ys, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared) {
+    dim3 grid((g.hd / 4 + 255) / 256, M);
+    hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, st, M, g.hd, g.tk, use_shared, s.y, s.pair_of,
+                       s.pair_shared, ys, wts, out, out_routed, out_shared);
 }
 
 // --------------------------------------------------------------------- copy

@@ -190,6 +190,36 @@ def test_router_ties_and_hash(fa, oracle, router_ctx):
     assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
 
 
+def test_router_tie_heavy(fa, oracle, router_ctx):
+    """Groups of 8 exactly tied experts (identical router columns, spread
+    over lanes and per-lane slots by a permutation), all 256 tied, and E not
+    a multiple of 64: the selection must return the lowest ids of a tied
+    group in id order, as the oracle's (score desc, id asc) order does."""
+    ctx = router_ctx
+    base = fa.synth_normal_bf16(41, 0, (HD, 32), 0.0, 0.02)
+    w = np.ascontiguousarray(np.repeat(base, 8, axis=1)[:, np.random.default_rng(5).permutation(256)])
+    h = fa.synth_normal_bf16(42, 0, (16, HD))
+    note("router tie-heavy")
+    ctx.upload_router_bf16(3, w)
+    e, wt = ctx.router(3, h)
+    re_, rw, _ = oracle.router(h, w, None, 6)
+    assert np.array_equal(e, re_)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    wall = np.ascontiguousarray(np.repeat(base[:, :1], 256, axis=1))
+    ctx.upload_router_bf16(3, wall)
+    e, wt = ctx.router(3, h)
+    assert (e == np.arange(6, dtype=np.int32)[None, :]).all()
+    re_, rw, _ = oracle.router(h, wall, None, 6)
+    assert np.array_equal(e, re_) and np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    with fa.Context(n_experts=200, top_k=8, max_tokens=16) as c2:
+        w2 = fa.synth_normal_bf16(43, 0, (HD, 200), 0.0, 0.02)
+        w2[:, 150:200] = w2[:, 0:50]
+        c2.upload_router_bf16(0, w2)
+        e, wt = c2.router(0, h)
+        re_, rw, _ = oracle.router(h, w2, None, 8)
+        assert np.array_equal(e, re_) and np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+
+
 # ------------------------------------------------------------ MoE layer (C2)
 
 @pytest.mark.parametrize("M", [8, 32])
