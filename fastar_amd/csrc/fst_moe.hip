@@ -39,6 +39,66 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t b) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
 }
 
+// Wave-wide max / min of a uint32 held by every lane (all 64 lanes active):
+// DPP within each row of 16 lanes, then the four row results.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t x) {  // bound_ctrl off: lanes without a source read 0
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float fdpp(float x) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(uint32_t, x)));
+}
+// Wave-wide fmaxf (order-free: fmaxf ignores NaN operands).
+__device__ __forceinline__ float wave_fmax(float x) {
+    x = fmaxf(x, fdpp<0xb1>(x));
+    x = fmaxf(x, fdpp<0x4e>(x));
+    x = fmaxf(x, fdpp<0x124>(x));
+    x = fmaxf(x, fdpp<0x128>(x));
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    x = max(x, dpp<0xb1>(x));   // quad_perm [1,0,3,2]
+    x = max(x, dpp<0x4e>(x));   // quad_perm [2,3,0,1]
+    x = max(x, dpp<0x124>(x));  // row_ror 4
+    x = max(x, dpp<0x128>(x));  // row_ror 8
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+    x = min(x, dpp<0xb1>(x));
+    x = min(x, dpp<0x4e>(x));
+    x = min(x, dpp<0x124>(x));
+    x = min(x, dpp<0x128>(x));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return min(min(a, b), min(c, d));
+}
+
+// Sum of the 64 lanes' values in the canonical halving-tree order, as lane 0
+// sees it: p[j] += p[j + off] for off = 32, 16, ..., 1.  The cross-row steps
+// use gfx950's permlane32/16 swaps (lanes j < 32 read lane j + 32; lanes of
+// even rows read the next row), the in-row steps DPP row shifts (lane j reads
+// lane j + off).  Only lane 0's result is meaningful.
+__device__ __forceinline__ float tree_sum64(float acc) {
+    const uint32_t a = __builtin_bit_cast(uint32_t, acc);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+    acc = acc + __builtin_bit_cast(float, (uint32_t)s32[1]);
+    const uint32_t b = __builtin_bit_cast(uint32_t, acc);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    acc = acc + __builtin_bit_cast(float, (uint32_t)s16[1]);
+    acc = acc + __builtin_bit_cast(float, dpp<0x108>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 8
+    acc = acc + __builtin_bit_cast(float, dpp<0x104>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 4
+    acc = acc + __builtin_bit_cast(float, dpp<0x102>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 2
+    acc = acc + __builtin_bit_cast(float, dpp<0x101>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 1
+    return acc;
+}
+
 // ---------------------------------------------------------------- router
 
 // Router logits: one wave per (expert, pair of tokens); lane j owns the
@@ -80,8 +140,7 @@ __device__ void router_block(const uint16_t* __restrict__ w_nk, const uint16_t* 
                 acc = fmaf(fst_bits_f32(xv[k] & 0xffff0000u), fst_bits_f32(wv[k] & 0xffff0000u), acc);
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_down(acc, off, 64);
+        acc = tree_sum64(acc);
         if (lane == 0) logits[(size_t)(t0 + t) * E + e] = acc;
     }
 }
@@ -89,31 +148,6 @@ __device__ void router_block(const uint16_t* __restrict__ w_nk, const uint16_t* 
 // ------------------------------------------------------------ route + bucket
 
 constexpr int kMaxExperts = 1024;
-
-// Wave-wide max / min of a uint32 held by every lane (all 64 lanes active):
-// DPP within each row of 16 lanes, then the four row results.
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp(uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-    x = max(x, dpp<0xb1>(x));   // quad_perm [1,0,3,2]
-    x = max(x, dpp<0x4e>(x));   // quad_perm [2,3,0,1]
-    x = max(x, dpp<0x124>(x));  // row_ror 4
-    x = max(x, dpp<0x128>(x));  // row_ror 8
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
-    return max(max(a, b), max(c, d));
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
-    x = min(x, dpp<0xb1>(x));
-    x = min(x, dpp<0x4e>(x));
-    x = min(x, dpp<0x124>(x));
-    x = min(x, dpp<0x128>(x));
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
-    return min(min(a, b), min(c, d));
-}
 
 // Total order used for top-k: larger score first, then lower expert id; NaN
 // scores rank below every number (and among themselves by id).  Encoded as a
@@ -454,8 +488,7 @@ __device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __
         xv[i] = v;
         m = fmaxf(m, fabsf(v));
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    m = wave_fmax(m);
     if (lane == 0) red[wave] = m;
     __syncthreads();
     float a = red[0];
@@ -487,11 +520,14 @@ __device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __
         *reinterpret_cast<h8_t*>(dst + (size_t)q * 8) = v;
         float s0 = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
         float s1 = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
-#pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
-            s0 += __shfl_xor(s0, o, 64);
-            s1 += __shfl_xor(s1, o, 64);
-        }
+        // butterfly over the 8 lanes of the group; lane c == 0 holds
+        // ((l0 + l1) + (l2 + l3)) + ((l4 + l5) + (l6 + l7))
+        s0 = s0 + fdpp<0xb1>(s0);  // quad_perm [1,0,3,2]
+        s1 = s1 + fdpp<0xb1>(s1);
+        s0 = s0 + fdpp<0x4e>(s0);  // quad_perm [2,3,0,1]
+        s1 = s1 + fdpp<0x4e>(s1);
+        s0 = s0 + fdpp<0x104>(s0);  // row_shl 4
+        s1 = s1 + fdpp<0x104>(s1);
         if (c == 0) {
             const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
             const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
