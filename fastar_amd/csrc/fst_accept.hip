@@ -78,27 +78,20 @@ __global__ __launch_bounds__(256) void acc_stats_kernel(const float* __restrict_
         if (l != l) continue;
         if (bi == 0x7fffffff || l > best) { best = l; bi = v; }
     }
-    __shared__ float sm[256];
-    __shared__ int si[256];
-    sm[threadIdx.x] = best;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int off = 128; off >= 1; off >>= 1) {
-        if ((int)threadIdx.x < off) {
-            const float ob = sm[threadIdx.x + off];
-            const int oi = si[threadIdx.x + off];
-            const int mi = si[threadIdx.x];
-            if (oi != 0x7fffffff &&
-                (mi == 0x7fffffff || ob > sm[threadIdx.x] || (ob == sm[threadIdx.x] && oi < mi))) {
-                sm[threadIdx.x] = ob;
-                si[threadIdx.x] = oi;
-            }
-        }
-        __syncthreads();
+    if (bi == 0x7fffffff) bi = -1;
+    wave_argmax(best, bi);
+    __shared__ float sm[4];
+    __shared__ int si[4];
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sm[wave] = best;
+        si[wave] = bi;
     }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        part_max[(size_t)r * kChunks + c] = sm[0];
-        part_idx[(size_t)r * kChunks + c] = si[0] == 0x7fffffff ? -1 : si[0];
+        for (int q = 1; q < 4; ++q) argmax_merge(best, bi, sm[q], si[q]);
+        part_max[(size_t)r * kChunks + c] = best;
+        part_idx[(size_t)r * kChunks + c] = bi;
     }
 }
 
@@ -110,28 +103,12 @@ __device__ __forceinline__ void wave_row_argmax(const float* part_max, const int
     const int lane = threadIdx.x & 63;
     float m = part_max[(size_t)r * kChunks + lane];
     int i = part_idx[(size_t)r * kChunks + lane];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float om = __shfl_xor(m, off, 64);
-        const int oi = __shfl_xor(i, off, 64);
-        if (oi >= 0 && (i < 0 || om > m || (om == m && oi < i))) {
-            m = om;
-            i = oi;
-        }
-    }
+    wave_argmax(m, i);
     *mx = m;
     *idx = i;
 }
 
-__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const unsigned lo = __shfl_xor((unsigned)v, off, 64);
-        const unsigned hi = __shfl_xor((unsigned)(v >> 32), off, 64);
-        v += ((unsigned long long)hi << 32) | lo;
-    }
-    return v;
-}
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) { return wave_sum_u64_dpp(v); }
 
 // One wave per sequence: rows reduced one after another, chunks across lanes.
 __global__ __launch_bounds__(64) void acc_greedy_final_kernel(const float* __restrict__ target, int k,
@@ -504,15 +481,8 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
         for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) take(row[v], v);
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ob = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (oi != 0x7fffffff && (bi == 0x7fffffff || ob > best || (ob == best && oi < bi))) {
-            best = ob;
-            bi = oi;
-        }
-    }
+    if (bi == 0x7fffffff) bi = -1;
+    wave_argmax(best, bi);
     __shared__ float sm[4];
     __shared__ int si[4];
     __shared__ int s_last;
@@ -522,13 +492,9 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int q = 1; q < 4; ++q)
-            if (si[q] != 0x7fffffff && (bi == 0x7fffffff || sm[q] > best || (sm[q] == best && si[q] < bi))) {
-                best = sm[q];
-                bi = si[q];
-            }
+        for (int q = 1; q < 4; ++q) argmax_merge(best, bi, sm[q], si[q]);
         st_coherent(&w.part_max[(size_t)r * kChunks + c], best);
-        st_coherent(&w.part_idx[(size_t)r * kChunks + c], bi == 0x7fffffff ? -1 : bi);
+        st_coherent(&w.part_idx[(size_t)r * kChunks + c], bi);
         publish_wait();
         s_last = signal_add(&w.row_done[r], 1) == CH - 1;
     }
@@ -541,15 +507,7 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
             m = ld_coherent(&w.part_max[(size_t)r * kChunks + lane]);
             i = ld_coherent(&w.part_idx[(size_t)r * kChunks + lane]);
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float om = __shfl_xor(m, off, 64);
-            const int oi = __shfl_xor(i, off, 64);
-            if (oi >= 0 && (i < 0 || om > m || (om == m && oi < i))) {
-                m = om;
-                i = oi;
-            }
-        }
+        wave_argmax(m, i);
         int seq_last = 0;
         const int s = r / (k + 1);
         if (lane == 0) {

@@ -112,6 +112,95 @@ __device__ __forceinline__ int signal_add(int* c, int v) {
     return r;
 }
 
+// ---- wave-level DPP reductions (all 64 lanes active) ----
+// Wave-wide max / min of a uint32 held by every lane (all 64 lanes active):
+// DPP within each row of 16 lanes, then the four row results.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t x) {  // bound_ctrl off: lanes without a source read 0
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float fdpp(float x) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(uint32_t, x)));
+}
+// Wave-wide fmaxf (order-free: fmaxf ignores NaN operands).
+__device__ __forceinline__ float wave_fmax(float x) {
+    x = fmaxf(x, fdpp<0xb1>(x));
+    x = fmaxf(x, fdpp<0x4e>(x));
+    x = fmaxf(x, fdpp<0x124>(x));
+    x = fmaxf(x, fdpp<0x128>(x));
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    x = max(x, dpp<0xb1>(x));   // quad_perm [1,0,3,2]
+    x = max(x, dpp<0x4e>(x));   // quad_perm [2,3,0,1]
+    x = max(x, dpp<0x124>(x));  // row_ror 4
+    x = max(x, dpp<0x128>(x));  // row_ror 8
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+    x = min(x, dpp<0xb1>(x));
+    x = min(x, dpp<0x4e>(x));
+    x = min(x, dpp<0x124>(x));
+    x = min(x, dpp<0x128>(x));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+    return min(min(a, b), min(c, d));
+}
+
+// Wave-wide argmax over (m, i) pairs, i < 0 meaning "no element": larger m
+// first, then lower i.  The merge is associative and commutative, so the
+// DPP tree gives the same result as any other order.  Result in every lane.
+__device__ __forceinline__ void argmax_merge(float& m, int& i, float om, int oi) {
+    if (oi >= 0 && (i < 0 || om > m || (om == m && oi < i))) {
+        m = om;
+        i = oi;
+    }
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& m, int& i) {
+    const float om = fdpp<CTRL>(m);
+    const int oi = (int)dpp<CTRL>((uint32_t)i);
+    argmax_merge(m, i, om, oi);
+}
+__device__ __forceinline__ void wave_argmax(float& m, int& i) {
+    argmax_step<0xb1>(m, i);
+    argmax_step<0x4e>(m, i);
+    argmax_step<0x124>(m, i);
+    argmax_step<0x128>(m, i);
+    float rm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 0));
+    int ri = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16)
+        argmax_merge(rm, ri, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), r)),
+                     __builtin_amdgcn_readlane(i, r));
+    m = rm;
+    i = ri;
+}
+// Wave-wide sum of a uint64 (integer: any order gives the same result).
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    return ((unsigned long long)dpp<CTRL>((uint32_t)(v >> 32)) << 32) | dpp<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ unsigned long long wave_sum_u64_dpp(unsigned long long v) {
+    v += dpp_u64<0xb1>(v);
+    v += dpp_u64<0x4e>(v);
+    v += dpp_u64<0x124>(v);
+    v += dpp_u64<0x128>(v);
+    unsigned long long t = 0;
+#pragma unroll
+    for (int r = 0; r < 64; r += 16)
+        t += ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), r) << 32) |
+             (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, r);
+    return t;
+}
+
 // ---- launchers (each enqueues on `st`) ----
 // Router logits with the fp16 operand prep of h (prep, Q4_K), then top-k (or
 // hash rows) and the bucketing of the call (two launches).

@@ -39,47 +39,6 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t b) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
 }
 
-// Wave-wide max / min of a uint32 held by every lane (all 64 lanes active):
-// DPP within each row of 16 lanes, then the four row results.
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp(uint32_t x) {  // bound_ctrl off: lanes without a source read 0
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float fdpp(float x) {
-    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(uint32_t, x)));
-}
-// Wave-wide fmaxf (order-free: fmaxf ignores NaN operands).
-__device__ __forceinline__ float wave_fmax(float x) {
-    x = fmaxf(x, fdpp<0xb1>(x));
-    x = fmaxf(x, fdpp<0x4e>(x));
-    x = fmaxf(x, fdpp<0x124>(x));
-    x = fmaxf(x, fdpp<0x128>(x));
-    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
-    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16));
-    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32));
-    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
-    return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-    x = max(x, dpp<0xb1>(x));   // quad_perm [1,0,3,2]
-    x = max(x, dpp<0x4e>(x));   // quad_perm [2,3,0,1]
-    x = max(x, dpp<0x124>(x));  // row_ror 4
-    x = max(x, dpp<0x128>(x));  // row_ror 8
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
-    return max(max(a, b), max(c, d));
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
-    x = min(x, dpp<0xb1>(x));
-    x = min(x, dpp<0x4e>(x));
-    x = min(x, dpp<0x124>(x));
-    x = min(x, dpp<0x128>(x));
-    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
-    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
-    return min(min(a, b), min(c, d));
-}
-
 // Sum of the 64 lanes' values in the canonical halving-tree order, as lane 0
 // sees it: p[j] += p[j + off] for off = 32, 16, ..., 1.  The cross-row steps
 // use gfx950's permlane32/16 swaps (lanes j < 32 read lane j + 32; lanes of
