@@ -5,6 +5,7 @@
 // is a fixed chain of launches on that stream (router -> bucket -> prep ->
 // gate/up -> prep -> down -> combine) with no host synchronisation inside;
 // host-pointer entry points add one H2D copy, one D2H copy and one sync.
+#include <cstdlib>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -487,10 +488,14 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     hipStream_t st = ctx->st;
     ctx->mark_begin();
     const bool mx = c.codec == FST_CODEC_MXFP4;  // bf16 operands: no fp16 operand prep
+    // top-k + bucketing run inside the gate||up launch when the expert count allows
+    static const bool fuse_env = !getenv("FST_SEPARATE_TOPK");  // A/B switch for measurements
+    const bool fuse_topk = fuse_env && do_router && c.n_experts <= fst::kFusedRouteMaxExperts;
+    const fst::RouteReq rq{d_ids, use_hash, use_shared && !sh16, d_eids, d_wts};
     if (do_router) {
-        // logits, operand prep (Q4_K) and top-k + bucketing in one launch
+        // logits and operand prep (Q4_K) in one launch, then (unless fused) top-k + bucketing
         fst::launch_route(st, g, L, d_h, M, mx ? 0 : 1, d_ids, use_hash, use_shared && !sh16, d_eids, d_wts,
-                          ctx->s);
+                          ctx->s, fuse_topk ? 0 : 1);
         ctx->mark("route");
     }
     if (sh16) {
@@ -516,7 +521,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
             ctx->mark("prep_x");
         }
     }
-    fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h);
+    fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h, fuse_topk ? &rq : nullptr);
     ctx->mark("q4k_gate_up");
     if (!mx) {
         fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p,

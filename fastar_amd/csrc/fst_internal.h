@@ -154,6 +154,62 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
     return min(min(a, b), min(c, d));
 }
 
+// Wave-wide max of a uint64 held by every lane, in every lane: DPP within
+// each row of 16 lanes, then gfx950's row-pair and half swaps (with both
+// operands x, permlane16_swap returns {x of the even row, x of the odd row}
+// of each row pair in both rows, permlane32_swap the same for the halves).
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    return ((unsigned long long)dpp<CTRL>((uint32_t)(v >> 32)) << 32) | dpp<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) {
+    return a > b ? a : b;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
+    x = max_u64(x, dpp_u64<0xb1>(x));   // quad_perm [1,0,3,2]
+    x = max_u64(x, dpp_u64<0x4e>(x));   // quad_perm [2,3,0,1]
+    x = max_u64(x, dpp_u64<0x124>(x));  // row_ror 4
+    x = max_u64(x, dpp_u64<0x128>(x));  // row_ror 8
+    {
+        const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+        const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        x = max_u64(((unsigned long long)(uint32_t)h[0] << 32) | (uint32_t)l[0],
+                    ((unsigned long long)(uint32_t)h[1] << 32) | (uint32_t)l[1]);
+    }
+    {
+        const uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+        const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        x = max_u64(((unsigned long long)(uint32_t)h[0] << 32) | (uint32_t)l[0],
+                    ((unsigned long long)(uint32_t)h[1] << 32) | (uint32_t)l[1]);
+    }
+    return ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(x >> 32)) << 32) |
+           (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+}
+// Wave-wide max / min of a uint32, in every lane (DPP within rows, then the
+// row-pair and half swaps as in wave_max_u64).
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_ext_u32_all(uint32_t x) {
+    auto f = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    x = f(x, dpp<0xb1>(x));
+    x = f(x, dpp<0x4e>(x));
+    x = f(x, dpp<0x124>(x));
+    x = f(x, dpp<0x128>(x));
+    const auto p16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = f((uint32_t)p16[0], (uint32_t)p16[1]);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    x = f((uint32_t)p32[0], (uint32_t)p32[1]);
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+__device__ __forceinline__ uint32_t wave_max_u32_all(uint32_t x) { return wave_ext_u32_all<true>(x); }
+__device__ __forceinline__ uint32_t wave_min_u32_all(uint32_t x) { return wave_ext_u32_all<false>(x); }
+// Number of set bits of mask below bit `lane` (mbcnt).
+__device__ __forceinline__ int lane_prefix(unsigned long long mask, int lane) {
+    (void)lane;
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 // Wave-wide argmax over (m, i) pairs, i < 0 meaning "no element": larger m
 // first, then lower i.  The merge is associative and commutative, so the
 // DPP tree gives the same result as any other order.  Result in every lane.
@@ -184,10 +240,6 @@ __device__ __forceinline__ void wave_argmax(float& m, int& i) {
     i = ri;
 }
 // Wave-wide sum of a uint64 (integer: any order gives the same result).
-template <int CTRL>
-__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
-    return ((unsigned long long)dpp<CTRL>((uint32_t)(v >> 32)) << 32) | dpp<CTRL>((uint32_t)v);
-}
 __device__ __forceinline__ unsigned long long wave_sum_u64_dpp(unsigned long long v) {
     v += dpp_u64<0xb1>(v);
     v += dpp_u64<0x4e>(v);
@@ -204,9 +256,22 @@ __device__ __forceinline__ unsigned long long wave_sum_u64_dpp(unsigned long lon
 // ---- launchers (each enqueues on `st`) ----
 // Router logits with the fp16 operand prep of h (prep, Q4_K), then top-k (or
 // hash rows) and the bucketing of the call (two launches).
+// With topk = 0 only the logits (and the operand prep) are launched: the
+// top-k and bucketing then run in the gate||up launch (RouteReq).
 void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M, int prep,
                   const int32_t* input_ids, int use_hash, int use_shared, int32_t* eids, float* wts,
-                  const Scratch& s);
+                  const Scratch& s, int topk = 1);
+// Routing that the gate||up launch performs itself from s.logits (every
+// workgroup computes the call's top-k and bucket tables into LDS; workgroup 0
+// also writes eids/wts and the tables to global memory for later launches).
+struct RouteReq {
+    const int32_t* input_ids;
+    int use_hash, use_shared;
+    int32_t* eids;
+    float* wts;
+};
+// Largest expert count the in-launch routing handles (4 experts per lane).
+constexpr int kFusedRouteMaxExperts = 256;
 // Bucketing of caller-given routing eids [M][tk].
 void launch_bucket(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
                    const Scratch& s);
@@ -240,7 +305,7 @@ void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_ro
 // gate/up writes h = silu(gate)*up; down writes y[pair] (fp32), combined by
 // launch_combine.
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
-                        const uint16_t* h_in);
+                        const uint16_t* h_in, const RouteReq* route = nullptr);
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
 // Host-side reorder of one packed Q4_K expert (gate|up|down, each [N][K/256]
 // blocks of 144 B) into the device layout the linear kernel streams.

@@ -28,6 +28,11 @@
 #include "fst_internal.h"
 #include "../../include/fst_exact_math.h"
 
+// Timing hook for probe builds (empty in the library).
+#ifndef FST_PROBE_MARK
+#define FST_PROBE_MARK(i)
+#endif
+
 namespace fst {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -63,12 +68,13 @@ __device__ __forceinline__ float tree_sum64(float acc) {
 // Router logits: one wave per (expert, pair of tokens); lane j owns the
 // contiguous K/64 chunk j, sums it with a sequential fmaf chain, then the 64
 // partials are combined by the halving tree p[j] += p[j+off] (off = 32..1)
-// that lane 0 sees through shfl_down.  All loads of a wave are issued before
+// that lane 0 sees through shfl_down.  Lane 0 stores the logit's score
+// (sigmoid or sqrt(softplus), after the optional bf16 rounding).  All loads of a wave are issued before
 // the math.  Workgroups past the router part each prepare one token row of
 // the expert operand (prep_row), so both consumers of h share one launch.
 template <int CH, int TPW>
 __device__ void router_block(const uint16_t* __restrict__ w_nk, const uint16_t* __restrict__ h, int M, int K,
-                             int E, int bx, int by, float* __restrict__ logits) {
+                             int E, int bx, int by, int score_func, int round_bf16, float* __restrict__ scores) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int e = bx * 4 + wave;
     const int t0 = by * TPW;
@@ -100,7 +106,13 @@ __device__ void router_block(const uint16_t* __restrict__ w_nk, const uint16_t* 
             }
         }
         acc = tree_sum64(acc);
-        if (lane == 0) logits[(size_t)(t0 + t) * E + e] = acc;
+        if (lane == 0) {
+            // the score of the logit (src/fst_engine.cpp:974-983), computed
+            // where the logit is produced so the top-k only compares
+            float x = acc;
+            if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
+            scores[(size_t)(t0 + t) * E + e] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+        }
     }
 }
 
@@ -133,10 +145,8 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
                              int* __restrict__ meta, int* __restrict__ slot_eid, int* __restrict__ slot_M,
                              int* __restrict__ slot_off, int* __restrict__ pair_tok,
                              int* __restrict__ pair_of, int* __restrict__ pair_shared) {
-    constexpr int NW = NT / 64;
     __shared__ unsigned long long hitmask[kMaxExperts];
     __shared__ int eoff[kMaxExperts];
-    __shared__ int wave_tot[2][NW];
     __shared__ int err;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (tid == 0) err = 0;
@@ -151,47 +161,55 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
             atomicOr(&hitmask[e], 1ull << t);
     }
     __syncthreads();
+    FST_PROBE_MARK(5);
     const int s0 = use_shared ? 1 : 0, p0 = use_shared ? M : 0;
+    // Slots and pairs numbered in ascending expert id, one expert per
+    // thread: exclusive prefix counts within each wave from ballots (a count
+    // of at most 64 tokens summed bit-plane by bit-plane), then the totals of
+    // the waves before it.
+    constexpr int NW = NT / 64;
+    __shared__ int s_wtot[2][NW];
     int slot_base = s0, pair_base = p0;
     for (int e0 = 0; e0 < E; e0 += NT) {
         const int e = e0 + tid;
         const int cnt = (e < E) ? __popcll(hitmask[e]) : 0;
-        const int act = cnt > 0;
-        int sa = act, sc = cnt;
+        const unsigned long long ba = __ballot(cnt > 0);
+        int ex_a = lane_prefix(ba, lane), ex_c = 0, tot_c = 0;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int ua = __shfl_up(sa, off, 64), uc = __shfl_up(sc, off, 64);
-            if (lane >= off) {
-                sa += ua;
-                sc += uc;
-            }
+        for (int bit = 0; bit < 7; ++bit) {
+            const unsigned long long bb = __ballot((cnt >> bit) & 1);
+            ex_c += lane_prefix(bb, lane) << bit;
+            tot_c += __popcll(bb) << bit;
         }
-        if (lane == 63) {
-            wave_tot[0][wave] = sa;
-            wave_tot[1][wave] = sc;
+        if (lane == 0) {
+            s_wtot[0][wave] = __popcll(ba);
+            s_wtot[1][wave] = tot_c;
         }
         __syncthreads();
-        int pa = slot_base, pc = pair_base;
-        for (int w = 0; w < wave; ++w) {
-            pa += wave_tot[0][w];
-            pc += wave_tot[1][w];
+        int ta = 0, tc = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int a = s_wtot[0][w], c = s_wtot[1][w];
+            if (w < wave) {
+                ex_a += a;
+                ex_c += c;
+            }
+            ta += a;
+            tc += c;
         }
-        const int ex_a = pa + sa - act, ex_c = pc + sc - cnt;
-        if (act) {
+        ex_a += slot_base;
+        ex_c += pair_base;
+        if (cnt > 0) {
             slot_eid[ex_a] = e;
             slot_M[ex_a] = cnt;
             slot_off[ex_a] = ex_c;
         }
         if (e < E) eoff[e] = ex_c;
-        int tot_a = 0, tot_c = 0;
-        for (int w = 0; w < NW; ++w) {
-            tot_a += wave_tot[0][w];
-            tot_c += wave_tot[1][w];
-        }
-        slot_base += tot_a;
-        pair_base += tot_c;
+        slot_base += ta;
+        pair_base += tc;
         __syncthreads();
     }
+    FST_PROBE_MARK(6);
     for (int i = tid; i < M * tk; i += NT) {
         const int t = i / tk;
         const int e = eids_s[i];
@@ -213,6 +231,7 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
         slot_off[0] = 0;
     }
     __syncthreads();
+    FST_PROBE_MARK(4);
     if (tid == 0) {
         meta[META_N_ROUTED] = slot_base - s0;
         meta[META_N_SLOTS] = slot_base;
@@ -240,7 +259,7 @@ __global__ __launch_bounds__(kRouteThreads) void bucket_kernel(
 struct RouteArgs {
     int M, E, tk, score_func, round_bf16;
     float route_scale;
-    const float* logits;
+    const float* scores;  // [M][E] router scores (router_block)
     const float* bias;
     const int32_t* hash;
     const int32_t* ids;
@@ -260,12 +279,13 @@ struct RouteArgs {
 // ... (src/fst_engine.cpp:974-1061 semantics with the order of topk_key) or
 // reads their hash-table rows (:1015-1021) and writes eids/wts; after one
 // barrier the same workgroup groups all tokens' (token, expert) pairs.  PER =
-// experts per lane.
+// experts per lane.  gw: write eids/wts (the bucket tables always go to the
+// pointers in ra, global or LDS).
 template <int PER, int NT>
-__device__ void topk_bucket_block(const RouteArgs& ra) {
-    const int M = ra.M, E = ra.E, tk = ra.tk, score_func = ra.score_func, round_bf16 = ra.round_bf16;
+__device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
+    const int M = ra.M, E = ra.E, tk = ra.tk;
     const float route_scale = ra.route_scale;
-    const float* __restrict__ logits = ra.logits;
+    const float* __restrict__ scores = ra.scores;
     const float* __restrict__ bias = ra.bias;
     const int32_t* __restrict__ hash = ra.hash;
     const int32_t* __restrict__ ids = ra.ids;
@@ -275,13 +295,13 @@ __device__ void topk_bucket_block(const RouteArgs& ra) {
     constexpr int NW = NT / 64;
     __shared__ int s_eids[kMaxTokens * kMaxTopK];
     __shared__ int s_err;
-    __shared__ float s_rank_sc[NW][kMaxTopK];
-    __shared__ int s_rank_id[NW][kMaxTopK];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const float zero_score = ra.score_func == 0 ? fst_sigmoidf(0.0f) : fst_sqrtsoftplusf(0.0f);
+    FST_PROBE_MARK(0);
     if (tid == 0) s_err = 0;
     __syncthreads();
     for (int t = wave; t < M; t += NW) {
-        const float* row = logits + (size_t)t * E;
+        const float* row = scores + (size_t)t * E;
         if (hash) {
             if (lane == 0) {
                 const int tok = ids ? ids[t] : -1;
@@ -289,94 +309,106 @@ __device__ void topk_bucket_block(const RouteArgs& ra) {
                     atomicOr(&s_err, 2);
                     for (int k = 0; k < tk; ++k) {
                         s_eids[t * tk + k] = -1;
-                        eids[(size_t)t * tk + k] = -1;
-                        wts[(size_t)t * tk + k] = 0.0f;
+                        if (gw) {
+                            eids[(size_t)t * tk + k] = -1;
+                            wts[(size_t)t * tk + k] = 0.0f;
+                        }
                     }
                 } else {
                     float sc[kMaxTopK];
                     float sum = 0.0f;
                     for (int k = 0; k < tk; ++k) {
                         const int e = hash[(size_t)tok * tk + k];
-                        float x = (e >= 0 && e < E) ? row[e] : 0.0f;
-                        if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
-                        sc[k] = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
+                        // an out-of-range id scores as a zero logit
+                        sc[k] = (e >= 0 && e < E) ? row[e] : zero_score;
                         sum += sc[k];
                         s_eids[t * tk + k] = e;
-                        eids[(size_t)t * tk + k] = e;
+                        if (gw) eids[(size_t)t * tk + k] = e;
                     }
                     const float inv = 1.0f / (sum + 1e-12f);
-                    for (int k = 0; k < tk; ++k) wts[(size_t)t * tk + k] = sc[k] * inv * route_scale;
+                    if (gw)
+                        for (int k = 0; k < tk; ++k) wts[(size_t)t * tk + k] = sc[k] * inv * route_scale;
                 }
             }
             continue;
         }
-        // Exact top-k by extraction in rank order (order bits of topk_key
-        // descending, then id ascending): each round the wave takes the best
-        // head over its lanes (a lane's head is its best remaining expert;
-        // id = lane + 64 i, so a lane's candidates ascend in id) with a DPP
-        // max, breaks an exact tie by the lowest id, and the winning lane
-        // retires that expert.
-        uint32_t o[PER];
+        // Exact top-k by extraction in rank order (topk_key: order bits of
+        // score+bias descending, then lower id; 1 + order bits here so that
+        // 0 marks a retired slot below every live one).  Each lane keeps its
+        // experts sorted, so its head is slot 0; each round the wave takes
+        // the largest head (DPP + lane swaps), an exact tie going to the
+        // lowest id, and that lane retires its head.  Lane r keeps rank r;
+        // the weight sum runs in selection order as the reference sums.
+        uint32_t key[PER];
         float sc[PER];
-        bool live[PER];
+        int id[PER];
+        {
+            float x[PER], bv[PER];
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int e = lane + 64 * i;
-            o[i] = 0u;
-            sc[i] = 0.0f;
-            live[i] = e < E;
-            if (live[i]) {
-                float x = row[e];
-                if (round_bf16) x = fst_bf16_to_f32(fst_f32_to_bf16(x));
-                const float sv = score_func == 0 ? fst_sigmoidf(x) : fst_sqrtsoftplusf(x);
-                sc[i] = sv;
-                o[i] = (uint32_t)(topk_key(sv + (bias ? bias[e] : 0.0f), e) >> 32);
+            for (int i = 0; i < PER; ++i) x[i] = row[min(lane + 64 * i, E - 1)];
+#pragma unroll
+            for (int i = 0; i < PER; ++i) bv[i] = bias ? bias[min(lane + 64 * i, E - 1)] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int e = lane + 64 * i;
+                sc[i] = x[i];
+                id[i] = e;
+                key[i] = e < E ? (uint32_t)(topk_key(x[i] + bv[i], e) >> 32) + 1u : 0u;
             }
         }
-        for (int r = 0; r < tk; ++r) {
-            uint32_t ho = 0u, hid = 0xffffffffu;
-            float hsc = 0.0f;
-            int hi = -1;
+        // stable sort descending by key (ids ascend within a lane)
 #pragma unroll
-            for (int i = 0; i < PER; ++i)
-                if (live[i] && (hi < 0 || o[i] > ho)) {
-                    ho = o[i];
-                    hid = (uint32_t)(lane + 64 * i);
-                    hsc = sc[i];
-                    hi = i;
+        for (int i = 0; i < PER; ++i)
+#pragma unroll
+            for (int j = 0; j + 1 < PER - i; ++j)
+                if (key[j + 1] > key[j]) {
+                    const uint32_t a = key[j];
+                    key[j] = key[j + 1];
+                    key[j + 1] = a;
+                    const float b = sc[j];
+                    sc[j] = sc[j + 1];
+                    sc[j + 1] = b;
+                    const int c = id[j];
+                    id[j] = id[j + 1];
+                    id[j + 1] = c;
                 }
-            const uint32_t mo = wave_max_u32(hi >= 0 ? ho : 0u);
-            const unsigned long long tie = __ballot(hi >= 0 && ho == mo);
-            const uint32_t wid = __popcll(tie) == 1
-                                     ? (uint32_t)__builtin_amdgcn_readlane((int)hid, __ffsll((long long)tie) - 1)
-                                     : wave_min_u32((tie >> lane) & 1ull ? hid : 0xffffffffu);
-            const int wl = (int)(wid & 63u);
-            const float wsc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, hsc), wl));
-            if (lane == wl) {
+        FST_PROBE_MARK(1);
+        float wsum = 0.0f, my_sc = 0.0f;
+        int my_id = -1;
+        for (int r = 0; r < tk; ++r) {
+            const uint32_t m = wave_max_u32_all(key[0]);
+            const unsigned long long tie = __ballot(key[0] == m);
+            int wl = __ffsll((long long)tie) - 1;
+            if (__popcll(tie) > 1) wl = (int)(wave_min_u32_all((tie >> lane) & 1ull ? (uint32_t)id[0] : 0xffffffffu) & 63u);
+            const float wsc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc[0]), wl));
+            const int wid = __builtin_amdgcn_readlane(id[0], wl);
+            if (lane == wl) {  // retire the head: shift the list up
 #pragma unroll
-                for (int i = 0; i < PER; ++i)
-                    if (i == hi) live[i] = false;
+                for (int i = 0; i + 1 < PER; ++i) {
+                    key[i] = key[i + 1];
+                    sc[i] = sc[i + 1];
+                    id[i] = id[i + 1];
+                }
+                key[PER - 1] = 0u;
             }
-            if (lane == 0) {
-                s_rank_id[wave][r] = (int)wid;
-                s_rank_sc[wave][r] = wsc;
+            wsum += wsc;
+            if (lane == r) {
+                my_id = wid;
+                my_sc = wsc;
             }
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        FST_PROBE_MARK(2);
         if (lane < tk) {
-            float sum = 0.0f;
-            for (int j = 0; j < tk; ++j) sum += s_rank_sc[wave][j];  // selection order, as the reference sums
-            const float inv = 1.0f / (sum + 1e-12f);
-            const int id = s_rank_id[wave][lane];
-            s_eids[t * tk + lane] = id;
-            eids[(size_t)t * tk + lane] = id;
-            wts[(size_t)t * tk + lane] = s_rank_sc[wave][lane] * inv * route_scale;
+            const float inv = 1.0f / (wsum + 1e-12f);
+            s_eids[t * tk + lane] = my_id;
+            if (gw) {
+                eids[(size_t)t * tk + lane] = my_id;
+                wts[(size_t)t * tk + lane] = my_sc * inv * route_scale;
+            }
         }
-        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
+    FST_PROBE_MARK(3);
     bucket_block<NT>(M, E, tk, ra.use_shared, s_eids, s_err, ra.meta, ra.slot_eid, ra.slot_M, ra.slot_off,
                      ra.pair_tok, ra.pair_of, ra.pair_shared);
 }
@@ -523,7 +555,8 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
 template <int CH, int TPW>
 __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __restrict__ w_nk,
                                                           const uint16_t* __restrict__ h, int M, int K, int E,
-                                                          float* __restrict__ logits, int nbx, int nrb,
+                                                          int score_func, int round_bf16,
+                                                          float* __restrict__ scores, int nbx, int nrb,
                                                           _Float16* __restrict__ x16p, uint4* __restrict__ sxp,
                                                           int* __restrict__ xs) {
     __shared__ float xv[kMaxPrepK];
@@ -532,18 +565,18 @@ __global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __rest
         prep_row<256>(SrcBf16{h}, b - nrb, K, xv, x16p, sxp, xs);
         return;
     }
-    router_block<CH, TPW>(w_nk, h, M, K, E, b % nbx, b / nbx, logits);
+    router_block<CH, TPW>(w_nk, h, M, K, E, b % nbx, b / nbx, score_func, round_bf16, scores);
 }
 
 void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M, int prep,
                   const int32_t* input_ids, int use_hash, int use_shared, int32_t* eids, float* wts,
-                  const Scratch& s) {
+                  const Scratch& s, int topk) {
     constexpr int TPW = 2;
     const int nbx = (g.E + 3) / 4, nby = (M + TPW - 1) / TPW, nrb = nbx * nby;
     const dim3 grid(nrb + (prep ? M : 0));
 #define FST_RP(CHV)                                                                                       \
     hipLaunchKernelGGL((router_prep_kernel<CHV, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd, g.E, \
-                       s.logits, nbx, nrb, s.x16p, s.sxp, s.xs)
+                       g.score_func, g.round_logits_bf16, s.logits, nbx, nrb, s.x16p, s.sxp, s.xs)
     if (g.hd == 4096)
         FST_RP(64);
     else if (g.hd == 2048)
@@ -553,6 +586,7 @@ void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const u
     else
         FST_RP(8);
 #undef FST_RP
+    if (!topk) return;
     const RouteArgs ra = route_args(g, L, M, s.logits, input_ids, use_hash, use_shared, eids, wts, s);
     const int per = (g.E + 63) / 64;
 #define FST_TOPK(PERV) hipLaunchKernelGGL(topk_bucket_kernel<PERV>, dim3(1), dim3(kRouteThreads), 0, st, ra)
@@ -808,12 +842,16 @@ struct EpiArgs {
 //  - the slot's activation operands are staged into LDS in macro-stages of MS
 //    super-blocks (double-buffered, prefetched one macro-stage ahead into
 //    registers), one workgroup barrier per macro-stage.
-template <int TOKS, int MS, int WAVES, int MODE, int CODEC = 0, int PF = FST_Q4K_PF>
+//  - RPER > 0 (gate||up only): the launch routes the call itself first
+//    (topk_bucket_block over ra.scores with RPER experts per lane) into LDS
+//    tables, which then replace meta/slot_*/a_row; workgroup 0 also writes
+//    eids/wts and the tables to the global arrays of ra for later launches.
+template <int TOKS, int MS, int WAVES, int MODE, int CODEC = 0, int RPER = 0, int PF = FST_Q4K_PF>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : (TOKS <= 32 ? FST_Q4K_WPE_MID : 3)))) void q4k_linear_kernel(
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
-    const int* __restrict__ meta, const int* __restrict__ slot_eid, const int* __restrict__ slot_M,
-    const int* __restrict__ slot_off, const int* __restrict__ a_row, const _Float16* __restrict__ A,
-    const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out, EpiArgs ep) {
+    const int* meta_g, const int* slot_eid_g, const int* slot_M_g,
+    const int* slot_off_g, const int* a_row_g, const _Float16* __restrict__ A,
+    const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out, EpiArgs ep, RouteArgs ra) {
     static_assert(MODE != 1 || WAVES % 2 == 0, "gate||up pairs waves");
     constexpr bool MX = CODEC == 1;                  // MXFP4 weights, bf16 operand, bf16 MFMA
     constexpr int CHUNK = MX ? 2176 : 2304;          // bytes per (16 rows x 256 weights)
@@ -829,6 +867,44 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     constexpr int U = (MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R);  // lcm(MS, R)
     static_assert(U % MS == 0 && U % R == 0, "unroll must cover whole stages and ring turns");
     __shared__ uint4 lds[2 * STAGE + 1];
+
+    // in-launch routing tables (one int each when unused)
+    constexpr int RPAIR = RPER > 0 ? TOKS * kMaxTopK : 1;  // routed pairs (M <= TOKS)
+    constexpr int RTOK = RPER > 0 ? TOKS : 1;
+    __shared__ int r_meta[META_WORDS], r_seid[RPAIR + 1], r_sM[RPAIR + 1], r_soff[RPAIR + 1];
+    __shared__ int r_ptok[RPAIR + RTOK], r_pof[RPAIR], r_psh[RTOK];
+    if constexpr (RPER > 0) {
+        static_assert(MODE == 1, "in-launch routing is the gate||up launch's");
+        RouteArgs la = ra;
+        la.meta = r_meta;
+        la.slot_eid = r_seid;
+        la.slot_M = r_sM;
+        la.slot_off = r_soff;
+        la.pair_tok = r_ptok;
+        la.pair_of = r_pof;
+        la.pair_shared = r_psh;
+        topk_bucket_block<RPER, 64 * WAVES>(la, blockIdx.x == 0);
+        __syncthreads();
+        if (blockIdx.x == 0) {
+            const int ns = r_meta[META_N_SLOTS], np = r_meta[META_N_PAIRS];
+            const int t = threadIdx.x;
+            if (t <= META_N_ROUTED_PAIRS) ra.meta[t] = r_meta[t];
+            for (int i = t; i < ns; i += 64 * WAVES) {
+                ra.slot_eid[i] = r_seid[i];
+                ra.slot_M[i] = r_sM[i];
+                ra.slot_off[i] = r_soff[i];
+            }
+            for (int i = t; i < np; i += 64 * WAVES) ra.pair_tok[i] = r_ptok[i];
+            for (int i = t; i < ra.M * ra.tk; i += 64 * WAVES) ra.pair_of[i] = r_pof[i];
+            if (ra.use_shared)
+                for (int i = t; i < ra.M; i += 64 * WAVES) ra.pair_shared[i] = r_psh[i];
+        }
+    }
+    const int* meta = RPER > 0 ? r_meta : meta_g;
+    const int* slot_eid = RPER > 0 ? r_seid : slot_eid_g;
+    const int* slot_M = RPER > 0 ? r_sM : slot_M_g;
+    const int* slot_off = RPER > 0 ? r_soff : slot_off_g;
+    const int* a_row = RPER > 0 ? r_ptok : a_row_g;
 
     const int tiles = N / (16 * WAVES);
     const int total = meta[META_N_SLOTS] * tiles;
@@ -1115,10 +1191,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
 #ifndef FST_Q4K_WG_PER_CU
 #define FST_Q4K_WG_PER_CU 2
 #endif
-template <int MODE, int CODEC = 0>
+template <int MODE, int CODEC = 0, int RPER = 0>
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
-                              const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep) {
+                              const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep,
+                              const RouteArgs& ra = RouteArgs{}) {
 #ifndef FST_Q4K_W
 #define FST_Q4K_W 8
 #endif
@@ -1130,9 +1207,9 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
         (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1)) * (8 / W);
     const dim3 grid(std::min(items, (unsigned)s.n_cu * wg_per_cu));
 #define FST_Q4K_LAUNCH(T, MSV)                                                                               \
-    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE, CODEC>), grid, dim3(64 * W), 0, st, bank, stride,  \
-                       mat_off, \
-                       K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep)
+    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE, CODEC, RPER>), grid, dim3(64 * W), 0, st, bank,      \
+                       stride, mat_off, K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep, \
+                       ra)
     // K is a multiple of 512 (checked at context creation): nsb is even
 #ifndef FST_MS8
 #define FST_MS8 1
@@ -1159,17 +1236,31 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 // h = silu(gate)*up (fp32 for Q4_K, bf16 for MXFP4).  The Q4_K operand is the
 // prescaled fp16 one (router_prep); MXFP4 stages the bf16 rows of h_in as is.
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
-                        const uint16_t* h_in) {
+                        const uint16_t* h_in, const RouteReq* rq) {
     EpiArgs ep{};
     ep.swiglu_limit = g.swiglu_limit;
     ep.h = s.act;
     ep.h16 = reinterpret_cast<uint16_t*>(s.a16p);
+    const unsigned S = (unsigned)s.max_slots;
+    const _Float16* hx = reinterpret_cast<const _Float16*>(h_in);
+    if (rq && g.E <= kFusedRouteMaxExperts) {
+        static_assert(kFusedRouteMaxExperts == 64 * 4, "4 experts per lane");
+        const RouteArgs ra = route_args(g, L, M, s.logits, rq->input_ids, rq->use_hash, rq->use_shared, rq->eids,
+                                        rq->wts, s);
+        if (g.codec == 1)
+            launch_q4k_linear<1, 1, 4>(st, M, S, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s, s.pair_tok, hx,
+                                       nullptr, nullptr, nullptr, ep, ra);
+        else
+            launch_q4k_linear<1, 0, 4>(st, M, S, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s, s.pair_tok,
+                                       s.x16p, s.sxp, s.xs, nullptr, ep, ra);
+        return;
+    }
     if (g.codec == 1)
-        launch_q4k_linear<1, 1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
-                                s.pair_tok, reinterpret_cast<const _Float16*>(h_in), nullptr, nullptr, nullptr, ep);
+        launch_q4k_linear<1, 1>(st, M, S, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s, s.pair_tok, hx, nullptr,
+                                nullptr, nullptr, ep);
     else
-        launch_q4k_linear<1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s,
-                             s.pair_tok, s.x16p, s.sxp, s.xs, nullptr, ep);
+        launch_q4k_linear<1>(st, M, S, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s, s.pair_tok, s.x16p, s.sxp,
+                             s.xs, nullptr, ep);
 }
 
 // down: y[pair][n] (fp32) for every (token, expert) pair of the call.

@@ -70,17 +70,18 @@ FST_HD float fst_bf16_to_f32(uint16_t b) { return fst_bits_f32((uint32_t)b << 16
 /* 2^n for integer n in [-126, 127]. */
 FST_HD float fst_pow2i(int n) { return fst_bits_f32((uint32_t)(n + 127) << 23); }
 
+/* Written without early returns so that a GPU build evaluates it with
+ * selects (no divergent branches); the arithmetic is the same for every x. */
 FST_HD float fst_expf(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return fst_bits_f32(0x7f800000u);
-    if (x < -87.33654022216797f) return 0.0f;    /* below 2^-126: flushed */
+    const float HI = 88.72283935546875f, LO = -87.33654022216797f; /* LO: below 2^-126 -> flushed */
     const float LOG2E = 1.44269502162933349609f;
     const float LN2_HI = 0.693145751953125f;       /* 0x3f317200 */
     const float LN2_LO = 1.42860676533018704504e-06f; /* 0x35bfbe8e */
     const float SHIFT = 12582912.0f;               /* 1.5 * 2^23 */
-    float t = fmaf(x, LOG2E, SHIFT);
+    const float xc = (x > HI) ? HI : ((x < LO) ? LO : x);  /* NaN passes through */
+    float t = fmaf(xc, LOG2E, SHIFT);
     float n = t - SHIFT;                           /* round(x*log2e) */
-    float r = fmaf(-n, LN2_HI, x);
+    float r = fmaf(-n, LN2_HI, xc);
     r = fmaf(-n, LN2_LO, r);
     float p = 1.98412698412698412526e-04f;         /* 1/5040 */
     p = fmaf(p, r, 1.38888888888888894189e-03f);   /* 1/720  */
@@ -90,10 +91,15 @@ FST_HD float fst_expf(float x) {
     p = fmaf(p, r, 0.5f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    int ni = (int)n;
-    if (ni > 127) return (p * 2.0f) * fst_pow2i(127);
-    if (ni < -126) return (p * 0.5f) * fst_pow2i(-126);
-    return p * fst_pow2i(ni);
+    int ni = (n == n) ? (int)n : 0;
+    ni = ni > 128 ? 128 : (ni < -127 ? -127 : ni);
+    const float big = (p * 2.0f) * fst_pow2i(127);
+    const float small = (p * 0.5f) * fst_pow2i(-126);
+    const float mid = p * fst_pow2i(ni > 127 ? 127 : (ni < -126 ? -126 : ni));
+    float res = (ni > 127) ? big : ((ni < -126) ? small : mid);
+    res = (x > HI) ? fst_bits_f32(0x7f800000u) : res;
+    res = (x < LO) ? 0.0f : res;
+    return (x != x) ? x : res;
 }
 
 FST_HD float fst_logf(float x) {
