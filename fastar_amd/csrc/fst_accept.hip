@@ -57,6 +57,39 @@ size_t accept_ws_bytes(int n_seq, int k, int V) {
            256;
 }
 
+// Calls f(x, v) for v = v0, v0 + stride, ... < v1 in that order, with the
+// loads of each batch of NB elements issued before any of them is used (a
+// plain loop waits for every load in turn); addresses past v1 are clamped to
+// v1 - 1 and their values unused.
+template <int NB, typename F>
+__device__ __forceinline__ void for_strided(const float* __restrict__ p, int v0, int v1, int stride, F&& f) {
+    for (int base = v0; base < v1; base += NB * stride) {
+        float x[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) x[u] = p[min(base + u * stride, v1 - 1)];
+#pragma unroll
+        for (int u = 0; u < NB; ++u)
+            if (base + u * stride < v1) f(x[u], base + u * stride);
+    }
+}
+// Two rows at once (the same indices of p and q).
+template <int NB, typename F>
+__device__ __forceinline__ void for_strided2(const float* __restrict__ p, const float* __restrict__ q, int v0,
+                                             int v1, int stride, F&& f) {
+    for (int base = v0; base < v1; base += NB * stride) {
+        float x[NB], y[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int v = min(base + u * stride, v1 - 1);
+            x[u] = p[v];
+            y[u] = q ? q[v] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u)
+            if (base + u * stride < v1) f(x[u], y[u], base + u * stride);
+    }
+}
+
 __device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int n_tgt_rows,
                                                 int r, int V) {
     return r < n_tgt_rows ? target + (size_t)r * V : draft + (size_t)(r - n_tgt_rows) * V;
@@ -73,11 +106,11 @@ __global__ __launch_bounds__(256) void acc_stats_kernel(const float* __restrict_
     const int b0 = c * clen, b1 = min(V, b0 + clen);
     float best = 0.0f;
     int bi = 0x7fffffff;
-    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) {
-        const float l = row[v] * inv_t;
-        if (l != l) continue;
+    for_strided<8>(row, b0 + (int)threadIdx.x, b1, 256, [&](float x, int v) {
+        const float l = x * inv_t;
+        if (l != l) return;
         if (bi == 0x7fffffff || l > best) { best = l; bi = v; }
-    }
+    });
     if (bi == 0x7fffffff) bi = -1;
     wave_argmax(best, bi);
     __shared__ float sm[4];
@@ -182,7 +215,7 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
     const int clen = (V + kChunks - 1) / kChunks;
     const int b0 = c * clen, b1 = min(V, b0 + clen);
     unsigned long long acc = 0;
-    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) acc += fixed_prob(row[v], inv_t, mx, any);
+    for_strided<8>(row, b0 + (int)threadIdx.x, b1, 256, [&](float x, int) { acc += fixed_prob(x, inv_t, mx, any); });
     __shared__ unsigned long long sm[256];
     sm[threadIdx.x] = acc;
     __syncthreads();
@@ -262,14 +295,19 @@ __global__ __launch_bounds__(64 * kDecideWaves) void acc_decide_kernel(
     }
 }
 
+// Residual weight of one element from its target (xt) and draft (xd) logits.
+__device__ __forceinline__ u128 res_of(float xt, float xd, float inv_t, float mp, int ap, float mq, int aq,
+                                       unsigned long long Sp, unsigned long long Sq, int mode) {
+    const unsigned long long P = fixed_prob(xt, inv_t, mp, ap);
+    if (mode) return (u128)P;
+    const unsigned long long Q = fixed_prob(xd, inv_t, mq, aq);
+    const u128 a = (u128)P * Sq, b = (u128)Q * Sp;
+    return a > b ? a - b : (u128)0;
+}
 __device__ __forceinline__ u128 res_value(const float* trow, const float* drow, int v, float inv_t,
                                           float mp, int ap, float mq, int aq, unsigned long long Sp,
                                           unsigned long long Sq, int mode) {
-    const unsigned long long P = fixed_prob(trow[v], inv_t, mp, ap);
-    if (mode) return (u128)P;
-    const unsigned long long Q = fixed_prob(drow[v], inv_t, mq, aq);
-    const u128 a = (u128)P * Sq, b = (u128)Q * Sp;
-    return a > b ? a - b : (u128)0;
+    return res_of(trow[v], mode ? 0.0f : drow[v], inv_t, mp, ap, mq, aq, Sp, Sq, mode);
 }
 
 struct RowCtx {
@@ -317,8 +355,9 @@ __global__ __launch_bounds__(256) void acc_res_chunks_kernel(
     const int clen = (V + kChunks - 1) / kChunks;
     const int b0 = c * clen, b1 = min(V, b0 + clen);
     u128 acc = 0;
-    for (int v = b0 + (int)threadIdx.x; v < b1; v += 256)
-        acc += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+    for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, b0 + (int)threadIdx.x, b1, 256, [&](float xt, float xd, int) {
+        acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+    });
     __shared__ u128 sm[256];
     sm[threadIdx.x] = acc;
     __syncthreads();
@@ -409,8 +448,9 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
         const int per = (clen + 255) / 256;
         const int v0 = b0 + tid * per, v1 = min(b1, v0 + per);
         u128 acc = 0;
-        for (int v = v0; v < v1; ++v)
-            acc += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+        for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, v0, v1, 1, [&](float xt, float xd, int) {
+            acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+        });
         const u128 pre = wave_incl_scan_u128(acc);
         if (lane == 63) wtot[wave] = pre;
         if (tid == 0) s_owner = 0x7fffffff;
@@ -469,16 +509,27 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
         }
     };
     if ((V & 3) == 0) {
-        // 16-byte loads: thread t takes elements b0 + 4(t + 256 j) .. +3, in index order
-        for (int v = b0 + 4 * (int)threadIdx.x; v < b1; v += 1024) {
-            const float4 q = *reinterpret_cast<const float4*>(row + v);
-            take(q.x, v);
-            take(q.y, v + 1);
-            take(q.z, v + 2);
-            take(q.w, v + 3);
+        // 16-byte loads: thread t takes elements b0 + 4(t + 256 j) .. +3, in
+        // index order; each batch of 8 loads is issued before any is used
+        // (b1 - b0 is a multiple of 4 here, so b1 - 4 is a valid clamp)
+        constexpr int NB = 8;
+        for (int base = b0 + 4 * (int)threadIdx.x; base < b1; base += NB * 1024) {
+            float4 q[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) q[u] = *reinterpret_cast<const float4*>(row + min(base + u * 1024, b1 - 4));
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int v = base + u * 1024;
+                if (v < b1) {
+                    take(q[u].x, v);
+                    take(q[u].y, v + 1);
+                    take(q[u].z, v + 2);
+                    take(q[u].w, v + 3);
+                }
+            }
         }
     } else {
-        for (int v = b0 + (int)threadIdx.x; v < b1; v += 256) take(row[v], v);
+        for_strided<8>(row, b0 + (int)threadIdx.x, b1, 256, [&](float x, int v) { take(x, v); });
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (bi == 0x7fffffff) bi = -1;

@@ -140,13 +140,13 @@ __device__ __forceinline__ unsigned long long topk_key(float sel, int id) {
 // distinct pairs (the number of down contributions its combine waits for).
 // eids_s: the call's [M][tk] expert ids, already in LDS.  One workgroup of NT
 // threads.
-template <int NT>
+template <int NT, int MAXE = kMaxExperts>
 __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* eids_s, int topk_err,
                              int* __restrict__ meta, int* __restrict__ slot_eid, int* __restrict__ slot_M,
                              int* __restrict__ slot_off, int* __restrict__ pair_tok,
                              int* __restrict__ pair_of, int* __restrict__ pair_shared) {
-    __shared__ unsigned long long hitmask[kMaxExperts];
-    __shared__ int eoff[kMaxExperts];
+    __shared__ unsigned long long hitmask[MAXE];
+    __shared__ int eoff[MAXE];
     __shared__ int err;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     if (tid == 0) err = 0;
@@ -281,7 +281,7 @@ struct RouteArgs {
 // barrier the same workgroup groups all tokens' (token, expert) pairs.  PER =
 // experts per lane.  gw: write eids/wts (the bucket tables always go to the
 // pointers in ra, global or LDS).
-template <int PER, int NT>
+template <int PER, int NT, int MAXT = kMaxTokens>
 __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
     const int M = ra.M, E = ra.E, tk = ra.tk;
     const float route_scale = ra.route_scale;
@@ -293,7 +293,7 @@ __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
     int32_t* __restrict__ eids = ra.eids;
     float* __restrict__ wts = ra.wts;
     constexpr int NW = NT / 64;
-    __shared__ int s_eids[kMaxTokens * kMaxTopK];
+    __shared__ int s_eids[MAXT * kMaxTopK];
     __shared__ int s_err;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const float zero_score = ra.score_func == 0 ? fst_sigmoidf(0.0f) : fst_sqrtsoftplusf(0.0f);
@@ -409,7 +409,7 @@ __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
     }
     __syncthreads();
     FST_PROBE_MARK(3);
-    bucket_block<NT>(M, E, tk, ra.use_shared, s_eids, s_err, ra.meta, ra.slot_eid, ra.slot_M, ra.slot_off,
+    bucket_block<NT, (PER * 64 < kMaxExperts ? PER * 64 : kMaxExperts)>(M, E, tk, ra.use_shared, s_eids, s_err, ra.meta, ra.slot_eid, ra.slot_M, ra.slot_off,
                      ra.pair_tok, ra.pair_of, ra.pair_shared);
 }
 
@@ -883,7 +883,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         la.pair_tok = r_ptok;
         la.pair_of = r_pof;
         la.pair_shared = r_psh;
-        topk_bucket_block<RPER, 64 * WAVES>(la, blockIdx.x == 0);
+        topk_bucket_block<RPER, 64 * WAVES, TOKS>(la, blockIdx.x == 0);
         __syncthreads();
         if (blockIdx.x == 0) {
             const int ns = r_meta[META_N_SLOTS], np = r_meta[META_N_PAIRS];
