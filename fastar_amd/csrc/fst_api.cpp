@@ -546,10 +546,17 @@ static int check_meta_error(fst_ctx* ctx) {
     return FST_OK;
 }
 
+// Device activation / logits buffers are read with 16-byte loads (null
+// pointers, i.e. absent optional buffers, pass).
+static bool misaligned(const void* a, const void* b = nullptr, const void* c = nullptr, const void* d = nullptr) {
+    return (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)d) & 15u) != 0;
+}
+
 int fst_moe_layer_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_input_ids,
                       uint16_t* d_out, int32_t* d_eids, float* d_wts) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (!d_h || !d_out) return fail(FST_EINVAL, "null device buffer");
+    if (misaligned(d_h, d_out)) return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
     int32_t* e = d_eids ? d_eids : ctx->s.eids;
     float* w = d_wts ? d_wts : ctx->s.wts;
     return run_moe(ctx, lid, d_h, M, d_input_ids, 1, e, w, ctx->cfg.top_k, 1, ctx->cfg.has_shared, d_out,
@@ -561,6 +568,8 @@ int fst_moe_ffn_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int
                     uint16_t* d_out_shared) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (!d_h || !d_eids || !d_wts) return fail(FST_EINVAL, "null device buffer");
+    if (misaligned(d_h, d_out, d_out_routed, d_out_shared))
+        return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
     return run_moe(ctx, lid, d_h, M, nullptr, 0, const_cast<int32_t*>(d_eids), const_cast<float*>(d_wts),
                    ctx->cfg.top_k, 1, use_shared, d_out, d_out_routed, d_out_shared);
 }
@@ -679,6 +688,7 @@ int fst_accept_greedy_dev(fst_ctx* ctx, const float* d_target, int n_seq, int k,
                           int32_t* d_n_acc, int32_t* d_tokens) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (int rc = check_accept_args(n_seq, k, V)) return rc;
+    if (misaligned(d_target)) return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
     if (int rc = accept_ws(ctx, n_seq, k, V)) return rc;
     ctx->mark_begin();
     fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens, ctx->acc_ws);
@@ -917,6 +927,7 @@ int fst_rmsnorm_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, const uint16_t* 
     if (lid < 0 || lid > ctx->cfg.n_layers) return fail(FST_EINVAL, "norm id must be in [0, n_layers]");
     if (!ctx->has_norm[lid]) return fail(FST_ENOTREADY, "norm weights not uploaded");
     if (!d_h || !d_normed) return fail(FST_EINVAL, "null device buffer");
+    if (misaligned(d_h, d_y, d_h_out, d_normed)) return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
     if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
     const int hd = ctx->cfg.hidden_dim;
     fst::launch_resid_norm(ctx->st, d_h, d_y, ctx->norms + (size_t)lid * hd, M, hd, kNormEps, d_h_out, d_normed,
@@ -949,6 +960,7 @@ static int final_head(fst_ctx* ctx, uint16_t* d_h, const uint16_t* d_y, int M, f
 int fst_lm_head_dev(fst_ctx* ctx, const uint16_t* d_h, int M, float* d_logits) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (!d_h || !d_logits) return fail(FST_EINVAL, "null device buffer");
+    if (misaligned(d_h, d_logits)) return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
     if (M <= 0 || M > ctx->cfg.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
     ctx->mark_begin();
     if (int rc = final_head(ctx, const_cast<uint16_t*>(d_h), nullptr, M, d_logits)) return rc;
@@ -1030,6 +1042,7 @@ int fst_hc_head_dev(fst_ctx* ctx, const uint16_t* d_h_hc, int M, uint16_t* d_pla
 int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_input_ids, float* d_logits) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (!d_h || !d_logits) return fail(FST_EINVAL, "null device buffer");
+    if (misaligned(d_h, d_logits)) return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
     const fst_config& c = ctx->cfg;
     if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
     for (int l = 0; l < c.n_layers; ++l)

@@ -439,15 +439,39 @@ void launch_bucket(hipStream_t st, const Geometry& g, int M, int use_shared, con
 
 // Element sources for the prep kernel: bf16 activations, or the fp32
 // h = silu(gate)*up rows written by the gate/up kernel.
+// (kVec: elements per 16-byte vector load; vec() loads vector q of a row,
+// unpack() widens it to floats)
 struct SrcBf16 {
+    static constexpr int kVec = 8;
     const uint16_t* p;
     __device__ __forceinline__ float at(size_t row, int K, int i) const {
         return fst_bf16_to_f32(p[row * K + i]);
     }
+    __device__ __forceinline__ uint4 vec(size_t row, int K, int q) const {
+        return reinterpret_cast<const uint4*>(p + row * K)[q];
+    }
+    __device__ __forceinline__ void unpack(const uint4& v, float* f) const {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = fst_bits_f32(w[i] << 16);
+            f[2 * i + 1] = fst_bits_f32(w[i] & 0xffff0000u);
+        }
+    }
 };
 struct SrcF32 {
+    static constexpr int kVec = 4;
     const float* p;
     __device__ __forceinline__ float at(size_t row, int K, int i) const { return p[row * K + i]; }
+    __device__ __forceinline__ uint4 vec(size_t row, int K, int q) const {
+        return reinterpret_cast<const uint4*>(p + row * K)[q];
+    }
+    __device__ __forceinline__ void unpack(const uint4& v, float* f) const {
+        f[0] = fst_bits_f32(v.x);
+        f[1] = fst_bits_f32(v.y);
+        f[2] = fst_bits_f32(v.z);
+        f[3] = fst_bits_f32(v.w);
+    }
 };
 constexpr int kMaxPrepK = 8192;
 
@@ -474,10 +498,34 @@ __device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __
     __shared__ float red[NT / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float m = 0.0f;
-    for (int i = tid; i < K; i += NT) {
-        const float v = src.at(row, K, i);
-        xv[i] = v;
-        m = fmaxf(m, fabsf(v));
+    if constexpr (Src::kVec > 0) {
+        // 16-byte loads, each thread's batch issued before any is used
+        constexpr int VE = Src::kVec, NB = 4;
+        const int nv = K / VE;
+        for (int q0 = tid; q0 < nv; q0 += NB * NT) {
+            uint4 v[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) v[u] = src.vec(row, K, min(q0 + u * NT, nv - 1));
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int q = q0 + u * NT;
+                if (q < nv) {
+                    float f[VE];
+                    src.unpack(v[u], f);
+#pragma unroll
+                    for (int e = 0; e < VE; ++e) {
+                        xv[q * VE + e] = f[e];
+                        m = fmaxf(m, fabsf(f[e]));
+                    }
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < K; i += NT) {
+            const float v = src.at(row, K, i);
+            xv[i] = v;
+            m = fmaxf(m, fabsf(v));
+        }
     }
     m = wave_fmax(m);
     if (lane == 0) red[wave] = m;
@@ -612,6 +660,7 @@ void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float
 
 // Element source reading a row already held in LDS.
 struct SrcRow {
+    static constexpr int kVec = 0;  // already in LDS: element loads
     const float* p;
     __device__ __forceinline__ float at(size_t, int, int i) const { return p[i]; }
 };
@@ -646,11 +695,39 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
         slot_tab[META_WORDS + 1] = M;  // slot_M
         slot_tab[META_WORDS + 2] = 0;  // slot_off
     }
-    for (int j = tid; j < d; j += 256) {
-        float x = fst_bf16_to_f32(h[(size_t)t * d + j]);
-        if (y) x = fst_bf16_to_f32(fst_f32_to_bf16(x + fst_bf16_to_f32(y[(size_t)t * d + j])));
-        xrow[j] = x;
-        if (h_out) h_out[(size_t)t * d + j] = fst_f32_to_bf16(x);
+    // 8 elements per 16-byte load (d is a multiple of 256), each thread's
+    // loads issued before any is used
+    const int nv = d / 8;
+    constexpr int NB = 4;
+    for (int q0 = tid; q0 < nv; q0 += NB * 256) {
+        uint4 hv[NB], yv[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int q = min(q0 + u * 256, nv - 1);
+            hv[u] = reinterpret_cast<const uint4*>(h + (size_t)t * d)[q];
+            yv[u] = y ? reinterpret_cast<const uint4*>(y + (size_t)t * d)[q] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int q = q0 + u * 256;
+            if (q >= nv) continue;
+            const uint32_t hw[4] = {hv[u].x, hv[u].y, hv[u].z, hv[u].w};
+            const uint32_t yw[4] = {yv[u].x, yv[u].y, yv[u].z, yv[u].w};
+            uint32_t ow[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t o2 = 0u;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float x = fst_bf16_to_f32((uint16_t)(hw[i] >> (16 * hh)));
+                    if (y) x = fst_bf16_to_f32(fst_f32_to_bf16(x + fst_bf16_to_f32((uint16_t)(yw[i] >> (16 * hh)))));
+                    xrow[8 * q + 2 * i + hh] = x;
+                    o2 |= (uint32_t)fst_f32_to_bf16(x) << (16 * hh);
+                }
+                ow[i] = o2;
+            }
+            if (h_out) reinterpret_cast<uint4*>(h_out + (size_t)t * d)[q] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        }
     }
     __syncthreads();
     if (tid < 64) {
@@ -670,10 +747,30 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
     }
     __syncthreads();
     const float r = s_r;
-    for (int j = tid; j < d; j += 256) {
-        const uint16_t o = fst_f32_to_bf16((xrow[j] * r) * fst_bf16_to_f32(w[j]));
-        nrow[j] = fst_bf16_to_f32(o);
-        if (normed) normed[(size_t)t * d + j] = o;
+    for (int q0 = tid; q0 < nv; q0 += NB * 256) {
+        uint4 wv[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) wv[u] = reinterpret_cast<const uint4*>(w)[min(q0 + u * 256, nv - 1)];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int q = q0 + u * 256;
+            if (q >= nv) continue;
+            const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+            uint32_t ow[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t o2 = 0u;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int j = 8 * q + 2 * i + hh;
+                    const uint16_t o = fst_f32_to_bf16((xrow[j] * r) * fst_bf16_to_f32((uint16_t)(ww[i] >> (16 * hh))));
+                    nrow[j] = fst_bf16_to_f32(o);
+                    o2 |= (uint32_t)o << (16 * hh);
+                }
+                ow[i] = o2;
+            }
+            if (normed) reinterpret_cast<uint4*>(normed + (size_t)t * d)[q] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        }
     }
     __syncthreads();
     if (x16p) prep_row<256>(SrcRow{nrow}, t, d, xrow, x16p, sxp, xs);
@@ -1293,6 +1390,7 @@ void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, con
 // term (weight 1.0), one RNE rounding.  The shared term is its pair's row of y,
 // or row t of ys when the shared expert ran from bf16 weights.  One thread per
 // 4 consecutive columns of one token.
+template <int TK>
 __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int use_shared,
                                                       const float* __restrict__ y,
                                                       const int* __restrict__ pair_of,
@@ -1305,20 +1403,28 @@ __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int
     const int t = blockIdx.y;
     const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (t >= M || n >= hd) return;
-    int p[kMaxTopK];
-    float w[kMaxTopK];
-    for (int j = 0; j < tk; ++j) {
-        p[j] = pair_of[t * tk + j];
-        w[j] = wts[t * tk + j];
+    // every load issued before the sums (slots past tk or without a pair
+    // read row 0 of y and are not summed)
+    int p[TK];
+    float w[TK];
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+        p[j] = pair_of[t * tk + min(j, tk - 1)];
+        w[j] = wts[t * tk + min(j, tk - 1)];
     }
+    float4 v[TK];
+#pragma unroll
+    for (int j = 0; j < TK; ++j) v[j] = *reinterpret_cast<const float4*>(y + (size_t)max(p[j], 0) * hd + n);
+    const float4 vs = use_shared ? *reinterpret_cast<const float4*>((ys ? ys + (size_t)t * hd : y + (size_t)pair_shared[t] * hd) + n)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < tk; ++j) {
-        if (p[j] < 0) continue;
-        const float4 v = *reinterpret_cast<const float4*>(y + (size_t)p[j] * hd + n);
-        a.x = a.x + w[j] * v.x;
-        a.y = a.y + w[j] * v.y;
-        a.z = a.z + w[j] * v.z;
-        a.w = a.w + w[j] * v.w;
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+        if (j >= tk || p[j] < 0) continue;
+        a.x = a.x + w[j] * v[j].x;
+        a.y = a.y + w[j] * v[j].y;
+        a.z = a.z + w[j] * v[j].z;
+        a.w = a.w + w[j] * v[j].w;
     }
     auto put = [&](uint16_t* o, const float4& v) {
         if (!o) return;
@@ -1328,13 +1434,11 @@ __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int
     };
     put(out_routed, a);
     if (use_shared) {
-        const float* src = ys ? ys + (size_t)t * hd : y + (size_t)pair_shared[t] * hd;
-        const float4 v = *reinterpret_cast<const float4*>(src + n);
-        put(out_shared, v);
-        a.x = a.x + v.x;
-        a.y = a.y + v.y;
-        a.z = a.z + v.z;
-        a.w = a.w + v.w;
+        put(out_shared, vs);
+        a.x = a.x + vs.x;
+        a.y = a.y + vs.y;
+        a.z = a.z + vs.z;
+        a.w = a.w + vs.w;
     }
     put(out, a);
 }
@@ -1342,8 +1446,14 @@ __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int
 void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
                     const float* wts, const float* ys, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared) {
     dim3 grid((g.hd / 4 + 255) / 256, M);
-    hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, st, M, g.hd, g.tk, use_shared, s.y, s.pair_of,
-                       s.pair_shared, ys, wts, out, out_routed, out_shared);
+#define FST_COMB(T)                                                                                              \
+    hipLaunchKernelGGL(combine_kernel<T>, grid, dim3(256), 0, st, M, g.hd, g.tk, use_shared, s.y, s.pair_of, \
+                       s.pair_shared, ys, wts, out, out_routed, out_shared)
+    if (g.tk <= 8)
+        FST_COMB(8);
+    else
+        FST_COMB(kMaxTopK);
+#undef FST_COMB
 }
 
 // --------------------------------------------------------------------- copy

@@ -19,8 +19,11 @@
  * FST_* status code; fst_last_error() gives the message of the last failure
  * on the calling thread.  Host-pointer entry points are synchronous.  The
  * *_dev entry points take device pointers and are asynchronous on the
- * context's stream (fst_stream()); fst_sync() waits for them.  A context is
- * not re-entrant: calls on one context must not overlap.
+ * context's stream (fst_stream()); fst_sync() waits for them.  Their
+ * activation and logits buffers must be 16-byte aligned (hipMalloc and
+ * fst_device_alloc give 256; FST_EINVAL otherwise), as the kernels read them
+ * with 16-byte loads.  A context is not re-entrant: calls on one context
+ * must not overlap.
  */
 #ifndef FST_HIP_H
 #define FST_HIP_H
