@@ -121,3 +121,24 @@ def test_moe_layer_dev_matches_host_entry(fa, c2_layer):
             ctx.dev_free(p)
     assert np.array_equal(e, e_h) and np.array_equal(w, w_h)
     assert np.array_equal(out, out_h)   # same inputs, same launch chain: deterministic
+
+
+def test_dev_entry_points_reject_misaligned_buffers(fa, c2_layer):
+    """The kernels read activations and logits with 16-byte loads: a device
+    pointer off a 16-byte boundary is rejected with FST_EINVAL, nothing runs."""
+    ctx, seed, _ = c2_layer
+    L = fa.lib()
+    M = 2
+    note("misaligned device buffers -> EINVAL")
+    dh, do = ctx.dev_alloc(M * HD * 2 + 64), ctx.dev_alloc(M * HD * 2 + 64)
+    dl = ctx.dev_alloc(8 * 1024 * 4 + 64)
+    try:
+        assert L.fst_moe_layer_dev(ctx.h, 0, dh + 2, M, None, do, None, None) == fa.FST_EINVAL
+        assert L.fst_moe_layer_dev(ctx.h, 0, dh, M, None, do + 8, None, None) == fa.FST_EINVAL
+        assert L.fst_accept_greedy_dev(ctx.h, dl + 4, 1, 7, 1024, dh, do, do) == fa.FST_EINVAL
+        # the same buffers aligned run
+        fa._check(L.fst_moe_layer_dev(ctx.h, 0, dh, M, None, do, None, None))
+        ctx.sync()
+    finally:
+        for p in (dh, do, dl):
+            ctx.dev_free(p)
