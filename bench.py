@@ -30,6 +30,7 @@ PROJ_BYTES = INTER * (HD // 256) * 144          # one Q4_K projection, 4,718,592
 EXPERT_BYTES = 3 * PROJ_BYTES                    # 14,155,776 B
 ROUTER_BYTES = HD * E * 2
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 
 
 def log(*a):
@@ -350,6 +351,11 @@ def main():
     n_acc = int(ctx.to_host(bufs["nacc"], (1,), np.int32)[0])
 
     gu_achieved = np.mean(bytes_gu) / np.mean(dur_gu) / 1e9
+    # MFMA work of the gate|up launch: every 16-row x 256-weight chunk (2304 B)
+    # issues 8 fp16 16x16x32 MFMAs plus 1 for the min term (16,384 flops each);
+    # useful flops are 2 x (M*top_k routed + M shared pairs) x K x N
+    gu_issued = np.mean(bytes_gu) / 2304.0 * 9 * 16384
+    gu_useful = 2.0 * (M * TK + M) * HD * (2 * INTER)
     dn_achieved = np.mean(bytes_dn) / np.mean(dur_dn) / 1e9
     mean_act = float(np.mean(n_act))
     step_bytes = (mean_act + 1) * EXPERT_BYTES + ROUTER_BYTES
@@ -406,6 +412,13 @@ def main():
             "frac": round(gu_achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
             "algorithmic_bytes": int(np.mean(bytes_gu)),
+        },
+        "mfma": {
+            "kernel": "q4k_linear gate+up",
+            "issued_tflops": round(gu_issued / np.mean(dur_gu) / 1e12, 1),
+            "useful_tflops": round(gu_useful / np.mean(dur_gu) / 1e12, 1),
+            "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+            "util": round(gu_issued / np.mean(dur_gu) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
         },
         "packed_weight_GBps_step": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         "down_kernel_GBps": round(dn_achieved, 1),
