@@ -1029,11 +1029,29 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         return bank + (size_t)slot_eid[sl] * expert_stride + mat_offset +
                (size_t)wave_tile(tt - sl * tiles) * nsb * CHUNK;
     };
-    auto load_w = [&](const uint8_t* chunk) -> WRaw {
-        if constexpr (MX)
-            return load_wraw_mx(chunk, lane);
-        else
-            return load_wraw(chunk, lane);
+    // Weight loads go through a buffer resource on the wave's run (uniform:
+    // scalar base, the chunk offset in soffset, constant lane offsets), so no
+    // per-step 64-bit address arithmetic runs on the vector ALUs.
+    auto rsrc = [&](const uint8_t* p) -> __amdgpu_buffer_rsrc_t {
+        const uint64_t u = (uint64_t)(uintptr_t)p;
+        const uint64_t us = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
+                            (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+        // num_records: the run; dword 3: 32-bit data format (raw loads)
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)us, (short)0, nsb * CHUNK, 0x00020000);
+    };
+    constexpr int kNT = 2;  // cache policy: non-temporal (streamed once)
+    auto load_w = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WRaw {
+        WRaw x;
+        x.a = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, off, kNT);
+        x.b = __builtin_amdgcn_raw_buffer_load_b128(rs, 1024 + 16 * lane, off, kNT);
+        if constexpr (MX) {
+            typedef uint32_t u2v_t __attribute__((ext_vector_type(2)));
+            const u2v_t hv = __builtin_amdgcn_raw_buffer_load_b64(rs, 2048 + 8 * (lane & 15), off, kNT);
+            x.h = u4v_t{hv.x, hv.y, 0u, 0u};
+        } else {
+            x.h = __builtin_amdgcn_raw_buffer_load_b128(rs, 2048 + 16 * (lane & 15), off, kNT);
+        }
+        return x;
     };
 
     // Every global load below is unconditional, with clamped addresses, and
@@ -1041,10 +1059,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     // position: the number of loads in flight is then the same on every path
     // and the compiler waits only for the oldest super-block instead of
     // draining the prefetch ring at each step.
-    const uint8_t* wbase = wave_base(blockIdx.x);
+    __amdgpu_buffer_rsrc_t wrs = rsrc(wave_base(blockIdx.x));
     WRaw w[R];
 #pragma unroll
-    for (int j = 0; j < PF; ++j) w[j] = load_w(wbase + (size_t)j * CHUNK);
+    for (int j = 0; j < PF; ++j) w[j] = load_w(wrs, j * CHUNK);
     for (int i = tid; i < 2 * STAGE + 1; i += NT) lds[i] = z4;
 
     // Staging map: chunk q = tid + NT*i of a macro-stage -> (super-block u,
@@ -1119,7 +1137,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         const int slot = t / tiles;
         const int tile = t - slot * tiles;
         const int tn = t + (int)gridDim.x;
-        const uint8_t* nbase = tn < total ? wave_base(tn) : wbase;
+        const __amdgpu_buffer_rsrc_t nrs = tn < total ? rsrc(wave_base(tn)) : wrs;
         const int Me = min(slot_M[slot], TOKS), off = slot_off[slot];
         const int row = wave_tile(tile) * 16 + r;
         int ar_next[NS];
@@ -1207,7 +1225,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                     }
                 }
                 const int pf = sb + PF;
-                w[(j + PF) % R] = load_w(pf < nsb ? wbase + (size_t)pf * CHUNK : nbase + (size_t)(pf - nsb) * CHUNK);
+                w[(j + PF) % R] = pf < nsb ? load_w(wrs, pf * CHUNK) : load_w(nrs, (pf - nsb) * CHUNK);
                 // keep the prefetches where they are issued (the scheduler
                 // would otherwise sink them next to their use to save registers)
                 __builtin_amdgcn_sched_barrier(0);
@@ -1218,7 +1236,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                 }
             }
         }
-        wbase = nbase;
+        wrs = nrs;
 
         // D layout: lane holds token rows 4g+i (i=0..3) of the group, column r.
         auto unscale = [&](int pidx) -> int {
