@@ -143,6 +143,16 @@ __device__ __forceinline__ void wave_row_argmax(const float* part_max, const int
 
 __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) { return wave_sum_u64_dpp(v); }
 
+// Wave-wide sum of a u128 as four 32-bit limbs summed exactly in u64, then
+// recombined (result in every lane).
+__device__ __forceinline__ u128 wave_sum_u128(u128 v) {
+    u128 t = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t += (u128)wave_sum_u64_dpp((uint32_t)(v >> (32 * k))) << (32 * k);
+    return t;
+}
+
+
 // One wave per sequence: rows reduced one after another, chunks across lanes.
 __global__ __launch_bounds__(64) void acc_greedy_final_kernel(const float* __restrict__ target, int k,
                                                               int V, const float* __restrict__ part_max,
@@ -216,14 +226,12 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
     const int b0 = c * clen, b1 = min(V, b0 + clen);
     unsigned long long acc = 0;
     for_strided<8>(row, b0 + (int)threadIdx.x, b1, 256, [&](float x, int) { acc += fixed_prob(x, inv_t, mx, any); });
-    __shared__ unsigned long long sm[256];
-    sm[threadIdx.x] = acc;
+    // integer sums: any order gives the same total
+    __shared__ unsigned long long sm[4];
+    acc = wave_sum_u64_dpp(acc);
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
     __syncthreads();
-    for (int off = 128; off >= 1; off >>= 1) {
-        if ((int)threadIdx.x < off) sm[threadIdx.x] += sm[threadIdx.x + off];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) part_sum[(size_t)r * kChunks + c] = sm[0];
+    if (threadIdx.x == 0) part_sum[(size_t)r * kChunks + c] = (sm[0] + sm[1]) + (sm[2] + sm[3]);
 }
 
 // dec layout per sequence: [0] n_acc, [1] sampling target row, [2] mode
@@ -358,17 +366,16 @@ __global__ __launch_bounds__(256) void acc_res_chunks_kernel(
     for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, b0 + (int)threadIdx.x, b1, 256, [&](float xt, float xd, int) {
         acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
     });
-    __shared__ u128 sm[256];
-    sm[threadIdx.x] = acc;
+    // integer sums: any order gives the same total
+    __shared__ u128 sm[4];
+    acc = wave_sum_u128(acc);
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
     __syncthreads();
-    for (int off = 128; off >= 1; off >>= 1) {
-        if ((int)threadIdx.x < off) sm[threadIdx.x] += sm[threadIdx.x + off];
-        __syncthreads();
-    }
     if (threadIdx.x == 0) {
+        const u128 tot = (sm[0] + sm[1]) + (sm[2] + sm[3]);
         unsigned long long* o = part_res + ((size_t)s * kChunks + c) * 2;
-        o[0] = (unsigned long long)sm[0];
-        o[1] = (unsigned long long)(sm[0] >> 64);
+        o[0] = (unsigned long long)tot;
+        o[1] = (unsigned long long)(tot >> 64);
     }
 }
 
@@ -447,10 +454,30 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
         const int b0 = c * clen, b1 = min(V, b0 + clen);
         const int per = (clen + 255) / 256;
         const int v0 = b0 + tid * per, v1 = min(b1, v0 + per);
+        // the thread's residual values stay in registers for the owner's walk
+        // (runs of up to kCache elements; longer ones are recomputed there)
+        constexpr int kCache = 16;
+        u128 cache[kCache];
         u128 acc = 0;
-        for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, v0, v1, 1, [&](float xt, float xd, int) {
-            acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
-        });
+        if (per <= kCache) {
+            float xt[kCache], xd[kCache];
+#pragma unroll
+            for (int u = 0; u < kCache; ++u) {
+                const int v = max(min(v0 + u, v1 - 1), 0);
+                xt[u] = rc.trow[v];
+                xd[u] = rc.mode ? 0.0f : rc.drow[v];
+            }
+#pragma unroll
+            for (int u = 0; u < kCache; ++u) {
+                cache[u] = v0 + u < v1 ? res_of(xt[u], xd[u], inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode)
+                                       : (u128)0;
+                acc += cache[u];
+            }
+        } else {
+            for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, v0, v1, 1, [&](float xt, float xd, int) {
+                acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+            });
+        }
         const u128 pre = wave_incl_scan_u128(acc);
         if (lane == 63) wtot[wave] = pre;
         if (tid == 0) s_owner = 0x7fffffff;
@@ -465,12 +492,24 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
         if (tid == s_owner) {
             u128 run = s_run;
             int tok = v1 - 1;
-            for (int v = v0; v < v1; ++v) {
-                run += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq,
-                                 rc.mode);
-                if (run > s_target) {
-                    tok = v;
-                    break;
+            if (per <= kCache) {
+#pragma unroll
+                for (int u = 0; u < kCache; ++u) {
+                    if (v0 + u >= v1) break;
+                    run += cache[u];
+                    if (run > s_target) {
+                        tok = v0 + u;
+                        break;
+                    }
+                }
+            } else {
+                for (int v = v0; v < v1; ++v) {
+                    run += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq,
+                                     rc.mode);
+                    if (run > s_target) {
+                        tok = v;
+                        break;
+                    }
                 }
             }
             s_tok = tok;

@@ -28,11 +28,6 @@
 #include "fst_internal.h"
 #include "../../include/fst_exact_math.h"
 
-// Timing hook for probe builds (empty in the library).
-#ifndef FST_PROBE_MARK
-#define FST_PROBE_MARK(i)
-#endif
-
 namespace fst {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -161,7 +156,6 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
             atomicOr(&hitmask[e], 1ull << t);
     }
     __syncthreads();
-    FST_PROBE_MARK(5);
     const int s0 = use_shared ? 1 : 0, p0 = use_shared ? M : 0;
     // Slots and pairs numbered in ascending expert id, one expert per
     // thread: exclusive prefix counts within each wave from ballots (a count
@@ -209,7 +203,6 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
         pair_base += tc;
         __syncthreads();
     }
-    FST_PROBE_MARK(6);
     for (int i = tid; i < M * tk; i += NT) {
         const int t = i / tk;
         const int e = eids_s[i];
@@ -231,7 +224,6 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
         slot_off[0] = 0;
     }
     __syncthreads();
-    FST_PROBE_MARK(4);
     if (tid == 0) {
         meta[META_N_ROUTED] = slot_base - s0;
         meta[META_N_SLOTS] = slot_base;
@@ -297,7 +289,6 @@ __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
     __shared__ int s_err;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const float zero_score = ra.score_func == 0 ? fst_sigmoidf(0.0f) : fst_sqrtsoftplusf(0.0f);
-    FST_PROBE_MARK(0);
     if (tid == 0) s_err = 0;
     __syncthreads();
     for (int t = wave; t < M; t += NW) {
@@ -372,7 +363,6 @@ __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
                     id[j] = id[j + 1];
                     id[j + 1] = c;
                 }
-        FST_PROBE_MARK(1);
         float wsum = 0.0f, my_sc = 0.0f;
         int my_id = -1;
         for (int r = 0; r < tk; ++r) {
@@ -397,7 +387,6 @@ __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
                 my_sc = wsc;
             }
         }
-        FST_PROBE_MARK(2);
         if (lane < tk) {
             const float inv = 1.0f / (wsum + 1e-12f);
             s_eids[t * tk + lane] = my_id;
@@ -408,7 +397,6 @@ __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
         }
     }
     __syncthreads();
-    FST_PROBE_MARK(3);
     bucket_block<NT, (PER * 64 < kMaxExperts ? PER * 64 : kMaxExperts)>(M, E, tk, ra.use_shared, s_eids, s_err, ra.meta, ra.slot_eid, ra.slot_M, ra.slot_off,
                      ra.pair_tok, ra.pair_of, ra.pair_shared);
 }
