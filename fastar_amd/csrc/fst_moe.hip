@@ -951,7 +951,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     constexpr int R = PF + 1;                        // weight register ring
     constexpr int U = (MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R);  // lcm(MS, R)
     static_assert(U % MS == 0 && U % R == 0, "unroll must cover whole stages and ring turns");
-    __shared__ uint4 lds[2 * STAGE + 1];
+    __shared__ uint4 lds[2 * STAGE];
 
     // in-launch routing tables (one int each when unused)
     constexpr int RPAIR = RPER > 0 ? TOKS * kMaxTopK : 1;  // routed pairs (M <= TOKS)
@@ -1051,11 +1051,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     WRaw w[R];
 #pragma unroll
     for (int j = 0; j < PF; ++j) w[j] = load_w(wrs, j * CHUNK);
-    for (int i = tid; i < 2 * STAGE + 1; i += NT) lds[i] = z4;
+    for (int i = tid; i < 2 * STAGE; i += NT) lds[i] = z4;
 
     // Staging map: chunk q = tid + NT*i of a macro-stage -> (super-block u,
     // token tl, part).  Chunks past the slot's tokens read a valid address
-    // and land in the spare LDS slot 2*STAGE.  The next item's token rows are
+    // (their LDS rows feed only discarded outputs).  The next item's token rows are
     // fetched when an item starts and its map is built (and its first stage
     // loaded) during the current item's last macro-stage.
     int su[NS], stl[NS], spart[NS];
@@ -1083,7 +1083,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         for (int i = 0; i < NS; ++i) {
             const int u = su[i], part = spart[i];
             ssrc[i] = reinterpret_cast<const u4v_t*>(MX ? (const void*)A : (const void*)SX);
-            sdst[i] = 2 * STAGE;
+            // chunks of the stage go to their own LDS slot even for a token
+            // the slot does not have (that row only feeds discarded MFMA
+            // outputs); chunks past the stage are not stored
+            sdst[i] = stl[i] < TOKS ? u * TS + stl[i] * kTokStride + part : -1;
             sstep[i] = 0;
             if (ar[i] >= 0) {
                 if (part < 32) {
@@ -1093,7 +1096,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                     ssrc[i] = reinterpret_cast<const u4v_t*>(SX + (size_t)ar[i] * nsb * 4 + u * 4 + (part - 32));
                     sstep[i] = 4 * MS;
                 }
-                sdst[i] = u * TS + stl[i] * kTokStride + part;
             }
         }
     };
@@ -1111,7 +1113,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         const int base = (m & 1) * STAGE;
 #pragma unroll
         for (int i = 0; i < NS; ++i)
-            *reinterpret_cast<u4v_t*>(&lds[sdst[i] < 2 * STAGE ? base + sdst[i] : 2 * STAGE]) = sv[i];
+            if (sdst[i] >= 0) *reinterpret_cast<u4v_t*>(&lds[base + sdst[i]]) = sv[i];
     };
     {
         int ar0[NS];
