@@ -1144,7 +1144,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
 
         auto compute = [&](int sb, const WRaw& cur) {
             const int m = sb / MS, u = sb - m * MS;
-            const uint4* st = lds + (m & 1) * STAGE + u * TS + r * kTokStride;
+            // at a capacity of 8 tokens, MFMA rows 8..15 (discarded) read rows
+            // 0..7: the same addresses (a broadcast) instead of 8 more rows
+            // whose 37-chunk stride lands on the same LDS banks
+            const uint4* st = lds + (m & 1) * STAGE + u * TS + (TOKS < 16 ? (r & (TOKS - 1)) : r) * kTokStride;
             const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
             if constexpr (MX) {
                 // lane (g, r): blocks 2g (cur.a) and 2g+1 (cur.b) of row r; the
