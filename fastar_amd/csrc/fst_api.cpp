@@ -413,8 +413,26 @@ void* fst_expert_device_ptr(fst_ctx* ctx, int lid, int eid) {
     return ctx->bank + ((size_t)lid * (ctx->cfg.n_experts + 1) + eid) * ctx->expert_stride;
 }
 
-static int upload_router_common(fst_ctx* ctx, int lid, const std::vector<uint16_t>& nk, const float* bias) {
+// Device layout of one layer's router: per expert, the hd bf16 weights
+// in 16-byte pieces, piece i of lane j's K/64 chunk (elements
+// [j*hd/64 + 8i, +8)) at piece index 64 i + j, so that the router kernel's
+// per-lane chunk loads are contiguous across the wave.
+static std::vector<uint16_t> router_interleave(const std::vector<uint16_t>& nk, int E, int hd) {
+    const int nv = hd / 512;
+    std::vector<uint16_t> il(nk.size());
+    for (int e = 0; e < E; ++e) {
+        const uint16_t* src = nk.data() + (size_t)e * hd;
+        uint16_t* dst = il.data() + (size_t)e * hd;
+        for (int j = 0; j < 64; ++j)
+            for (int i = 0; i < nv; ++i)
+                std::memcpy(dst + (size_t)(i * 64 + j) * 8, src + (size_t)(j * nv + i) * 8, 16);
+    }
+    return il;
+}
+
+static int upload_router_common(fst_ctx* ctx, int lid, const std::vector<uint16_t>& nk_rows, const float* bias) {
     const int E = ctx->cfg.n_experts, hd = ctx->cfg.hidden_dim;
+    const std::vector<uint16_t> nk = router_interleave(nk_rows, E, hd);
     FST_HIP_TRY(hipMemcpyAsync(ctx->router + (size_t)lid * E * hd, nk.data(), nk.size() * 2,
                                hipMemcpyHostToDevice, ctx->st));
     if (bias)

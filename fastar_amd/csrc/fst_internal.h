@@ -66,7 +66,7 @@ struct Scratch {
 struct LayerView {
     const uint8_t* bank;       // expert 0 of the layer; expert e at bank + e*expert_stride
     size_t expert_stride;
-    const uint16_t* router_nk; // bf16 [E][hd] (transposed at upload)
+    const uint16_t* router_nk; // bf16 [E][hd], transposed and lane-interleaved at upload (router_interleave)
     const float* router_bias;  // [E] or null
     const int32_t* hash;       // [vocab][tk] or null
 };

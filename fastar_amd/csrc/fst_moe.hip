@@ -60,40 +60,62 @@ __device__ __forceinline__ float tree_sum64(float acc) {
 
 // ---------------------------------------------------------------- router
 
-// Router logits: one wave per (expert, pair of tokens); lane j owns the
-// contiguous K/64 chunk j, sums it with a sequential fmaf chain, then the 64
-// partials are combined by the halving tree p[j] += p[j+off] (off = 32..1)
-// that lane 0 sees through shfl_down.  Lane 0 stores the logit's score
-// (sigmoid or sqrt(softplus), after the optional bf16 rounding).  All loads of a wave are issued before
-// the math.  Workgroups past the router part each prepare one token row of
-// the expert operand (prep_row), so both consumers of h share one launch.
-template <int CH, int TPW>
-__device__ void router_block(const uint16_t* __restrict__ w_nk, const uint16_t* __restrict__ h, int M, int K,
-                             int E, int bx, int by, int score_func, int round_bf16, float* __restrict__ scores) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// Router logits: one wave per (expert, TPW tokens); lane j owns the
+// contiguous K/64 chunk j (NV = K/512 16-byte pieces), sums it with a
+// sequential fmaf chain, then the 64 partials are combined by the halving
+// tree p[j] += p[j+off] (off = 32..1) that lane 0 sees through shfl_down.
+// Lane 0 stores the logit's score (sigmoid or sqrt(softplus), after the
+// optional bf16 rounding).
+//  - weights: the router is stored lane-interleaved per expert (piece i of
+//    lane j at 16-byte index 64 i + j, router_interleave), so load i of a
+//    wave is one contiguous kilobyte;
+//  - activations: the workgroup copies its TPW rows once into LDS (sm) with
+//    the same interleave, rows padded to 65 pieces per i so that both the
+//    copy and the per-lane reads spread over the banks; the 4 waves share it.
+// Workgroups past the router part each prepare one token row of the expert
+// operand (prep_row), so both consumers of h share one launch.
+template <int NV, int TPW>
+__device__ void router_block(const uint4* __restrict__ w_il, const uint16_t* __restrict__ h, int M, int E,
+                             int bx, int by, int score_func, int round_bf16, float* __restrict__ scores,
+                             uint4* sm) {
+    constexpr int RU = 64 * NV;                      // 16-byte pieces per row
+    constexpr int NL = (TPW * RU + 255) / 256;       // copy loads per thread
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int e = bx * 4 + wave;
     const int t0 = by * TPW;
-    if (e >= E) return;
-    uint4 wq[CH / 8], xq[TPW][CH / 8];
-    const uint4* wp = reinterpret_cast<const uint4*>(w_nk + (size_t)e * K + (size_t)lane * CH);
+    uint4 wq[NV];
+    if (e < E) {
+        const uint4* wp = w_il + (size_t)e * RU + lane;
 #pragma unroll
-    for (int i = 0; i < CH / 8; ++i) wq[i] = wp[i];
+        for (int i = 0; i < NV; ++i) wq[i] = wp[i * 64];
+    }
+    {
+        const uint4* h4 = reinterpret_cast<const uint4*>(h);
+        uint4 v[NL];
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-        if (t0 + t < M) {
-            const uint4* xp = reinterpret_cast<const uint4*>(h + (size_t)(t0 + t) * K + (size_t)lane * CH);
+        for (int u = 0; u < NL; ++u) {
+            const int q = tid + 256 * u, t = q / RU;
+            v[u] = make_uint4(0u, 0u, 0u, 0u);
+            if (q < TPW * RU && t0 + t < M) v[u] = h4[(size_t)(t0 + t) * RU + (q - t * RU)];
+        }
 #pragma unroll
-            for (int i = 0; i < CH / 8; ++i) xq[t][i] = xp[i];
+        for (int u = 0; u < NL; ++u) {
+            const int q = tid + 256 * u, t = q / RU, qq = q - t * RU;
+            const int j = qq / NV, i = qq - j * NV;
+            if (q < TPW * RU) sm[(t * NV + i) * 65 + j] = v[u];
         }
     }
+    __syncthreads();
+    if (e >= E) return;
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
         if (t0 + t >= M) continue;
         float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < CH / 8; ++i) {
+        for (int i = 0; i < NV; ++i) {
+            const uint4 xq = sm[(t * NV + i) * 65 + lane];
             const uint32_t wv[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
-            const uint32_t xv[4] = {xq[t][i].x, xq[t][i].y, xq[t][i].z, xq[t][i].w};
+            const uint32_t xv[4] = {xq.x, xq.y, xq.z, xq.w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 acc = fmaf(fst_bits_f32(xv[k] << 16), fst_bits_f32(wv[k] << 16), acc);
@@ -588,20 +610,21 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
 // topk_bucket_kernel.  (A single launch whose last router workgroup runs the
 // top-k was measured slower: the hand-off through device-coherent stores and
 // a contended completion counter costs more than the kernel boundary.)
-template <int CH, int TPW>
-__global__ __launch_bounds__(256) void router_prep_kernel(const uint16_t* __restrict__ w_nk,
+template <int NV, int TPW>
+__global__ __launch_bounds__(256) void router_prep_kernel(const uint4* __restrict__ w_il,
                                                           const uint16_t* __restrict__ h, int M, int K, int E,
                                                           int score_func, int round_bf16,
                                                           float* __restrict__ scores, int nbx, int nrb,
                                                           _Float16* __restrict__ x16p, uint4* __restrict__ sxp,
                                                           int* __restrict__ xs) {
-    __shared__ float xv[kMaxPrepK];
+    static_assert(TPW >= 2, "the router stage must also hold a prep row (K floats)");
+    __shared__ uint4 sm[TPW * NV * 65];
     const int b = blockIdx.x;
     if (b >= nrb) {
-        prep_row<256>(SrcBf16{h}, b - nrb, K, xv, x16p, sxp, xs);
+        prep_row<256>(SrcBf16{h}, b - nrb, K, reinterpret_cast<float*>(sm), x16p, sxp, xs);
         return;
     }
-    router_block<CH, TPW>(w_nk, h, M, K, E, b % nbx, b / nbx, score_func, round_bf16, scores);
+    router_block<NV, TPW>(w_il, h, M, E, b % nbx, b / nbx, score_func, round_bf16, scores, sm);
 }
 
 void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M, int prep,
@@ -610,17 +633,18 @@ void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const u
     constexpr int TPW = 2;
     const int nbx = (g.E + 3) / 4, nby = (M + TPW - 1) / TPW, nrb = nbx * nby;
     const dim3 grid(nrb + (prep ? M : 0));
-#define FST_RP(CHV)                                                                                       \
-    hipLaunchKernelGGL((router_prep_kernel<CHV, TPW>), grid, dim3(256), 0, st, L.router_nk, h, M, g.hd, g.E, \
-                       g.score_func, g.round_logits_bf16, s.logits, nbx, nrb, s.x16p, s.sxp, s.xs)
-    if (g.hd == 4096)
-        FST_RP(64);
-    else if (g.hd == 2048)
-        FST_RP(32);
-    else if (g.hd == 1024)
-        FST_RP(16);
-    else
-        FST_RP(8);
+#define FST_RP(NVV)                                                                                        \
+    case NVV:                                                                                              \
+        hipLaunchKernelGGL((router_prep_kernel<NVV, TPW>), grid, dim3(256), 0, st,                         \
+                           reinterpret_cast<const uint4*>(L.router_nk), h, M, g.hd, g.E, g.score_func,     \
+                           g.round_logits_bf16, s.logits, nbx, nrb, s.x16p, s.sxp, s.xs);                   \
+        break
+    // hidden_dim is a multiple of 512 in [512, 8192] (checked at context creation)
+    switch (g.hd / 512) {
+        FST_RP(1); FST_RP(2); FST_RP(3); FST_RP(4); FST_RP(5); FST_RP(6); FST_RP(7); FST_RP(8);
+        FST_RP(9); FST_RP(10); FST_RP(11); FST_RP(12); FST_RP(13); FST_RP(14); FST_RP(15); FST_RP(16);
+        default: break;
+    }
 #undef FST_RP
     if (!topk) return;
     const RouteArgs ra = route_args(g, L, M, s.logits, input_ids, use_hash, use_shared, eids, wts, s);

@@ -166,6 +166,21 @@ def test_router_bit_exact(fa, oracle, router_ctx, mode, M):
     assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
 
 
+@pytest.mark.parametrize("hd", [512, 1536, 3072, 7168, 8192])
+def test_router_hidden_sizes(fa, oracle, hd):
+    """Every legal hidden size (a multiple of 512 up to 8192) gets the
+    canonical K/64-chunk sum: sizes other than powers of two included."""
+    w = fa.synth_normal_bf16(51, hd, (hd, 64), 0.0, 0.02)
+    h = fa.synth_normal_bf16(52, hd, (8, hd))
+    note("router hidden=%d" % hd)
+    with fa.Context(n_experts=64, top_k=4, max_tokens=16, hidden_dim=hd, inter_dim=512) as c:
+        c.upload_router_bf16(0, w)
+        e, wt = c.router(0, h)
+    re_, rw, _ = oracle.router(h, w, None, 4)
+    assert np.array_equal(e, re_)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+
+
 def test_router_ties_and_hash(fa, oracle, router_ctx):
     ctx = router_ctx
     w = fa.synth_normal_bf16(31, 0, (HD, 256), 0.0, 0.02)
