@@ -1078,8 +1078,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     for (int i = tid; i < 2 * STAGE; i += NT) lds[i] = z4;
 
     // Staging map: chunk q = tid + NT*i of a macro-stage -> (super-block u,
-    // token tl, part).  Chunks past the slot's tokens read a valid address
-    // (their LDS rows feed only discarded outputs).  The next item's token rows are
+    // token tl, part).  Chunks of token rows the slot does not have are not
+    // stored: those LDS rows keep whatever an earlier item left there and
+    // feed only discarded MFMA output rows (an output row reads only its own
+    // operand row).  Their loads read a valid address, and a chunk slot
+    // holding no live row at all is not loaded.  The next item's token rows are
     // fetched when an item starts and its map is built (and its first stage
     // loaded) during the current item's last macro-stage.
     int su[NS], stl[NS], spart[NS];
@@ -1091,26 +1094,33 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         stl[i] = q < NCH ? rem / PARTS : TOKS;
         spart[i] = rem - (rem / PARTS) * PARTS;
     }
-    auto load_rows = [&](int tt, int* ar) {
+    auto load_rows = [&](int tt, int* ar) -> int {
         const int sl = tt / tiles;
         const int Mi = min(slot_M[sl], TOKS), offi = slot_off[sl];
 #pragma unroll
         for (int i = 0; i < NS; ++i)
             ar[i] = stl[i] < Mi ? (a_row ? a_row[offi + stl[i]] : offi + stl[i]) : -1;
+        return Mi;
     };
+    // Lowest token row that chunk slot i of any thread covers (0 when the
+    // slot spans two super-blocks): an item with at most that many tokens
+    // has nothing live in slot i, and its loads are skipped (uniformly).
+    auto slot_minrow = [](int i) constexpr -> int {
+        const int q0 = NT * i, q1 = (NT * i + NT < NCH ? NT * i + NT : NCH) - 1;
+        return q0 / (TOKS * PARTS) != q1 / (TOKS * PARTS) ? 0 : (q0 % (TOKS * PARTS)) / PARTS;
+    };
+    int st_me = 0;  // token count of the item the staging map belongs to
     const u4v_t* ssrc[NS];
     int sdst[NS];
     int sstep[NS];
     u4v_t sv[NS];
-    auto build_map = [&](const int* ar) {
+    auto build_map = [&](const int* ar, int me) {
+        st_me = me;
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int u = su[i], part = spart[i];
             ssrc[i] = reinterpret_cast<const u4v_t*>(MX ? (const void*)A : (const void*)SX);
-            // chunks of the stage go to their own LDS slot even for a token
-            // the slot does not have (that row only feeds discarded MFMA
-            // outputs); chunks past the stage are not stored
-            sdst[i] = stl[i] < TOKS ? u * TS + stl[i] * kTokStride + part : -1;
+            sdst[i] = ar[i] >= 0 ? u * TS + stl[i] * kTokStride + part : -1;
             sstep[i] = 0;
             if (ar[i] >= 0) {
                 if (part < 32) {
@@ -1128,6 +1138,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     auto stage_load = [&](int m) {
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
+            if (i > 0 && st_me <= slot_minrow(i)) continue;
             const bool live = m * MS + su[i] < nsb;
             const size_t o = live ? (size_t)m * sstep[i] : 0;
             sv[i] = ssrc[i][o];
@@ -1141,8 +1152,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     };
     {
         int ar0[NS];
-        load_rows(blockIdx.x, ar0);
-        build_map(ar0);
+        const int me0 = load_rows(blockIdx.x, ar0);
+        build_map(ar0, me0);
         stage_load(0);
     }
     const int nms = nsb / MS;
@@ -1155,7 +1166,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         const int Me = min(slot_M[slot], TOKS), off = slot_off[slot];
         const int row = wave_tile(tile) * 16 + r;
         int ar_next[NS];
-        load_rows(tn < total ? tn : t, ar_next);
+        const int me_next = load_rows(tn < total ? tn : t, ar_next);
 
         __syncthreads();  // the previous item's readers of the LDS are done
         stage_store(0);
@@ -1237,7 +1248,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                     if (sb / MS + 1 < nms) {
                         stage_load(sb / MS + 1);
                     } else {
-                        build_map(ar_next);
+                        build_map(ar_next, me_next);
                         stage_load(0);
                     }
                 }
@@ -1331,17 +1342,20 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 #ifndef FST_Q4K_W
 #define FST_Q4K_W 8
 #endif
-    constexpr int W = FST_Q4K_W;
+#ifndef FST_Q4K_W32
+#define FST_Q4K_W32 16
+#endif
+    // waves per workgroup: the 17..32-token capacity may use larger workgroups
+    const int W = (M > 16 && M <= 32 && N % (16 * FST_Q4K_W32) == 0) ? FST_Q4K_W32 : FST_Q4K_W;
     // persistent grid: FST_Q4K_WG_PER_CU workgroups per CU at most
     const unsigned items = slots * (unsigned)(N / (16 * W));
-    // (token capacities above 8 run at 3 waves per SIMD: one 8-wave workgroup per CU)
-    const unsigned wg_per_cu =
-        (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1)) * (8 / W);
-    const dim3 grid(std::min(items, (unsigned)s.n_cu * wg_per_cu));
-#define FST_Q4K_LAUNCH(T, MSV)                                                                               \
-    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, W, MODE, CODEC, RPER>), grid, dim3(64 * W), 0, st, bank,      \
+    const unsigned waves_per_cu = 8u * (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1));
+    const dim3 grid(std::min(items, (unsigned)s.n_cu * std::max(1u, waves_per_cu / (unsigned)W)));
+#define FST_Q4K_LAUNCH_W(T, MSV, WV)                                                                         \
+    hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, WV, MODE, CODEC, RPER>), grid, dim3(64 * WV), 0, st, bank,    \
                        stride, mat_off, K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep, \
                        ra)
+#define FST_Q4K_LAUNCH(T, MSV) FST_Q4K_LAUNCH_W(T, MSV, FST_Q4K_W)
     // K is a multiple of 512 (checked at context creation): nsb is even
 #ifndef FST_MS8
 #define FST_MS8 1
@@ -1356,11 +1370,14 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
         FST_Q4K_LAUNCH(8, 2);
     else if (M <= 16)
         FST_Q4K_LAUNCH(16, 2);
+    else if (M <= 32 && W == FST_Q4K_W32)
+        FST_Q4K_LAUNCH_W(32, 1, FST_Q4K_W32);
     else if (M <= 32)
         FST_Q4K_LAUNCH(32, 1);
     else
         FST_Q4K_LAUNCH(64, 1);
 #undef FST_Q4K_LAUNCH
+#undef FST_Q4K_LAUNCH_W
 }
 
 // gate||up: the two [inter][hd/K-block] matrices are contiguous; each
