@@ -1342,11 +1342,17 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 #ifndef FST_Q4K_W
 #define FST_Q4K_W 8
 #endif
+#ifndef FST_Q4K_W16
+#define FST_Q4K_W16 16
+#endif
 #ifndef FST_Q4K_W32
 #define FST_Q4K_W32 16
 #endif
-    // waves per workgroup: the 17..32-token capacity may use larger workgroups
-    const int W = (M > 16 && M <= 32 && N % (16 * FST_Q4K_W32) == 0) ? FST_Q4K_W32 : FST_Q4K_W;
+    // waves per workgroup by token capacity (larger capacities stage more
+    // operand chunks per super-block; more threads hold fewer each), when N
+    // is a multiple of the workgroup's 16*W rows
+    const int WC = M <= 8 ? FST_Q4K_W : (M <= 16 ? FST_Q4K_W16 : (M <= 32 ? FST_Q4K_W32 : FST_Q4K_W));
+    const int W = N % (16 * WC) == 0 ? WC : FST_Q4K_W;
     // persistent grid: FST_Q4K_WG_PER_CU workgroups per CU at most
     const unsigned items = slots * (unsigned)(N / (16 * W));
     const unsigned waves_per_cu = 8u * (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1));
@@ -1368,6 +1374,8 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
         FST_Q4K_LAUNCH(8, ms8);
     else if (M <= 8)
         FST_Q4K_LAUNCH(8, 2);
+    else if (M <= 16 && W == FST_Q4K_W16)
+        FST_Q4K_LAUNCH_W(16, 2, FST_Q4K_W16);
     else if (M <= 16)
         FST_Q4K_LAUNCH(16, 2);
     else if (M <= 32 && W == FST_Q4K_W32)
