@@ -698,7 +698,6 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
                                                          int* __restrict__ slot_tab) {
     __shared__ float xrow[kMaxPrepK];
     __shared__ float nrow[kMaxPrepK];
-    __shared__ double part[64];
     __shared__ float s_r;
     const int t = blockIdx.x, tid = threadIdx.x;
     if (slot_tab && t == 0 && tid == 0) {
@@ -707,39 +706,39 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
         slot_tab[META_WORDS + 1] = M;  // slot_M
         slot_tab[META_WORDS + 2] = 0;  // slot_off
     }
-    // 8 elements per 16-byte load (d is a multiple of 256), each thread's
-    // loads issued before any is used
+    // 8 elements per 16-byte load (d is a multiple of 512, at most 8192: at
+    // most NB loads of each row per thread); every load, the norm weights
+    // included, is issued before any is used
     const int nv = d / 8;
     constexpr int NB = 4;
-    for (int q0 = tid; q0 < nv; q0 += NB * 256) {
-        uint4 hv[NB], yv[NB];
+    uint4 hv[NB], yv[NB], wv[NB];
 #pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            const int q = min(q0 + u * 256, nv - 1);
-            hv[u] = reinterpret_cast<const uint4*>(h + (size_t)t * d)[q];
-            yv[u] = y ? reinterpret_cast<const uint4*>(y + (size_t)t * d)[q] : make_uint4(0u, 0u, 0u, 0u);
-        }
+    for (int u = 0; u < NB; ++u) {
+        const int q = min(tid + u * 256, nv - 1);
+        hv[u] = reinterpret_cast<const uint4*>(h + (size_t)t * d)[q];
+        yv[u] = y ? reinterpret_cast<const uint4*>(y + (size_t)t * d)[q] : make_uint4(0u, 0u, 0u, 0u);
+        wv[u] = reinterpret_cast<const uint4*>(w)[q];
+    }
 #pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            const int q = q0 + u * 256;
-            if (q >= nv) continue;
-            const uint32_t hw[4] = {hv[u].x, hv[u].y, hv[u].z, hv[u].w};
-            const uint32_t yw[4] = {yv[u].x, yv[u].y, yv[u].z, yv[u].w};
-            uint32_t ow[4];
+    for (int u = 0; u < NB; ++u) {
+        const int q = tid + u * 256;
+        if (q >= nv) continue;
+        const uint32_t hw[4] = {hv[u].x, hv[u].y, hv[u].z, hv[u].w};
+        const uint32_t yw[4] = {yv[u].x, yv[u].y, yv[u].z, yv[u].w};
+        uint32_t ow[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t o2 = 0u;
+        for (int i = 0; i < 4; ++i) {
+            uint32_t o2 = 0u;
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    float x = fst_bf16_to_f32((uint16_t)(hw[i] >> (16 * hh)));
-                    if (y) x = fst_bf16_to_f32(fst_f32_to_bf16(x + fst_bf16_to_f32((uint16_t)(yw[i] >> (16 * hh)))));
-                    xrow[8 * q + 2 * i + hh] = x;
-                    o2 |= (uint32_t)fst_f32_to_bf16(x) << (16 * hh);
-                }
-                ow[i] = o2;
+            for (int hh = 0; hh < 2; ++hh) {
+                float x = fst_bf16_to_f32((uint16_t)(hw[i] >> (16 * hh)));
+                if (y) x = fst_bf16_to_f32(fst_f32_to_bf16(x + fst_bf16_to_f32((uint16_t)(yw[i] >> (16 * hh)))));
+                xrow[8 * q + 2 * i + hh] = x;
+                o2 |= (uint32_t)fst_f32_to_bf16(x) << (16 * hh);
             }
-            if (h_out) reinterpret_cast<uint4*>(h_out + (size_t)t * d)[q] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+            ow[i] = o2;
         }
+        if (h_out) reinterpret_cast<uint4*>(h_out + (size_t)t * d)[q] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
     __syncthreads();
     if (tid < 64) {
@@ -749,40 +748,33 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
             const double v = (double)xrow[tid * C + i];
             a = a + v * v;
         }
-        part[tid] = a;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        for (int off = 32; off >= 1; off >>= 1)
-            for (int j = 0; j < off; ++j) part[j] = part[j] + part[j + off];
-        s_r = (float)(1.0 / sqrt(part[0] / (double)d + (double)eps));
+        // halving tree p[j] += p[j+off], off = 32..1: lane j < off adds
+        // lane j+off's partial (the upper lanes' values are not used again)
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) a = a + __shfl_down(a, off, 64);
+        if (tid == 0) s_r = (float)(1.0 / sqrt(a / (double)d + (double)eps));
     }
     __syncthreads();
     const float r = s_r;
-    for (int q0 = tid; q0 < nv; q0 += NB * 256) {
-        uint4 wv[NB];
 #pragma unroll
-        for (int u = 0; u < NB; ++u) wv[u] = reinterpret_cast<const uint4*>(w)[min(q0 + u * 256, nv - 1)];
+    for (int u = 0; u < NB; ++u) {
+        const int q = tid + u * 256;
+        if (q >= nv) continue;
+        const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+        uint32_t ow[4];
 #pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            const int q = q0 + u * 256;
-            if (q >= nv) continue;
-            const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
-            uint32_t ow[4];
+        for (int i = 0; i < 4; ++i) {
+            uint32_t o2 = 0u;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t o2 = 0u;
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int j = 8 * q + 2 * i + hh;
-                    const uint16_t o = fst_f32_to_bf16((xrow[j] * r) * fst_bf16_to_f32((uint16_t)(ww[i] >> (16 * hh))));
-                    nrow[j] = fst_bf16_to_f32(o);
-                    o2 |= (uint32_t)o << (16 * hh);
-                }
-                ow[i] = o2;
+            for (int hh = 0; hh < 2; ++hh) {
+                const int j = 8 * q + 2 * i + hh;
+                const uint16_t o = fst_f32_to_bf16((xrow[j] * r) * fst_bf16_to_f32((uint16_t)(ww[i] >> (16 * hh))));
+                nrow[j] = fst_bf16_to_f32(o);
+                o2 |= (uint32_t)o << (16 * hh);
             }
-            if (normed) reinterpret_cast<uint4*>(normed + (size_t)t * d)[q] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+            ow[i] = o2;
         }
+        if (normed) reinterpret_cast<uint4*>(normed + (size_t)t * d)[q] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
     __syncthreads();
     if (x16p) prep_row<256>(SrcRow{nrow}, t, d, xrow, x16p, sxp, xs);
