@@ -21,14 +21,12 @@ constexpr int kChunks = 64;
 typedef unsigned __int128 u128;
 
 struct AccWs {
-    int* row_done;            // [R] completion counters (zero between calls)
-    int* seq_done;            // [n_seq]
-    int* pred;                // [R] greedy argmax per row
     float* part_max;          // [R][kChunks]
     int* part_idx;            // [R][kChunks]
     unsigned long long* part_sum;  // [R][kChunks]
     unsigned long long* part_res;  // [n_seq][kChunks][2] (u128 as lo, hi)
     unsigned long long* dec;       // [n_seq][8]
+    unsigned long long* gslot;     // [R][kChunks] greedy chunk partials (zero between calls)
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -37,24 +35,21 @@ static AccWs carve(void* ws, int n_seq, int k) {
     const int R = n_seq * (k + 1) + n_seq * k;
     char* p = (char*)ws;
     AccWs w;
-    w.row_done = (int*)p; p += align256(sizeof(int) * R);
-    w.seq_done = (int*)p; p += align256(sizeof(int) * n_seq);
-    w.pred = (int*)p; p += align256(sizeof(int) * R);
     w.part_max = (float*)p; p += align256(sizeof(float) * R * kChunks);
     w.part_idx = (int*)p; p += align256(sizeof(int) * R * kChunks);
     w.part_sum = (unsigned long long*)p; p += align256(8ull * R * kChunks);
     w.part_res = (unsigned long long*)p; p += align256(16ull * n_seq * kChunks);
-    w.dec = (unsigned long long*)p;
+    w.dec = (unsigned long long*)p; p += align256(64ull * n_seq);
+    w.gslot = (unsigned long long*)p;
     return w;
 }
 
 size_t accept_ws_bytes(int n_seq, int k, int V) {
     (void)V;
     const int R = n_seq * (k + 1) + n_seq * k;
-    return align256(sizeof(int) * R) * 2 + align256(sizeof(int) * n_seq) +
-           align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
+    return align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
            align256(8ull * R * kChunks) + align256(16ull * n_seq * kChunks) + align256(64ull * n_seq) +
-           256;
+           align256(8ull * R * kChunks) + 256;
 }
 
 // Calls f(x, v) for v = v0, v0 + stride, ... < v1 in that order, with the
@@ -521,25 +516,30 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
     }
 }
 
-// Greedy acceptance in one launch: every (row, chunk) workgroup reduces its
-// chunk; the last workgroup to finish a row reduces the row's CH partials
-// (argmax with the reference's rules), and the last row to finish a sequence
-// resolves the longest matching prefix and the bonus token.  Counters are
-// re-armed to zero by the workgroup that consumes them.  CH is small on
-// purpose: increments of one device-scope counter serialise at the memory
-// side (a few hundred ns each), so a row waits on CH of them.
+// Greedy acceptance in one launch, without counters.  Every (row, chunk)
+// workgroup reduces its chunk to (max, lowest index) and publishes it as one
+// 64-bit word {max bits, index + 2} (0 = not yet written).  The workgroup
+// with the highest linear id of a sequence (last chunk of its last row) then
+// collects the sequence's (k+1)*CH words with coherent loads, resolves each
+// row's argmax with the reference's rules, the longest matching prefix and
+// the bonus token, and clears the words for the next call.  Workgroups are
+// dispatched in linear-id order on each XCD, so every workgroup it waits for
+// is resident or finished (the lowest unfinished id never waits), and the
+// wait ends.  (Counters instead of flags serialise: increments of one
+// device-scope counter complete a few hundred ns apart at the memory side.)
+__device__ __forceinline__ void st_coherent_u64(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_coherent_u64(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int CH>
-__global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict__ target, int k, int V,
-                                                         const int32_t* __restrict__ draft, AccWs w,
-                                                         int32_t* __restrict__ n_acc,
-                                                         int32_t* __restrict__ tokens) {
-    static_assert(CH <= 64, "one lane per chunk partial");
-    const int c = blockIdx.x, r = blockIdx.y;
-    const float* row = target + (size_t)r * V;
+__device__ __forceinline__ void greedy_chunk(const float* __restrict__ row, int V, int c, float& best, int& bi) {
     const int clen = ((V + CH - 1) / CH + 3) & ~3;  // multiple of 4 elements
     const int b0 = min(V, c * clen), b1 = min(V, b0 + clen);
-    float best = 0.0f;
-    int bi = 0x7fffffff;
+    best = 0.0f;
+    bi = 0x7fffffff;
     auto take = [&](float l, int v) {
         if (l != l) return;
         if (bi == 0x7fffffff || l > best) {
@@ -575,54 +575,85 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
     wave_argmax(best, bi);
     __shared__ float sm[4];
     __shared__ int si[4];
-    __shared__ int s_last;
     if (lane == 0) {
         sm[wave] = best;
         si[wave] = bi;
     }
     __syncthreads();
+    for (int q = 1; q < 4; ++q) argmax_merge(best, bi, sm[q], si[q]);
+}
+
+template <int CH, int NU>
+__global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict__ target, int k, int V,
+                                                         const int32_t* __restrict__ draft, AccWs w,
+                                                         int32_t* __restrict__ n_acc,
+                                                         int32_t* __restrict__ tokens) {
+    static_assert(CH == 16, "a row's chunk words fill one 16-lane DPP row");
+    const int c = blockIdx.x, r = blockIdx.y;
+    const int s = r / (k + 1);
+    const int lane = threadIdx.x & 63;
+    const bool owner = c == CH - 1 && r == s * (k + 1) + k;
+    // the owner's row-0 values and draft tokens, loaded before anything waits
+    int32_t dv = 0;
+    float x0 = 0.0f;
+    if (owner && threadIdx.x < 64) {
+        if (lane < k) dv = draft[s * k + lane];
+        if (lane <= k) x0 = target[(size_t)(s * (k + 1) + lane) * V];
+    }
+    float best;
+    int bi;
+    greedy_chunk<CH>(target + (size_t)r * V, V, c, best, bi);
+    unsigned long long* words = w.gslot + (size_t)s * (k + 1) * CH;
+    const int me = (r - s * (k + 1)) * CH + c;
     if (threadIdx.x == 0) {
-        for (int q = 1; q < 4; ++q) argmax_merge(best, bi, sm[q], si[q]);
-        st_coherent(&w.part_max[(size_t)r * kChunks + c], best);
-        st_coherent(&w.part_idx[(size_t)r * kChunks + c], bi);
+        st_coherent_u64(&words[me], ((unsigned long long)(uint32_t)(bi + 2) << 32) | fst_f32_bits(best));
         publish_wait();
-        s_last = signal_add(&w.row_done[r], 1) == CH - 1;
     }
-    __syncthreads();
-    if (!s_last) return;
-    if (threadIdx.x < 64) {
-        float m = 0.0f;
-        int i = -1;
-        if (lane < CH) {
-            m = ld_coherent(&w.part_max[(size_t)r * kChunks + lane]);
-            i = ld_coherent(&w.part_idx[(size_t)r * kChunks + lane]);
-        }
-        wave_argmax(m, i);
-        int seq_last = 0;
-        const int s = r / (k + 1);
-        if (lane == 0) {
-            w.row_done[r] = 0;
-            const float x0 = row[0];
-            st_coherent(&w.pred[r], (x0 != x0 || i < 0) ? 0 : i);
-            publish_wait();
-            seq_last = signal_add(&w.seq_done[s], 1) == k;
-            if (seq_last) w.seq_done[s] = 0;
-        }
-        seq_last = __shfl(seq_last, 0, 64);
-        if (seq_last) {
-            // lane j holds row j's prediction and draft token j; the accepted
-            // length is the first mismatching lane (ballot), the bonus its prediction
-            const int pv = lane <= k ? __hip_atomic_load(&w.pred[s * (k + 1) + lane], __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT)
-                                     : 0;
-            const int dv = lane < k ? draft[s * k + lane] : 0;
-            const unsigned long long match = __ballot(lane < k && pv == dv);
-            const int n = min(k, __ffsll((long long)~match) - 1);
-            const int bonus = __shfl(pv, n, 64);
-            if (lane <= k) tokens[s * (k + 1) + lane] = lane < n ? dv : (lane == n ? bonus : -1);
-            if (lane == 0) n_acc[s] = n;
-        }
+    if (!owner || threadIdx.x >= 64) return;
+    // collect: lane l holds words l + 64u (row 4u + l/16, chunk l%16)
+    const int nw = (k + 1) * CH;
+    unsigned long long v[NU];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        v[u] = 0ull;
+        if (lane + 64 * u < nw) pend |= 1u << u;
     }
+    for (;;) {
+        unsigned long long t[NU];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) t[u] = ld_coherent_u64(&words[min(lane + 64 * u, nw - 1)]);
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+            if (((pend >> u) & 1u) && (t[u] >> 32) != 0ull) {
+                v[u] = t[u];
+                pend &= ~(1u << u);
+            }
+        if (!__any(pend != 0u)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    // per row: argmax over its 16 chunk words (one DPP row); lane l then
+    // takes row l's result from lane 16 (l % 4) of iteration l / 4
+    int pv = 0;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        float m = fst_bits_f32((uint32_t)v[u]);
+        int i = (lane + 64 * u < nw) ? (int)(v[u] >> 32) - 2 : -1;
+        argmax_step<0xb1>(m, i);
+        argmax_step<0x4e>(m, i);
+        argmax_step<0x124>(m, i);
+        argmax_step<0x128>(m, i);
+        const int ti = __shfl(i, 16 * (lane & 3), 64);
+        if ((lane >> 2) == u) pv = ti;
+        if (lane + 64 * u < nw) st_coherent_u64(&words[lane + 64 * u], 0ull);
+    }
+    // the reference's rules: first max wins, a NaN at index 0 pins row 0
+    if (lane <= k) pv = (x0 != x0 || pv < 0) ? 0 : pv;
+    const unsigned long long match = __ballot(lane < k && pv == dv);
+    const int n = min(k, __ffsll((long long)~match) - 1);
+    const int bonus = __shfl(pv, n, 64);
+    if (lane <= k) tokens[s * (k + 1) + lane] = lane < n ? dv : (lane == n ? bonus : -1);
+    if (lane == 0) n_acc[s] = n;
 }
 
 #ifndef FST_GREEDY_CHUNKS
@@ -633,8 +664,21 @@ void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k,
     AccWs w = carve(ws, n_seq, k);
     const int R = n_seq * (k + 1);
     constexpr int CH = FST_GREEDY_CHUNKS;
-    hipLaunchKernelGGL(acc_greedy_kernel<CH>, dim3(CH, R), dim3(256), 0, st, target, k, V, draft, w, n_acc,
-                       tokens);
+    // words per sequence (k+1)*16 <= 1024: NU = 64-lane passes
+    const int nu = ((k + 1) * CH + 63) / 64;
+#define FST_GK(NUV) \
+    hipLaunchKernelGGL((acc_greedy_kernel<CH, NUV>), dim3(CH, R), dim3(256), 0, st, target, k, V, draft, w, n_acc, tokens)
+    if (nu <= 1)
+        FST_GK(1);
+    else if (nu <= 2)
+        FST_GK(2);
+    else if (nu <= 4)
+        FST_GK(4);
+    else if (nu <= 8)
+        FST_GK(8);
+    else
+        FST_GK(16);
+#undef FST_GK
 }
 
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
