@@ -248,7 +248,8 @@ def bench_c2mx(fa, args):
 def bench_c5(fa, args):
     """C5: 4 sequences x block 8 (M = 32): 8 MoE layers (RMSNorm + router +
     256 routed / 1 shared Q4_K experts each, 29 GB resident) + final norm +
-    Q4_K LM head 4096 -> 129,280 + greedy acceptance per sequence."""
+    Q4_K LM head 4096 -> 129,280 + greedy and stochastic (T = 1) acceptance
+    per sequence."""
     L = fa.lib()
     NL, n_seq = 8, 4
     M = n_seq * (K_DRAFT + 1)
@@ -267,11 +268,16 @@ def bench_c5(fa, args):
     dl = ctx.dev_alloc(M * VOCAB * 4)
     dr = ctx.to_device(np.zeros((n_seq, K_DRAFT), np.int32))
     dn, dk = ctx.dev_alloc(4 * n_seq), ctx.dev_alloc(4 * n_seq * (K_DRAFT + 1))
+    dn2, dk2 = ctx.dev_alloc(4 * n_seq), ctx.dev_alloc(4 * n_seq * (K_DRAFT + 1))
+    # draft-model logits for the stochastic mode: fp32 ~ N(0, 2^2) per draft position
+    dq = ctx.to_device(fa.synth_normal_f32(SEED, 5000, (n_seq * K_DRAFT, VOCAB), 0.0, 2.0))
 
     def step(i):
         fa._check(L.fst_device_copy(ctx.h, dh, dsrc[i % N_BATCH], M * HD * 2))
         fa._check(L.fst_verify_forward_dev(ctx.h, dh, M, None, dl))
         fa._check(L.fst_accept_greedy_dev(ctx.h, dl, n_seq, K_DRAFT, VOCAB, dr, dn, dk))
+        fa._check(L.fst_accept_stochastic_dev(ctx.h, dl, dq, n_seq, K_DRAFT, VOCAB, dr, 1.0, SEED, i * n_seq,
+                                              dn2, dk2))
     t = timed(ctx, step, args.steps, args.warmup)
     ctx.set_profiling(True)
     fa._check(L.fst_device_copy(ctx.h, dh, dsrc[0], M * HD * 2))
@@ -285,7 +291,7 @@ def bench_c5(fa, args):
             "ms_per_step": round(t * 1e3, 4), "parts_us": parts,
             "lm_head_GBps": round(lm_bytes / (parts.get("lm_head", 1e9) * 1e-6) / 1e9, 1),
             "config": {"workload": "C5: M=32, 8 layers x (RMSNorm + router + 256+1 Q4_K experts), "
-                                   "Q4_K LM head 4096->129280, greedy acceptance x4"}}
+                                   "Q4_K LM head 4096->129280, greedy and stochastic acceptance x4"}}
 
 
 def main():

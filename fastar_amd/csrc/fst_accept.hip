@@ -148,36 +148,6 @@ __device__ __forceinline__ u128 wave_sum_u128(u128 v) {
 }
 
 
-// One wave per sequence: rows reduced one after another, chunks across lanes.
-__global__ __launch_bounds__(64) void acc_greedy_final_kernel(const float* __restrict__ target, int k,
-                                                              int V, const float* __restrict__ part_max,
-                                                              const int* __restrict__ part_idx,
-                                                              const int32_t* __restrict__ draft,
-                                                              int32_t* __restrict__ n_acc,
-                                                              int32_t* __restrict__ tokens) {
-    const int s = blockIdx.x, lane = threadIdx.x;
-    __shared__ int pred[64];
-    for (int i = 0; i <= k; ++i) {
-        const int r = s * (k + 1) + i;
-        float mx;
-        int am;
-        wave_row_argmax(part_max, part_idx, r, &mx, &am);
-        if (lane == 0) {
-            const float x0 = target[(size_t)r * V];
-            pred[i] = (x0 != x0 || am < 0) ? 0 : am;
-        }
-    }
-    __syncthreads();
-    if (lane == 0) {
-        int n = 0;
-        while (n < k && pred[n] == draft[s * k + n]) ++n;
-        for (int i = 0; i < n; ++i) tokens[s * (k + 1) + i] = draft[s * k + i];
-        tokens[s * (k + 1) + n] = pred[n];
-        for (int i = n + 1; i <= k; ++i) tokens[s * (k + 1) + i] = -1;
-        n_acc[s] = n;
-    }
-}
-
 __device__ __forceinline__ unsigned long long fixed_prob(float x, float inv_t, float mx, int any) {
     const float l = x * inv_t;
     if (!any || l != l) return 0ull;
