@@ -531,13 +531,13 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
             return FST_OK;
         }
     }
+    // one routed pair per token and no shared expert: the down launch writes
+    // the bf16 result itself (the combine of one term), no combine launch
+    const bool direct = use_routed && g.tk == 1 && !use_shared;
     if (!do_router) {
-        fst::launch_bucket(st, g, M, use_shared && !sh16, d_eids, ctx->s);
-        ctx->mark("bucket");
-        if (!mx) {
-            fst::launch_prep_bf16(st, d_h, M, c.hidden_dim, ctx->s.x16p, ctx->s.sxp, ctx->s.xs);
-            ctx->mark("prep_x");
-        }
+        fst::launch_bucket_prep(st, g, M, use_shared && !sh16, d_eids, ctx->s, mx ? nullptr : d_h,
+                                direct ? d_out : nullptr, direct ? d_out_routed : nullptr);
+        ctx->mark("bucket_prep");
     }
     fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h, fuse_topk ? &rq : nullptr);
     ctx->mark("q4k_gate_up");
@@ -546,11 +546,16 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
                              ctx->s.sx2p, ctx->s.xs2);
         ctx->mark("prep_h");
     }
-    fst::launch_q4k_down(st, g, L, M, ctx->s);
-    ctx->mark("q4k_down");
-    fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out, d_out_routed,
-                        d_out_shared);
-    ctx->mark("combine");
+    if (direct) {
+        fst::launch_q4k_down(st, g, L, M, ctx->s, d_wts, d_out, d_out_routed);
+        ctx->mark("q4k_down");
+    } else {
+        fst::launch_q4k_down(st, g, L, M, ctx->s);
+        ctx->mark("q4k_down");
+        fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out, d_out_routed,
+                            d_out_shared);
+        ctx->mark("combine");
+    }
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;
 }

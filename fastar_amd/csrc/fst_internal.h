@@ -277,6 +277,11 @@ void launch_bucket(hipStream_t st, const Geometry& g, int M, int use_shared, con
                    const Scratch& s);
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p,
                       uint4* sxp, int* xs);
+// launch_bucket and (h given: Q4_K) launch_prep_bf16 of the M rows in one
+// launch; o1/o2: the outputs the down launch will write directly (their
+// rows of tokens with an invalid expert id are zeroed here).
+void launch_bucket_prep(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
+                        const Scratch& s, const uint16_t* h, uint16_t* o1, uint16_t* o2);
 // Residual add + RMSNorm per token row (see resid_norm_kernel); optional
 // outputs: h_out (x), normed (bf16), the fp16 operand in prep->x16p/sxp/xs,
 // and a one-slot table for launch_q4k_dense in slot_tab (META_WORDS + 3 ints).
@@ -306,7 +311,10 @@ void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_ro
 // launch_combine.
 void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
                         const uint16_t* h_in, const RouteReq* route = nullptr);
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s);
+// With o1/o2 (one routed pair per token, no shared expert) it writes
+// out = bf16(wts[token] * y) there instead of y, and no combine is needed.
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                     const float* wts = nullptr, uint16_t* o1 = nullptr, uint16_t* o2 = nullptr);
 // Host-side reorder of one packed Q4_K expert (gate|up|down, each [N][K/256]
 // blocks of 144 B) into the device layout the linear kernel streams.
 void repack_q4k_expert(const uint8_t* src, uint8_t* dst, int hd, int inter);

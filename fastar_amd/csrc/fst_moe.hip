@@ -445,6 +445,7 @@ void launch_bucket(hipStream_t st, const Geometry& g, int M, int use_shared, con
                        s.slot_eid, s.slot_M, s.slot_off, s.pair_tok, s.pair_of, s.pair_shared);
 }
 
+
 // -------------------------------------------------------------- operand prep
 
 // Element sources for the prep kernel: bf16 activations, or the fp32
@@ -596,6 +597,42 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
     if (row >= nrows) return;
     __shared__ float xv[kMaxPrepK];
     prep_row<256>(src, row, K, xv, x16p, sxp, xs);
+}
+
+// Caller-given routing (process_expert_ffn): workgroup 0 buckets the eids
+// (bucket_block), workgroups 1..M prepare each token row's fp16 operand
+// (Q4_K only), in one launch.  When the down launch writes the result
+// itself (o1/o2 given: one routed pair per token, no shared expert),
+// workgroup 0 also zeroes the output rows of tokens whose expert id is
+// invalid, which the combine would have written as zeros.
+__global__ __launch_bounds__(kRouteThreads) void bucket_prep_kernel(
+    int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids, Scratch s, const uint16_t* h, int K,
+    uint16_t* o1, uint16_t* o2, int hd) {
+    if (blockIdx.x > 0) {
+        __shared__ float xv[kMaxPrepK];
+        prep_row<kRouteThreads>(SrcBf16{h}, blockIdx.x - 1, K, xv, s.x16p, s.sxp, s.xs);
+        return;
+    }
+    __shared__ int s_eids[kMaxTokens * kMaxTopK];
+    for (int i = threadIdx.x; i < M * tk; i += kRouteThreads) s_eids[i] = eids[i];
+    __syncthreads();
+    bucket_block<kRouteThreads>(M, E, tk, use_shared, s_eids, 0, s.meta, s.slot_eid, s.slot_M, s.slot_off,
+                                s.pair_tok, s.pair_of, s.pair_shared);
+    if (o1 || o2)
+        for (int i = threadIdx.x; i < M * (hd / 8); i += kRouteThreads) {
+            const int t = i / (hd / 8), q = i - t * (hd / 8);
+            const int e = s_eids[t * tk];
+            if (e >= 0 && e < E) continue;
+            const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+            if (o1) reinterpret_cast<uint4*>(o1 + (size_t)t * hd)[q] = z;
+            if (o2) reinterpret_cast<uint4*>(o2 + (size_t)t * hd)[q] = z;
+        }
+}
+
+void launch_bucket_prep(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
+                        const Scratch& s, const uint16_t* h, uint16_t* o1, uint16_t* o2) {
+    hipLaunchKernelGGL(bucket_prep_kernel, dim3(1 + (h ? M : 0)), dim3(kRouteThreads), 0, st, M, g.E, g.tk,
+                       use_shared, eids, s, h, g.hd, o1, o2, g.hd);
 }
 
 // The routing front of a layer call in one launch: workgroups [0, nrb) compute
@@ -927,6 +964,12 @@ struct EpiArgs {
     float swiglu_limit;
     float* h;
     uint16_t* h16;
+    // mode 2 with one routed pair per token and no shared expert: write
+    // out = bf16(w[token] * y) to o1/o2 (either may be null) instead of y
+    const float* wts;
+    const int* pair_tok;
+    uint16_t* o1;
+    uint16_t* o2;
 };
 
 #ifndef FST_Q4K_PF
@@ -1307,6 +1350,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
             }
             continue;
         }
+        const bool direct = MODE == 2 && (ep.o1 || ep.o2);
 #pragma unroll
         for (int q = 0; q < NGRP; ++q) {
             if (q * 16 >= Me) continue;
@@ -1315,7 +1359,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                 const int tl = q * 16 + 4 * g + i;
                 if (tl >= Me) continue;
                 const int pidx = off + tl;
-                out[(size_t)pidx * N + row] = ldexpf(acc[q][i], unscale(pidx));
+                const float yv = ldexpf(acc[q][i], unscale(pidx));
+                if (direct) {
+                    // the combine of a single pair: bf16(w * y) (src/fst_engine.cpp:4196-4201)
+                    const int tok = ep.pair_tok[pidx];
+                    const uint16_t o = fst_f32_to_bf16(ep.wts[tok] * yv);
+                    if (ep.o1) ep.o1[(size_t)tok * N + row] = o;
+                    if (ep.o2) ep.o2[(size_t)tok * N + row] = o;
+                } else {
+                    out[(size_t)pidx * N + row] = yv;
+                }
             }
         }
     }
@@ -1413,14 +1466,22 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
 }
 
 // down: y[pair][n] (fp32) for every (token, expert) pair of the call.
-void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s) {
+void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                     const float* wts, uint16_t* o1, uint16_t* o2) {
     const size_t proj = g.codec == 1 ? (size_t)g.inter * (g.hd / 32) * 17 : (size_t)g.inter * (g.hd / 256) * 144;
+    EpiArgs ep{};
+    if (o1 || o2) {
+        ep.wts = wts;
+        ep.pair_tok = s.pair_tok;
+        ep.o1 = o1;
+        ep.o2 = o2;
+    }
     if (g.codec == 1)
         launch_q4k_linear<2, 1>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd,
-                                s, nullptr, s.a16p, nullptr, nullptr, s.y, EpiArgs{});
+                                s, nullptr, s.a16p, nullptr, nullptr, s.y, ep);
     else
         launch_q4k_linear<2>(st, M, (unsigned)s.max_slots, L.bank, L.expert_stride, 2 * proj, g.inter, g.hd, s,
-                             nullptr, s.a16p, s.sx2p, s.xs2, s.y, EpiArgs{});
+                             nullptr, s.a16p, s.sx2p, s.xs2, s.y, ep);
 }
 
 // Dense Q4_K linear over M rows (the LM head): logits[m][n] = sum_k W[n][k] x[m][k],

@@ -103,6 +103,30 @@ def test_weighted_multi_expert(fa, oracle, small_ctx):
     assert rel_l2(bf16_to_f32(out), ref) < FFN_TOL
 
 
+def test_single_pair_per_token(fa, oracle, small_ctx):
+    """tk = 1 and no shared expert: the down launch writes bf16(w * y) itself
+    instead of a separate combine.  Checked against the oracle, and bit for
+    bit against the combine path (the same tokens at tk = 2 with a second
+    pair of weight 0)."""
+    ctx, experts = small_ctx
+    M = 6
+    h = fa.synth_normal_bf16(9, 4, (M, HD))
+    eids = np.array([[0], [1], [2], [3], [1], [0]], np.int32)
+    wts = np.array([[0.7], [1.0], [-0.5], [2.0], [0.25], [1.5]], np.float32)
+    note("expert_ffn tk=1 M=6 (direct down output)")
+    out = ctx.expert_ffn(0, h, eids, wts)
+    note("expert_ffn tk=2 M=6 (combine)")
+    out2 = ctx.expert_ffn(0, h, np.concatenate([eids, (eids + 1) % 4], 1),
+                          np.concatenate([wts, np.zeros_like(wts)], 1))
+    assert np.array_equal(out, out2)
+    ys = [oracle.expert_ffn(0, experts[e], h) for e in range(4)]
+    ref = np.stack([wts[m, 0] * ys[eids[m, 0]][m] for m in range(M)])
+    assert rel_l2(bf16_to_f32(out), ref) < FFN_TOL
+    with pytest.raises(fa.FstError) as ei:
+        ctx.expert_ffn(0, h[:2], np.array([[0], [7]], np.int32), np.ones((2, 1), np.float32))
+    assert ei.value.code == fa.FST_EINVAL
+
+
 def test_invalid_expert_rejected(fa, small_ctx):
     ctx, _ = small_ctx
     h = np.zeros((2, HD), np.uint16)
