@@ -539,11 +539,17 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
                                 direct ? d_out : nullptr, direct ? d_out_routed : nullptr);
         ctx->mark("bucket_prep");
     }
-    fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h, fuse_topk ? &rq : nullptr);
+    const int sh_q = use_shared && !sh16 ? 1 : 0;  // the shared expert runs as slot 0
+    const int ksplit = fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h, fuse_topk ? &rq : nullptr,
+                                               std::min(c.n_experts, M * g.tk) + sh_q, M * (g.tk + sh_q));
     ctx->mark("q4k_gate_up");
     if (!mx) {
-        fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p,
-                             ctx->s.sx2p, ctx->s.xs2);
+        if (ksplit > 1)
+            fst::launch_prep_act_split(st, ctx->s.act, ksplit, M * (g.tk + sh_q), c.swiglu_limit, ctx->s.meta,
+                                       c.inter_dim, ctx->s.a16p, ctx->s.sx2p, ctx->s.xs2);
+        else
+            fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p,
+                                 ctx->s.sx2p, ctx->s.xs2);
         ctx->mark("prep_h");
     }
     if (direct) {

@@ -309,8 +309,18 @@ void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_ro
 // Weights must be in the wave-tiled device layout (repack_q4k_expert).
 // gate/up writes h = silu(gate)*up; down writes y[pair] (fp32), combined by
 // launch_combine.
-void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
-                        const uint16_t* h_in, const RouteReq* route = nullptr);
+// slots_bound / pairs_bound: upper bounds of the call's slots and (token,
+// expert) pairs (0: unknown).  Returns the split-K factor it chose: with
+// ksplit > 1 (Q4_K only) each (slot, tile) is split into ksplit super-block
+// ranges that write partial gate and up sums over s.act
+// ([ksplit][pairs_bound][2*inter]), and the caller runs
+// launch_prep_act_split (which adds them up and applies the SwiGLU) instead
+// of launch_prep_act.
+int launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                       const uint16_t* h_in, const RouteReq* route = nullptr, int slots_bound = 0,
+                       int pairs_bound = 0);
+void launch_prep_act_split(hipStream_t st, const float* part, int S, int rows, float swiglu_limit, const int* meta,
+                           int inter, _Float16* a16p, uint4* sxp, int* xs);
 // With o1/o2 (one routed pair per token, no shared expert) it writes
 // out = bf16(wts[token] * y) there instead of y, and no combine is needed.
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,

@@ -484,6 +484,53 @@ struct SrcF32 {
         f[3] = fst_bits_f32(v.w);
     }
 };
+// h = silu(gate) * up from the split-K partials of the gate||up launch:
+// part[ks][row][2*inter] (gate in [0, inter), up in [inter, 2*inter)), the S
+// partials added in ks order, then the same SwiGLU (and clamp) as the
+// unsplit launch's epilogue.
+template <int S>
+struct SrcSplit {
+    static constexpr int kVec = 4;
+    const float* part;
+    int rows, inter;
+    float lim;
+    __device__ __forceinline__ float4 ld(int ks, size_t row, int off) const {
+        return *reinterpret_cast<const float4*>(part + ((size_t)ks * rows + row) * (2 * inter) + off);
+    }
+    __device__ __forceinline__ uint4 vec(size_t row, int, int q) const {
+        // all 2S loads issued before the sums
+        float4 g[S], u[S];
+#pragma unroll
+        for (int ks = 0; ks < S; ++ks) {
+            g[ks] = ld(ks, row, 4 * q);
+            u[ks] = ld(ks, row, inter + 4 * q);
+        }
+        float4 gs = g[0], us = u[0];
+#pragma unroll
+        for (int ks = 1; ks < S; ++ks) {
+            gs.x += g[ks].x; gs.y += g[ks].y; gs.z += g[ks].z; gs.w += g[ks].w;
+            us.x += u[ks].x; us.y += u[ks].y; us.z += u[ks].z; us.w += u[ks].w;
+        }
+        const float gv[4] = {gs.x, gs.y, gs.z, gs.w}, uv[4] = {us.x, us.y, us.z, us.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float a = gv[e], b = uv[e];
+            if (lim > 0.0f) {
+                a = fminf(a, lim);
+                b = fminf(fmaxf(b, -lim), lim);
+            }
+            o[e] = fst_f32_bits((a / (1.0f + expf(-a))) * b);
+        }
+        return make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    __device__ __forceinline__ void unpack(const uint4& v, float* f) const {
+        f[0] = fst_bits_f32(v.x);
+        f[1] = fst_bits_f32(v.y);
+        f[2] = fst_bits_f32(v.z);
+        f[3] = fst_bits_f32(v.w);
+    }
+};
 constexpr int kMaxPrepK = 8192;
 
 // Power-of-two prescale of a row whose largest finite |x| is a: the s with
@@ -831,6 +878,21 @@ void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_ro
                        max_rows, K, a16p, sxp, xs);
 }
 
+void launch_prep_act_split(hipStream_t st, const float* part, int S, int rows, float swiglu_limit, const int* meta,
+                           int inter, _Float16* a16p, uint4* sxp, int* xs) {
+#define FST_PS(SV)                                                                                          \
+    hipLaunchKernelGGL(prep_kernel<SrcSplit<SV>>, dim3(rows), dim3(256), 0, st,                             \
+                       SrcSplit<SV>{part, rows, inter, swiglu_limit}, meta + META_N_PAIRS, rows, inter, a16p, sxp, \
+                       xs)
+    if (S <= 2)
+        FST_PS(2);
+    else if (S <= 4)
+        FST_PS(4);
+    else
+        FST_PS(8);
+#undef FST_PS
+}
+
 // ------------------------------------------------------- Q4_K linear kernel
 
 // Per-lane decode of one super-block row slice.  Lane (row r = lane&15, group
@@ -970,6 +1032,11 @@ struct EpiArgs {
     const int* pair_tok;
     uint16_t* o1;
     uint16_t* o2;
+    // mode 1 split-K: S > 1 items per (slot, tile), partial sums written to
+    // part[ks][pair][N] (part_rows pairs per split) instead of h
+    int ksplit;
+    float* part;
+    int part_rows;
 };
 
 #ifndef FST_Q4K_PF
@@ -1050,12 +1117,17 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     const int* slot_off = RPER > 0 ? r_soff : slot_off_g;
     const int* a_row = RPER > 0 ? r_ptok : a_row_g;
 
+    // split-K (gate||up of calls with few slots, ep.ksplit > 1): work item
+    // t = ((slot * tiles) + tile) * S + ks covers super-blocks [ks*nsb,
+    // (ks+1)*nsb) of the rows and writes partial sums
+    const int S = MODE == 1 ? max(ep.ksplit, 1) : 1;
     const int tiles = N / (16 * WAVES);
-    const int total = meta[META_N_SLOTS] * tiles;
+    const int total = meta[META_N_SLOTS] * tiles * S;
     if ((int)blockIdx.x >= total) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane & 15, g = lane >> 4;
-    const int nsb = K >> 8;
+    const int nsb_row = K >> 8;      // super-blocks per row
+    const int nsb = nsb_row / S;     // super-blocks per work item
     const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
     const f4_t zf = f4_t{0.f, 0.f, 0.f, 0.f};
     const uint32_t magic = 0x64006400u;
@@ -1072,9 +1144,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     // wave-tiled device layout (see repack_q4k_matrix): the wave's 16 rows are
     // one contiguous run of nsb 2304-byte chunks read front to back
     auto wave_base = [&](int tt) -> const uint8_t* {
-        const int sl = tt / tiles;
+        const int sl = tt / (tiles * S), rm = tt - sl * tiles * S, ti = rm / S, ks = rm - ti * S;
         return bank + (size_t)slot_eid[sl] * expert_stride + mat_offset +
-               (size_t)wave_tile(tt - sl * tiles) * nsb * CHUNK;
+               ((size_t)wave_tile(ti) * nsb_row + (size_t)ks * nsb) * CHUNK;
     };
     // Weight loads go through a buffer resource on the wave's run (uniform:
     // scalar base, the chunk offset in soffset, constant lane offsets), so no
@@ -1130,7 +1202,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         spart[i] = rem - (rem / PARTS) * PARTS;
     }
     auto load_rows = [&](int tt, int* ar) -> int {
-        const int sl = tt / tiles;
+        const int sl = tt / (tiles * S);
         const int Mi = min(slot_M[sl], TOKS), offi = slot_off[sl];
 #pragma unroll
         for (int i = 0; i < NS; ++i)
@@ -1149,7 +1221,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     int sdst[NS];
     int sstep[NS];
     u4v_t sv[NS];
-    auto build_map = [&](const int* ar, int me) {
+    // sbo: the item's first super-block within the row
+    auto build_map = [&](const int* ar, int me, int sbo) {
         st_me = me;
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
@@ -1159,10 +1232,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
             sstep[i] = 0;
             if (ar[i] >= 0) {
                 if (part < 32) {
-                    ssrc[i] = reinterpret_cast<const u4v_t*>(A + (size_t)ar[i] * K) + u * 32 + part;
+                    ssrc[i] = reinterpret_cast<const u4v_t*>(A + (size_t)ar[i] * K) + (sbo + u) * 32 + part;
                     sstep[i] = 32 * MS;
                 } else {
-                    ssrc[i] = reinterpret_cast<const u4v_t*>(SX + (size_t)ar[i] * nsb * 4 + u * 4 + (part - 32));
+                    ssrc[i] = reinterpret_cast<const u4v_t*>(SX + (size_t)ar[i] * nsb_row * 4 + (sbo + u) * 4 +
+                                                               (part - 32));
                     sstep[i] = 4 * MS;
                 }
             }
@@ -1188,14 +1262,15 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     {
         int ar0[NS];
         const int me0 = load_rows(blockIdx.x, ar0);
-        build_map(ar0, me0);
+        build_map(ar0, me0, ((int)blockIdx.x % S) * nsb);
         stage_load(0);
     }
     const int nms = nsb / MS;
 
     for (int t = blockIdx.x; t < total; t += gridDim.x) {
-        const int slot = t / tiles;
-        const int tile = t - slot * tiles;
+        const int slot = t / (tiles * S);
+        const int tile = (t - slot * tiles * S) / S;
+        const int ks = t % S;
         const int tn = t + (int)gridDim.x;
         const __amdgpu_buffer_rsrc_t nrs = tn < total ? rsrc(wave_base(tn)) : wrs;
         const int Me = min(slot_M[slot], TOKS), off = slot_off[slot];
@@ -1283,7 +1358,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                     if (sb / MS + 1 < nms) {
                         stage_load(sb / MS + 1);
                     } else {
-                        build_map(ar_next, me_next);
+                        build_map(ar_next, me_next, (tn < total ? tn % S : ks) * nsb);
                         stage_load(0);
                     }
                 }
@@ -1308,6 +1383,22 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
             else
                 return xs[a_row ? a_row[pidx] : pidx];
         };
+        if (MODE == 1 && S > 1) {
+            // split-K: this item's partial gate and up sums (rows of the
+            // [gate | up] matrix) for the prep launch to add up
+#pragma unroll
+            for (int q = 0; q < NGRP; ++q) {
+                if (q * 16 >= Me) break;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tl = q * 16 + 4 * g + i;
+                    if (tl >= Me) continue;
+                    ep.part[((size_t)ks * ep.part_rows + off + tl) * N + row] =
+                        ldexpf(acc[q][i], unscale(off + tl));
+                }
+            }
+            continue;
+        }
         if constexpr (MODE == 1) {
             // gate waves hand their rows to the up waves through LDS (the
             // staging ring is free: the loop ended on a barrier)
@@ -1379,11 +1470,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
 #ifndef FST_Q4K_WG_PER_CU
 #define FST_Q4K_WG_PER_CU 2
 #endif
-template <int MODE, int CODEC = 0, int RPER = 0>
-static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
-                              size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
-                              const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep,
-                              const RouteArgs& ra = RouteArgs{}) {
 #ifndef FST_Q4K_W
 #define FST_Q4K_W 8
 #endif
@@ -1393,14 +1479,27 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 #ifndef FST_Q4K_W32
 #define FST_Q4K_W32 16
 #endif
-    // waves per workgroup by token capacity (larger capacities stage more
-    // operand chunks per super-block; more threads hold fewer each), when N
-    // is a multiple of the workgroup's 16*W rows
+// Waves per workgroup of the linear kernel by token capacity (larger
+// capacities stage more operand chunks per super-block; more threads hold
+// fewer each), when N is a multiple of the workgroup's 16*W rows.
+static int linear_waves(int M, int N) {
     const int WC = M <= 8 ? FST_Q4K_W : (M <= 16 ? FST_Q4K_W16 : (M <= 32 ? FST_Q4K_W32 : FST_Q4K_W));
-    const int W = N % (16 * WC) == 0 ? WC : FST_Q4K_W;
+    return N % (16 * WC) == 0 ? WC : FST_Q4K_W;
+}
+// Resident waves per CU the persistent grid is sized for.
+static int linear_waves_per_cu(int M) {
+    return 8 * (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1));
+}
+
+template <int MODE, int CODEC = 0, int RPER = 0>
+static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
+                              size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
+                              const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep,
+                              const RouteArgs& ra = RouteArgs{}) {
+    const int W = linear_waves(M, N);
     // persistent grid: FST_Q4K_WG_PER_CU workgroups per CU at most
-    const unsigned items = slots * (unsigned)(N / (16 * W));
-    const unsigned waves_per_cu = 8u * (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1));
+    const unsigned items = slots * (unsigned)(N / (16 * W)) * (unsigned)(MODE == 1 ? std::max(ep.ksplit, 1) : 1);
+    const unsigned waves_per_cu = (unsigned)linear_waves_per_cu(M);
     const dim3 grid(std::min(items, (unsigned)s.n_cu * std::max(1u, waves_per_cu / (unsigned)W)));
 #define FST_Q4K_LAUNCH_W(T, MSV, WV)                                                                         \
     hipLaunchKernelGGL((q4k_linear_kernel<T, MSV, WV, MODE, CODEC, RPER>), grid, dim3(64 * WV), 0, st, bank,    \
@@ -1437,12 +1536,30 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
 // workgroup takes 64 gate rows and the same 64 up rows and writes
 // h = silu(gate)*up (fp32 for Q4_K, bf16 for MXFP4).  The Q4_K operand is the
 // prescaled fp16 one (router_prep); MXFP4 stages the bf16 rows of h_in as is.
-void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
-                        const uint16_t* h_in, const RouteReq* rq) {
+int launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                       const uint16_t* h_in, const RouteReq* rq, int slots_bound, int pairs_bound) {
+    // split-K when the call's (slot, tile) items would leave most of the
+    // persistent grid idle: more, shorter items (each wave's chain of
+    // dependent super-block loads gets shorter); Q4_K only (the prep launch
+    // adds the partials up), at most 8 ways, 2 super-blocks per item at least
+    int ksplit = 1;
+    if (g.codec == 0 && slots_bound > 0 && pairs_bound > 0) {
+        const int N = 2 * g.inter, W = linear_waves(M, N);
+        const long items = (long)slots_bound * (N / (16 * W));
+        const long cap = (long)s.n_cu * std::max(1, linear_waves_per_cu(M) / W);
+        const int nsb_row = g.hd >> 8;
+        while (ksplit < 8 && items * ksplit * 2 <= cap && 2L * ksplit * 2 * pairs_bound <= s.max_pairs &&
+               nsb_row % (ksplit * 4) == 0)
+            ksplit *= 2;
+    }
+    const int part_rows = pairs_bound;
     EpiArgs ep{};
     ep.swiglu_limit = g.swiglu_limit;
     ep.h = s.act;
     ep.h16 = reinterpret_cast<uint16_t*>(s.a16p);
+    ep.ksplit = ksplit;
+    ep.part = s.act;
+    ep.part_rows = part_rows;
     const unsigned S = (unsigned)s.max_slots;
     const _Float16* hx = reinterpret_cast<const _Float16*>(h_in);
     if (rq && g.E <= kFusedRouteMaxExperts) {
@@ -1455,7 +1572,7 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
         else
             launch_q4k_linear<1, 0, 4>(st, M, S, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s, s.pair_tok,
                                        s.x16p, s.sxp, s.xs, nullptr, ep, ra);
-        return;
+        return ksplit;
     }
     if (g.codec == 1)
         launch_q4k_linear<1, 1>(st, M, S, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s, s.pair_tok, hx, nullptr,
@@ -1463,6 +1580,7 @@ void launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, i
     else
         launch_q4k_linear<1>(st, M, S, L.bank, L.expert_stride, 0, g.hd, 2 * g.inter, s, s.pair_tok, s.x16p, s.sxp,
                              s.xs, nullptr, ep);
+    return ksplit;
 }
 
 // down: y[pair][n] (fp32) for every (token, expert) pair of the call.
