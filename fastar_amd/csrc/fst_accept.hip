@@ -497,12 +497,6 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
 // is resident or finished (the lowest unfinished id never waits), and the
 // wait ends.  (Counters instead of flags serialise: increments of one
 // device-scope counter complete a few hundred ns apart at the memory side.)
-__device__ __forceinline__ void st_coherent_u64(unsigned long long* p, unsigned long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long ld_coherent_u64(const unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 template <int CH>
 __device__ __forceinline__ void greedy_chunk(const float* __restrict__ row, int V, int c, float& best, int& bi) {

@@ -82,21 +82,13 @@ struct Geometry {
 // On this multi-XCD GPU each XCD has its own L2; an agent-scope fence
 // (__threadfence) writes back and invalidates the whole L2, which is far too
 // expensive to issue per workgroup.  Data handed to another workgroup is
-// instead written with device-coherent stores (sc1), the writer waits for its
-// stores to complete, then signals with a relaxed device-scope atomic; the
-// reader uses device-coherent loads.
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coherent(int* p, int v) {
+// instead written with device-coherent stores (sc1) that carry their own
+// "written" marker, the writer waits for its stores to complete, and the
+// reader polls with device-coherent loads.
+__device__ __forceinline__ void st_coherent_u64(unsigned long long* p, unsigned long long v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_coherent(const float* p) {
-    return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT));
-}
-__device__ __forceinline__ int ld_coherent(const int* p) {
+__device__ __forceinline__ unsigned long long ld_coherent_u64(const unsigned long long* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait until this thread's stores are complete (and keep the compiler from
@@ -105,11 +97,6 @@ __device__ __forceinline__ void publish_wait() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-__device__ __forceinline__ int signal_add(int* c, int v) {
-    const int r = __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    return r;
 }
 
 // ---- wave-level DPP reductions (all 64 lanes active) ----
