@@ -1042,6 +1042,12 @@ struct EpiArgs {
 #ifndef FST_Q4K_PF
 #define FST_Q4K_PF 1
 #endif
+#ifndef FST_SKIP_DEAD_SLOTS
+#define FST_SKIP_DEAD_SLOTS 1
+#endif
+#ifndef FST_UNROLL_X
+#define FST_UNROLL_X 1
+#endif
 // Y[pair][row] = 2^xs[a] * sum_k W[row][k] * A[a][k] for the rows of one
 // Q4_K matrix (N rows x K/256 super-blocks per row) of each slot's expert.
 // Work item t = (slot, tile) covers 16*WAVES rows: wave w owns 16 rows and up
@@ -1075,7 +1081,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     constexpr int NS = (NCH + NT - 1) / NT;          // staged chunks per thread
     constexpr int HALF = WAVES / 2;
     constexpr int R = PF + 1;                        // weight register ring
-    constexpr int U = (MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R);  // lcm(MS, R)
+    constexpr int U = FST_UNROLL_X * ((MS % R == 0) ? MS : (R % MS == 0 ? R : MS * R));  // lcm(MS, R)
     static_assert(U % MS == 0 && U % R == 0, "unroll must cover whole stages and ring turns");
     __shared__ uint4 lds[2 * STAGE];
 
@@ -1161,14 +1167,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     constexpr int kNT = 2;  // cache policy: non-temporal (streamed once)
     auto load_w = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WRaw {
         WRaw x;
+        // (the header first: issued last, its register was taken by a live
+        // staging address and got a copy at the loop back-edge, which waits
+        // for the load: vmcnt(0) once per loop iteration)
+        if constexpr (!MX) x.h = __builtin_amdgcn_raw_buffer_load_b128(rs, 2048 + 16 * (lane & 15), off, kNT);
         x.a = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, off, kNT);
         x.b = __builtin_amdgcn_raw_buffer_load_b128(rs, 1024 + 16 * lane, off, kNT);
         if constexpr (MX) {
             typedef uint32_t u2v_t __attribute__((ext_vector_type(2)));
             const u2v_t hv = __builtin_amdgcn_raw_buffer_load_b64(rs, 2048 + 8 * (lane & 15), off, kNT);
             x.h = u4v_t{hv.x, hv.y, 0u, 0u};
-        } else {
-            x.h = __builtin_amdgcn_raw_buffer_load_b128(rs, 2048 + 16 * (lane & 15), off, kNT);
         }
         return x;
     };
@@ -1247,7 +1255,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     auto stage_load = [&](int m) {
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
+#if FST_SKIP_DEAD_SLOTS
             if (i > 0 && st_me <= slot_minrow(i)) continue;
+#endif
             const bool live = m * MS + su[i] < nsb;
             const size_t o = live ? (size_t)m * sstep[i] : 0;
             sv[i] = ssrc[i][o];
@@ -1355,15 +1365,18 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
             for (int j = 0; j < U; ++j) {
                 const int sb = sb0 + j;
                 if (j % MS == 0) {
-                    if (sb / MS + 1 < nms) {
-                        stage_load(sb / MS + 1);
-                    } else {
-                        build_map(ar_next, me_next, (tn < total ? tn % S : ks) * nsb);
-                        stage_load(0);
-                    }
+                    // one call site for the staging loads: loads issued on two
+                    // paths leave their registers to a copy at the merge,
+                    // and the copy waits for the load (vmcnt(0))
+                    const bool last = sb / MS + 1 >= nms;
+                    if (last) build_map(ar_next, me_next, (tn < total ? tn % S : ks) * nsb);
+                    stage_load(last ? 0 : sb / MS + 1);
                 }
                 const int pf = sb + PF;
-                w[(j + PF) % R] = pf < nsb ? load_w(wrs, pf * CHUNK) : load_w(nrs, (pf - nsb) * CHUNK);
+                // one load call site (resource and offset selected first), for
+                // the same reason as the staging loads
+                const bool pnx = pf >= nsb;
+                w[(j + PF) % R] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHUNK);
                 // keep the prefetches where they are issued (the scheduler
                 // would otherwise sink them next to their use to save registers)
                 __builtin_amdgcn_sched_barrier(0);
