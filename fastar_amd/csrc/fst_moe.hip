@@ -1531,12 +1531,18 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
         FST_Q4K_LAUNCH(8, ms8);
     else if (M <= 8)
         FST_Q4K_LAUNCH(8, 2);
+#ifndef FST_MS16
+#define FST_MS16 2
+#endif
+#ifndef FST_MS32
+#define FST_MS32 1
+#endif
     else if (M <= 16 && W == FST_Q4K_W16)
-        FST_Q4K_LAUNCH_W(16, 2, FST_Q4K_W16);
+        FST_Q4K_LAUNCH_W(16, FST_MS16, FST_Q4K_W16);
     else if (M <= 16)
         FST_Q4K_LAUNCH(16, 2);
     else if (M <= 32 && W == FST_Q4K_W32)
-        FST_Q4K_LAUNCH_W(32, 1, FST_Q4K_W32);
+        FST_Q4K_LAUNCH_W(32, FST_MS32, FST_Q4K_W32);
     else if (M <= 32)
         FST_Q4K_LAUNCH(32, 1);
     else
