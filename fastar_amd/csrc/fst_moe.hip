@@ -1042,6 +1042,9 @@ struct EpiArgs {
 #ifndef FST_Q4K_PF
 #define FST_Q4K_PF 1
 #endif
+#ifndef FST_SHARED_PREFETCH
+#define FST_SHARED_PREFETCH 1
+#endif
 #ifndef FST_SKIP_DEAD_SLOTS
 #define FST_SKIP_DEAD_SLOTS 1
 #endif
@@ -1100,7 +1103,30 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         la.pair_tok = r_ptok;
         la.pair_of = r_pof;
         la.pair_shared = r_psh;
+#if FST_SHARED_PREFETCH
+        // The shared expert (slot 0, bank index E) is the one expert known
+        // before routing: every workgroup reads its slice of the shared
+        // gate||up weights while it routes, so that stream overlaps the
+        // routing instead of following it, and the shared-expert items later
+        // find the lines in the device-wide cache.  The values are discarded.
+        uint4 pfv[3];
+        const int npf = ra.use_shared ? 3 : 0;
+        {
+            const size_t pieces = (size_t)(N / 16) * (K >> 8) * (CHUNK / 16);  // 16-byte pieces of gate||up
+            const uint4* src = reinterpret_cast<const uint4*>(bank + (size_t)ra.E * expert_stride + mat_offset);
+            const size_t step = (size_t)gridDim.x * (64 * WAVES);
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const size_t q = (size_t)blockIdx.x * (64 * WAVES) + threadIdx.x + i * step;
+                pfv[i] = i < npf ? src[q < pieces ? q : 0] : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+#endif
         topk_bucket_block<RPER, 64 * WAVES, TOKS>(la, blockIdx.x == 0);
+#if FST_SHARED_PREFETCH
+#pragma unroll
+        for (int i = 0; i < 3; ++i) asm volatile("" ::"v"(pfv[i].x));
+#endif
         __syncthreads();
         if (blockIdx.x == 0) {
             const int ns = r_meta[META_N_SLOTS], np = r_meta[META_N_PAIRS];
