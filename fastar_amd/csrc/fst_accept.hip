@@ -380,12 +380,19 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
     __shared__ u128 s_run;
     __shared__ int s_tok;
     unsigned long long* d = dec + (size_t)s * 8;
-    if (tid < 64) load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
+    // the chunk totals do not depend on the row context: load them first so
+    // that both round trips overlap
+    unsigned long long o0 = 0, o1 = 0;
+    if (tid < 64) {
+        const unsigned long long* o = part_res + ((size_t)s * kChunks + lane) * 2;
+        o0 = o[0];
+        o1 = o[1];
+        load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
+    }
     __syncthreads();
     if (tid < 64) {
         const unsigned long long U2 = d[3];
-        const unsigned long long* o = part_res + ((size_t)s * kChunks + lane) * 2;
-        u128 cs = ((u128)o[1] << 64) | (u128)o[0];
+        u128 cs = ((u128)o1 << 64) | (u128)o0;
         u128 pre = wave_incl_scan_u128(cs);
         u128 tot = shfl_u128(pre, 63);
         int mode = rc.mode;
@@ -425,17 +432,23 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
         u128 cache[kCache];
         u128 acc = 0;
         if (per <= kCache) {
+            // slots past the run length `per` (uniform) are skipped, not
+            // computed and discarded: each slot costs two exponentials and
+            // 128-bit products
             float xt[kCache], xd[kCache];
 #pragma unroll
             for (int u = 0; u < kCache; ++u) {
+                if (u >= per) break;
                 const int v = max(min(v0 + u, v1 - 1), 0);
                 xt[u] = rc.trow[v];
                 xd[u] = rc.mode ? 0.0f : rc.drow[v];
             }
 #pragma unroll
             for (int u = 0; u < kCache; ++u) {
-                cache[u] = v0 + u < v1 ? res_of(xt[u], xd[u], inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode)
-                                       : (u128)0;
+                cache[u] = 0;
+                if (u >= per) continue;
+                if (v0 + u < v1)
+                    cache[u] = res_of(xt[u], xd[u], inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
                 acc += cache[u];
             }
         } else {
