@@ -18,6 +18,10 @@
 namespace fst {
 
 constexpr int kChunks = 64;
+// threads of the per-sequence residual and sampling workgroups (two
+// exponentials and 128-bit products per element, few workgroups: compute
+// bound per thread; the per-row sums keep 256, their grid is large)
+constexpr int kProbThreads = 1024;
 typedef unsigned __int128 u128;
 
 struct AccWs {
@@ -192,11 +196,15 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
     unsigned long long acc = 0;
     for_strided<8>(row, b0 + (int)threadIdx.x, b1, 256, [&](float x, int) { acc += fixed_prob(x, inv_t, mx, any); });
     // integer sums: any order gives the same total
-    __shared__ unsigned long long sm[4];
+    __shared__ unsigned long long sm[256 / 64];
     acc = wave_sum_u64_dpp(acc);
     if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
     __syncthreads();
-    if (threadIdx.x == 0) part_sum[(size_t)r * kChunks + c] = (sm[0] + sm[1]) + (sm[2] + sm[3]);
+    if (threadIdx.x == 0) {
+        unsigned long long t = 0;
+        for (int w = 0; w < 256 / 64; ++w) t += sm[w];
+        part_sum[(size_t)r * kChunks + c] = t;
+    }
 }
 
 // dec layout per sequence: [0] n_acc, [1] sampling target row, [2] mode
@@ -316,7 +324,7 @@ __device__ void load_rowctx_wave(const float* target, const float* draftl, int n
 }
 
 // Residual (or target) chunk sums for the one sampling row of each sequence.
-__global__ __launch_bounds__(256) void acc_res_chunks_kernel(
+__global__ __launch_bounds__(kProbThreads) void acc_res_chunks_kernel(
     const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
     float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
     const unsigned long long* __restrict__ dec, unsigned long long* __restrict__ part_res) {
@@ -328,16 +336,17 @@ __global__ __launch_bounds__(256) void acc_res_chunks_kernel(
     const int clen = (V + kChunks - 1) / kChunks;
     const int b0 = c * clen, b1 = min(V, b0 + clen);
     u128 acc = 0;
-    for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, b0 + (int)threadIdx.x, b1, 256, [&](float xt, float xd, int) {
+    for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, b0 + (int)threadIdx.x, b1, kProbThreads, [&](float xt, float xd, int) {
         acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
     });
     // integer sums: any order gives the same total
-    __shared__ u128 sm[4];
+    __shared__ u128 sm[kProbThreads / 64];
     acc = wave_sum_u128(acc);
     if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
     __syncthreads();
     if (threadIdx.x == 0) {
-        const u128 tot = (sm[0] + sm[1]) + (sm[2] + sm[3]);
+        u128 tot = 0;
+        for (int w = 0; w < kProbThreads / 64; ++w) tot += sm[w];
         unsigned long long* o = part_res + ((size_t)s * kChunks + c) * 2;
         o[0] = (unsigned long long)tot;
         o[1] = (unsigned long long)(tot >> 64);
@@ -366,7 +375,7 @@ __device__ __forceinline__ u128 wave_incl_scan_u128(u128 v) {
 // target = (U' * total) >> 24.  Chunk sums are scanned by one wave (lane c
 // = chunk c), then the chosen chunk by the whole workgroup (thread t owns a
 // contiguous run), and only the owning thread walks its few elements.
-__global__ __launch_bounds__(256) void acc_sample_kernel(
+__global__ __launch_bounds__(kProbThreads) void acc_sample_kernel(
     const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
     float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
     const unsigned long long* __restrict__ part_sum, unsigned long long* __restrict__ dec,
@@ -375,7 +384,7 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
     __shared__ RowCtx rc;
     __shared__ u128 s_target, s_before;
     __shared__ int s_chunk;
-    __shared__ u128 wtot[4];
+    __shared__ u128 wtot[kProbThreads / 64];
     __shared__ int s_owner;
     __shared__ u128 s_run;
     __shared__ int s_tok;
@@ -424,7 +433,7 @@ __global__ __launch_bounds__(256) void acc_sample_kernel(
     if (c >= 0) {
         const int clen = (V + kChunks - 1) / kChunks;
         const int b0 = c * clen, b1 = min(V, b0 + clen);
-        const int per = (clen + 255) / 256;
+        const int per = (clen + kProbThreads - 1) / kProbThreads;
         const int v0 = b0 + tid * per, v1 = min(b1, v0 + per);
         // the thread's residual values stay in registers for the owner's walk
         // (runs of up to kCache elements; longer ones are recomputed there)
@@ -672,9 +681,9 @@ void launch_accept_stochastic(hipStream_t st, const float* target, const float* 
     hipLaunchKernelGGL(acc_decide_kernel, dim3(n_seq), dim3(64 * kDecideWaves), 0, st, target, draft_logits, n_seq, k, V,
                        inv_t, draft, seed, seq_base, w.part_max, w.part_idx, w.part_sum, w.dec, n_acc,
                        tokens);
-    hipLaunchKernelGGL(acc_res_chunks_kernel, dim3(kChunks, n_seq), dim3(256), 0, st, target, draft_logits,
+    hipLaunchKernelGGL(acc_res_chunks_kernel, dim3(kChunks, n_seq), dim3(kProbThreads), 0, st, target, draft_logits,
                        n_seq, k, V, inv_t, w.part_max, w.part_idx, w.dec, w.part_res);
-    hipLaunchKernelGGL(acc_sample_kernel, dim3(n_seq), dim3(256), 0, st, target, draft_logits, n_seq, k, V,
+    hipLaunchKernelGGL(acc_sample_kernel, dim3(n_seq), dim3(kProbThreads), 0, st, target, draft_logits, n_seq, k, V,
                        inv_t, w.part_max, w.part_idx, w.part_sum, w.dec, w.part_res, tokens);
 }
 
