@@ -176,6 +176,16 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
                                                        const int* __restrict__ part_idx,
                                                        unsigned long long* __restrict__ part_sum) {
     const int c = blockIdx.x, r = blockIdx.y;
+    const float* row = row_ptr(target, draft, n_tgt_rows, r, V);
+    const int clen = (V + kChunks - 1) / kChunks;
+    const int b0 = c * clen, b1 = min(V, b0 + clen);
+    // the first 8 elements of each thread are loaded before the row maximum
+    // is known (they do not depend on it), so both round trips overlap
+    constexpr int NB = 8;
+    const int v0 = b0 + (int)threadIdx.x;
+    float x0[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) x0[u] = row[max(min(v0 + u * 256, b1 - 1), 0)];
     __shared__ float s_mx;
     __shared__ int s_any;
     if (threadIdx.x < 64) {
@@ -190,11 +200,11 @@ __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__
     __syncthreads();
     const float mx = s_mx;
     const int any = s_any;
-    const float* row = row_ptr(target, draft, n_tgt_rows, r, V);
-    const int clen = (V + kChunks - 1) / kChunks;
-    const int b0 = c * clen, b1 = min(V, b0 + clen);
     unsigned long long acc = 0;
-    for_strided<8>(row, b0 + (int)threadIdx.x, b1, 256, [&](float x, int) { acc += fixed_prob(x, inv_t, mx, any); });
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+        if (v0 + u * 256 < b1) acc += fixed_prob(x0[u], inv_t, mx, any);
+    for_strided<8>(row, v0 + NB * 256, b1, 256, [&](float x, int) { acc += fixed_prob(x, inv_t, mx, any); });
     // integer sums: any order gives the same total
     __shared__ unsigned long long sm[256 / 64];
     acc = wave_sum_u64_dpp(acc);
@@ -329,16 +339,35 @@ __global__ __launch_bounds__(kProbThreads) void acc_res_chunks_kernel(
     float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
     const unsigned long long* __restrict__ dec, unsigned long long* __restrict__ part_res) {
     const int c = blockIdx.x, s = blockIdx.y;
-    __shared__ RowCtx rc;
-    if (threadIdx.x < 64)
-        load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, dec + (size_t)s * 8, rc);
-    __syncthreads();
+    const unsigned long long* d = dec + (size_t)s * 8;
     const int clen = (V + kChunks - 1) / kChunks;
     const int b0 = c * clen, b1 = min(V, b0 + clen);
+    // the thread's first elements are loaded as soon as the sampling rows are
+    // known, before their maxima (round trips overlap)
+    constexpr int NB = 2;
+    const int v0 = b0 + (int)threadIdx.x;
+    const int mode0 = (int)d[2];
+    const float* trow0 = target + (size_t)d[1] * V;
+    const float* drow0 = mode0 == 0 ? draftl + ((size_t)d[6] - (size_t)n_seq * (k + 1)) * V : trow0;
+    float xt0[NB], xd0[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const int v = max(min(v0 + u * kProbThreads, b1 - 1), 0);
+        xt0[u] = trow0[v];
+        xd0[u] = drow0[v];
+    }
+    __shared__ RowCtx rc;
+    if (threadIdx.x < 64) load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
+    __syncthreads();
     u128 acc = 0;
-    for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, b0 + (int)threadIdx.x, b1, kProbThreads, [&](float xt, float xd, int) {
-        acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
-    });
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+        if (v0 + u * kProbThreads < b1)
+            acc += res_of(xt0[u], rc.mode ? 0.0f : xd0[u], inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+    for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, v0 + NB * kProbThreads, b1, kProbThreads,
+                    [&](float xt, float xd, int) {
+                        acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
+                    });
     // integer sums: any order gives the same total
     __shared__ u128 sm[kProbThreads / 64];
     acc = wave_sum_u128(acc);
