@@ -714,7 +714,10 @@ __global__ __launch_bounds__(256) void router_prep_kernel(const uint4* __restric
 void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const uint16_t* h, int M, int prep,
                   const int32_t* input_ids, int use_hash, int use_shared, int32_t* eids, float* wts,
                   const Scratch& s, int topk) {
-    constexpr int TPW = 2;
+#ifndef FST_RTPW
+#define FST_RTPW 2
+#endif
+    constexpr int TPW = FST_RTPW;  // tokens per router wave
     const int nbx = (g.E + 3) / 4, nby = (M + TPW - 1) / TPW, nrb = nbx * nby;
     const dim3 grid(nrb + (prep ? M : 0));
 #define FST_RP(NVV)                                                                                        \
