@@ -91,19 +91,19 @@ struct fst_ctx {
     fst_timings last{};
 
     ~fst_ctx() {
-        if (st) hipStreamSynchronize(st);
-        for (void* p : allocs) hipFree(p);
+        if (st) (void)hipStreamSynchronize(st);
+        for (void* p : allocs) (void)hipFree(p);
         for (int32_t* p : hash)
-            if (p) hipFree(p);
-        if (lm_head) hipFree(lm_head);
-        if (lm_head16) hipFree(lm_head16);
+            if (p) (void)hipFree(p);
+        if (lm_head) (void)hipFree(lm_head);
+        if (lm_head16) (void)hipFree(lm_head16);
         for (uint16_t* p : shared16)
-            if (p) hipFree(p);
-        if (acc_ws) hipFree(acc_ws);
-        if (acc_logits) hipFree(acc_logits);
-        if (acc_io) hipFree(acc_io);
-        for (hipEvent_t e : ev) hipEventDestroy(e);
-        if (st) hipStreamDestroy(st);
+            if (p) (void)hipFree(p);
+        if (acc_ws) (void)hipFree(acc_ws);
+        if (acc_logits) (void)hipFree(acc_logits);
+        if (acc_io) (void)hipFree(acc_io);
+        for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+        if (st) (void)hipStreamDestroy(st);
     }
 
     template <typename T>
@@ -133,22 +133,22 @@ struct fst_ctx {
         if (nested) return;
         n_ev = 0;
         if (!profiling) return;
-        hipEventRecord(ev[0], st);
+        (void)hipEventRecord(ev[0], st);
         n_ev = 1;
     }
     void mark(const char* name, bool outer = false) {
         if ((nested && !outer) || !profiling || n_ev >= (int)ev.size()) return;
-        hipEventRecord(ev[n_ev], st);
+        (void)hipEventRecord(ev[n_ev], st);
         ev_names[n_ev] = name;
         ++n_ev;
     }
     void collect() {
         last.n = 0;
         if (!profiling || n_ev < 2) return;
-        hipEventSynchronize(ev[n_ev - 1]);
+        (void)hipEventSynchronize(ev[n_ev - 1]);
         for (int i = 1; i < n_ev && last.n < 16; ++i) {
             float ms = 0.0f;
-            hipEventElapsedTime(&ms, ev[i - 1], ev[i]);
+            (void)hipEventElapsedTime(&ms, ev[i - 1], ev[i]);
             last.name[last.n] = ev_names[i];
             last.ms[last.n] = ms;
             ++last.n;
@@ -357,8 +357,8 @@ void* fst_device_alloc(fst_ctx* ctx, size_t bytes) {
 }
 
 void fst_device_free(fst_ctx* ctx, void* p) {
-    if (ctx) hipStreamSynchronize(ctx->st);
-    if (p) hipFree(p);
+    if (ctx) (void)hipStreamSynchronize(ctx->st);
+    if (p) (void)hipFree(p);
 }
 
 int fst_copy_to_device(fst_ctx* ctx, void* dst, const void* src, size_t bytes) {
@@ -683,8 +683,8 @@ int fst_shared_expert(fst_ctx* ctx, int lid, const uint16_t* h, uint16_t* out, i
 static int grow(hipStream_t st, void** p, size_t* cap, size_t need) {
     if (*cap >= need) return FST_OK;
     if (*p) {
-        hipStreamSynchronize(st);
-        hipFree(*p);
+        (void)hipStreamSynchronize(st);
+        (void)hipFree(*p);
     }
     *p = nullptr;
     *cap = 0;
@@ -794,9 +794,9 @@ int fst_dequant(fst_ctx* ctx, int codec, const void* blocks, size_t nblocks, flo
     const size_t bb = codec == FST_CODEC_Q4K ? 144 : 17, be = codec == FST_CODEC_Q4K ? 256 : 32;
     void *din = nullptr, *df = nullptr, *db = nullptr;
     auto cleanup = [&]() {
-        if (din) hipFree(din);
-        if (df) hipFree(df);
-        if (db) hipFree(db);
+        if (din) (void)hipFree(din);
+        if (df) (void)hipFree(df);
+        if (db) (void)hipFree(db);
     };
     if (hipMalloc(&din, nblocks * bb) != hipSuccess || (out_f32 && hipMalloc(&df, nblocks * be * 4) != hipSuccess) ||
         (out_bf16 && hipMalloc(&db, nblocks * be * 2) != hipSuccess)) {
@@ -1139,8 +1139,8 @@ int fst_verify_forward(fst_ctx* ctx, uint16_t* h, int M, const int32_t* input_id
         }
         rc = check_meta_error(ctx);
     } while (0);
-    hipStreamSynchronize(ctx->st);
-    hipFree(d_logits);
+    (void)hipStreamSynchronize(ctx->st);  // (the error, if any, is already in rc)
+    (void)hipFree(d_logits);
     return rc;
 }
 

@@ -1070,7 +1070,7 @@ struct EpiArgs {
 //    tables, which then replace meta/slot_*/a_row; workgroup 0 also writes
 //    eids/wts and the tables to the global arrays of ra for later launches.
 template <int TOKS, int MS, int WAVES, int MODE, int CODEC = 0, int RPER = 0, int PF = FST_Q4K_PF>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : (TOKS <= 32 ? FST_Q4K_WPE_MID : 3)))) void q4k_linear_kernel(
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : (TOKS <= 32 ? FST_Q4K_WPE_MID : 2)))) void q4k_linear_kernel(
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
     const int* meta_g, const int* slot_eid_g, const int* slot_M_g,
     const int* slot_off_g, const int* a_row_g, const _Float16* __restrict__ A,
