@@ -203,9 +203,28 @@ def bench_c4(fa, args):
         t = timed(ctx, lambda i: fa._check(L.fst_moe_ffn_dev(ctx.h, 0, dh, M, de[i % N_BATCH], dw[i % N_BATCH], 1,
                                                              do, None, None)), args.steps, args.warmup)
         byts = (distinct + 1) * EXPERT_BYTES
+        # MFMA work of the gate|up launch per routing batch: each 16-row x
+        # 256-weight chunk issues 9 fp16 16x16x32 MFMAs (16,384 flops) per
+        # live 16-token group of its expert; useful = 2 x pairs x K x N
+        ctx.set_profiling(True)
+        issued, useful, t_gu = [], [], []
+        for b, (eids, _) in enumerate(batches):
+            fa._check(L.fst_moe_ffn_dev(ctx.h, 0, dh, M, de[b], dw[b], 1, do, None, None))
+            t_gu.append(dict(ctx.last_timings())["q4k_gate_up"] * 1e-3)
+            counts = np.bincount(eids.ravel(), minlength=E)
+            groups = int(np.sum((counts[counts > 0] + 15) // 16)) + (M + 15) // 16  # routed + shared
+            issued.append(groups * (2 * INTER // 16) * (HD // 256) * 9 * 16384.0)
+            useful.append(2.0 * (M * TK + M) * HD * 2 * INTER)
+        ctx.set_profiling(False)
+        iss = float(np.mean(np.array(issued) / np.array(t_gu))) / 1e12
+        use = float(np.mean(np.array(useful) / np.array(t_gu))) / 1e12
         out["M%d" % M] = {"tokens_per_s": round(M / t, 1), "us_per_step": round(t * 1e6, 2),
                           "mean_distinct_routed": round(distinct, 2),
-                          "packed_weight_GBps": round(byts / t / 1e9, 1)}
+                          "packed_weight_GBps": round(byts / t / 1e9, 1),
+                          "gate_up_us": round(float(np.mean(t_gu)) * 1e6, 2),
+                          "mfma_gate_up": {"issued_tflops": round(iss, 1), "useful_tflops": round(use, 1),
+                                           "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                                           "util": round(iss / MFMA_F16_PEAK_TFLOPS, 4)}}
     ctx.close()
     return {"metric": "C4 Zipf-routed MoE verify throughput", "value": out["M32"]["tokens_per_s"],
             "unit": "tokens/s", "higher_is_better": True, "blocks": out,
