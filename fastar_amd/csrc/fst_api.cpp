@@ -544,12 +544,16 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
                                                std::min(c.n_experts, M * g.tk) + sh_q, M * (g.tk + sh_q));
     ctx->mark("q4k_gate_up");
     if (!mx) {
+        // the shared expert's down matrix (slot 0 of the down launch) is read
+        // into the device-wide cache during the prep launch
+        const size_t proj = (size_t)c.inter_dim * (c.hidden_dim / 256) * 144;
+        const void* pf = sh_q ? L.bank + (size_t)c.n_experts * L.expert_stride + 2 * proj : nullptr;
         if (ksplit > 1)
             fst::launch_prep_act_split(st, ctx->s.act, ksplit, M * (g.tk + sh_q), c.swiglu_limit, ctx->s.meta,
-                                       c.inter_dim, ctx->s.a16p, ctx->s.sx2p, ctx->s.xs2);
+                                       c.inter_dim, ctx->s.a16p, ctx->s.sx2p, ctx->s.xs2, pf, proj);
         else
             fst::launch_prep_act(st, ctx->s.act, ctx->s.meta, ctx->s.max_pairs, c.inter_dim, ctx->s.a16p,
-                                 ctx->s.sx2p, ctx->s.xs2);
+                                 ctx->s.sx2p, ctx->s.xs2, pf, proj);
         ctx->mark("prep_h");
     }
     if (direct) {

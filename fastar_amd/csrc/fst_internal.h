@@ -291,8 +291,10 @@ void launch_hc_post(hipStream_t st, const uint16_t* bo, uint16_t* h_hc, const fl
 void launch_hc_head(hipStream_t st, const uint16_t* h_hc, const uint16_t* fnT, float scale, const float* base, int M,
                     int d, uint16_t* plain);
 // h rows -> the down projection's operand (one workgroup per pair).
+// pf/pf_bytes (optional): weights the next launch streams first, read into
+// the device-wide cache by extra workgroups of this latency-bound launch.
 void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
-                     uint4* sxp, int* xs);
+                     uint4* sxp, int* xs, const void* pf = nullptr, size_t pf_bytes = 0);
 // Weights must be in the wave-tiled device layout (repack_q4k_expert).
 // gate/up writes h = silu(gate)*up; down writes y[pair] (fp32), combined by
 // launch_combine.
@@ -307,7 +309,8 @@ int launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, in
                        const uint16_t* h_in, const RouteReq* route = nullptr, int slots_bound = 0,
                        int pairs_bound = 0);
 void launch_prep_act_split(hipStream_t st, const float* part, int S, int rows, float swiglu_limit, const int* meta,
-                           int inter, _Float16* a16p, uint4* sxp, int* xs);
+                           int inter, _Float16* a16p, uint4* sxp, int* xs, const void* pf = nullptr,
+                           size_t pf_bytes = 0);
 // With o1/o2 (one routed pair per token, no shared expert) it writes
 // out = bf16(wts[token] * y) there instead of y, and no combine is needed.
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,

@@ -638,8 +638,21 @@ __device__ void prep_row(const Src& src, int row, int K, float* xv, _Float16* __
 template <typename Src>
 __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restrict__ nrows_dev, int nrows_host,
                                                    int K, _Float16* __restrict__ x16p,
-                                                   uint4* __restrict__ sxp, int* __restrict__ xs) {
+                                                   uint4* __restrict__ sxp, int* __restrict__ xs,
+                                                   const uint4* __restrict__ pf, size_t pf_pieces) {
     const int row = blockIdx.x;
+    if (row >= nrows_host) {
+        // workgroups past the rows read pf (the weights the next launch
+        // streams first) into the device-wide cache while this latency-bound
+        // launch leaves HBM idle; the loads land in a scratch LDS line
+        __shared__ __attribute__((aligned(16))) uint4 pf_lds[64];
+        const size_t step = (size_t)(gridDim.x - nrows_host) * 256;
+        for (size_t q = (size_t)(row - nrows_host) * 256 + threadIdx.x; q < pf_pieces; q += step)
+            __builtin_amdgcn_global_load_lds((const void*)(pf + q), (__attribute__((address_space(3))) void*)pf_lds,
+                                             16, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
+    }
     const int nrows = nrows_dev ? nrows_dev[0] : nrows_host;
     if (row >= nrows) return;
     __shared__ float xv[kMaxPrepK];
@@ -753,7 +766,7 @@ void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const u
 void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float16* x16p, uint4* sxp,
                       int* xs) {
     hipLaunchKernelGGL(prep_kernel<SrcBf16>, dim3(rows), dim3(256), 0, st, SrcBf16{x}, nullptr, rows, K,
-                       x16p, sxp, xs);
+                       x16p, sxp, xs, nullptr, (size_t)0);
 }
 // ---------------------------------------------------- residual + RMSNorm
 
@@ -875,18 +888,23 @@ void launch_resid_norm(hipStream_t st, const uint16_t* h, const uint16_t* y, con
                        slot_tab);
 }
 
+// prefetch workgroups added to a prep launch (when pf is given)
+constexpr int kPrepPrefetchWGs = 128;
+
 void launch_prep_act(hipStream_t st, const float* h, const int* meta, int max_rows, int K, _Float16* a16p,
-                     uint4* sxp, int* xs) {
-    hipLaunchKernelGGL(prep_kernel<SrcF32>, dim3(max_rows), dim3(256), 0, st, SrcF32{h}, meta + META_N_PAIRS,
-                       max_rows, K, a16p, sxp, xs);
+                     uint4* sxp, int* xs, const void* pf, size_t pf_bytes) {
+    const int extra = pf ? kPrepPrefetchWGs : 0;
+    hipLaunchKernelGGL(prep_kernel<SrcF32>, dim3(max_rows + extra), dim3(256), 0, st, SrcF32{h},
+                       meta + META_N_PAIRS, max_rows, K, a16p, sxp, xs, static_cast<const uint4*>(pf), pf_bytes / 16);
 }
 
 void launch_prep_act_split(hipStream_t st, const float* part, int S, int rows, float swiglu_limit, const int* meta,
-                           int inter, _Float16* a16p, uint4* sxp, int* xs) {
+                           int inter, _Float16* a16p, uint4* sxp, int* xs, const void* pf, size_t pf_bytes) {
+    const int extra = pf ? kPrepPrefetchWGs : 0;
 #define FST_PS(SV)                                                                                          \
-    hipLaunchKernelGGL(prep_kernel<SrcSplit<SV>>, dim3(rows), dim3(256), 0, st,                             \
+    hipLaunchKernelGGL(prep_kernel<SrcSplit<SV>>, dim3(rows + extra), dim3(256), 0, st,                     \
                        SrcSplit<SV>{part, rows, inter, swiglu_limit}, meta + META_N_PAIRS, rows, inter, a16p, sxp, \
-                       xs)
+                       xs, static_cast<const uint4*>(pf), pf_bytes / 16)
     if (S <= 2)
         FST_PS(2);
     else if (S <= 4)
