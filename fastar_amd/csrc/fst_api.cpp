@@ -535,8 +535,13 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     // the bf16 result itself (the combine of one term), no combine launch
     const bool direct = use_routed && g.tk == 1 && !use_shared;
     if (!do_router) {
+        // the shared expert's gate||up weights (Q4_K) are read into the
+        // device-wide cache during this latency-bound launch
+        const size_t gu_bytes = (size_t)2 * c.inter_dim * (c.hidden_dim / 256) * 144;
+        const bool pf = !mx && use_shared && !sh16;
         fst::launch_bucket_prep(st, g, M, use_shared && !sh16, d_eids, ctx->s, mx ? nullptr : d_h,
-                                direct ? d_out : nullptr, direct ? d_out_routed : nullptr);
+                                direct ? d_out : nullptr, direct ? d_out_routed : nullptr,
+                                pf ? L.bank + (size_t)c.n_experts * L.expert_stride : nullptr, pf ? gu_bytes : 0);
         ctx->mark("bucket_prep");
     }
     const int sh_q = use_shared && !sh16 ? 1 : 0;  // the shared expert runs as slot 0

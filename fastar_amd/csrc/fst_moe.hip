@@ -667,7 +667,19 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
 // invalid, which the combine would have written as zeros.
 __global__ __launch_bounds__(kRouteThreads) void bucket_prep_kernel(
     int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids, Scratch s, const uint16_t* h, int K,
-    uint16_t* o1, uint16_t* o2, int hd) {
+    uint16_t* o1, uint16_t* o2, int hd, int nprep, const uint4* __restrict__ pf, size_t pf_pieces) {
+    if ((int)blockIdx.x > nprep) {
+        // workgroups past the prep rows read pf (the shared expert's gate||up
+        // weights, streamed first by the next launch) into the device-wide
+        // cache while this latency-bound launch leaves HBM idle
+        __shared__ __attribute__((aligned(16))) uint4 pf_lds[64];
+        const size_t step = (size_t)(gridDim.x - 1 - nprep) * kRouteThreads;
+        for (size_t q = (size_t)(blockIdx.x - 1 - nprep) * kRouteThreads + threadIdx.x; q < pf_pieces; q += step)
+            __builtin_amdgcn_global_load_lds((const void*)(pf + q), (__attribute__((address_space(3))) void*)pf_lds,
+                                             16, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
+    }
     if (blockIdx.x > 0) {
         __shared__ float xv[kMaxPrepK];
         prep_row<kRouteThreads>(SrcBf16{h}, blockIdx.x - 1, K, xv, s.x16p, s.sxp, s.xs);
@@ -690,9 +702,13 @@ __global__ __launch_bounds__(kRouteThreads) void bucket_prep_kernel(
 }
 
 void launch_bucket_prep(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
-                        const Scratch& s, const uint16_t* h, uint16_t* o1, uint16_t* o2) {
-    hipLaunchKernelGGL(bucket_prep_kernel, dim3(1 + (h ? M : 0)), dim3(kRouteThreads), 0, st, M, g.E, g.tk,
-                       use_shared, eids, s, h, g.hd, o1, o2, g.hd);
+                        const Scratch& s, const uint16_t* h, uint16_t* o1, uint16_t* o2, const void* pf,
+                        size_t pf_bytes) {
+    const int nprep = h ? M : 0;
+    const int extra = pf ? 32 : 0;  // 1024-thread prefetch workgroups
+    hipLaunchKernelGGL(bucket_prep_kernel, dim3(1 + nprep + extra), dim3(kRouteThreads), 0, st, M, g.E, g.tk,
+                       use_shared, eids, s, h, g.hd, o1, o2, g.hd, nprep, static_cast<const uint4*>(pf),
+                       pf_bytes / 16);
 }
 
 // The routing front of a layer call in one launch: workgroups [0, nrb) compute
