@@ -327,7 +327,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; the verify path is not sharded across GPUs "
-              "(see DESIGN.md, 'How the path would shard'). Run with --gpus 1.", file=sys.stderr)
+              "(it would shard by expert: a share of the routed experts per GPU, the shared expert and router "
+              "replicated, one all-reduce of the combine per layer). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import fastar_amd as fa
