@@ -1079,6 +1079,9 @@ struct EpiArgs {
 #ifndef FST_Q4K_PF
 #define FST_Q4K_PF 1
 #endif
+#ifndef FST_WNT
+#define FST_WNT 2
+#endif
 #ifndef FST_SHARED_PREFETCH
 #define FST_SHARED_PREFETCH 1
 #endif
@@ -1227,7 +1230,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         // num_records: the run; dword 3: 32-bit data format (raw loads)
         return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)us, (short)0, nsb * CHUNK, 0x00020000);
     };
-    constexpr int kNT = 2;  // cache policy: non-temporal (streamed once)
+    constexpr int kNT = FST_WNT;  // cache policy: non-temporal (streamed once)
     auto load_w = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WRaw {
         WRaw x;
         // (the header first: issued last, its register was taken by a live
