@@ -82,39 +82,87 @@ def step(fa, ctx, bufs, i):
                                       bufs["tok"]))
 
 
-def cpu_baseline(hs, w, threads, min_seconds=10.0, max_steps=64):
-    """CPU oracle on whole verify steps (router + every routed expert touched +
-    shared expert + combine, fp64-accumulated, `threads` OpenMP threads), over
-    successive hidden batches until at least `min_seconds` of CPU work."""
+def cpu_threads_all():
+    """Host threads for the all-core CPU leg: the CPUs this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when the host sets it (a
+    GPU box grants each GPU a 16-CPU share and exports OMP_NUM_THREADS=16)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def build_cpu_baseline():
+    """Compiles oracle/fst_cpu_baseline.c for this host (-O3 -march=native,
+    OpenMP, fp32) and loads it."""
+    import ctypes as C
+    import subprocess
+    out = os.path.join(ROOT, "oracle", "_build", "libfst_cpu_baseline_native.so")
+    subprocess.run(["bash", os.path.join(ROOT, "oracle", "build_cpu_baseline.sh"), out], check=True)
+    L = C.CDLL(out)
+    P = C.c_void_p
+    L.fcb_moe_step.argtypes = [P, C.c_int, P, C.c_int, C.c_int, P, C.c_int, C.c_int, P, P]
+    L.fcb_moe_step.restype = C.c_int
+    L.fcb_set_threads.argtypes = [C.c_int]
+    L.fcb_set_threads.restype = None
+    return L
+
+
+def cpu_baseline(hs, w, min_seconds=8.0, max_steps=400):
+    """The CPU port (oracle/fst_cpu_baseline.c: router + every routed expert
+    touched + shared expert + combine, fp32, -O3 -march=native) on whole
+    verify steps, once on 1 thread and once on all the host threads this
+    process may use, each over successive hidden batches until `min_seconds`
+    of CPU time.  Returns the cpu_baseline record."""
+    import ctypes as C
     import fastar_amd as fa
+    L = build_cpu_baseline()
+    ptrs = (C.c_void_p * (E + 1))()
+    keep = {}
+
+    def expert(e):
+        if e not in keep:
+            keep[e] = fa.synth_q4k_expert(SEED, e)
+            ptrs[e] = keep[e].ctypes.data
+        return keep[e]
+
+    expert(E)
+    wc = np.ascontiguousarray(w, np.uint16)
+    out = np.empty((M, HD), np.uint16)
+    eids = np.empty((M, TK), np.int32)
+    # every expert any batch routes to is generated before the timed steps
+    # (the routing of a batch does not depend on the experts)
     from oracle import pyoracle as po
-    po.set_threads(threads)
-    cache = {}
-    steps, tokens, secs, nexp = 0, 0, 0.0, 0
-    while steps < max_steps and secs < min_seconds:
-        h = hs[steps % len(hs)]
-        e, _, _ = po.router(h, w, None, TK)
-        distinct = sorted(set(int(x) for x in e.ravel()))
-        for ex in distinct + [E]:
-            if ex not in cache:
-                cache[ex] = fa.synth_q4k_expert(SEED, ex)
-        t0 = time.perf_counter()
-        e, wt, _ = po.router(h, w, None, TK)
-        y = np.zeros((M, TK, HD), np.float32)
-        for ex in distinct:
-            rows = [m for m in range(M) if ex in e[m]]
-            ye = po.expert_ffn(0, cache[ex], h[rows])
-            for r, m in enumerate(rows):
-                for j in range(TK):
-                    if e[m, j] == ex:
-                        y[m, j] = ye[r]
-        ys = po.expert_ffn(0, cache[E], h)
-        po.combine(y, ys, wt)
-        secs += time.perf_counter() - t0
-        steps += 1
-        tokens += M
-        nexp += len(distinct) + 1
-    return tokens / secs, secs, steps, nexp / steps
+    for b in range(len(hs)):
+        e, _, _ = po.router(hs[b], w, None, TK)
+        for x in set(int(v) for v in e.ravel()):
+            expert(x)
+
+    def run(threads):
+        L.fcb_set_threads(threads)
+        h = np.ascontiguousarray(hs[0])  # untimed warm-up (thread pool, page tables)
+        L.fcb_moe_step(h.ctypes.data, M, wc.ctypes.data, E, TK, ptrs, HD, INTER, out.ctypes.data, eids.ctypes.data)
+        steps, secs, nexp = 0, 0.0, 0
+        while steps < max_steps and secs < min_seconds:
+            h = np.ascontiguousarray(hs[steps % len(hs)])
+            t0 = time.perf_counter()
+            n = L.fcb_moe_step(h.ctypes.data, M, wc.ctypes.data, E, TK, ptrs, HD, INTER, out.ctypes.data,
+                               eids.ctypes.data)
+            secs += time.perf_counter() - t0
+            steps += 1
+            nexp += n + 1
+        return M * steps / secs, steps, secs, nexp / steps
+
+    t_all = cpu_threads_all()
+    v1, s1, sec1, nexp = run(1)
+    va, sa, seca, _ = run(t_all)
+    return {"value": round(va, 2), "unit": "tokens/s", "cores": t_all, "kind": "port",
+            "value_1t": round(v1, 3), "value_all": round(va, 2),
+            "host_cpus": os.cpu_count(), "cpus_allowed": len(os.sched_getaffinity(0)),
+            "sample": "C2 block-8 verify steps (router + %.1f Q4_K experts each + combine) through "
+                      "oracle/fst_cpu_baseline.c built -O3 -march=native, fp32, OpenMP: %d steps on 1 thread "
+                      "(%.1f s), %d steps on %d threads (%.1f s)" % (nexp, s1, sec1, sa, t_all, seca)}
 
 
 # ------------------------------------------------------------ other configs
@@ -319,7 +367,6 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="also run N launches of the plain copy kernel (512 MiB) for PMC calibration")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c2mx", "c3", "c4", "c5"],
@@ -399,11 +446,7 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        v, secs, nsteps, nexp = cpu_baseline(hs, w, threads)
-        cpu = {"value": round(v, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": "%d block-8 verify steps (router + %.1f Q4_K experts each + combine, fp64-accumulated) "
-                         "through the C oracle (oracle/fst_oracle.c), %.1f s of compute" % (nsteps, nexp, secs)}
+        cpu = cpu_baseline(hs, w)
 
     res = {
         "metric": "verified tokens/s for block-8 MoE-layer verify",

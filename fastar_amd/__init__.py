@@ -76,6 +76,11 @@ _SIGS = {
     "fst_accept_stochastic": (C.c_int, [P, P, P, C.c_int, C.c_int, C.c_int, P, C.c_float, U64, U64, P, P]),
     "fst_accept_greedy_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P, P]),
     "fst_accept_stochastic_dev": (C.c_int, [P, P, P, C.c_int, C.c_int, C.c_int, P, C.c_float, U64, U64, P, P]),
+    "fst_set_wait_limit": (C.c_int, [P, C.c_int]),
+    "fst_final_head": (C.c_int, [P, P, C.c_int, P]),
+    "fst_sample_token": (C.c_int, [P, P, C.c_int, C.c_float, C.c_float, U64, U64, P]),
+    "fst_sample_token_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_float, C.c_float, U64, U64, P]),
+    "fst_accept_check": (C.c_int, [P, C.c_int]),
     "fst_dequant": (C.c_int, [P, C.c_int, P, SZ, P, P]),
     "fst_set_profiling": (C.c_int, [P, C.c_int]),
     "fst_last_timings": (C.c_int, [P, P]),
@@ -323,6 +328,21 @@ class Context:
         _check(lib().fst_accept_stochastic(self.h, _ptr(target), _ptr(dl), n_seq, k, V, _ptr(draft),
                                            temperature, seed, seq_base, _ptr(n_acc), _ptr(tok)))
         return n_acc, tok
+
+    def final_head(self, hs):
+        """apply_final_norm_and_lm_head: hs [M][4][hidden] with the HC head
+        uploaded, else [M][hidden] -> fp32 logits [M][vocab]."""
+        hs = np.ascontiguousarray(hs, dtype=np.uint16)
+        M = hs.shape[0]
+        out = np.empty((M, self.cfg.vocab_size), np.float32)
+        _check(lib().fst_final_head(self.h, _ptr(hs), M, _ptr(out)))
+        return out
+
+    def sample_token(self, logits, temperature, top_p, seed, seq=0):
+        x = np.ascontiguousarray(logits, dtype=np.float32)
+        t = C.c_int32()
+        _check(lib().fst_sample_token(self.h, _ptr(x), x.shape[-1], temperature, top_p, seed, seq, C.byref(t)))
+        return t.value
 
     # verify forward (norms, residual stream, LM head)
     def upload_norm(self, lid, w_bf16):

@@ -12,7 +12,12 @@
 // E = floor(exp(l - max) * 2^32) with the shared fst_expf, integer sums, and
 // 128-bit integer comparisons/prefix sums, so the accept decisions and the
 // resampled token are identical to the CPU oracle for identical logits.
+#include <atomic>
+#include <mutex>
+#include <string>
+
 #include "fst_internal.h"
+#include "../../include/fst_hip.h"
 #include "../../include/fst_exact_math.h"
 
 namespace fst {
@@ -539,15 +544,25 @@ __global__ __launch_bounds__(kProbThreads) void acc_sample_kernel(
 
 // Greedy acceptance in one launch, without counters.  Every (row, chunk)
 // workgroup reduces its chunk to (max, lowest index) and publishes it as one
-// 64-bit word {max bits, index + 2} (0 = not yet written).  The workgroup
-// with the highest linear id of a sequence (last chunk of its last row) then
-// collects the sequence's (k+1)*CH words with coherent loads, resolves each
-// row's argmax with the reference's rules, the longest matching prefix and
-// the bonus token, and clears the words for the next call.  Workgroups are
+// 64-bit word {tag, max bits}, tag = epoch << 20 | (index + 1): a word is
+// valid for this call only when its tag carries the call's epoch (1..4095),
+// so words left by an earlier or abandoned call are never taken.  The
+// workgroup with the highest linear id of a sequence (last chunk of its last
+// row) then collects the sequence's (k+1)*CH words with coherent loads,
+// resolves each row's argmax with the reference's rules, the longest
+// matching prefix and the bonus token, and clears the words.  Workgroups are
 // dispatched in linear-id order on each XCD, so every workgroup it waits for
 // is resident or finished (the lowest unfinished id never waits), and the
-// wait ends.  (Counters instead of flags serialise: increments of one
-// device-scope counter complete a few hundred ns apart at the memory side.)
+// wait ends.  The wait is still bounded (spin_limit polls): past it the
+// owner gives up, writes n_acc = -1 and tokens = -1 for its sequence (the
+// host turns that into FST_EHIP) and exits normally.  (Counters instead of
+// flags serialise: increments of one device-scope counter complete a few
+// hundred ns apart at the memory side.)
+constexpr int kGreedyIdxBits = 20;
+#ifndef FST_GREEDY_CHUNKS
+#define FST_GREEDY_CHUNKS 16
+#endif
+static_assert(FST_GREEDY_CHUNKS == kGreedyChunks, "greedy chunk count");  // index + 1 < 2^20: V <= kMaxAcceptVocab
 
 template <int CH>
 __device__ __forceinline__ void greedy_chunk(const float* __restrict__ row, int V, int c, float& best, int& bi) {
@@ -600,8 +615,9 @@ __device__ __forceinline__ void greedy_chunk(const float* __restrict__ row, int 
 
 template <int CH, int NU>
 __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict__ target, int k, int V,
-                                                         const int32_t* __restrict__ draft, AccWs w,
-                                                         int32_t* __restrict__ n_acc,
+                                                         const int32_t* __restrict__ draft,
+                                                         unsigned long long* __restrict__ gslot, uint32_t epoch,
+                                                         int spin_limit, int32_t* __restrict__ n_acc,
                                                          int32_t* __restrict__ tokens) {
     static_assert(CH == 16, "a row's chunk words fill one 16-lane DPP row");
     const int c = blockIdx.x, r = blockIdx.y;
@@ -618,10 +634,11 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
     float best;
     int bi;
     greedy_chunk<CH>(target + (size_t)r * V, V, c, best, bi);
-    unsigned long long* words = w.gslot + (size_t)s * (k + 1) * CH;
+    unsigned long long* words = gslot + (size_t)s * (k + 1) * CH;
     const int me = (r - s * (k + 1)) * CH + c;
     if (threadIdx.x == 0) {
-        st_coherent_u64(&words[me], ((unsigned long long)(uint32_t)(bi + 2) << 32) | fst_f32_bits(best));
+        const uint32_t tag = (epoch << kGreedyIdxBits) | (uint32_t)(bi + 1);
+        st_coherent_u64(&words[me], ((unsigned long long)tag << 32) | fst_f32_bits(best));
         publish_wait();
     }
     if (!owner || threadIdx.x >= 64) return;
@@ -634,18 +651,32 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
         v[u] = 0ull;
         if (lane + 64 * u < nw) pend |= 1u << u;
     }
-    for (;;) {
+    bool timed_out = false;
+    for (int spin = 0;; ++spin) {
         unsigned long long t[NU];
 #pragma unroll
         for (int u = 0; u < NU; ++u) t[u] = ld_coherent_u64(&words[min(lane + 64 * u, nw - 1)]);
 #pragma unroll
         for (int u = 0; u < NU; ++u)
-            if (((pend >> u) & 1u) && (t[u] >> 32) != 0ull) {
+            if (((pend >> u) & 1u) && (uint32_t)(t[u] >> (32 + kGreedyIdxBits)) == epoch) {
                 v[u] = t[u];
                 pend &= ~(1u << u);
             }
         if (!__any(pend != 0u)) break;
+        if (spin >= spin_limit) {
+            timed_out = true;
+            break;
+        }
         __builtin_amdgcn_s_sleep(1);
+    }
+    if (timed_out) {
+        // late words carry this call's epoch, which the next call does not accept
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+            if (lane + 64 * u < nw) st_coherent_u64(&words[lane + 64 * u], 0ull);
+        if (lane <= k) tokens[s * (k + 1) + lane] = -1;
+        if (lane == 0) n_acc[s] = -1;
+        return;
     }
     // per row: argmax over its 16 chunk words (one DPP row); lane l then
     // takes row l's result from lane 16 (l % 4) of iteration l / 4
@@ -653,7 +684,7 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
         float m = fst_bits_f32((uint32_t)v[u]);
-        int i = (lane + 64 * u < nw) ? (int)(v[u] >> 32) - 2 : -1;
+        int i = (lane + 64 * u < nw) ? (int)((v[u] >> 32) & ((1u << kGreedyIdxBits) - 1u)) - 1 : -1;
         argmax_step<0xb1>(m, i);
         argmax_step<0x4e>(m, i);
         argmax_step<0x124>(m, i);
@@ -671,18 +702,18 @@ __global__ __launch_bounds__(256) void acc_greedy_kernel(const float* __restrict
     if (lane == 0) n_acc[s] = n;
 }
 
-#ifndef FST_GREEDY_CHUNKS
-#define FST_GREEDY_CHUNKS 16
-#endif
+void* accept_greedy_words(void* ws, int n_seq, int k) { return carve(ws, n_seq, k).gslot; }
+
 void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k, int V,
-                          const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* ws) {
-    AccWs w = carve(ws, n_seq, k);
+                          const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* words, uint32_t epoch,
+                          int spin_limit) {
     const int R = n_seq * (k + 1);
     constexpr int CH = FST_GREEDY_CHUNKS;
     // words per sequence (k+1)*16 <= 1024: NU = 64-lane passes
     const int nu = ((k + 1) * CH + 63) / 64;
 #define FST_GK(NUV) \
-    hipLaunchKernelGGL((acc_greedy_kernel<CH, NUV>), dim3(CH, R), dim3(256), 0, st, target, k, V, draft, w, n_acc, tokens)
+    hipLaunchKernelGGL((acc_greedy_kernel<CH, NUV>), dim3(CH, R), dim3(256), 0, st, target, k, V, draft, \
+                       static_cast<unsigned long long*>(words), epoch, spin_limit, n_acc, tokens)
     if (nu <= 1)
         FST_GK(1);
     else if (nu <= 2)
@@ -715,5 +746,205 @@ void launch_accept_stochastic(hipStream_t st, const float* target, const float* 
     hipLaunchKernelGGL(acc_sample_kernel, dim3(n_seq), dim3(kProbThreads), 0, st, target, draft_logits, n_seq, k, V,
                        inv_t, w.part_max, w.part_idx, w.part_sum, w.dec, w.part_res, tokens);
 }
+
+// ---------------------------------------------------------- sample_token
+//
+// FSTEngine::sample_token (src/fst_engine.cpp:4491-4528) on the device, one
+// workgroup per row of logits.  temperature <= 0 is the reference's plain
+// argmax (first maximum, NaN skipped, a NaN at index 0 pins 0).  Otherwise
+// the build's reproducible form of its softmax / top-p / draw (the reference
+// draws from an unseeded mt19937): E[v] = floor(exp(x_v*(1/T) - max)*2^32),
+// S = sum E; tokens ordered by E descending, ties by lower index; the kept
+// set is the shortest prefix whose mass C has C*2^32 >= q*S (q = top_p in
+// 2^-32 units), at least one token; the token is the first of the kept
+// prefix whose running mass exceeds (U*C) >> 24, U = uniform24(seed, seq, 0,
+// stream 2).  Both searches ("first position of the descending order whose
+// running mass reaches T") run as radix selects over the 33-bit E values:
+// E = 2^32 (the maxima) first, then 4 levels of 8-bit digits with LDS
+// histograms of the digit's mass, then the rank among equal values in index
+// order.  Integer sums: any reduction order gives the same result.
+constexpr int kSampleThreads = 1024;
+constexpr unsigned long long kOne32 = 4294967296ull;
+
+__device__ __forceinline__ unsigned long long block_sum_u64(unsigned long long v, unsigned long long* red) {
+    const int tid = threadIdx.x;
+    v = wave_sum_u64_dpp(v);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = v;
+    __syncthreads();
+    unsigned long long t = 0;
+#pragma unroll
+    for (int w = 0; w < kSampleThreads / 64; ++w) t += red[w];
+    return t;
+}
+
+struct Cross {
+    unsigned long long t;  // value E of the position
+    unsigned long long G;  // mass of all values above t
+    unsigned long long r;  // 1-based rank of the position among values == t
+};
+
+// First position of the (E desc, index asc) order whose running mass reaches
+// T (1 <= T <= S); n_top = number of E == 2^32.
+__device__ Cross find_cross(const unsigned long long* __restrict__ E, int V, unsigned long long T,
+                            unsigned long long n_top, unsigned long long* hist, unsigned long long* bc) {
+    const int tid = threadIdx.x;
+    Cross c;
+    if ((u128)T <= (u128)n_top * kOne32) {
+        c.t = kOne32;
+        c.G = 0;
+        c.r = (T + kOne32 - 1) >> 32;
+        return c;
+    }
+    unsigned long long G = n_top * kOne32, rem = T - G, prefix = 0;
+    for (int lvl = 0; lvl < 4; ++lvl) {
+        const int shift = 24 - 8 * lvl;
+        __syncthreads();
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        for (int v = tid; v < V; v += kSampleThreads) {
+            const unsigned long long e = E[v];
+            if (e < kOne32 && (e >> (shift + 8)) == prefix) atomicAdd(&hist[(e >> shift) & 255u], e);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long acc = 0;
+            int b = 255;
+            for (; b > 0; --b) {
+                if (acc + hist[b] >= rem) break;
+                acc += hist[b];
+            }
+            bc[0] = acc;
+            bc[1] = (unsigned long long)b;
+        }
+        __syncthreads();
+        rem -= bc[0];
+        G += bc[0];
+        prefix = (prefix << 8) | bc[1];
+    }
+    c.t = prefix;
+    c.G = G;
+    c.r = prefix ? (rem + prefix - 1) / prefix : 1;
+    return c;
+}
+
+// Index of the r-th (1-based) element with E == t, in index order.
+__device__ int nth_equal(const unsigned long long* __restrict__ E, int V, unsigned long long t,
+                         unsigned long long r, int* cnt, int* bc) {
+    const int tid = threadIdx.x;
+    const int per = (V + kSampleThreads - 1) / kSampleThreads;
+    const int v0 = min(V, tid * per), v1 = min(V, v0 + per);
+    int n = 0;
+    for (int v = v0; v < v1; ++v) n += E[v] == t;
+    __syncthreads();
+    cnt[tid] = n;
+    if (tid == 0) bc[0] = V - 1;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int i = 0; i < kSampleThreads; ++i) {
+            const int c = cnt[i];
+            cnt[i] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    const long long want = (long long)r - 1;  // 0-based
+    const int pre = cnt[tid];
+    if (want >= pre && want < pre + n) {
+        int k = pre;
+        for (int v = v0; v < v1; ++v)
+            if (E[v] == t) {
+                if (k == want) {
+                    bc[0] = v;
+                    break;
+                }
+                ++k;
+            }
+    }
+    __syncthreads();
+    return bc[0];
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_token_kernel(const float* __restrict__ logits, int V,
+                                                                      float inv_t, int greedy, unsigned long long q,
+                                                                      uint64_t seed, uint64_t seq_base,
+                                                                      unsigned long long* __restrict__ Ews,
+                                                                      int32_t* __restrict__ tokens) {
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* x = logits + (size_t)row * V;
+    unsigned long long* E = Ews + (size_t)row * V;
+    __shared__ float s_m[kSampleThreads / 64];
+    __shared__ int s_i[kSampleThreads / 64];
+    __shared__ unsigned long long red[kSampleThreads / 64];
+    __shared__ unsigned long long hist[256];
+    __shared__ unsigned long long bc[2];
+    __shared__ int cnt[kSampleThreads];
+    __shared__ int ibc[1];
+    // (max, lowest index) of l = x*inv_t over non-NaN values (greedy: of x)
+    const float sc = greedy ? 1.0f : inv_t;
+    float best = 0.0f;
+    int bi = -1;
+    for_strided<8>(x, tid, V, kSampleThreads, [&](float xv, int v) {
+        const float l = xv * sc;
+        if (l != l) return;
+        if (bi < 0 || l > best) {
+            best = l;
+            bi = v;
+        }
+    });
+    wave_argmax(best, bi);
+    if (lane == 0) {
+        s_m[wave] = best;
+        s_i[wave] = bi;
+    }
+    __syncthreads();
+    for (int w = 0; w < kSampleThreads / 64; ++w) argmax_merge(best, bi, s_m[w], s_i[w]);
+    if (greedy) {
+        if (tid == 0) tokens[row] = (bi < 0 || x[0] != x[0]) ? 0 : bi;
+        return;
+    }
+    const int any = bi >= 0;
+    unsigned long long s = 0, ntop = 0;
+    for_strided<8>(x, tid, V, kSampleThreads, [&](float xv, int v) {
+        const unsigned long long e = fixed_prob(xv, inv_t, best, any);
+        E[v] = e;
+        s += e;
+        ntop += e == kOne32;
+    });
+    const unsigned long long S = block_sum_u64(s, red);
+    const unsigned long long n_top = block_sum_u64(ntop, red);
+    if (S == 0) {
+        if (tid == 0) tokens[row] = 0;
+        return;
+    }
+    __syncthreads();  // E stores of every thread are visible to the searches
+    u128 need = ((u128)q * S + (kOne32 - 1)) >> 32;
+    const unsigned long long Tp = need == 0 ? 1ull : (unsigned long long)need;
+    const Cross k = find_cross(E, V, Tp, n_top, hist, bc);
+    const unsigned long long C = k.G + k.r * k.t;
+    const uint32_t U = fst_uniform24(seed, seq_base + (uint64_t)row, 0u, 2u);
+    const unsigned long long tgt = (unsigned long long)(((u128)U * C) >> 24);
+    const Cross d = find_cross(E, V, tgt + 1, n_top, hist, bc);
+    const int tok = nth_equal(E, V, d.t, d.r, cnt, ibc);
+    if (tid == 0) tokens[row] = tok;
+}
+
+void launch_sample_token(hipStream_t st, const float* logits, int n_rows, int V, float temperature, float top_p,
+                         uint64_t seed, uint64_t seq_base, void* ws, int32_t* tokens) {
+    const int greedy = !(temperature > 0.0f);
+    const float inv_t = greedy ? 1.0f : 1.0f / temperature;
+    unsigned long long q;
+    if (!(top_p > 0.0f))
+        q = 0;
+    else if (top_p >= 1.0f)
+        q = kOne32;
+    else
+        q = (unsigned long long)((double)top_p * 4294967296.0);  // exact product, truncated
+    hipLaunchKernelGGL(sample_token_kernel, dim3(n_rows), dim3(kSampleThreads), 0, st, logits, V, inv_t, greedy, q,
+                       seed, seq_base, static_cast<unsigned long long*>(ws), tokens);
+}
+
+size_t sample_ws_bytes(int n_rows, int V) { return (size_t)n_rows * V * 8 + 256; }
 
 }  // namespace fst

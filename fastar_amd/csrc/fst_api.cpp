@@ -79,10 +79,17 @@ struct fst_ctx {
     void* acc_ws = nullptr;
     size_t acc_ws_cap = 0;
     int acc_ws_nseq = -1, acc_ws_k = -1;  // shape whose counter layout the workspace holds
+    uint32_t acc_epoch = 0;                  // greedy words of acc_ws: epoch of the last call
+    int spin_limit = fst::kDefaultSpinLimit; // polls before a cross-workgroup wait gives up
+    int max_grid_y = 65535;                  // device grid limit (acceptance rows)
     float* acc_logits = nullptr;
     size_t acc_logits_cap = 0;
     int32_t* acc_io = nullptr;
     size_t acc_io_cap = 0;
+    float* head_logits = nullptr;            // [T][vocab] logits of the host-pointer final head
+    size_t head_logits_cap = 0;
+    void* samp_ws = nullptr;                 // sample_token: fixed-point masses [rows][V]
+    size_t samp_ws_cap = 0;
     // profiling
     bool profiling = false;
     std::vector<hipEvent_t> ev;
@@ -102,6 +109,8 @@ struct fst_ctx {
         if (acc_ws) (void)hipFree(acc_ws);
         if (acc_logits) (void)hipFree(acc_logits);
         if (acc_io) (void)hipFree(acc_io);
+        if (samp_ws) (void)hipFree(samp_ws);
+        if (head_logits) (void)hipFree(head_logits);
         for (hipEvent_t e : ev) (void)hipEventDestroy(e);
         if (st) (void)hipStreamDestroy(st);
     }
@@ -225,6 +234,7 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
 
     fst_ctx* x = new fst_ctx();
     x->cfg = c;
+    x->max_grid_y = prop.maxGridSize[1] > 0 ? prop.maxGridSize[1] : 65535;
     int rc = FST_OK;
     auto bail = [&](int code) {
         delete x;
@@ -715,23 +725,51 @@ static int accept_ws(fst_ctx* ctx, int n_seq, int k, int V) {
     return FST_OK;
 }
 
-static int check_accept_args(int n_seq, int k, int V) {
+static int check_accept_args(fst_ctx* ctx, int n_seq, int k, int V) {
     if (n_seq <= 0 || n_seq > 4096) return fail(FST_EINVAL, "n_seq must be in [1, 4096]");
     if (k < 0 || k > 63) return fail(FST_EINVAL, "k must be in [0, 63]");
-    if (V <= 0) return fail(FST_EINVAL, "V must be positive");
+    if (V <= 0 || V > fst::kMaxAcceptVocab)
+        return fail(FST_EINVAL, "V must be in [1, " + std::to_string(fst::kMaxAcceptVocab) + "]");
+    // the launches put one row of logits per grid row: n_seq*(2k+1) rows
+    // (target and draft) for rejection sampling, n_seq*(k+1) for greedy
+    if ((long)n_seq * (2 * k + 1) > (long)ctx->max_grid_y)
+        return fail(FST_EINVAL, "n_seq*(2k+1) exceeds the device grid limit " + std::to_string(ctx->max_grid_y));
     return FST_OK;
+}
+
+static uint32_t next_epoch(uint32_t* e) {
+    *e = *e % 4095u + 1u;  // 1..4095
+    return *e;
 }
 
 int fst_accept_greedy_dev(fst_ctx* ctx, const float* d_target, int n_seq, int k, int V, const int32_t* d_draft,
                           int32_t* d_n_acc, int32_t* d_tokens) {
     if (!ctx) return fail(FST_EINVAL, "null context");
-    if (int rc = check_accept_args(n_seq, k, V)) return rc;
+    if (int rc = check_accept_args(ctx, n_seq, k, V)) return rc;
     if (misaligned(d_target)) return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
     if (int rc = accept_ws(ctx, n_seq, k, V)) return rc;
     ctx->mark_begin();
-    fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens, ctx->acc_ws);
+    fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens,
+                              fst::accept_greedy_words(ctx->acc_ws, n_seq, k), next_epoch(&ctx->acc_epoch),
+                              ctx->spin_limit);
     ctx->mark("accept_greedy");
     FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_set_wait_limit(fst_ctx* ctx, int spins) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (spins < 0) return fail(FST_EINVAL, "spins must be >= 0");
+    ctx->spin_limit = spins == 0 ? fst::kDefaultSpinLimit : spins;
+    return FST_OK;
+}
+
+int fst_accept_check(const int32_t* n_acc, int n_seq) {
+    if (!n_acc || n_seq <= 0) return fail(FST_EINVAL, "fst_accept_check: null n_acc or n_seq <= 0");
+    for (int s = 0; s < n_seq; ++s)
+        if (n_acc[s] < 0)
+            return fail(FST_EHIP, "acceptance of sequence " + std::to_string(s) +
+                                      " abandoned: its cross-workgroup wait exceeded the spin limit");
     return FST_OK;
 }
 
@@ -739,7 +777,7 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
                               int V, const int32_t* d_draft, float temperature, uint64_t seed, uint64_t seq_base,
                               int32_t* d_n_acc, int32_t* d_tokens) {
     if (!ctx) return fail(FST_EINVAL, "null context");
-    if (int rc = check_accept_args(n_seq, k, V)) return rc;
+    if (int rc = check_accept_args(ctx, n_seq, k, V)) return rc;
     if (!(temperature > 0.0f)) return fail(FST_EINVAL, "temperature must be > 0");
     if (int rc = accept_ws(ctx, n_seq, k, V)) return rc;
     const float inv_t = 1.0f / temperature;
@@ -755,7 +793,7 @@ static int accept_host(fst_ctx* ctx, const float* target, const float* draft_log
                        const int32_t* draft, float temperature, uint64_t seed, uint64_t seq_base, int32_t* n_acc,
                        int32_t* tokens, int stochastic) {
     if (!ctx) return fail(FST_EINVAL, "null context");
-    if (int rc = check_accept_args(n_seq, k, V)) return rc;
+    if (int rc = check_accept_args(ctx, n_seq, k, V)) return rc;
     if (!target || !n_acc || !tokens || (k > 0 && !draft) || (stochastic && k > 0 && !draft_logits))
         return fail(FST_EINVAL, "null host buffer");
     for (int i = 0; i < n_seq * k; ++i)
@@ -778,7 +816,7 @@ static int accept_host(fst_ctx* ctx, const float* target, const float* draft_log
     FST_HIP_TRY(hipMemcpyAsync(n_acc, d_nacc, n_seq * 4, hipMemcpyDeviceToHost, ctx->st));
     FST_HIP_TRY(hipMemcpyAsync(tokens, d_tok, (size_t)n_seq * (k + 1) * 4, hipMemcpyDeviceToHost, ctx->st));
     FST_HIP_TRY(hipStreamSynchronize(ctx->st));
-    return FST_OK;
+    return fst_accept_check(n_acc, n_seq);
 }
 
 int fst_accept_greedy(fst_ctx* ctx, const float* target, int n_seq, int k, int V, const int32_t* draft,
@@ -791,6 +829,42 @@ int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_
                           int32_t* tokens) {
     if (!(temperature > 0.0f)) return fail(FST_EINVAL, "temperature must be > 0");
     return accept_host(ctx, target, draft_logits, n_seq, k, V, draft, temperature, seed, seq_base, n_acc, tokens, 1);
+}
+
+// ------------------------------------------------------------ sample_token
+
+int fst_sample_token_dev(fst_ctx* ctx, const float* d_logits, int n_rows, int V, float temperature, float top_p,
+                         uint64_t seed, uint64_t seq_base, int32_t* d_tokens) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!d_logits || !d_tokens) return fail(FST_EINVAL, "null device buffer");
+    if (n_rows <= 0 || n_rows > ctx->max_grid_y) return fail(FST_EINVAL, "n_rows out of range");
+    if (V <= 0 || V > fst::kMaxAcceptVocab)
+        return fail(FST_EINVAL, "V must be in [1, " + std::to_string(fst::kMaxAcceptVocab) + "]");
+    if (temperature != temperature || top_p != top_p) return fail(FST_EINVAL, "temperature/top_p is NaN");
+    if (temperature > 0.0f)
+        if (int rc = grow(ctx->st, &ctx->samp_ws, &ctx->samp_ws_cap, fst::sample_ws_bytes(n_rows, V))) return rc;
+    ctx->mark_begin();
+    fst::launch_sample_token(ctx->st, d_logits, n_rows, V, temperature, top_p, seed, seq_base, ctx->samp_ws,
+                             d_tokens);
+    ctx->mark("sample_token");
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_sample_token(fst_ctx* ctx, const float* logits, int V, float temperature, float top_p, uint64_t seed,
+                     uint64_t seq, int32_t* token) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!logits || !token) return fail(FST_EINVAL, "null host buffer");
+    if (V <= 0 || V > fst::kMaxAcceptVocab)
+        return fail(FST_EINVAL, "V must be in [1, " + std::to_string(fst::kMaxAcceptVocab) + "]");
+    if (int rc = grow(ctx->st, (void**)&ctx->acc_logits, &ctx->acc_logits_cap, (size_t)V * 4 + 256)) return rc;
+    if (int rc = grow(ctx->st, (void**)&ctx->acc_io, &ctx->acc_io_cap, 256)) return rc;
+    FST_HIP_TRY(hipMemcpyAsync(ctx->acc_logits, logits, (size_t)V * 4, hipMemcpyHostToDevice, ctx->st));
+    if (int rc = fst_sample_token_dev(ctx, ctx->acc_logits, 1, V, temperature, top_p, seed, seq, ctx->acc_io))
+        return rc;
+    FST_HIP_TRY(hipMemcpyAsync(token, ctx->acc_io, 4, hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    return FST_OK;
 }
 
 // ------------------------------------------------------------ dequant
@@ -1074,6 +1148,37 @@ int fst_hc_head_dev(fst_ctx* ctx, const uint16_t* d_h_hc, int M, uint16_t* d_pla
     fst::launch_hc_head(ctx->st, d_h_hc, ctx->hc_head_fn, ctx->hc_head_scale, ctx->hc_head_base, M,
                         ctx->cfg.hidden_dim, d_plain);
     FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_final_head(fst_ctx* ctx, const uint16_t* hs, int M, float* logits) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (!hs || !logits) return fail(FST_EINVAL, "null host buffer");
+    const fst_config& c = ctx->cfg;
+    if (M <= 0 || M > c.max_tokens) return fail(FST_EINVAL, "M must be in [1, max_tokens]");
+    if (!ctx->lm_kind) return fail(FST_ENOTREADY, "LM head not uploaded");
+    // one logits buffer for the context's largest call, kept across calls
+    const size_t lbytes = (size_t)c.max_tokens * c.vocab_size * sizeof(float);
+    if (int rc = grow(ctx->st, (void**)&ctx->head_logits, &ctx->head_logits_cap, lbytes)) return rc;
+    const int hd = c.hidden_dim;
+    uint16_t* plain = ctx->s.h;
+    ctx->mark_begin();
+    if (ctx->has_hc_head) {
+        // the 4-stream residual [M][4][hd] collapses through output_hc_head
+        // before the final norm and the head (src/fst_engine.cpp:2120-2128)
+        FST_HIP_TRY(hipMemcpyAsync(ctx->hc_h, hs, (size_t)M * 4 * hd * 2, hipMemcpyHostToDevice, ctx->st));
+        fst::launch_hc_head(ctx->st, ctx->hc_h, ctx->hc_head_fn, ctx->hc_head_scale, ctx->hc_head_base, M, hd,
+                            ctx->hc_cur);
+        plain = ctx->hc_cur;
+        ctx->mark("hc_head");
+    } else {
+        FST_HIP_TRY(hipMemcpyAsync(plain, hs, (size_t)M * hd * 2, hipMemcpyHostToDevice, ctx->st));
+    }
+    if (int rc = final_head(ctx, plain, nullptr, M, ctx->head_logits)) return rc;
+    ctx->mark("lm_head");
+    FST_HIP_TRY(hipMemcpyAsync(logits, ctx->head_logits, (size_t)M * c.vocab_size * 4, hipMemcpyDeviceToHost,
+                               ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
     return FST_OK;
 }
 

@@ -338,8 +338,22 @@ void launch_dequant(hipStream_t st, int codec, const uint8_t* blocks, size_t nbl
 
 // Acceptance.  Work buffers are carved from `ws` (bytes given by accept_ws_bytes).
 size_t accept_ws_bytes(int n_seq, int k, int V);
+// Greedy acceptance: chunk words at `words` (n_seq*(k+1)*kGreedyChunks
+// 64-bit words; accept_greedy_words gives them inside a workspace), tagged
+// with epoch (1..4095, a new one per call on the same words); the owner's
+// wait gives up after spin_limit polls and reports n_acc = -1.
+constexpr int kGreedyChunks = 16;
+constexpr int kMaxAcceptVocab = (1 << 20) - 2;   // index + 1 fits the word's 20-bit field
+constexpr int kDefaultSpinLimit = 1 << 20;
+void* accept_greedy_words(void* ws, int n_seq, int k);
 void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k, int V,
-                          const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* ws);
+                          const int32_t* draft, int32_t* n_acc, int32_t* tokens, void* words, uint32_t epoch,
+                          int spin_limit);
+// sample_token over n_rows rows of V logits (one token per row; row r draws
+// with Philox (seed, seq_base + r)); ws holds sample_ws_bytes.
+size_t sample_ws_bytes(int n_rows, int V);
+void launch_sample_token(hipStream_t st, const float* logits, int n_rows, int V, float temperature, float top_p,
+                         uint64_t seed, uint64_t seq_base, void* ws, int32_t* tokens);
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
                               int n_seq, int k, int V, const int32_t* draft, float inv_t,
                               uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,

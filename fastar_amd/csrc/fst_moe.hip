@@ -1031,7 +1031,7 @@ __device__ __forceinline__ WRaw load_wraw_mx(const uint8_t* chunk, int lane) {
 }
 
 // e8m0 block scale as float: 2^(e-127); the reference kernel maps e = 0 and
-// e = 255 to 0 (kernels/fst_dequant_v4_vectorized_kernel.cc:280-351).
+// e = 255 to 0 (kernels/fst_dequant_v4_vectorized_kernel.cc:19-37,60-80).
 __device__ __forceinline__ float e8m0_scale(uint32_t e) {
     return (e == 0u || e == 255u) ? 0.0f : __uint_as_float(e << 23);
 }

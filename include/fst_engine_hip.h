@@ -8,6 +8,7 @@
 //   process_shared_expert include/fst_engine.h:319   src/fst_engine.cpp:4373-4489
 //   accept/reject         src/fst_engine.cpp:6021-6063 (inline in generate_dspark)
 //   apply_final_norm_and_lm_head include/fst_engine.h:276 src/fst_engine.cpp:2115-2160
+//   sample_token          include/fst_engine.h:277   src/fst_engine.cpp:4491-4528
 //   process_layer (FFN half, non-HC residual) include/fst_engine.h:308
 //                         src/fst_engine.cpp:2734-2917
 //
@@ -102,22 +103,35 @@ public:
         return n_acc;
     }
 
-    // include/fst_engine.h:276: logits[M][vocab] = LMHead(RMSNorm_final(hidden_state)).
-    // The final norm weights go in with upload_norm(n_layers, w), the Q4_K head
-    // with upload_lm_head.  hidden_state is the plain [M][hidden] residual
-    // (the HC collapse of the reference's 4-stream residual is not on this path).
+    // include/fst_engine.h:276 (src/fst_engine.cpp:2115-2160): logits[M][vocab]
+    // = LMHead(RMSNorm_final(plain)).  As in the reference, hidden_state is the
+    // 4-stream HC residual [M][4][hidden] once the HC head is uploaded
+    // (upload_hc_head), collapsed by output_hc_head first (:2120-2128); without
+    // an HC head it is a plain [M][hidden].  The final norm weights go in with
+    // upload_norm(n_layers, w), the head with upload_lm_head.  The device
+    // buffers belong to the context: nothing is allocated per call.
     void apply_final_norm_and_lm_head(bf16_t* hidden_state, int M, float* logits) {
-        const size_t hbytes = (size_t)M * cfg_.hidden_dim * sizeof(bf16_t);
-        const size_t lbytes = (size_t)M * cfg_.vocab_size * sizeof(float);
-        void* dh = fst_device_alloc(ctx_, hbytes);
-        void* dl = fst_device_alloc(ctx_, lbytes);
-        int rc = (dh && dl) ? FST_OK : FST_ENOMEM;
-        if (rc == FST_OK) rc = fst_copy_to_device(ctx_, dh, hidden_state, hbytes);
-        if (rc == FST_OK) rc = fst_lm_head_dev(ctx_, static_cast<const uint16_t*>(dh), M, static_cast<float*>(dl));
-        if (rc == FST_OK) rc = fst_copy_to_host(ctx_, logits, dl, lbytes);
-        fst_device_free(ctx_, dh);
-        fst_device_free(ctx_, dl);
-        check(rc, "apply_final_norm_and_lm_head");
+        check(fst_final_head(ctx_, hidden_state, M, logits), "apply_final_norm_and_lm_head");
+    }
+    void upload_hc_head(const bf16_t* fn, float scale, const float* base) {
+        check(fst_upload_hc_head(ctx_, fn, scale, base), "fst_upload_hc_head");
+    }
+
+    // include/fst_engine.h:277 (src/fst_engine.cpp:4491-4528): temperature <= 0
+    // is the argmax; otherwise softmax(logits/T), top-p, one draw.  The draw is
+    // reproducible: Philox keyed by (sample seed, call number) instead of the
+    // reference's unseeded std::mt19937 (fst_sample_token gives the exact
+    // fixed-point definition).  logits are left unchanged (the reference
+    // overwrites them with probabilities; its callers do not read them again).
+    int sample_token(float* logits, int vocab_size, float temperature, float top_p) {
+        int32_t tok = 0;
+        check(fst_sample_token(ctx_, logits, vocab_size, temperature, top_p, sample_seed_, sample_calls_++, &tok),
+              "fst_sample_token");
+        return tok;
+    }
+    void set_sample_seed(uint64_t seed) {
+        sample_seed_ = seed;
+        sample_calls_ = 0;
     }
 
     // The FFN half of process_layer without HC (src/fst_engine.cpp:2738-2741,
@@ -153,6 +167,7 @@ private:
     fst_config cfg_;
     fst_ctx* ctx_ = nullptr;
     std::vector<const float*> router_src_, bias_src_;
+    uint64_t sample_seed_ = 0x5eed5eedull, sample_calls_ = 0;
 };
 
 }  // namespace fst_hip

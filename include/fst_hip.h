@@ -149,6 +149,31 @@ int fst_accept_greedy_dev(fst_ctx* ctx, const float* d_target, int n_seq, int k,
 int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* d_draft_logits,
                               int n_seq, int k, int V, const int32_t* d_draft, float temperature,
                               uint64_t seed, uint64_t seq_base, int32_t* d_n_acc, int32_t* d_tokens);
+/* Limits: V <= 1,048,574 and n_seq*(2k+1) within the device's grid rows.
+ * The greedy launch hands chunk results between workgroups; the collecting
+ * workgroup's wait is bounded (fst_set_wait_limit polls, default 2^20).  A
+ * wait that gives up writes n_acc[s] = -1 and tokens -1 for its sequence
+ * (the host-pointer entry points then return FST_EHIP); after an asynchronous
+ * *_dev call, fst_accept_check on the copied-back n_acc does the same. */
+int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default */
+int fst_accept_check(const int32_t* n_acc, int n_seq);  /* host memory; FST_EHIP if any n_acc < 0 */
+
+/* ---- sample_token (include/fst_engine.h:277, src/fst_engine.cpp:4491-4528) ----
+ * temperature <= 0: the plain argmax (first maximum wins, NaN skipped, a NaN
+ * at index 0 pins 0).  Otherwise a reproducible form of the reference's
+ * softmax(logits/T) -> top-p -> one draw (the reference draws from an unseeded
+ * std::mt19937): probabilities in 2^-32 fixed point E = floor(exp(x/T - max)
+ * * 2^32), tokens by E descending then lower index, the kept set the shortest
+ * prefix whose mass reaches floor(top_p * 2^32) / 2^32 of the total (at
+ * least one token), and the token the first of the kept prefix whose running
+ * mass exceeds (U * kept mass) >> 24 with U = 24-bit Philox-4x32-10 uniform of
+ * (seed, seq, position 0, stream 2).  The logits are not modified.
+ * _dev: n_rows rows [n_rows][V] on the device, row r with seq = seq_base + r,
+ * tokens [n_rows] int32 on the device. */
+int fst_sample_token(fst_ctx* ctx, const float* logits, int V, float temperature, float top_p, uint64_t seed,
+                     uint64_t seq, int32_t* token);
+int fst_sample_token_dev(fst_ctx* ctx, const float* d_logits, int n_rows, int V, float temperature, float top_p,
+                         uint64_t seed, uint64_t seq_base, int32_t* d_tokens);
 
 /* ---- standalone dequant (bit-exact check of the codec; kernels/fst_dequant_q4k_kernel.cc) ---- */
 /* codec blocks (host) -> fp32 and/or bf16 (host); either output may be NULL. */
@@ -191,6 +216,13 @@ int fst_rmsnorm_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, const uint16_t* 
                     uint16_t* d_normed);
 /* d_logits[M][vocab] fp32 = LMHead(RMSNorm_final(d_h)). */
 int fst_lm_head_dev(fst_ctx* ctx, const uint16_t* d_h, int M, float* d_logits);
+/* apply_final_norm_and_lm_head (include/fst_engine.h:276, src/fst_engine.cpp:2115-2160)
+ * with host buffers: logits[M][vocab] fp32.  When the HC head is uploaded
+ * (fst_upload_hc_head), hs is the reference's 4-stream residual [M][4][hidden]
+ * and is collapsed by output_hc_head first (:2120-2128); otherwise hs is a
+ * plain [M][hidden].  The device buffers are the context's own (the logits
+ * buffer is allocated on the first call and kept). */
+int fst_final_head(fst_ctx* ctx, const uint16_t* hs, int M, float* logits);
 /* For l in 0..n_layers-1: h = h + MoE_l(RMSNorm_l(h)); then logits =
  * LMHead(RMSNorm_final(h)).  d_h [M][hidden] bf16 is updated in place. */
 int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_input_ids, float* d_logits);

@@ -434,6 +434,71 @@ int fo_accept_stochastic(const float* target, const float* draft_logits, int k, 
     return 0;
 }
 
+/* ------------------------------------------------------------ sample_token */
+
+/* src/fst_engine.cpp:4491-4528 (FSTEngine::sample_token): temperature <= 0
+ * gives the plain argmax (:4495-4500, the rule of fo_argmax); otherwise the
+ * softmax of logits/T, the top-p set (tokens by descending probability,
+ * :4511-4517, kept until the cumulative mass reaches top_p), renormalised,
+ * and one draw by inverse CDF over the kept tokens in that order (:4519-4527).
+ * The reference draws from an unseeded std::mt19937, so this build defines
+ * a reproducible form with the fixed-point machinery of the acceptance:
+ *   E[v] = floor(exp(x_v*(1/T) - max)*2^32) (fo_softmax_fixed), S = sum E;
+ *   order: E descending, ties by lower index (the reference's partial_sort
+ *   leaves tie order unspecified);
+ *   kept = shortest prefix (at least one token) whose mass C satisfies
+ *   C*2^32 >= q*S, q = floor(top_p*2^32) clamped to [0, 2^32];
+ *   U = fst_uniform24(seed, seq, 0, 2); target = (U*C_kept) >> 24; the token
+ *   is the first of the kept prefix whose running mass exceeds target.
+ * Restated here with an explicit sort (the device kernel searches by radix
+ * histograms instead). */
+typedef struct { uint64_t e; int v; } fo_ev;
+static int fo_ev_cmp(const void* a, const void* b) {
+    const fo_ev* x = (const fo_ev*)a;
+    const fo_ev* y = (const fo_ev*)b;
+    if (x->e != y->e) return x->e > y->e ? -1 : 1;
+    return x->v < y->v ? -1 : (x->v > y->v ? 1 : 0);
+}
+
+uint64_t fo_top_p_fixed(float top_p) {
+    if (!(top_p > 0.0f)) return 0;
+    if (top_p >= 1.0f) return 4294967296ull;
+    return (uint64_t)floor((double)top_p * 4294967296.0);
+}
+
+int fo_sample_token(const float* logits, int V, float temperature, float top_p, uint64_t seed, uint64_t seq,
+                    int* n_kept) {
+    if (n_kept) *n_kept = 1;
+    if (!(temperature > 0.0f)) return fo_argmax(logits, V);
+    const float inv_t = 1.0f / temperature;
+    uint64_t* E = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    fo_ev* ord = (fo_ev*)malloc(sizeof(fo_ev) * (size_t)V);
+    const uint64_t S = fo_softmax_fixed(logits, V, inv_t, E);
+    if (S == 0) { free(E); free(ord); return 0; }
+    for (int v = 0; v < V; ++v) { ord[v].e = E[v]; ord[v].v = v; }
+    qsort(ord, (size_t)V, sizeof(fo_ev), fo_ev_cmp);
+    const u128 need = (u128)fo_top_p_fixed(top_p) * S;
+    uint64_t C = 0;
+    int n = 0;
+    while (n < V) {
+        C += ord[n].e;
+        ++n;
+        if (((u128)C << 32) >= need) break;
+    }
+    const uint32_t U = fst_uniform24(seed, seq, 0u, 2u);
+    const uint64_t tgt = (uint64_t)(((u128)U * C) >> 24);
+    uint64_t c = 0;
+    int tok = ord[n - 1].v;
+    for (int i = 0; i < n; ++i) {
+        c += ord[i].e;
+        if (c > tgt) { tok = ord[i].v; break; }
+    }
+    if (n_kept) *n_kept = n;
+    free(E);
+    free(ord);
+    return tok;
+}
+
 /* ----------------------------------------------------------------- RMSNorm */
 
 /* src/fst_engine.cpp:89-91 (rms_cpu): r = 1/sqrt(mean(x^2)+eps), out =

@@ -46,6 +46,11 @@ void fo_combine(const float* y_routed /* [M][tk][hd] */, const float* y_shared /
 
 /* Acceptance (one sequence).  target: [k+1][V], draft_logits: [k][V]. */
 int fo_argmax(const float* logits, int V);
+/* sample_token (src/fst_engine.cpp:4491-4528) in the build's reproducible
+ * fixed-point form; n_kept (nullable) gets the size of the top-p set. */
+uint64_t fo_top_p_fixed(float top_p);
+int fo_sample_token(const float* logits, int V, float temperature, float top_p, uint64_t seed, uint64_t seq,
+                    int* n_kept);
 int fo_accept_greedy(const float* target, int k, int V, const int32_t* draft,
                      int32_t* n_acc, int32_t* tokens);
 int fo_accept_stochastic(const float* target, const float* draft_logits, int k, int V,

@@ -41,6 +41,8 @@ def lib():
                                 P, P, P, P]),
         "fo_combine": (None, [P, P, P, C.c_int, C.c_int, C.c_int, P, P]),
         "fo_argmax": (C.c_int, [P, C.c_int]),
+        "fo_top_p_fixed": (C.c_uint64, [C.c_float]),
+        "fo_sample_token": (C.c_int, [P, C.c_int, C.c_float, C.c_float, C.c_uint64, C.c_uint64, P]),
         "fo_accept_greedy": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
         "fo_accept_stochastic": (C.c_int, [P, P, C.c_int, C.c_int, P, C.c_float, C.c_uint64, C.c_uint64, P, P]),
         "fo_rmsnorm": (None, [P, P, C.c_int, C.c_int, C.c_float, P]),
@@ -160,6 +162,14 @@ def accept_greedy(target, draft):
     tok = np.full(kp1, -1, np.int32)
     lib().fo_accept_greedy(_p(target), kp1 - 1, V, _p(draft), C.byref(n), _p(tok))
     return n.value, tok[: n.value + 1]
+
+
+def sample_token(logits, temperature, top_p, seed, seq):
+    """fo_sample_token: (token, size of the top-p set)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    n = C.c_int()
+    t = lib().fo_sample_token(_p(logits), logits.shape[-1], temperature, top_p, seed, seq, C.byref(n))
+    return t, n.value
 
 
 def accept_stochastic(target, draft_logits, draft, temperature, seed, seq):

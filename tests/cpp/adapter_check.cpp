@@ -80,6 +80,7 @@ int main(int argc, char** argv) {
     // one logit row recomputed here from the GPU dequant of the same blocks
     // and a double-precision RMSNorm must agree to 1e-2
     double head_rel = 1.0;
+    bool hc_equal = false, sample_ok = false;
     {
         fst_config c2 = cfg;
         c2.vocab_size = 256;
@@ -106,9 +107,46 @@ int main(int argc, char** argv) {
             hd2 += acc * acc;
         }
         head_rel = std::sqrt(hn / hd2);
+
+        // with the HC head uploaded the input is the 4-stream residual
+        // [M][4][hd] (src/fst_engine.cpp:2120-2128): the logits must equal
+        // output_hc_head -> final norm -> head run piece by piece on the device
+        std::vector<uint16_t> fn((size_t)4 * 4 * hd), hs((size_t)M * 4 * hd);
+        fst_synth_normal_bf16(99, 13, fn.size(), 0.0f, 0.02f, fn.data());
+        fst_synth_normal_bf16(99, 14, hs.size(), 0.0f, 1.0f, hs.data());
+        const float base[4] = {0.1f, -0.2f, 0.3f, 0.0f};
+        head.upload_hc_head(fn.data(), 0.5f, base);
+        std::vector<float> lg_hc((size_t)M * c2.vocab_size), lg_ref(lg_hc.size());
+        head.apply_final_norm_and_lm_head(hs.data(), M, lg_hc.data());
+        fst_ctx* hc = head.handle();
+        void* d_hs = fst_device_alloc(hc, hs.size() * 2);
+        void* d_plain = fst_device_alloc(hc, (size_t)M * hd * 2);
+        void* d_lg = fst_device_alloc(hc, lg_ref.size() * 4);
+        int rc = fst_copy_to_device(hc, d_hs, hs.data(), hs.size() * 2);
+        if (!rc) rc = fst_hc_head_dev(hc, (const uint16_t*)d_hs, M, (uint16_t*)d_plain);
+        if (!rc) rc = fst_lm_head_dev(hc, (const uint16_t*)d_plain, M, (float*)d_lg);
+        if (!rc) rc = fst_copy_to_host(hc, lg_ref.data(), d_lg, lg_ref.size() * 4);
+        fst_device_free(hc, d_hs);
+        fst_device_free(hc, d_plain);
+        fst_device_free(hc, d_lg);
+        hc_equal = rc == FST_OK && std::memcmp(lg_hc.data(), lg_ref.data(), lg_ref.size() * 4) == 0;
+
+        // sample_token (include/fst_engine.h:277): argmax at temperature 0,
+        // and the seeded draw equals fst_sample_token with (seed, call number)
+        std::vector<float> row(lg_hc.begin(), lg_hc.begin() + c2.vocab_size);
+        int am = 0;
+        for (int v = 1; v < c2.vocab_size; ++v)
+            if (row[v] > row[am]) am = v;
+        head.set_sample_seed(4242);
+        const int t0 = head.sample_token(row.data(), c2.vocab_size, 0.0f, 0.9f);
+        const int t1 = head.sample_token(row.data(), c2.vocab_size, 1.0f, 0.9f);
+        int32_t r1 = -1;
+        if (fst_sample_token(hc, row.data(), c2.vocab_size, 1.0f, 0.9f, 4242, 1, &r1) != FST_OK) return 1;
+        sample_ok = t0 == am && t1 == r1 && t1 >= 0 && t1 < c2.vocab_size;
     }
-    const bool ok = rel < 1e-2 && acc_ok && threw && head_rel < 1e-2;
-    std::printf("ADAPTER GPU %s: combine rel=%.3e accept n=%d threw_on_bad_shape=%d lm_head rel=%.3e\n",
-                ok ? "OK" : "FAIL", rel, n, (int)threw, head_rel);
+    const bool ok = rel < 1e-2 && acc_ok && threw && head_rel < 1e-2 && hc_equal && sample_ok;
+    std::printf("ADAPTER GPU %s: combine rel=%.3e accept n=%d threw_on_bad_shape=%d lm_head rel=%.3e "
+                "hc_head_equal=%d sample_ok=%d\n",
+                ok ? "OK" : "FAIL", rel, n, (int)threw, head_rel, (int)hc_equal, (int)sample_ok);
     return ok ? 0 : 1;
 }

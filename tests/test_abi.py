@@ -82,3 +82,16 @@ def test_f32_to_bf16_helper(fa):
     x = np.random.default_rng(0).normal(0, 10, 5000).astype(np.float32)
     ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(fa.f32_to_bf16(x), ref)
+
+
+def test_accept_check_flags_abandoned_sequences(fa):
+    # host-side handling of the greedy launch's bounded wait: a sequence
+    # whose owner gave up reports n_acc = -1, which becomes FST_EHIP
+    L = fa.lib()
+    ok = np.array([0, 7, 3], np.int32)
+    assert L.fst_accept_check(fa._ptr(ok), 3) == fa.FST_OK
+    bad = np.array([2, -1, 0], np.int32)
+    assert L.fst_accept_check(fa._ptr(bad), 3) == fa.FST_EHIP
+    assert b"sequence 1" in L.fst_last_error()
+    assert L.fst_accept_check(None, 3) == fa.FST_EINVAL
+    assert L.fst_accept_check(fa._ptr(ok), 0) == fa.FST_EINVAL

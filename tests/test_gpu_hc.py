@@ -118,3 +118,44 @@ def test_verify_forward_hc_mode_matches_composition(fa, oracle):
         blocks = fa.synth_q4k_blocks(seed, 999999, V * HD // 256)
         ref = oracle.q4k_linear(blocks, oracle.rmsnorm(bf16_to_f32(plain).reshape(M, HD), fnorm), V, HD)
         assert rel_l2(logits, ref) < 1e-2
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_final_head_collapses_hc_residual(fa, oracle, M):
+    # apply_final_norm_and_lm_head (src/fst_engine.cpp:2115-2160): with the HC
+    # head uploaded the input is the 4-stream residual, collapsed by
+    # output_hc_head before the final norm and the LM head (:2120-2128)
+    _log("final_head HC M=%d" % M)
+    V = 4096
+    hfn, hscale, hbase = _head_tensors(fa, SEED)
+    with fa.Context(n_experts=4, top_k=1, max_tokens=16, n_layers=1, vocab_size=V) as ctx:
+        nw = fa.synth_normal_bf16(SEED, 7300, (HD,), 1.0, 0.1)
+        ctx.upload_norm(1, nw)
+        head = fa.synth_q4k_blocks(SEED, 7301, V * HD // 256)
+        ctx.upload_lm_head(head)
+        h_hc = fa.synth_normal_bf16(SEED, 7200 + M, (M, 4, HD), 0.0, 1.5)
+        # plain mode first: only stream 0's shape [M][HD] is read
+        plain_in = np.ascontiguousarray(h_hc[:, 0, :])
+        lg_plain = ctx.final_head(plain_in)
+        ref_plain = oracle.q4k_linear(head, oracle.rmsnorm(bf16_to_f32(plain_in), nw), V, HD)
+        assert rel_l2(lg_plain, ref_plain) < 1e-2
+        ctx.upload_hc_head(hfn, hscale, hbase)
+        lg = ctx.final_head(h_hc)
+        # the composition of the public device pieces, bit for bit
+        L = fa.lib()
+        d_hs = ctx.to_device(h_hc)
+        d_pl = ctx.dev_alloc(M * HD * 2)
+        d_lg = ctx.dev_alloc(M * V * 4)
+        fa._check(L.fst_hc_head_dev(ctx.h, d_hs, M, d_pl))
+        fa._check(L.fst_lm_head_dev(ctx.h, d_pl, M, d_lg))
+        ctx.sync()
+        comp = ctx.to_host(d_lg, (M, V), np.float32)
+        assert np.array_equal(lg.view(np.uint32), comp.view(np.uint32))
+        # and the oracle: hc_head (bit-exact pieces) -> RMSNorm -> Q4_K head
+        plain = oracle.hc_head(h_hc, hfn, hscale, hbase)
+        ref = oracle.q4k_linear(head, oracle.rmsnorm(bf16_to_f32(plain), nw), V, HD)
+        assert rel_l2(lg, ref) < 1e-2
+        # reading the residual as plain rows instead gives different logits
+        assert rel_l2(lg, lg_plain) > 0.1
+        for p in (d_hs, d_pl, d_lg):
+            ctx.dev_free(p)

@@ -60,6 +60,31 @@ def test_zipf_variable_tokens_per_expert(fa, oracle, c2_layer, M):
     assert err < TOL
 
 
+@pytest.mark.parametrize("M", [16, 32])
+def test_zipf_with_shared_expert(fa, oracle, c2_layer, M):
+    """C4 as specified: top-6 Zipf-routed plus the shared expert, through the
+    device entry point with use_shared = 1 (the path bench.py C4 times)."""
+    ctx, seed, _ = c2_layer
+    L = fa.lib()
+    eids, wts = zipf_routing(400 + M, M)
+    note("zipf+shared M=%d distinct=%d" % (M, len(set(eids.ravel().tolist()))))
+    h = fa.synth_normal_bf16(seed, 4100 + M, (M, HD))
+    dh, de, dw = ctx.to_device(h), ctx.to_device(eids), ctx.to_device(wts)
+    do, ds = ctx.dev_alloc(M * HD * 2), ctx.dev_alloc(M * HD * 2)
+    try:
+        fa._check(L.fst_moe_ffn_dev(ctx.h, 0, dh, M, de, dw, 1, do, None, ds))
+        ctx.sync()
+        out = ctx.to_host(do, (M, HD), np.uint16)
+        outs = ctx.to_host(ds, (M, HD), np.uint16)
+    finally:
+        for p in (dh, de, dw, do, ds):
+            ctx.dev_free(p)
+    ref, _, ys = reference(fa, oracle, seed, h, eids, wts, shared=True)
+    err, errs = rel_l2(bf16_to_f32(out), ref), rel_l2(bf16_to_f32(outs), ys)
+    note("rel_l2 %.3e shared %.3e" % (err, errs))
+    assert err < TOL and errs < TOL
+
+
 def test_repeated_calls_changing_M(fa, oracle, c2_layer):
     """Completion counters are re-armed by their consumers: back-to-back calls
     with different M must each be correct."""

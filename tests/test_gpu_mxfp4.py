@@ -1,7 +1,7 @@
 """GPU tests of the MXFP4 expert path (the format the reference engine runs its experts in):
 fused FP4 decode with the block scale (hardware E2M1 -> bf16 conversion) +
 bf16 MFMA, through the same MoE chain and C-ABI, against the CPU oracle
-(dequantise per kernels/fst_dequant_v4_vectorized_kernel.cc:280-351, fp64
+(dequantise per kernels/fst_dequant_v4_vectorized_kernel.cc:19-37,60-80, fp64
 accumulation)."""
 import numpy as np
 import pytest

@@ -204,3 +204,25 @@ def test_c5_full_verify_step(fa, oracle):
         hn = oracle.rmsnorm(bf16_to_f32(h_fin).reshape(M, HD), norms[L])
         ref = oracle.q4k_linear(np.ascontiguousarray(blocks[rows]), hn, len(rows), HD)
         assert rel_l2(logits[:, rows], ref) < 1e-2
+        # layer 0 at full size (257 experts, M = 32): its norm and routing
+        # bit-exact, its MoE output (every distinct routed expert + shared,
+        # combined) within 1e-2 of the oracle
+        _log("C5: layer 0 MoE vs oracle")
+        _, mn0 = _rmsnorm_dev(fa, ctx, 0, h0)
+        assert np.array_equal(mn0, oracle.rmsnorm(bf16_to_f32(h0).reshape(M, HD), norms[0]))
+        out0, e0, w0 = ctx.moe_layer(0, mn0)
+        re_, rw, _ = oracle.router(mn0, routers[0], None, tk)
+        assert np.array_equal(e0, re_) and np.array_equal(w0.view(np.uint32), rw.view(np.uint32))
+        y = np.zeros((M, tk, HD), np.float32)
+        for ex in sorted(set(int(v) for v in e0.ravel())):
+            toks = [m for m in range(M) if ex in e0[m]]
+            ye = oracle.expert_ffn(0, fa.synth_q4k_expert(seed, ex), mn0[toks])
+            for r, m in enumerate(toks):
+                for j in range(tk):
+                    if e0[m, j] == ex:
+                        y[m, j] = ye[r]
+        ys = oracle.expert_ffn(0, fa.synth_q4k_expert(seed, E), mn0)
+        _, comb = oracle.combine(y, ys, rw)
+        err0 = rel_l2(bf16_to_f32(out0), comb)
+        _log("C5: layer 0 distinct experts %d rel_l2 %.3e" % (len(set(e0.ravel().tolist())), err0))
+        assert err0 < 1e-2

@@ -1,0 +1,87 @@
+"""CPU pins of the oracle's sample_token restatement (fo_sample_token,
+src/fst_engine.cpp:4491-4528, in the build's reproducible fixed-point form):
+closed forms on equal logits, the argmax path, top-p set sizes against the
+reference's own float64 algorithm (sort, cumulate until >= top_p), and the
+distribution of the draw (chi-square against softmax)."""
+import numpy as np
+import pytest
+
+
+def test_nonpositive_temperature_is_reference_argmax(oracle):
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1, 1000).astype(np.float32)
+    x[[17, 400]] = 9.0               # tie: first maximum wins
+    for T in (0.0, -1.0):
+        assert oracle.sample_token(x, T, 0.9, 1, 0)[0] == 17
+    x[5] = np.nan                    # NaN elsewhere is skipped
+    assert oracle.sample_token(x, 0.0, 0.9, 1, 0)[0] == 17
+    x[0] = np.nan                    # NaN at index 0 pins 0 (src/fst_engine.cpp:4496-4498)
+    assert oracle.sample_token(x, 0.0, 0.9, 1, 0)[0] == 0
+
+
+def test_equal_logits_closed_form(oracle):
+    # 8 equal logits: every E = 2^32; top_p = 3/8 keeps exactly tokens 0, 1, 2
+    # (ties by lower index); the draw is token floor(3 U / 2^24)
+    x = np.full(8, 0.25, np.float32)
+    for seq in range(200):
+        t, n = oracle.sample_token(x, 1.0, 0.375, 42, seq)
+        u = oracle.uniform24(42, seq, 0, 2)
+        assert n == 3
+        assert t == (3 * u) >> 24
+    # top_p = 1: all 8 kept, token floor(8 U / 2^24)
+    for seq in range(50):
+        t, n = oracle.sample_token(x, 2.0, 1.0, 7, seq)
+        assert n == 8 and t == (8 * oracle.uniform24(7, seq, 0, 2)) >> 24
+
+
+def test_tiny_top_p_keeps_the_maximum(oracle):
+    rng = np.random.default_rng(2)
+    for s in range(20):
+        x = rng.normal(0, 2, 5000).astype(np.float32)
+        for top_p in (0.0, 1e-9, -1.0):
+            t, n = oracle.sample_token(x, 0.8, top_p, 3, s)
+            assert n == 1 and t == int(np.argmax(x))
+
+
+def test_top_p_set_matches_float64_reference_algorithm(oracle):
+    # the reference: probabilities, indices sorted by descending probability,
+    # kept until the running sum >= top_p (:4511-4517), computed in float64;
+    # cases within 1e-6 of the boundary are skipped (fixed point vs float)
+    rng = np.random.default_rng(3)
+    checked = 0
+    for s in range(60):
+        V = int(rng.integers(50, 3000))
+        T = float(rng.choice([0.5, 1.0, 1.7]))
+        top_p = float(np.float32(rng.uniform(0.05, 0.99)))
+        x = rng.normal(0, 2, V).astype(np.float32)
+        l = x.astype(np.float64) / T
+        p = np.exp(l - l.max())
+        p /= p.sum()
+        order = np.lexsort((np.arange(V), -p))
+        c = np.cumsum(p[order])
+        n64 = int(np.searchsorted(c, top_p)) + 1
+        if abs(c[n64 - 1] - top_p) < 1e-6 or (n64 >= 2 and abs(c[n64 - 2] - top_p) < 1e-6):
+            continue
+        t, n = oracle.sample_token(x, T, top_p, 9, s)
+        assert n == n64, (s, n, n64)
+        assert t in set(order[:n64].tolist())
+        checked += 1
+    assert checked > 40
+
+
+def test_draw_follows_truncated_softmax(oracle):
+    # top_p = 1: the token follows softmax(x / T); chi-square over 6000 draws
+    x = np.array([1.0, 0.2, -0.5, 2.0, 0.0, -1.5], np.float32)
+    T = 1.3
+    p = np.exp(x.astype(np.float64) / T)
+    p /= p.sum()
+    draws = np.array([oracle.sample_token(x, T, 1.0, 11, s)[0] for s in range(6000)])
+    obs = np.bincount(draws, minlength=6)
+    exp = p * len(draws)
+    chi2 = float(((obs - exp) ** 2 / exp).sum())
+    assert chi2 < 25.0  # 5 degrees of freedom: p ~ 1e-4
+    # top_p = 0.6 keeps tokens 3 and 0 only (0.467 + 0.216 >= 0.6), renormalised
+    draws = np.array([oracle.sample_token(x, T, 0.6, 12, s)[0] for s in range(4000)])
+    assert set(draws.tolist()) == {0, 3}
+    frac3 = np.mean(draws == 3)
+    assert abs(frac3 - p[3] / (p[3] + p[0])) < 0.03
