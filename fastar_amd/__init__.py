@@ -81,6 +81,7 @@ _SIGS = {
     "fst_sample_token": (C.c_int, [P, P, C.c_int, C.c_float, C.c_float, U64, U64, P]),
     "fst_sample_token_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_float, C.c_float, U64, U64, P]),
     "fst_accept_check": (C.c_int, [P, C.c_int]),
+    "fst_accept_greedy_dev_noalloc": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P, P]),
     "fst_dequant": (C.c_int, [P, C.c_int, P, SZ, P, P]),
     "fst_set_profiling": (C.c_int, [P, C.c_int]),
     "fst_last_timings": (C.c_int, [P, P]),

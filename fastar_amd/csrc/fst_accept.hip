@@ -947,4 +947,47 @@ void launch_sample_token(hipStream_t st, const float* logits, int n_rows, int V,
 
 size_t sample_ws_bytes(int n_rows, int V) { return (size_t)n_rows * V * 8 + 256; }
 
+// ---- scratch of the allocation-free greedy entry point ----
+// The greedy hand-off words of fst_accept_greedy_dev_noalloc live in this
+// fixed device array instead of a context workspace: kStaticGreedyRows rows
+// of kGreedyChunks words (256 KiB), held by every device the library runs on
+// until the process ends.  Its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// handed to kernels: in host code the array's name is not a device address.
+// Every call on a device shares the array; calls that overlap on one device
+// race.  Each call takes the next epoch of the device, so no clearing is
+// needed between calls (zero-initialised words carry epoch 0, never used).
+static __device__ __align__(256) unsigned long long scratch[kStaticGreedyRows * kGreedyChunks];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+std::atomic<uint32_t> g_scratch_epoch[kMaxDevices];
+}  // namespace
+
+int accept_scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) return set_error(FST_ENODEV, "device ordinal beyond the scratch table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return 0;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return set_error(FST_EHIP, (std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e)).c_str());
+    g_scratch_ptr[device] = p;
+    return 0;
+}
+
+void* accept_scratch_ptr(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch_ptr[device];
+}
+
+uint32_t accept_scratch_epoch(int device) {
+    // 1..4095 in turn (the tag field of a greedy word holds 12 bits)
+    const uint32_t n = g_scratch_epoch[device].fetch_add(1u, std::memory_order_relaxed);
+    return n % 4095u + 1u;
+}
+
 }  // namespace fst

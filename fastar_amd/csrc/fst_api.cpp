@@ -232,6 +232,9 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(FST_ENODEV, std::string("fst_create: device is ") + prop.gcnArchName + ", need gfx950");
 
+    // the allocation-free greedy entry point's scratch address on this device
+    if (int rc0 = fst::accept_scratch_init(c.device)) return rc0;
+
     fst_ctx* x = new fst_ctx();
     x->cfg = c;
     x->max_grid_y = prop.maxGridSize[1] > 0 ? prop.maxGridSize[1] : 65535;
@@ -752,6 +755,25 @@ int fst_accept_greedy_dev(fst_ctx* ctx, const float* d_target, int n_seq, int k,
     fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens,
                               fst::accept_greedy_words(ctx->acc_ws, n_seq, k), next_epoch(&ctx->acc_epoch),
                               ctx->spin_limit);
+    ctx->mark("accept_greedy");
+    FST_HIP_TRY(hipGetLastError());
+    return FST_OK;
+}
+
+int fst_accept_greedy_dev_noalloc(fst_ctx* ctx, const float* d_target, int n_seq, int k, int V,
+                                  const int32_t* d_draft, int32_t* d_n_acc, int32_t* d_tokens) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (int rc = check_accept_args(ctx, n_seq, k, V)) return rc;
+    if ((long)n_seq * (k + 1) > fst::kStaticGreedyRows)
+        return fail(FST_EINVAL, "n_seq*(k+1) exceeds the fixed scratch of " + std::to_string(fst::kStaticGreedyRows) +
+                                    " rows");
+    if (!d_target || !d_n_acc || !d_tokens || (k > 0 && !d_draft)) return fail(FST_EINVAL, "null device buffer");
+    if (misaligned(d_target)) return fail(FST_EINVAL, "device buffers must be 16-byte aligned");
+    void* words = fst::accept_scratch_ptr(ctx->cfg.device);
+    if (!words) return fail(FST_EHIP, "scratch address of the device was not set up");
+    ctx->mark_begin();
+    fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens, words,
+                              fst::accept_scratch_epoch(ctx->cfg.device), ctx->spin_limit);
     ctx->mark("accept_greedy");
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;

@@ -354,6 +354,15 @@ void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k,
 size_t sample_ws_bytes(int n_rows, int V);
 void launch_sample_token(hipStream_t st, const float* logits, int n_rows, int V, float temperature, float top_p,
                          uint64_t seed, uint64_t seq_base, void* ws, int32_t* tokens);
+// The allocation-free greedy entry point's fixed device scratch (rows =
+// n_seq*(k+1) at most kStaticGreedyRows): accept_scratch_init looks its
+// address up for `device` (which must be current), once; accept_scratch_ptr
+// returns it (null before init); accept_scratch_epoch hands out the device's
+// next epoch.
+constexpr int kStaticGreedyRows = 2048;
+int accept_scratch_init(int device);
+void* accept_scratch_ptr(int device);
+uint32_t accept_scratch_epoch(int device);
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
                               int n_seq, int k, int V, const int32_t* draft, float inv_t,
                               uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,

@@ -157,6 +157,15 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
  * *_dev call, fst_accept_check on the copied-back n_acc does the same. */
 int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default */
 int fst_accept_check(const int32_t* n_acc, int n_seq);  /* host memory; FST_EHIP if any n_acc < 0 */
+/* fst_accept_greedy_dev without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workgroups' hand-off words live in a fixed per-device array of the
+ * library (256 KiB, n_seq*(k+1) <= 2048 rows; larger calls get FST_EINVAL)
+ * instead of the context's workspace.  All calls on one GPU share that array:
+ * calls that overlap on one GPU race.  Same results as fst_accept_greedy_dev. */
+int fst_accept_greedy_dev_noalloc(fst_ctx* ctx, const float* d_target, int n_seq, int k, int V,
+                                  const int32_t* d_draft, int32_t* d_n_acc, int32_t* d_tokens);
 
 /* ---- sample_token (include/fst_engine.h:277, src/fst_engine.cpp:4491-4528) ----
  * temperature <= 0: the plain argmax (first maximum wins, NaN skipped, a NaN
