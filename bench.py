@@ -62,10 +62,11 @@ def setup(fa):
     return ctx, w, hs, logits, draft, bufs
 
 
-def measured_traffic():
-    """HBM bytes per gate+up launch from the committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None."""
-    p = os.path.join(ROOT, "profiles", "q4k_moe_verify_c2_hbm_traffic.md")
+def measured_traffic(name):
+    """HBM bytes per launch of the dominant kernel from a committed rocprofv3
+    PMC summary under profiles/ (FETCH_SIZE + WRITE_SIZE, calibrated against
+    a copy kernel), or None."""
+    p = os.path.join(ROOT, "profiles", name)
     try:
         txt = open(p).read()
         blob = txt.split("```json", 1)[1].split("```", 1)[0]
@@ -402,7 +403,8 @@ def main():
     # Per-kernel durations (HIP events on the library stream) and distinct experts per step.
     ctx.set_profiling(True)
     per = {}
-    bytes_gu, bytes_dn, dur_gu, dur_dn, n_act = [], [], [], [], []
+    bytes_k, dur_k, n_act = [], [], []
+    fused = None
     nprof = min(args.steps, 64)
     for i in range(nprof):
         fa._check(L.fst_moe_layer_dev(ctx.h, 0, bufs["h"] + (i % N_BATCH) * M * HD * 2, M, None, bufs["out"],
@@ -413,26 +415,31 @@ def main():
         for name, ms in tm:
             per.setdefault(name, []).append(ms)
         d = dict(tm)
-        bytes_gu.append((a + 1) * 2 * PROJ_BYTES)
-        bytes_dn.append((a + 1) * PROJ_BYTES)
-        dur_gu.append(d["q4k_gate_up"] * 1e-3)
-        dur_dn.append(d["q4k_down"] * 1e-3)
+        fused = "moe_fused" in d
+        if fused:
+            # one launch streams every touched expert's gate, up and down
+            bytes_k.append((a + 1) * 3 * PROJ_BYTES)
+            dur_k.append(d["moe_fused"] * 1e-3)
+        else:
+            bytes_k.append((a + 1) * 2 * PROJ_BYTES)
+            dur_k.append(d["q4k_gate_up"] * 1e-3)
     ctx.set_profiling(False)
     fa._check(L.fst_accept_greedy_dev(ctx.h, bufs["logits"], 1, K_DRAFT, VOCAB, bufs["draft"], bufs["nacc"],
                                       bufs["tok"]))
     ctx.sync()
     n_acc = int(ctx.to_host(bufs["nacc"], (1,), np.int32)[0])
 
-    gu_achieved = np.mean(bytes_gu) / np.mean(dur_gu) / 1e9
-    # MFMA work of the gate|up launch: every 16-row x 256-weight chunk (2304 B)
-    # issues 8 fp16 16x16x32 MFMAs plus 1 for the min term (16,384 flops each);
-    # useful flops are 2 x (M*top_k routed + M shared pairs) x K x N
-    gu_issued = np.mean(bytes_gu) / 2304.0 * 9 * 16384
-    gu_useful = 2.0 * (M * TK + M) * HD * (2 * INTER)
-    dn_achieved = np.mean(bytes_dn) / np.mean(dur_dn) / 1e9
+    k_achieved = np.mean(bytes_k) / np.mean(dur_k) / 1e9
+    # MFMA work: every 16-row x 256-weight chunk (2304 B) issues 8 fp16
+    # 16x16x32 MFMAs plus 1 for the min term (16,384 flops each); useful flops
+    # are 2 x (M*top_k routed + M shared pairs) x (K x N of each projection)
+    k_issued = np.mean(bytes_k) / 2304.0 * 9 * 16384
+    k_useful = 2.0 * (M * TK + M) * HD * INTER * (3 if fused else 2)
     mean_act = float(np.mean(n_act))
     step_bytes = (mean_act + 1) * EXPERT_BYTES + ROUTER_BYTES
     kern = {k: round(float(np.mean(v)) * 1e3, 2) for k, v in per.items()}  # microseconds
+    kname = ("moe_fused: gate||up and down items of every touched expert in one persistent launch "
+             "(fused Q4_K decode, fp16 MFMA)") if fused else "q4k_linear gate+up (fused Q4_K decode, fp16 MFMA)"
 
     if args.calib_copy:
         nbytes = 512 << 20
@@ -473,24 +480,26 @@ def main():
             "parallelism": "1 GPU",
         },
         "roofline": {
-            "kernel": "q4k_linear gate+up (fused Q4_K decode, fp16 MFMA; each workgroup pairs 64 gate with 64 up rows and writes silu(g)*u)",
+            "kernel": kname,
             "bound": "hbm",
-            "achieved": round(gu_achieved, 1),
+            "achieved": round(k_achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gu_achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
-            "algorithmic_bytes": int(np.mean(bytes_gu)),
+            "frac": round(k_achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("moe_fused_c2_hbm_traffic.md" if fused else
+                                        "q4k_moe_verify_c2_hbm_traffic.md"),
+            "algorithmic_bytes": int(np.mean(bytes_k)),
+            "per_unit": ("14,155,776 B per touched expert (gate, up, down Q4_K) x (distinct routed + 1 shared) "
+                         "experts per launch") if fused else "9,437,184 B per touched expert (gate, up)",
         },
         "mfma": {
-            "kernel": "q4k_linear gate+up",
-            "issued_tflops": round(gu_issued / np.mean(dur_gu) / 1e12, 1),
-            "useful_tflops": round(gu_useful / np.mean(dur_gu) / 1e12, 1),
+            "kernel": kname.split(":")[0],
+            "issued_tflops": round(k_issued / np.mean(dur_k) / 1e12, 1),
+            "useful_tflops": round(k_useful / np.mean(dur_k) / 1e12, 1),
             "peak_tflops": MFMA_F16_PEAK_TFLOPS,
-            "util": round(gu_issued / np.mean(dur_gu) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "util": round(k_issued / np.mean(dur_k) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
         },
         "packed_weight_GBps_step": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
-        "down_kernel_GBps": round(dn_achieved, 1),
         "kernel_us": kern,
         "accepted_len_step": n_acc,
         "cpu_baseline": cpu,

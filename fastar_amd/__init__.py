@@ -77,6 +77,7 @@ _SIGS = {
     "fst_accept_greedy_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P, P]),
     "fst_accept_stochastic_dev": (C.c_int, [P, P, P, C.c_int, C.c_int, C.c_int, P, C.c_float, U64, U64, P, P]),
     "fst_set_wait_limit": (C.c_int, [P, C.c_int]),
+    "fst_set_fused": (C.c_int, [P, C.c_int]),
     "fst_final_head": (C.c_int, [P, P, C.c_int, P]),
     "fst_sample_token": (C.c_int, [P, P, C.c_int, C.c_float, C.c_float, U64, U64, P]),
     "fst_sample_token_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_float, C.c_float, U64, U64, P]),
@@ -329,6 +330,9 @@ class Context:
         _check(lib().fst_accept_stochastic(self.h, _ptr(target), _ptr(dl), n_seq, k, V, _ptr(draft),
                                            temperature, seed, seq_base, _ptr(n_acc), _ptr(tok)))
         return n_acc, tok
+
+    def set_fused(self, on):
+        _check(lib().fst_set_fused(self.h, 1 if on else 0))
 
     def final_head(self, hs):
         """apply_final_norm_and_lm_head: hs [M][4][hidden] with the HC head

@@ -73,6 +73,8 @@ struct fst_ctx {
     uint16_t* hc_h = nullptr;                // [T][4][hd] host-call staging
     bool nested = false;                     // inside verify_forward: no per-kernel marks
     fst::Scratch s{};
+    uint32_t fused_epoch = 0;                // fused MoE launches issued (tags of their h words)
+    bool fused = true;                       // use the fused launch where it applies
     std::vector<void*> allocs;
     std::vector<uint8_t> staging;            // host repack buffer for expert uploads
     // acceptance staging (grown on demand)
@@ -238,6 +240,7 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     fst_ctx* x = new fst_ctx();
     x->cfg = c;
     x->max_grid_y = prop.maxGridSize[1] > 0 ? prop.maxGridSize[1] : 65535;
+    x->fused = getenv("FST_NO_FUSED") == nullptr;  // A/B switch for measurements (fst_set_fused at run time)
     int rc = FST_OK;
     auto bail = [&](int code) {
         delete x;
@@ -298,8 +301,13 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.act, (size_t)P * inter)) || (rc = x->dalloc(&s.a16p, (size_t)P * inter)) ||
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
         (rc = x->dalloc(&s.y, (size_t)P * hd)) ||
-        (rc = x->dalloc(&s.sh_h16, (size_t)T * c.inter_dim)) || (rc = x->dalloc(&s.ys, (size_t)T * hd)))
+        (rc = x->dalloc(&s.sh_h16, (size_t)T * c.inter_dim)) || (rc = x->dalloc(&s.ys, (size_t)T * hd)) ||
+        (rc = x->dalloc(&s.hbuf, (size_t)P * inter)) ||
+        (rc = x->dalloc(&s.amaxw, (size_t)P * (inter / 16))) || (rc = x->dalloc(&s.fused_claim, 64)))
         return bail(rc);
+    if (hipMemsetAsync(s.hbuf, 0, sizeof(unsigned long long) * (size_t)P * inter, x->st) != hipSuccess ||
+        hipMemsetAsync(s.amaxw, 0, sizeof(unsigned long long) * (size_t)P * (inter / 16), x->st) != hipSuccess)
+        return bail(fail(FST_EHIP, "hipMemsetAsync(hand-off words) failed"));
     if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));
     x->ev.resize(17);
@@ -558,6 +566,18 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
         ctx->mark("bucket_prep");
     }
     const int sh_q = use_shared && !sh16 ? 1 : 0;  // the shared expert runs as slot 0
+    if (fuse_topk && ctx->fused && use_routed && fst::moe_fused_supported(g, M)) {
+        // gate||up and down in one persistent launch, then the combine
+        ctx->fused_epoch = ctx->fused_epoch == 0xffffffffu ? 1u : ctx->fused_epoch + 1u;
+        fst::launch_moe_fused(st, g, L, M, ctx->s, rq, ctx->fused_epoch, ctx->spin_limit);
+        ctx->mark("moe_fused");
+        // (a bf16 shared expert ran above; its fp32 rows are the combine's shared term)
+        fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out, d_out_routed,
+                            d_out_shared);
+        ctx->mark("combine");
+        FST_HIP_TRY(hipGetLastError());
+        return FST_OK;
+    }
     const int ksplit = fst::launch_q4k_gate_up(st, g, L, M, ctx->s, d_h, fuse_topk ? &rq : nullptr,
                                                std::min(c.n_experts, M * g.tk) + sh_q, M * (g.tk + sh_q));
     ctx->mark("q4k_gate_up");
@@ -594,6 +614,7 @@ static int check_meta_error(fst_ctx* ctx) {
     FST_HIP_TRY(hipStreamSynchronize(ctx->st));
     if (m[fst::META_ERROR] & 1) return fail(FST_EINVAL, "expert id out of range in routing");
     if (m[fst::META_ERROR] & 2) return fail(FST_EINVAL, "input id out of vocabulary range for hash routing");
+    if (m[5] & 1) return fail(FST_EHIP, "a cross-workgroup hand-off of the fused MoE launch exceeded its spin limit");
     return FST_OK;
 }
 
@@ -779,6 +800,12 @@ int fst_accept_greedy_dev_noalloc(fst_ctx* ctx, const float* d_target, int n_seq
     return FST_OK;
 }
 
+int fst_set_fused(fst_ctx* ctx, int on) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    ctx->fused = on != 0;
+    return FST_OK;
+}
+
 int fst_set_wait_limit(fst_ctx* ctx, int spins) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (spins < 0) return fail(FST_EINVAL, "spins must be >= 0");
@@ -852,6 +879,13 @@ int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_
     if (!(temperature > 0.0f)) return fail(FST_EINVAL, "temperature must be > 0");
     return accept_host(ctx, target, draft_logits, n_seq, k, V, draft, temperature, seed, seq_base, n_acc, tokens, 1);
 }
+
+#ifdef FST_TRACE
+extern "C++" {
+namespace fst { int trace_read(void* host, size_t bytes); }
+}
+int fst_debug_trace(void* host, size_t bytes) { return fst::trace_read(host, bytes); }
+#endif
 
 // ------------------------------------------------------------ sample_token
 

@@ -60,6 +60,11 @@ struct Scratch {
     float* y;              // [P][hd]
     uint16_t* sh_h16;      // [T][inter] bf16 shared-expert h (bf16 shared expert)
     float* ys;             // [T][hd] fp32 shared-expert output (bf16 shared expert)
+    // fused gate||up + down launch: {epoch, value} words handed between
+    // workgroups (h rows and their per-16-row maxima)
+    unsigned long long* hbuf;   // [P][inter]
+    unsigned long long* amaxw;  // [P][inter/16]
+    int* fused_claim;           // down-pair counter of the fused launch (zeroed by the router launch)
 };
 
 // Device expert bank: n_layers x (n_experts + 1) packed experts.
@@ -313,6 +318,13 @@ int launch_q4k_gate_up(hipStream_t st, const Geometry& g, const LayerView& L, in
 void launch_prep_act_split(hipStream_t st, const float* part, int S, int rows, float swiglu_limit, const int* meta,
                            int inter, _Float16* a16p, uint4* sxp, int* xs, const void* pf = nullptr,
                            size_t pf_bytes = 0);
+// The expert work of a routed block of at most 8 tokens in one persistent
+// launch (gate||up then down items, see moe_fused_kernel), after launch_route
+// with topk = 0; y rows go to s.y for launch_combine.  epoch: a new nonzero
+// value per call (tags the h words); spin_limit bounds each hand-off wait.
+bool moe_fused_supported(const Geometry& g, int M);
+int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                     const RouteReq& rq, uint32_t epoch, int spin_limit);
 // With o1/o2 (one routed pair per token, no shared expert) it writes
 // out = bf16(wts[token] * y) there instead of y, and no combine is needed.
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,

@@ -30,6 +30,15 @@
 
 namespace fst {
 
+#ifdef FST_TRACE
+// Timeline probe (measurement builds only): per workgroup of the linear
+// kernels, the wall clock (100 MHz) at launch entry, after routing, and at
+// the start / end of each work item.
+constexpr int kTraceWG = 1024, kTraceSlots = 32;
+__device__ long long g_trace[2][kTraceWG][kTraceSlots];
+__device__ int g_trace_kernel;
+#endif
+
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
@@ -729,8 +738,10 @@ __global__ __launch_bounds__(256) void router_prep_kernel(const uint4* __restric
                                                           int score_func, int round_bf16,
                                                           float* __restrict__ scores, int nbx, int nrb,
                                                           _Float16* __restrict__ x16p, uint4* __restrict__ sxp,
-                                                          int* __restrict__ xs) {
+                                                          int* __restrict__ xs, int* __restrict__ zero_word) {
     static_assert(TPW >= 2, "the router stage must also hold a prep row (K floats)");
+    // the fused launch that follows claims work from this counter
+    if (zero_word && blockIdx.x == 0 && threadIdx.x == 0) *zero_word = 0;
     __shared__ uint4 sm[TPW * NV * 65];
     const int b = blockIdx.x;
     if (b >= nrb) {
@@ -753,7 +764,7 @@ void launch_route(hipStream_t st, const Geometry& g, const LayerView& L, const u
     case NVV:                                                                                              \
         hipLaunchKernelGGL((router_prep_kernel<NVV, TPW>), grid, dim3(256), 0, st,                         \
                            reinterpret_cast<const uint4*>(L.router_nk), h, M, g.hd, g.E, g.score_func,     \
-                           g.round_logits_bf16, s.logits, nbx, nrb, s.x16p, s.sxp, s.xs);                   \
+                           g.round_logits_bf16, s.logits, nbx, nrb, s.x16p, s.sxp, s.xs, s.fused_claim);    \
         break
     // hidden_dim is a multiple of 512 in [512, 8192] (checked at context creation)
     switch (g.hd / 512) {
@@ -1183,6 +1194,15 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                 for (int i = t; i < ra.M; i += 64 * WAVES) ra.pair_shared[i] = r_psh[i];
         }
     }
+#ifdef FST_TRACE
+    const int tk_id = MODE == 2 ? 1 : 0;
+    long long* trc = blockIdx.x < kTraceWG ? g_trace[tk_id][blockIdx.x] : nullptr;
+    int trn = 2;
+    if (trc && threadIdx.x == 0) {
+        trc[0] = wall_clock64();
+        for (int i = 2; i < kTraceSlots; ++i) trc[i] = 0;
+    }
+#endif
     const int* meta = RPER > 0 ? r_meta : meta_g;
     const int* slot_eid = RPER > 0 ? r_seid : slot_eid_g;
     const int* slot_M = RPER > 0 ? r_sM : slot_M_g;
@@ -1343,7 +1363,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     }
     const int nms = nsb / MS;
 
+#ifdef FST_TRACE
+    if (trc && threadIdx.x == 0) trc[1] = wall_clock64();
+#endif
     for (int t = blockIdx.x; t < total; t += gridDim.x) {
+#ifdef FST_TRACE
+        if (trc && threadIdx.x == 0 && trn < kTraceSlots) trc[trn++] = wall_clock64();
+#endif
         const int slot = t / (tiles * S);
         const int tile = (t - slot * tiles * S) / S;
         const int ks = t % S;
@@ -1542,6 +1568,536 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
             }
         }
     }
+#ifdef FST_TRACE
+    if (trc && threadIdx.x == 0 && trn < kTraceSlots) trc[trn] = -wall_clock64();  // negative: the exit
+#endif
+}
+
+// --------------------------------------------- fused gate||up + down launch
+//
+// One persistent launch runs a block-8 MoE layer's expert work after the
+// router: the work items are every (slot, 64-row gate||up tile) and then
+// every (slot, 128-row down tile), dealt to the workgroups in static rounds
+// (t = blockIdx.x + k * gridDim.x).  The down items of the early rounds fill
+// the time that workgroups would otherwise spend idle at the end of a
+// separate gate||up launch, and no operand-prep launch runs between them.
+//  - routing: every workgroup computes the call's top-k and bucketing into
+//    LDS first (topk_bucket_block), as the gate||up launch does;
+//  - gate||up items: as q4k_linear_kernel MODE 1 (8 tokens, 8 waves: 64
+//    gate rows in waves 0..3 paired with the same up rows in waves 4..7); the
+//    up waves write h = silu(g)*u as 64-bit words {epoch, h bits} with
+//    device-coherent stores, and per 16 rows the largest |h| of each token
+//    in the same form (the down operand's prescale needs the row maximum);
+//  - down items: wait until the slot's maxima and h words carry this call's
+//    epoch (coherent loads, bounded polling), then build the slot's whole
+//    fp16 operand (prescale, k-interleave and sub-block sums exactly as
+//    prep_row) in LDS once per item, and stream the down weights with no
+//    staging or barrier inside the super-block loop; y rows go out in fp32
+//    for the combine launch.
+// Deadlock freedom: every workgroup finishes its gate||up items (lower
+// indices) before it reaches a down item, and the grid never exceeds the
+// workgroups the device holds at once (two per CU), so every item a down
+// item waits for is processed.  The waits are still bounded: past
+// spin_limit polls a workgroup sets meta[kMetaTimeout] and carries on (the
+// host-pointer entry points turn that into FST_EHIP).
+constexpr int kFuT = 8;                           // token capacity
+constexpr int kFuW = 8;                           // waves per workgroup
+constexpr int kFuHalf = kFuW / 2;
+constexpr int kFuChunk = 2304;                    // Q4_K bytes per 16 rows x 256 weights
+constexpr int kFuParts = 36;                      // staged chunks per token per super-block
+constexpr int kFuTS = kFuT * kTokStride;          // one gate||up stage (one super-block)
+constexpr int kFuNCH = kFuT * kFuParts;           // staged chunks per stage
+constexpr int kFuMaxDnSb = 8;                     // down K (inter) <= 2048
+constexpr int kFuOpStride = kFuMaxDnSb * 36 + 1;  // down operand row in LDS, uint4
+constexpr int kMetaTimeout = 5;                   // meta word: a hand-off wait gave up
+
+struct FusedArgs {
+    const uint8_t* bank;
+    size_t expert_stride;         // bytes per expert
+    const _Float16* A;            // gate||up operand [T][hd] (router_prep)
+    const uint4* SX;              // its sub-block sums
+    const int* xs;                // its prescale exponents
+    unsigned long long* hbuf;     // [P][inter] {epoch, h bits}
+    unsigned long long* amaxw;    // [P][inter/16] {epoch, max |h| over 16 rows}
+    size_t hbuf_bytes;
+    float* y;                     // [P][hd]
+    int* claim;                   // item counter, zero at launch (null: static rounds only)
+    float swiglu_limit;
+    uint32_t epoch;
+    int spin_limit;
+};
+
+// Largest value of the 16 lanes of each DPP row (all 64 lanes active).
+__device__ __forceinline__ float row16_fmax(float x) {
+    x = fmaxf(x, fdpp<0x128>(x));  // row_ror 8
+    x = fmaxf(x, fdpp<0x124>(x));  // row_ror 4
+    x = fmaxf(x, fdpp<0x122>(x));  // row_ror 2
+    x = fmaxf(x, fdpp<0x121>(x));  // row_ror 1
+    return x;
+}
+
+template <int HD, int INTER>
+__global__ __launch_bounds__(64 * kFuW) __attribute__((amdgpu_waves_per_eu(FST_Q4K_WAVES_PER_EU))) void
+moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
+    static_assert(INTER % 1024 == 0 && INTER <= 256 * kFuMaxDnSb && HD % 512 == 0, "fused geometry");
+    constexpr int NT = 64 * kFuW;
+    constexpr int NS = (kFuNCH + NT - 1) / NT;
+    static_assert(NS == 1, "one staged chunk per thread");
+    constexpr int RPER = 4;
+    constexpr int RPAIR = kFuT * kMaxTopK;
+    __shared__ uint4 lds[2 * kFuTS];
+    __shared__ uint4 opb[kFuT * kFuOpStride];
+    __shared__ float s_amax[kFuT][2];
+    __shared__ int s_xs2[kFuT];
+    __shared__ int s_claim;
+    __shared__ int r_meta[META_WORDS], r_seid[RPAIR + 1], r_sM[RPAIR + 1], r_soff[RPAIR + 1];
+    __shared__ int r_ptok[RPAIR + kFuT], r_pof[RPAIR], r_psh[kFuT];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    constexpr int hd = HD, inter = INTER;
+    const size_t stride = fa.expert_stride;
+    const uint8_t* bank = fa.bank;
+    {
+        RouteArgs la = ra;
+        la.meta = r_meta;
+        la.slot_eid = r_seid;
+        la.slot_M = r_sM;
+        la.slot_off = r_soff;
+        la.pair_tok = r_ptok;
+        la.pair_of = r_pof;
+        la.pair_shared = r_psh;
+        // the shared expert's gate||up slice of this workgroup, read while it
+        // routes (see q4k_linear_kernel)
+        uint4 pfv[3];
+        const int npf = ra.use_shared ? 3 : 0;
+        {
+            const size_t pieces = (size_t)(2 * inter / 16) * (hd >> 8) * (kFuChunk / 16);
+            const uint4* src = reinterpret_cast<const uint4*>(bank + (size_t)ra.E * stride);
+            const size_t step = (size_t)gridDim.x * NT;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const size_t q = (size_t)blockIdx.x * NT + tid + i * step;
+                pfv[i] = i < npf ? src[q < pieces ? q : 0] : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        topk_bucket_block<RPER, NT, kFuT>(la, blockIdx.x == 0);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) asm volatile("" ::"v"(pfv[i].x));
+        __syncthreads();
+        if (blockIdx.x == 0) {
+            const int ns = r_meta[META_N_SLOTS], np = r_meta[META_N_PAIRS];
+            if (tid <= META_N_ROUTED_PAIRS) ra.meta[tid] = r_meta[tid];
+            if (tid == kMetaTimeout) ra.meta[kMetaTimeout] = 0;
+            for (int i = tid; i < ns; i += NT) {
+                ra.slot_eid[i] = r_seid[i];
+                ra.slot_M[i] = r_sM[i];
+                ra.slot_off[i] = r_soff[i];
+            }
+            for (int i = tid; i < np; i += NT) ra.pair_tok[i] = r_ptok[i];
+            for (int i = tid; i < ra.M * ra.tk; i += NT) ra.pair_of[i] = r_pof[i];
+            if (ra.use_shared)
+                for (int i = tid; i < ra.M; i += NT) ra.pair_shared[i] = r_psh[i];
+        }
+    }
+    const int ns = r_meta[META_N_SLOTS];
+    constexpr int tiles_gu = inter / 64, tiles_dn = hd / 128;
+#ifdef FST_FUSED_GU_ONLY
+    const int ngu = ns * tiles_gu, total = ngu;  // measurement build: gate||up items only
+#else
+    const int ngu = ns * tiles_gu, total = ngu + ns * tiles_dn;
+#endif
+    const int ndn = total - ngu;
+#ifdef FST_TRACE
+    long long* trc = blockIdx.x < kTraceWG ? g_trace[0][blockIdx.x] : nullptr;
+    int trn = 2;
+    if (trc && threadIdx.x == 0) {
+        trc[1] = wall_clock64();
+        for (int i = 2; i < kTraceSlots; ++i) trc[i] = 0;
+    }
+#endif
+    if ((int)blockIdx.x >= total) return;
+    const int r = lane & 15, g = lane >> 4;
+    constexpr int nsb_gu = hd >> 8, nsb_dn = inter >> 8;
+    constexpr int aw = inter / 16;  // amax words per pair
+    constexpr size_t proj = (size_t)inter * (hd / 256) * 144;
+    const f4_t zf = f4_t{0.f, 0.f, 0.f, 0.f};
+    const uint32_t magic = 0x64006400u;
+    const uint32_t ssel = q4k_scale_sel(g);
+    const uint32_t epoch = fa.epoch;
+
+    // Item order: the gate||up items, then the down items, each in slot-major
+    // order, so down items 2p, 2p+1 are the tiles 2x, 2x+1 of one slot.  The
+    // first round is static (item blockIdx.x); after it workgroups claim work
+    // from the call's counter: claim k = G + counter is gate||up item k, or,
+    // past them, a down pair (both tiles, the second reusing the operand the
+    // first built in LDS) or, for the last G down items, a single item.  Workgroups that run faster take more
+    // work (the second workgroup of a CU runs measurably slower), and the
+    // launch ends within about one item of its average.  A claim's answer is
+    // needed only at the last super-block of the item before the claimed
+    // work: gate||up items and second halves of down pairs claim their
+    // successor early enough that thread 0 can store the answer to LDS three
+    // super-blocks before the end, where a barrier publishes it.  Work is
+    // claimed in increasing order, and a down item waits only for gate||up
+    // items of lower index, claimed earlier by running workgroups that never
+    // wait: no wait can close a cycle.  Without a counter (or with fewer
+    // gate||up items than workgroups) the rounds stay static.
+    // The last G down items go out one by one: claimed pairs are about two
+    // items long, and single items at the end keep the workgroups' finishing
+    // times within about one down item.
+    const int G = (int)gridDim.x;
+    const bool dyn = fa.claim != nullptr && ngu >= G;
+    const int D1 = max(ndn - G, 0) & ~1;  // down items [0, D1) go in pairs
+    auto dn_map = [&](int d, int& sl, int& ti) {
+        sl = d / tiles_dn;
+        ti = d - sl * tiles_dn;
+    };
+    auto claim_item = [&](int k) {
+        if (k < ngu) return k;
+        const int p = k - ngu;
+        return p < D1 / 2 ? ngu + 2 * p : ngu + D1 + (p - D1 / 2);
+    };
+    // the wave's contiguous run of 2304-byte chunks in item tt
+    auto wave_base = [&](int tt) -> const uint8_t* {
+        if (tt < ngu) {
+            const int sl = tt / tiles_gu, ti = tt - sl * tiles_gu;
+            const int wt = wave < kFuHalf ? ti * kFuHalf + wave : inter / 16 + ti * kFuHalf + (wave - kFuHalf);
+            return bank + (size_t)r_seid[sl] * stride + (size_t)wt * nsb_gu * kFuChunk;
+        }
+        int sl, ti;
+        dn_map(tt - ngu, sl, ti);
+        return bank + (size_t)r_seid[sl] * stride + 2 * proj + (size_t)(ti * kFuW + wave) * nsb_dn * kFuChunk;
+    };
+    auto rsrc = [&](const uint8_t* p, int nsb) -> __amdgpu_buffer_rsrc_t {
+        const uint64_t u = (uint64_t)(uintptr_t)p;
+        const uint64_t us = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
+                            (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)us, (short)0, nsb * kFuChunk, 0x00020000);
+    };
+    auto item_rsrc = [&](int tt) { return rsrc(wave_base(tt), tt < ngu ? nsb_gu : nsb_dn); };
+    constexpr int kNT = FST_WNT;
+    auto load_w = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WRaw {
+        WRaw x;
+        x.h = __builtin_amdgcn_raw_buffer_load_b128(rs, 2048 + 16 * (lane & 15), off, kNT);
+        x.a = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, off, kNT);
+        x.b = __builtin_amdgcn_raw_buffer_load_b128(rs, 1024 + 16 * lane, off, kNT);
+        return x;
+    };
+    // h words of the call, read with device-coherent 16-byte loads (sc1)
+    const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
+        fa.hbuf, (short)0, (int)(fa.hbuf_bytes < 0x7fffffffull ? fa.hbuf_bytes : 0x7fffffffull), 0x00020000);
+
+    __amdgpu_buffer_rsrc_t wrs = item_rsrc(blockIdx.x);
+    WRaw w[2];
+    w[0] = load_w(wrs, 0);
+    for (int i = tid; i < 2 * kFuTS; i += NT) lds[i] = make_uint4(0u, 0u, 0u, 0u);
+
+    // gate||up staging (one chunk per thread per super-block): chunk tid of a
+    // stage -> (token stl, part spart); down items stage nothing here
+    const int stl = tid < kFuNCH ? tid / kFuParts : kFuT;
+    const int spart = tid - (tid / kFuParts) * kFuParts;
+    auto load_row = [&](int tt) -> int {  // operand row of this thread's chunk in item tt (-1: none)
+        if (tt >= ngu) return -1;
+        const int sl = tt / tiles_gu;
+        const int Mi = min(r_sM[sl], kFuT), offi = r_soff[sl];
+        return stl < Mi ? r_ptok[offi + stl] : -1;
+    };
+    const u4v_t* ssrc;
+    int sdst, sstep;
+    u4v_t sv;
+    auto build_map = [&](int ar) {
+        ssrc = reinterpret_cast<const u4v_t*>(fa.SX);
+        sdst = ar >= 0 ? stl * kTokStride + spart : -1;
+        sstep = 0;
+        if (ar >= 0) {
+            if (spart < 32) {
+                ssrc = reinterpret_cast<const u4v_t*>(fa.A + (size_t)ar * hd) + spart;
+                sstep = 32;
+            } else {
+                ssrc = reinterpret_cast<const u4v_t*>(fa.SX + (size_t)ar * nsb_gu * 4 + (spart - 32));
+                sstep = 4;
+            }
+        }
+    };
+    auto stage_load = [&](int m) { sv = ssrc[(size_t)m * sstep]; };
+    auto stage_store = [&](int m) {
+        if (sdst >= 0) *reinterpret_cast<u4v_t*>(&lds[(m & 1) * kFuTS + sdst]) = sv;
+    };
+    build_map(load_row(blockIdx.x));
+    stage_load(0);
+
+    // one 16-row x 256-weight step: Q4_K decode + MFMA against the operand
+    // rows at st (row stride rs uint4), accumulated into acc
+    auto compute = [&](const uint4* st, const WRaw& cur, f4_t& acc) {
+        const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+        Q4kScale S;
+        q4k_scales(cur.h, g, ssel, S);
+        f4_t D = zf;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const h8_t b = q4k_bop(Dw[c], S, magic);
+            const h8_t a = __builtin_bit_cast(h8_t, st[8 * g + c]);
+            D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, D, 0, 0, 0);
+        }
+        const h8_t am = __builtin_bit_cast(h8_t, st[32 + g]);
+        const f4_t Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, S.m, zf, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[i] = fmaf(S.d, D[i], acc[i]);
+            acc[i] = fmaf(-S.dmin, Dm[i], acc[i]);
+        }
+    };
+    const int rsel = r & (kFuT - 1);  // MFMA rows 8..15 (discarded) read rows 0..7
+
+    int opb_slot = -1;  // slot whose down operand opb holds
+    int claimed = 0;    // thread 0: the item its last claim returned
+    for (int t = blockIdx.x, tn = total; t < total; t = tn) {
+        const bool dn = t >= ngu;
+#ifdef FST_TRACE
+        if (trc && tid == 0 && trn + 1 < kTraceSlots) {
+            trc[trn] = dn ? -wall_clock64() : wall_clock64();  // negative: a down item
+            trn += 2;
+        }
+#endif
+        __syncthreads();  // the previous item's readers of the LDS are done
+        const int nsb = dn ? nsb_dn : nsb_gu;
+        int slot = t / tiles_gu, tile = t - slot * tiles_gu;
+        if (dn) dn_map(t - ngu, slot, tile);
+        const int Me = min(r_sM[slot], kFuT), off = r_soff[slot];
+        // the item that follows: the second half of this down pair, or claimed
+        const bool pair1 = dyn && dn && t - ngu < D1 && ((t - ngu) & 1) == 0;
+        const bool claims = dyn && !pair1;
+        if (claims && dn && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
+        __amdgpu_buffer_rsrc_t nrs = wrs;
+        int ar_next = -1;
+        stage_store(0);
+        f4_t acc = zf;
+        if (!dn) {
+            __syncthreads();
+        } else {
+            // ---- the slot's down operand, built in LDS from the h words
+            // unless the previous item built it for the same slot.
+            // Each polling round issues the maxima loads (Me*aw words) and the
+            // first pass of h loads together, so a slot of one or two tokens
+            // (most routed slots) costs one round trip when its words are in.
+            int timed_out = 0;
+            const bool stage_op = slot != opb_slot;
+            opb_slot = slot;
+            constexpr int cpr = inter / 8;  // operand chunks per row
+            const int nwd = Me * aw;        // maxima words of the slot's rows
+            const int nch = Me * cpr;       // operand chunks of the slot's rows
+            for (int spin = 0; stage_op; ++spin) {
+                int ok = 1;
+                unsigned long long mv[2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {  // kFuT * aw <= 2 * NT
+                    const int i = k * NT + tid;
+                    const int ii = i < nwd ? i : 0;
+                    mv[k] = ld_coherent_u64(fa.amaxw + (size_t)(off + ii / aw) * aw + (ii - (ii / aw) * aw));
+                }
+                for (int base = 0; base < nch; base += NT) {
+                    const int qq = base + tid;
+                    const bool live = qq < nch;
+                    const int tl = live ? qq / cpr : 0, q = qq - (qq / cpr) * cpr;
+                    const int sb = q >> 5, gg = (q >> 3) & 3, c = q & 7;
+                    const int e0 = sb * 256 + 64 * gg + 4 * c;
+                    const int rowb = ((off + tl) * inter + e0) * 8;
+                    const u4v_t lo0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb, 0, 16);
+                    const u4v_t lo1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16, 0, 16);
+                    const u4v_t hi0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 256, 0, 16);
+                    const u4v_t hi1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 272, 0, 16);
+                    if (base == 0) {
+                        // the row maxima -> prescale exponents (the 64 words of a
+                        // wave belong to one row: aw is a multiple of 64)
+#pragma unroll
+                        for (int k = 0; k < 2; ++k) {
+                            const int i = k * NT + tid;
+                            float m = 0.0f;
+                            if (i < nwd) {
+                                if ((uint32_t)(mv[k] >> 32) != epoch)
+                                    ok = 0;
+                                else
+                                    m = fst_bits_f32((uint32_t)mv[k]);
+                            }
+                            m = wave_fmax(m);
+                            if (lane == 0 && i < nwd) s_amax[i / aw][(i - (i / aw) * aw) >> 6] = m;
+                        }
+                        __syncthreads();
+                        if (tid < Me) {
+                            float a = s_amax[tid][0];
+                            if (aw > 64) a = fmaxf(a, s_amax[tid][1]);
+                            s_xs2[tid] = prescale_exp(a);
+                        }
+                        __syncthreads();
+                    }
+                    // words {h bits, epoch}: .y / .w hold the tags
+                    if (live && (lo0.y != epoch || lo0.w != epoch || lo1.y != epoch || lo1.w != epoch ||
+                                 hi0.y != epoch || hi0.w != epoch || hi1.y != epoch || hi1.w != epoch))
+                        ok = 0;
+                    const int s = s_xs2[tl];
+                    h8_t v;
+                    v[0] = (_Float16)ldexpf(fst_bits_f32(lo0.x), -s);
+                    v[1] = (_Float16)ldexpf(fst_bits_f32(lo1.x), -s);
+                    v[2] = (_Float16)ldexpf(fst_bits_f32(lo0.z), -s);
+                    v[3] = (_Float16)ldexpf(fst_bits_f32(lo1.z), -s);
+                    v[4] = (_Float16)ldexpf(fst_bits_f32(hi0.x), -s);
+                    v[5] = (_Float16)ldexpf(fst_bits_f32(hi1.x), -s);
+                    v[6] = (_Float16)ldexpf(fst_bits_f32(hi0.z), -s);
+                    v[7] = (_Float16)ldexpf(fst_bits_f32(hi1.z), -s);
+                    if (live) opb[tl * kFuOpStride + sb * 36 + (q & 31)] = __builtin_bit_cast(uint4, v);
+                    float s0 = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+                    float s1 = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
+                    s0 = s0 + fdpp<0xb1>(s0);  // quad_perm [1,0,3,2]
+                    s1 = s1 + fdpp<0xb1>(s1);
+                    s0 = s0 + fdpp<0x4e>(s0);  // quad_perm [2,3,0,1]
+                    s1 = s1 + fdpp<0x4e>(s1);
+                    s0 = s0 + fdpp<0x104>(s0);  // row_shl 4
+                    s1 = s1 + fdpp<0x104>(s1);
+                    if (live && c == 0) {
+                        const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
+                        const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
+                        const _Float16 z = (_Float16)0.0f;
+                        opb[tl * kFuOpStride + sb * 36 + 32 + gg] =
+                            __builtin_bit_cast(uint4, h8_t{h0, h1, l0, l1, z, z, z, z});
+                    }
+                }
+                if (__syncthreads_and(ok)) break;
+                if (spin >= fa.spin_limit) {
+                    timed_out = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (timed_out && tid == 0) atomicOr(&ra.meta[kMetaTimeout], 1);
+            __syncthreads();
+#ifdef FST_TRACE
+            if (trc && tid == 0 && trn - 1 < kTraceSlots) trc[trn - 1] = wall_clock64();  // operand ready
+#endif
+        }
+        // One super-block loop for both kinds (one copy of the loop keeps the
+        // register budget of the gate||up path), U = 2 per iteration: weight
+        // ring slot j, the staging of the next super-block (gate||up: from
+        // the stage ring, the next item's first at the last one; down: a
+        // dummy reload until the last, where the next item's first stage is
+        // loaded), one barrier per super-block for gate||up only (down reads
+        // its whole operand from opb).
+        const uint4* opr = dn ? opb + rsel * kFuOpStride : lds + rsel * kTokStride;
+        for (int sb0 = 0; sb0 < nsb; sb0 += 2) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int sb = sb0 + j;
+                const bool last = sb + 1 >= nsb;
+                if (last) {
+                    // the next item (published three super-blocks earlier)
+                    tn = pair1 ? t + 1 : (dyn ? s_claim : t + G);
+                    tn = tn < total ? tn : total;
+                    if (tn < total) nrs = item_rsrc(tn);
+                    ar_next = load_row(tn < total ? tn : t);
+                    build_map(ar_next);
+                }
+                stage_load(last || dn ? 0 : sb + 1);
+                const int pf = sb + 1;
+                const bool pnx = pf >= nsb;
+                w[(j + 1) & 1] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * kFuChunk);
+                // gate||up items claim their successor four super-blocks
+                // before the end (issued after this step's loads, so only the
+                // publication one step later waits for it)
+                if (claims && !dn && sb == nsb - 4 && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
+                __builtin_amdgcn_sched_barrier(0);
+                compute(opr + (dn ? sb * 36 : (sb & 1) * kFuTS), w[j], acc);
+                if (sb == nsb - 3 && tid == 0) s_claim = claimed;
+                if (!dn) {
+                    if (!last) stage_store(sb + 1);
+                    __syncthreads();
+                } else if (sb == nsb - 3) {
+                    __syncthreads();  // publishes s_claim
+                }
+            }
+        }
+        wrs = nrs;
+
+        // D layout: lane holds token rows 4g+i (i = 0..3), column r
+        if (!dn) {
+            // gate waves hand their rows to the up waves through LDS (the
+            // staging ring is free: the loop ended on a barrier)
+            float* xg = reinterpret_cast<float*>(lds);
+            if (wave < kFuHalf) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tl = 4 * g + i;
+                    xg[(wave * 4 + i) * 64 + lane] = tl < Me ? ldexpf(acc[i], fa.xs[r_ptok[off + tl]]) : 0.0f;
+                }
+            }
+            __syncthreads();
+            if (wave >= kFuHalf) {
+                const int n = (tile * kFuHalf + wave - kFuHalf) * 16 + r;
+                const float lim = fa.swiglu_limit;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tl = 4 * g + i;
+                    float m = 0.0f;
+                    if (tl < Me) {
+                        float gv = xg[((wave - kFuHalf) * 4 + i) * 64 + lane];
+                        float uv = ldexpf(acc[i], fa.xs[r_ptok[off + tl]]);
+                        if (lim > 0.0f) {
+                            gv = fminf(gv, lim);
+                            uv = fminf(fmaxf(uv, -lim), lim);
+                        }
+                        const float hv = (gv / (1.0f + expf(-gv))) * uv;
+                        st_coherent_u64(fa.hbuf + (size_t)(off + tl) * inter + n,
+                                        ((unsigned long long)epoch << 32) | fst_f32_bits(hv));
+                        m = fabsf(hv);
+                    }
+                    m = row16_fmax(m);  // the 16 rows of this wave
+                    if (r == 0 && tl < Me)
+                        st_coherent_u64(fa.amaxw + (size_t)(off + tl) * aw + (n >> 4),
+                                        ((unsigned long long)epoch << 32) | fst_f32_bits(m));
+                }
+            }
+        } else {
+            const int row = (tile * kFuW + wave) * 16 + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tl = 4 * g + i;
+                if (tl < Me) fa.y[(size_t)(off + tl) * hd + row] = ldexpf(acc[i], s_xs2[tl]);
+            }
+        }
+    }
+#ifdef FST_TRACE
+    if (trc && tid == 0) trc[0] = wall_clock64();  // exit
+#endif
+}
+
+int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
+                     const RouteReq& rq, uint32_t epoch, int spin_limit) {
+    const RouteArgs ra = route_args(g, L, M, s.logits, rq.input_ids, rq.use_hash, rq.use_shared, rq.eids, rq.wts, s);
+    FusedArgs fa{};
+    fa.bank = L.bank;
+    fa.expert_stride = L.expert_stride;
+    fa.A = s.x16p;
+    fa.SX = s.sxp;
+    fa.xs = s.xs;
+    fa.hbuf = s.hbuf;
+    fa.amaxw = s.amaxw;
+    fa.hbuf_bytes = (size_t)s.max_pairs * g.inter * 8;
+    fa.y = s.y;
+    static const bool no_claim = getenv("FST_FUSED_STATIC") != nullptr;  // A/B switch for measurements
+    fa.claim = no_claim ? nullptr : s.fused_claim;
+    fa.swiglu_limit = g.swiglu_limit;
+    fa.epoch = epoch;
+    fa.spin_limit = spin_limit;
+    // two workgroups per CU, all resident at once (the down items' waits
+    // rely on it; the kernel's VGPR and LDS budget allows two per CU)
+    const unsigned items = (unsigned)s.max_slots * (unsigned)(g.inter / 64 + g.hd / 128);
+    const dim3 grid(std::min(items, (unsigned)s.n_cu * 2u));
+    if (g.hd == 4096 && g.inter == 2048)
+        hipLaunchKernelGGL((moe_fused_kernel<4096, 2048>), grid, dim3(64 * kFuW), 0, st, fa, ra);
+    else
+        return set_error(1, "fused MoE launch: geometry without an instantiation");
+    return 0;
+}
+
+bool moe_fused_supported(const Geometry& g, int M) {
+    // instantiated for the DeepSeek-V4-Flash-like expert (4096 -> 2048 -> 4096)
+    return g.codec == 0 && M <= kFuT && g.E <= kFusedRouteMaxExperts && g.hd == 4096 && g.inter == 2048;
 }
 
 // Token capacity of the launch (the call's M bounds every slot's M_e): 8, 16,
@@ -1575,6 +2131,7 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
                               const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep,
                               const RouteArgs& ra = RouteArgs{}) {
+
     const int W = linear_waves(M, N);
     // persistent grid: FST_Q4K_WG_PER_CU workgroups per CU at most
     const unsigned items = slots * (unsigned)(N / (16 * W)) * (unsigned)(MODE == 1 ? std::max(ep.ksplit, 1) : 1);
@@ -1699,6 +2256,12 @@ void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, con
     launch_q4k_linear<0>(st, M, 1u, W, 0, 0, K, N, t, nullptr, s.x16p, s.sxp, s.xs, out, EpiArgs{});
 }
 
+#ifdef FST_TRACE
+int trace_read(void* host, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes < sizeof(g_trace) ? bytes : sizeof(g_trace));
+}
+#endif
+
 // ------------------------------------------------------------------ combine
 
 // src/fst_engine.cpp:4196-4201 and :2851-2852: out = bf16(sum_j w[t][j] y[pair(t,j)]
@@ -1720,13 +2283,15 @@ __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int
     const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (t >= M || n >= hd) return;
     // every load issued before the sums (slots past tk or without a pair
-    // read row 0 of y and are not summed)
+    // read row 0 of y and are not summed; with tk = 0, a shared-only call,
+    // no routing entry is read at all)
     int p[TK];
     float w[TK];
 #pragma unroll
     for (int j = 0; j < TK; ++j) {
-        p[j] = pair_of[t * tk + min(j, tk - 1)];
-        w[j] = wts[t * tk + min(j, tk - 1)];
+        const int jj = t * tk + max(min(j, tk - 1), 0);
+        p[j] = tk > 0 ? pair_of[jj] : -1;
+        w[j] = tk > 0 ? wts[jj] : 0.0f;
     }
     float4 v[TK];
 #pragma unroll

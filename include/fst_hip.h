@@ -155,7 +155,13 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
  * wait that gives up writes n_acc[s] = -1 and tokens -1 for its sequence
  * (the host-pointer entry points then return FST_EHIP); after an asynchronous
  * *_dev call, fst_accept_check on the copied-back n_acc does the same. */
-int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default */
+int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default; also bounds the fused MoE launch's waits */
+/* Router-driven MoE calls (fst_moe_layer[_dev], the verify forward) of at
+ * most 8 tokens run gate||up and down as one persistent launch (default);
+ * on = 0 selects the separate launch chain.  Both give bit-identical
+ * results.  A fused launch whose hand-off wait exceeds the spin limit makes
+ * the host-pointer entry points return FST_EHIP. */
+int fst_set_fused(fst_ctx* ctx, int on);
 int fst_accept_check(const int32_t* n_acc, int n_seq);  /* host memory; FST_EHIP if any n_acc < 0 */
 /* fst_accept_greedy_dev without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under

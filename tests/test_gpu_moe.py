@@ -100,6 +100,33 @@ def test_repeated_calls_changing_M(fa, oracle, c2_layer):
             assert rel_l2(bf16_to_f32(out), ref) < TOL
 
 
+@pytest.mark.parametrize("M", [1, 2, 5, 8])
+def test_fused_launch_matches_launch_chain(fa, c2_layer, M):
+    """The fused gate||up + down launch (router-driven calls of at most 8
+    tokens) gives the same bits as the separate launch chain: same routing,
+    same fp16 operands (the down operand built in LDS from the epoch-tagged h
+    words), same MFMA order.  Several batches in a row, so the epoch tags of
+    one call must not leak into the next.  (At M = 1 the chain splits the
+    gate||up sums over K, a different order: there the two agree within the
+    FFN tolerance.)"""
+    ctx, seed, _ = c2_layer
+    try:
+        for b in range(3):
+            note("fused vs chain M=%d batch %d" % (M, b))
+            h = fa.synth_normal_bf16(seed, 8000 + 10 * M + b, (M, HD))
+            ctx.set_fused(True)
+            out_f, e_f, w_f = ctx.moe_layer(0, h)
+            ctx.set_fused(False)
+            out_c, e_c, w_c = ctx.moe_layer(0, h)
+            assert np.array_equal(e_f, e_c) and np.array_equal(w_f.view(np.uint32), w_c.view(np.uint32))
+            if M == 1:
+                assert rel_l2(bf16_to_f32(out_f), bf16_to_f32(out_c)) < 2e-3
+            else:
+                assert np.array_equal(out_f, out_c)
+    finally:
+        ctx.set_fused(True)
+
+
 def test_dev_entry_points_routed_and_shared_outputs(fa, oracle, c2_layer):
     ctx, seed, w = c2_layer
     L = fa.lib()
