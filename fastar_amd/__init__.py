@@ -78,6 +78,7 @@ _SIGS = {
     "fst_accept_stochastic_dev": (C.c_int, [P, P, P, C.c_int, C.c_int, C.c_int, P, C.c_float, U64, U64, P, P]),
     "fst_set_wait_limit": (C.c_int, [P, C.c_int]),
     "fst_set_fused": (C.c_int, [P, C.c_int]),
+    "fst_set_small_m": (C.c_int, [P, C.c_int]),
     "fst_final_head": (C.c_int, [P, P, C.c_int, P]),
     "fst_sample_token": (C.c_int, [P, P, C.c_int, C.c_float, C.c_float, U64, U64, P]),
     "fst_sample_token_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_float, C.c_float, U64, U64, P]),
@@ -333,6 +334,9 @@ class Context:
 
     def set_fused(self, on):
         _check(lib().fst_set_fused(self.h, 1 if on else 0))
+
+    def set_small_m(self, on):
+        _check(lib().fst_set_small_m(self.h, 1 if on else 0))
 
     def final_head(self, hs):
         """apply_final_norm_and_lm_head: hs [M][4][hidden] with the HC head

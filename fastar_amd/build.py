@@ -13,7 +13,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libfst_hip.so")
 
-SOURCES = ["fst_moe.hip", "fst_accept.hip", "fst_hc.hip", "fst_dense.hip", "fst_synth_dev.hip", "fst_api.cpp", "fst_bank.cpp", "fst_layout.cpp", "fst_synth.cpp"]
+SOURCES = ["fst_moe.hip", "fst_gemv.hip", "fst_accept.hip", "fst_hc.hip", "fst_dense.hip", "fst_synth_dev.hip", "fst_api.cpp", "fst_bank.cpp", "fst_layout.cpp", "fst_synth.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

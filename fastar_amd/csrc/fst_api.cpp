@@ -75,6 +75,7 @@ struct fst_ctx {
     fst::Scratch s{};
     uint32_t fused_epoch = 0;                // fused MoE launches issued (tags of their h words)
     bool fused = true;                       // use the fused launch where it applies
+    bool gemv = true;                        // use the small-M launch where it applies
     std::vector<void*> allocs;
     std::vector<uint8_t> staging;            // host repack buffer for expert uploads
     // acceptance staging (grown on demand)
@@ -241,6 +242,7 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     x->cfg = c;
     x->max_grid_y = prop.maxGridSize[1] > 0 ? prop.maxGridSize[1] : 65535;
     x->fused = getenv("FST_NO_FUSED") == nullptr;  // A/B switch for measurements (fst_set_fused at run time)
+    x->gemv = getenv("FST_NO_GEMV") == nullptr;    // likewise (fst_set_small_m)
     int rc = FST_OK;
     auto bail = [&](int code) {
         delete x;
@@ -302,13 +304,15 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.sx2p, (size_t)P * (inter / 256) * 4)) || (rc = x->dalloc(&s.xs2, P)) ||
         (rc = x->dalloc(&s.y, (size_t)P * hd)) ||
         (rc = x->dalloc(&s.sh_h16, (size_t)T * c.inter_dim)) || (rc = x->dalloc(&s.ys, (size_t)T * hd)) ||
-        (rc = x->dalloc(&s.hbuf, (size_t)P * inter)) ||
-        (rc = x->dalloc(&s.amaxw, (size_t)P * (inter / 16))) || (rc = x->dalloc(&s.fused_claim, 64)))
+        (rc = x->dalloc(&s.hbuf, (size_t)2 * P * inter)) ||
+        (rc = x->dalloc(&s.amaxw, (size_t)P * (inter / 16))) || (rc = x->dalloc(&s.fused_claim, 64)) ||
+        (rc = x->dalloc(&s.gemv_cnt, hd / 16 + 1)))
         return bail(rc);
-    if (hipMemsetAsync(s.hbuf, 0, sizeof(unsigned long long) * (size_t)P * inter, x->st) != hipSuccess ||
+    if (hipMemsetAsync(s.hbuf, 0, sizeof(unsigned long long) * (size_t)2 * P * inter, x->st) != hipSuccess ||
         hipMemsetAsync(s.amaxw, 0, sizeof(unsigned long long) * (size_t)P * (inter / 16), x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(hand-off words) failed"));
-    if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess)
+    if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess ||
+        hipMemsetAsync(s.gemv_cnt, 0, sizeof(int) * (hd / 16 + 1), x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));
     x->ev.resize(17);
     x->ev_names.assign(17, "");
@@ -551,6 +555,16 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
             FST_HIP_TRY(hipGetLastError());
             return FST_OK;
         }
+    }
+    if (!do_router && !mx && !sh16 && ctx->gemv && fst::gemv_supported(g, M, g.tk, use_shared, ctx->s)) {
+        // at one or two tokens: one launch from the caller's routing to the
+        // combined rows (VALU dot products; every workgroup finds the slots)
+        ctx->fused_epoch = ctx->fused_epoch == 0xffffffffu ? 1u : ctx->fused_epoch + 1u;
+        fst::launch_expert_gemv(st, g, L, M, g.tk, d_eids, d_wts, use_shared, d_h, ctx->s, ctx->fused_epoch,
+                                ctx->spin_limit, d_out, d_out_routed, d_out_shared);
+        ctx->mark("expert_gemv");
+        FST_HIP_TRY(hipGetLastError());
+        return FST_OK;
     }
     // one routed pair per token and no shared expert: the down launch writes
     // the bf16 result itself (the combine of one term), no combine launch
@@ -806,6 +820,12 @@ int fst_set_fused(fst_ctx* ctx, int on) {
     return FST_OK;
 }
 
+int fst_set_small_m(fst_ctx* ctx, int on) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    ctx->gemv = on != 0;
+    return FST_OK;
+}
+
 int fst_set_wait_limit(fst_ctx* ctx, int spins) {
     if (!ctx) return fail(FST_EINVAL, "null context");
     if (spins < 0) return fail(FST_EINVAL, "spins must be >= 0");
@@ -882,9 +902,10 @@ int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_
 
 #ifdef FST_TRACE
 extern "C++" {
-namespace fst { int trace_read(void* host, size_t bytes); }
+namespace fst { int trace_read(void* host, size_t bytes); int gemv_trace_read(void* host, size_t bytes); }
 }
 int fst_debug_trace(void* host, size_t bytes) { return fst::trace_read(host, bytes); }
+int fst_debug_trace_gemv(void* host, size_t bytes) { return fst::gemv_trace_read(host, bytes); }
 #endif
 
 // ------------------------------------------------------------ sample_token

@@ -62,9 +62,10 @@ struct Scratch {
     float* ys;             // [T][hd] fp32 shared-expert output (bf16 shared expert)
     // fused gate||up + down launch: {epoch, value} words handed between
     // workgroups (h rows and their per-16-row maxima)
-    unsigned long long* hbuf;   // [P][inter]
+    unsigned long long* hbuf;   // [2][P][inter] (the small-M launch uses both halves)
     unsigned long long* amaxw;  // [P][inter/16]
     int* fused_claim;           // down-pair counter of the fused launch (zeroed by the router launch)
+    int* gemv_cnt;              // [hd/16] arrival counters of the small-M launch (zero between calls)
 };
 
 // Device expert bank: n_layers x (n_experts + 1) packed experts.
@@ -323,6 +324,12 @@ void launch_prep_act_split(hipStream_t st, const float* part, int S, int rows, f
 // with topk = 0; y rows go to s.y for launch_combine.  epoch: a new nonzero
 // value per call (tags the h words); spin_limit bounds each hand-off wait.
 bool moe_fused_supported(const Geometry& g, int M);
+// Small-M expert FFN with caller-given routing (M <= 2, Q4_K): one launch
+// from the eids to the combined bf16 rows.
+bool gemv_supported(const Geometry& g, int M, int tk, int use_shared, const Scratch& s);
+int launch_expert_gemv(hipStream_t st, const Geometry& g, const LayerView& L, int M, int tk, const int32_t* eids,
+                       const float* wts, int use_shared, const uint16_t* h, const Scratch& s, uint32_t epoch,
+                       int spin_limit, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
                      const RouteReq& rq, uint32_t epoch, int spin_limit);
 // With o1/o2 (one routed pair per token, no shared expert) it writes

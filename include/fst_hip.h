@@ -162,6 +162,12 @@ int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default; also bounds
  * results.  A fused launch whose hand-off wait exceeds the spin limit makes
  * the host-pointer entry points return FST_EHIP. */
 int fst_set_fused(fst_ctx* ctx, int on);
+/* Caller-routed calls (fst_moe_ffn_dev, fst_expert_ffn, fst_shared_expert) of
+ * one or two tokens over Q4_K experts (hidden and intermediate sizes <= 4096)
+ * run as one launch with fp32 VALU dot products (default); on = 0 selects the
+ * MFMA launch chain.  The two agree to fp32 rounding, not bit for bit.  Its
+ * hand-off wait is bounded like the fused launch's. */
+int fst_set_small_m(fst_ctx* ctx, int on);
 int fst_accept_check(const int32_t* n_acc, int n_seq);  /* host memory; FST_EHIP if any n_acc < 0 */
 /* fst_accept_greedy_dev without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
