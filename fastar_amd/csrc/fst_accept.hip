@@ -36,6 +36,7 @@ struct AccWs {
     unsigned long long* part_res;  // [n_seq][kChunks][2] (u128 as lo, hi)
     unsigned long long* dec;       // [n_seq][8]
     unsigned long long* gslot;     // [R][kChunks] greedy chunk partials (zero between calls)
+    unsigned long long* tail;      // acc_tail_kernel: chunk sums and counters (counters zero between calls)
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -49,7 +50,8 @@ static AccWs carve(void* ws, int n_seq, int k) {
     w.part_sum = (unsigned long long*)p; p += align256(8ull * R * kChunks);
     w.part_res = (unsigned long long*)p; p += align256(16ull * n_seq * kChunks);
     w.dec = (unsigned long long*)p; p += align256(64ull * n_seq);
-    w.gslot = (unsigned long long*)p;
+    w.gslot = (unsigned long long*)p; p += align256(8ull * R * kChunks);
+    w.tail = (unsigned long long*)p;
     return w;
 }
 
@@ -58,7 +60,7 @@ size_t accept_ws_bytes(int n_seq, int k, int V) {
     const int R = n_seq * (k + 1) + n_seq * k;
     return align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
            align256(8ull * R * kChunks) + align256(16ull * n_seq * kChunks) + align256(64ull * n_seq) +
-           align256(8ull * R * kChunks) + 256;
+           align256(8ull * R * kChunks) + align256(8ull * ((size_t)n_seq * 256 * 3 + n_seq)) + 256;
 }
 
 // Calls f(x, v) for v = v0, v0 + stride, ... < v1 in that order, with the
@@ -727,10 +729,272 @@ void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k,
 #undef FST_GK
 }
 
+
+// ------------------------------- rejection sampling: decide, residual, pick
+//
+// The last three steps of the chain in one launch.  Workgroup (c, s) of
+// kTailChunks chunks per sequence:
+//   - loads chunk c of every row of sequence s, the draft tokens' logits and
+//     the row partials of the maxima and sums launches, all at once;
+//   - takes the accept decisions (every workgroup alike, as acc_decide_kernel);
+//   - sums the residual of its chunk (and the target row's E, for the case
+//     of an identically zero residual), writes the sums with device-coherent
+//     stores and counts itself in with one atomic per workgroup;
+//   - the last workgroup of the sequence to arrive (the counter is left at
+//     zero) scans the chunk sums, loads the chosen chunk and picks the token
+//     (as acc_sample_kernel), then writes n_acc and the tokens.
+// No workgroup waits for another, so any grid size is safe.  The arithmetic
+// is the chain's, and the results are identical to it and to the CPU oracle.
+#ifdef FST_TRACE
+__device__ long long g_tail_trace[1024][8];
+#define TAIL_STAMP(i)                                                  \
+    do {                                                               \
+        if (tid == 0 && blockIdx.x < 1024) {                           \
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");           \
+            g_tail_trace[blockIdx.x][i] = wall_clock64();              \
+        }                                                              \
+    } while (0)
+#else
+#define TAIL_STAMP(i) \
+    do {              \
+    } while (0)
+#endif
+constexpr int kTailThreads = 512;
+constexpr int kTailChunks = 256;
+constexpr int kTailRows = 17;  // 2k + 1, k <= 8
+constexpr int kTailPer = 2;    // chunk length <= 1024
+constexpr int kTailWaves = kTailThreads / 64;
+
+// [n_seq][kTailChunks][3] chunk sums (residual lo, hi; target E), [n_seq] counters.
+static size_t tail_words(int n_seq) { return (size_t)n_seq * kTailChunks * 3 + (size_t)n_seq; }
+
+__global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
+    const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V, float inv_t,
+    const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base, const float* __restrict__ part_max,
+    const int* __restrict__ part_idx, const unsigned long long* __restrict__ part_sum,
+    unsigned long long* __restrict__ tw, int32_t* __restrict__ n_acc, int32_t* __restrict__ tokens) {
+    const int c = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n_tgt = n_seq * (k + 1), NR = 2 * k + 1;
+    const int clen = (V + kTailChunks - 1) / kTailChunks, b0 = min(V, c * clen), b1 = min(V, b0 + clen);
+    unsigned long long* cw = tw + (size_t)s * kTailChunks * 3;  // this sequence's chunk sums
+    int* cnt = reinterpret_cast<int*>(tw + (size_t)n_seq * kTailChunks * 3) + s;
+    auto grow = [&](int rr) { return rr <= k ? s * (k + 1) + rr : n_tgt + s * k + (rr - k - 1); };
+    auto rowp = [&](int rr) {
+        return rr <= k ? target + (size_t)(s * (k + 1) + rr) * V : draftl + (size_t)(s * k + rr - k - 1) * V;
+    };
+    __shared__ float s_M[kTailRows];
+    __shared__ int s_any[kTailRows];
+    __shared__ unsigned long long s_S[kTailRows];
+    __shared__ int s_n, s_last, s_chunk, s_owner, s_tok, s_mode;
+    __shared__ u128 s_wtot[kTailWaves], s_rem;
+    __shared__ u128 s_rc[kTailChunks];
+    __shared__ unsigned long long s_ce[kTailChunks];
+
+    TAIL_STAMP(0);
+    // ---- loads: the chunk of every row, the draft tokens' logits
+    float xv[kTailRows][kTailPer];
+#pragma unroll
+    for (int rr = 0; rr < kTailRows; ++rr)
+#pragma unroll
+        for (int u = 0; u < kTailPer; ++u) {
+            const int v = b0 + tid + u * kTailThreads;
+            xv[rr][u] = (rr < NR && v < b1) ? rowp(rr)[v] : __builtin_nanf("");
+        }
+    float xp = 0.0f, xq = 0.0f;
+    int xok = 0;
+    if (wave == 0 && lane < k) {
+        const int x = draft[s * k + lane];
+        if (x >= 0 && x < V) {
+            xok = 1;
+            xp = rowp(lane)[x];
+            xq = rowp(k + 1 + lane)[x];
+        }
+    }
+    // ---- row maxima and sums from the 64 chunk partials (wave w: rows w, w + 8, ...)
+    for (int rr = wave; rr < NR; rr += kTailWaves) {
+        float mx;
+        int any;
+        wave_row_max_any(part_max, part_idx, grow(rr), &mx, &any);
+        const unsigned long long S = wave_sum_u64(part_sum[(size_t)grow(rr) * kChunks + lane]);
+        if (lane == 0) {
+            s_M[rr] = mx;
+            s_any[rr] = any;
+            s_S[rr] = S;
+        }
+    }
+    __syncthreads();
+    TAIL_STAMP(1);
+    // ---- the decisions (acc_decide_kernel's): lane i < k decides position i
+    if (wave == 0) {
+        int ok = 0;
+        if (lane < k && xok) {
+            const int rt = lane, rd = k + 1 + lane;
+            const unsigned long long P = fixed_prob(xp, inv_t, s_M[rt], s_any[rt]);
+            const unsigned long long Q = fixed_prob(xq, inv_t, s_M[rd], s_any[rd]);
+            const uint32_t U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 0);
+            const u128 lhs = (u128)U * (u128)Q * (u128)s_S[rt];
+            const u128 rhs = ((u128)P * (u128)s_S[rd]) << 24;
+            ok = lhs < rhs;
+        }
+        const unsigned long long rej = __ballot(lane < k && !ok);
+        if (lane == 0) s_n = rej ? __ffsll((long long)rej) - 1 : k;
+    }
+    __syncthreads();
+    const int n = s_n, mode0 = n < k ? 0 : 1, tr = n, dr = min(k + 1 + n, NR - 1);
+    const unsigned long long Sp = s_S[tr], Sq = mode0 == 0 ? s_S[dr] : 0ull;
+    const float mp = s_M[tr], mq = mode0 == 0 ? s_M[dr] : 0.0f;
+    const int ap = s_any[tr], aq = mode0 == 0 ? s_any[dr] : 0;
+    // this thread's values of the sampling rows (uniform branches: no
+    // dynamic register indexing)
+    float xt[kTailPer], xd[kTailPer];
+#pragma unroll
+    for (int u = 0; u < kTailPer; ++u) xt[u] = xd[u] = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < kTailRows; ++rr)
+#pragma unroll
+        for (int u = 0; u < kTailPer; ++u) {
+            if (rr == tr) xt[u] = xv[rr][u];
+            if (mode0 == 0 && rr == dr) xd[u] = xv[rr][u];
+        }
+    // ---- the chunk's residual and target-E sums (exact, any order)
+    u128 ra = 0;
+    unsigned long long ea = 0;
+#pragma unroll
+    for (int u = 0; u < kTailPer; ++u) {
+        ra += res_of(xt[u], xd[u], inv_t, mp, ap, mq, aq, Sp, Sq, mode0);
+        ea += fixed_prob(xt[u], inv_t, mp, ap);
+    }
+    ra = wave_sum_u128(ra);
+    ea = wave_sum_u64(ea);
+    __shared__ unsigned long long s_ew[kTailWaves];
+    if (lane == 0) {
+        s_wtot[wave] = ra;
+        s_ew[wave] = ea;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        u128 rt = 0;
+        unsigned long long et = 0;
+        for (int w = 0; w < kTailWaves; ++w) {
+            rt += s_wtot[w];
+            et += s_ew[w];
+        }
+        st_coherent_u64(cw + (size_t)c * 3, (unsigned long long)rt);
+        st_coherent_u64(cw + (size_t)c * 3 + 1, (unsigned long long)(rt >> 64));
+        st_coherent_u64(cw + (size_t)c * 3 + 2, et);
+        publish_wait();
+        TAIL_STAMP(2);
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == kTailChunks - 1;
+        if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    TAIL_STAMP(3);
+    if (!s_last) return;
+
+    // ---- the last workgroup: the chunk holding the inverse-CDF target
+    for (int i = tid; i < kTailChunks; i += kTailThreads) {
+        const unsigned long long lo = ld_coherent_u64(cw + (size_t)i * 3), hi = ld_coherent_u64(cw + (size_t)i * 3 + 1);
+        s_rc[i] = ((u128)hi << 64) | (u128)lo;
+        s_ce[i] = ld_coherent_u64(cw + (size_t)i * 3 + 2);
+    }
+    __syncthreads();
+    TAIL_STAMP(4);
+    if (wave == 0) {
+        const uint32_t U2 = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)n, 1);
+        u128 tot = 0;
+        for (int g = 0; g < kTailChunks; g += 64) tot += wave_sum_u128(s_rc[g + lane]);
+        int mode = mode0;
+        if (mode == 0 && tot == 0) {
+            // the residual is identically zero: sample from the target row
+            mode = 1;
+            tot = 0;
+            for (int g = 0; g < kTailChunks; g += 64) tot += wave_sum_u128((u128)s_ce[g + lane]);
+        }
+        int chunk = -1;
+        u128 rem = 0;
+        if (tot != 0) {
+            const u128 tg = ((u128)U2 * tot) >> 24;
+            u128 run = 0;
+            for (int g = 0; g < kTailChunks && chunk < 0; g += 64) {
+                const u128 cs = mode == mode0 ? s_rc[g + lane] : (u128)s_ce[g + lane];
+                const u128 pre = wave_incl_scan_u128(cs) + run;
+                const unsigned long long hit = __ballot(pre > tg);
+                if (hit) {
+                    const int ln = __ffsll((long long)hit) - 1;
+                    chunk = g + ln;
+                    rem = tg - (shfl_u128(pre, ln) - shfl_u128(cs, ln));
+                }
+                run = shfl_u128(pre, 63);
+            }
+        }
+        if (lane == 0) {
+            s_chunk = chunk;
+            s_rem = rem;
+            s_mode = mode;
+            s_owner = 0x7fffffff;
+            s_tok = 0;  // (as the chain: no crossing in the chunk gives token 0)
+        }
+    }
+    __syncthreads();
+    const int cc = s_chunk;
+    if (cc >= 0) {
+        // ---- the token: the first v of the chunk (order v = b0 + u*T + tid)
+        // whose inclusive prefix exceeds the remaining target
+        const int mode = s_mode;
+        const int cb0 = min(V, cc * clen), cb1 = min(V, cb0 + clen);
+        u128 rv[kTailPer];
+#pragma unroll
+        for (int u = 0; u < kTailPer; ++u) {
+            const int v = cb0 + tid + u * kTailThreads;
+            const float a = v < cb1 ? rowp(tr)[v] : __builtin_nanf("");
+            const float b = (mode == 0 && v < cb1) ? rowp(dr)[v] : 0.0f;
+            rv[u] = res_of(a, b, inv_t, mp, ap, mq, aq, Sp, Sq, mode);
+        }
+        u128 base = 0;
+#pragma unroll
+        for (int u = 0; u < kTailPer; ++u) {
+            const u128 pre = wave_incl_scan_u128(rv[u]);
+            __syncthreads();
+            if (lane == 63) s_wtot[wave] = pre;
+            __syncthreads();
+            u128 wb = base;
+            for (int w = 0; w < wave; ++w) wb += s_wtot[w];
+            const unsigned long long hit = __ballot(wb + pre > s_rem);
+            if (hit && lane == __ffsll((long long)hit) - 1) atomicMin(&s_owner, tid);
+            __syncthreads();
+            if (s_owner != 0x7fffffff) {
+                if (tid == s_owner) s_tok = cb0 + u * kTailThreads + tid;
+                break;
+            }
+            for (int w = 0; w < kTailWaves; ++w) base += s_wtot[w];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        for (int i = 0; i < n; ++i) tokens[s * (k + 1) + i] = draft[s * k + i];
+        tokens[s * (k + 1) + n] = cc >= 0 ? s_tok : 0;
+        for (int i = n + 1; i <= k; ++i) tokens[s * (k + 1) + i] = -1;
+        n_acc[s] = n;
+    }
+    TAIL_STAMP(5);
+}
+
+#ifdef FST_TRACE
+int tail_trace_read(void* host, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_tail_trace), bytes < sizeof(g_tail_trace) ? bytes : sizeof(g_tail_trace));
+}
+#endif
+
+// The tail launch applies when every row's chunk fits the registers.
+static bool tail_fits(int k, int V) {
+    return k >= 0 && 2 * k + 1 <= kTailRows && (V + kTailChunks - 1) / kTailChunks <= kTailPer * kTailThreads;
+}
+
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
                               int n_seq, int k, int V, const int32_t* draft, float inv_t,
                               uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,
-                              void* ws) {
+                              void* ws, bool tail) {
     AccWs w = carve(ws, n_seq, k);
     const int n_tgt = n_seq * (k + 1);
     const int R = n_tgt + n_seq * k;
@@ -738,6 +1002,12 @@ void launch_accept_stochastic(hipStream_t st, const float* target, const float* 
                        inv_t, w.part_max, w.part_idx);
     hipLaunchKernelGGL(acc_sums_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
                        inv_t, w.part_max, w.part_idx, w.part_sum);
+    if (tail && tail_fits(k, V)) {
+        hipLaunchKernelGGL(acc_tail_kernel, dim3(kTailChunks, n_seq), dim3(kTailThreads), 0, st, target,
+                           draft_logits, n_seq, k, V, inv_t, draft, seed, seq_base, w.part_max, w.part_idx,
+                           w.part_sum, w.tail, n_acc, tokens);
+        return;
+    }
     hipLaunchKernelGGL(acc_decide_kernel, dim3(n_seq), dim3(64 * kDecideWaves), 0, st, target, draft_logits, n_seq, k, V,
                        inv_t, draft, seed, seq_base, w.part_max, w.part_idx, w.part_sum, w.dec, n_acc,
                        tokens);

@@ -852,7 +852,7 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
     const float inv_t = 1.0f / temperature;
     ctx->mark_begin();
     fst::launch_accept_stochastic(ctx->st, d_target, d_draft_logits, n_seq, k, V, d_draft, inv_t, seed, seq_base,
-                                  d_n_acc, d_tokens, ctx->acc_ws);
+                                  d_n_acc, d_tokens, ctx->acc_ws, ctx->fused);
     ctx->mark("accept_stochastic");
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;
@@ -902,8 +902,10 @@ int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_
 
 #ifdef FST_TRACE
 extern "C++" {
-namespace fst { int trace_read(void* host, size_t bytes); int gemv_trace_read(void* host, size_t bytes); }
+namespace fst { int trace_read(void* host, size_t bytes); int gemv_trace_read(void* host, size_t bytes);
+                int tail_trace_read(void* host, size_t bytes); }
 }
+int fst_debug_trace_tail(void* host, size_t bytes) { return fst::tail_trace_read(host, bytes); }
 int fst_debug_trace(void* host, size_t bytes) { return fst::trace_read(host, bytes); }
 int fst_debug_trace_gemv(void* host, size_t bytes) { return fst::gemv_trace_read(host, bytes); }
 #endif

@@ -382,9 +382,11 @@ constexpr int kStaticGreedyRows = 2048;
 int accept_scratch_init(int device);
 void* accept_scratch_ptr(int device);
 uint32_t accept_scratch_epoch(int device);
+// Rejection sampling: row maxima and sums, then (tail, when the rows' chunks
+// fit) one launch for the decisions, residual and pick, else three.
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
                               int n_seq, int k, int V, const int32_t* draft, float inv_t,
                               uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,
-                              void* ws);
+                              void* ws, bool tail);
 
 }  // namespace fst

@@ -157,9 +157,10 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
  * *_dev call, fst_accept_check on the copied-back n_acc does the same. */
 int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default; also bounds the fused MoE launch's waits */
 /* Router-driven MoE calls (fst_moe_layer[_dev], the verify forward) of at
- * most 8 tokens run gate||up and down as one persistent launch (default);
- * on = 0 selects the separate launch chain.  Both give bit-identical
- * results.  A fused launch whose hand-off wait exceeds the spin limit makes
+ * most 8 tokens run gate||up and down as one persistent launch, and
+ * rejection sampling runs its decisions, residual sums and pick as one
+ * launch (default; k <= 8, V <= 262144); on = 0 selects the separate launch
+ * chains.  Both give bit-identical results.  A fused launch whose hand-off wait exceeds the spin limit makes
  * the host-pointer entry points return FST_EHIP. */
 int fst_set_fused(fst_ctx* ctx, int on);
 /* Caller-routed calls (fst_moe_ffn_dev, fst_expert_ffn, fst_shared_expert) of
