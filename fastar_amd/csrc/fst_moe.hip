@@ -24,6 +24,8 @@
 // Activations are prescaled per token by a power of two (exact) so the fp16
 // operand covers their range.
 #include <algorithm>
+#include <cstdlib>
+#include <type_traits>
 
 #include "fst_internal.h"
 #include "fst_q4k_dev.h"
@@ -803,10 +805,13 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
                                                          uint16_t* __restrict__ normed, _Float16* __restrict__ x16p,
                                                          uint4* __restrict__ sxp, int* __restrict__ xs,
                                                          int* __restrict__ slot_tab) {
-    __shared__ float xrow[kMaxPrepK];
+    // x in LDS with one pad word per 64 (xi): lane p's sequential pass over
+    // its contiguous chunk then reads 64 different banks at each step, not one
+    __shared__ float xrow[kMaxPrepK + kMaxPrepK / 64];
     __shared__ float nrow[kMaxPrepK];
     __shared__ float s_r;
     const int t = blockIdx.x, tid = threadIdx.x;
+    auto xi = [](int e) { return e + (e >> 6); };
     if (slot_tab && t == 0 && tid == 0) {
         slot_tab[META_N_SLOTS] = 1;
         slot_tab[META_WORDS + 0] = 0;  // slot_eid
@@ -840,7 +845,7 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
             for (int hh = 0; hh < 2; ++hh) {
                 float x = fst_bf16_to_f32((uint16_t)(hw[i] >> (16 * hh)));
                 if (y) x = fst_bf16_to_f32(fst_f32_to_bf16(x + fst_bf16_to_f32((uint16_t)(yw[i] >> (16 * hh)))));
-                xrow[8 * q + 2 * i + hh] = x;
+                xrow[xi(8 * q + 2 * i + hh)] = x;
                 o2 |= (uint32_t)fst_f32_to_bf16(x) << (16 * hh);
             }
             ow[i] = o2;
@@ -851,8 +856,9 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
     if (tid < 64) {
         const int C = d / 64;
         double a = 0.0;
+#pragma unroll 8
         for (int i = 0; i < C; ++i) {
-            const double v = (double)xrow[tid * C + i];
+            const double v = (double)xrow[xi(tid * C + i)];
             a = a + v * v;
         }
         // halving tree p[j] += p[j+off], off = 32..1: lane j < off adds
@@ -875,7 +881,7 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int j = 8 * q + 2 * i + hh;
-                const uint16_t o = fst_f32_to_bf16((xrow[j] * r) * fst_bf16_to_f32((uint16_t)(ww[i] >> (16 * hh))));
+                const uint16_t o = fst_f32_to_bf16((xrow[xi(j)] * r) * fst_bf16_to_f32((uint16_t)(ww[i] >> (16 * hh))));
                 nrow[j] = fst_bf16_to_f32(o);
                 o2 |= (uint32_t)o << (16 * hh);
             }
@@ -961,6 +967,12 @@ constexpr int kTokStride = 37;
 #ifndef FST_Q4K_WPE_MID
 #define FST_Q4K_WPE_MID 4
 #endif
+#ifndef FST_MF32_WPE
+#define FST_MF32_WPE 2
+#endif
+#ifndef FST_MF32_PF
+#define FST_MF32_PF 1
+#endif
 // What a linear-kernel launch does besides Y = W.A (mode 1, gate||up:
 // workgroup tile T holds gate rows [64T, 64T+64) in waves 0..3 and the
 // matching up rows in waves 4..7; it writes h = silu(gate) * up for its 64
@@ -1012,13 +1024,23 @@ struct EpiArgs {
 //    (topk_bucket_block over ra.scores with RPER experts per lane) into LDS
 //    tables, which then replace meta/slot_*/a_row; workgroup 0 also writes
 //    eids/wts and the tables to the global arrays of ra for later launches.
-template <int TOKS, int MS, int WAVES, int MODE, int CODEC = 0, int RPER = 0, int PF = FST_Q4K_PF>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : (TOKS <= 32 ? FST_Q4K_WPE_MID : 2)))) void q4k_linear_kernel(
+// MF (mode 0, Q4_K, 17..32 tokens): each wave owns 32 rows (two 16-row
+// tiles) and computes with v_mfma_f32_32x32x16_f16: one 16-byte LDS read per
+// lane feeds 32 rows x 16 k x 32 tokens, half the operand reads per weight of
+// two 16x16x32 token groups.  Lane (n = lane % 32, h = lane / 32) takes row n
+// and bytes [64h, 64h+64) of its nibbles (sub-blocks 4h..4h+3); MFMA j of a
+// super-block uses nibble dword j of that range, whose weights are the
+// elements of operand chunk 16h + j (the layout prep_row writes), so the
+// staged operand is read as it is.
+template <int TOKS, int MS, int WAVES, int MODE, int CODEC = 0, int RPER = 0, int PF = FST_Q4K_PF, bool MF = false>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ? FST_MF32_WPE : (TOKS <= 8 ? FST_Q4K_WAVES_PER_EU : (TOKS <= 32 ? FST_Q4K_WPE_MID : 2))))) void q4k_linear_kernel(
     const uint8_t* __restrict__ bank, size_t expert_stride, size_t mat_offset, int K, int N,
     const int* meta_g, const int* slot_eid_g, const int* slot_M_g,
     const int* slot_off_g, const int* a_row_g, const _Float16* __restrict__ A,
     const uint4* __restrict__ SX, const int* __restrict__ xs, float* __restrict__ out, EpiArgs ep, RouteArgs ra) {
     static_assert(MODE != 1 || WAVES % 2 == 0, "gate||up pairs waves");
+    static_assert(!MF || (MODE == 0 && CODEC == 0 && TOKS == 32), "32x32 tiles: mode 0, Q4_K, 32 tokens");
+    constexpr int WROWS = MF ? 32 : 16;              // rows per wave
     constexpr bool MX = CODEC == 1;                  // MXFP4 weights, bf16 operand, bf16 MFMA
     constexpr int CHUNK = MX ? 2176 : 2304;          // bytes per (16 rows x 256 weights)
     constexpr int PARTS = MX ? 32 : 36;              // staged 16-byte chunks per token per super-block
@@ -1108,7 +1130,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     // t = ((slot * tiles) + tile) * S + ks covers super-blocks [ks*nsb,
     // (ks+1)*nsb) of the rows and writes partial sums
     const int S = MODE == 1 ? max(ep.ksplit, 1) : 1;
-    const int tiles = N / (16 * WAVES);
+    const int tiles = N / (WROWS * WAVES);
     const int total = meta[META_N_SLOTS] * tiles * S;
     if ((int)blockIdx.x >= total) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1126,7 +1148,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         if constexpr (MODE == 1)
             return wave < HALF ? tile * HALF + wave : (N / 32) + tile * HALF + (wave - HALF);
         else
-            return tile * WAVES + wave;
+            return (tile * WAVES + wave) * (WROWS / 16);
     };
     // wave-tiled device layout (see repack_q4k_matrix): the wave's 16 rows are
     // one contiguous run of nsb 2304-byte chunks read front to back
@@ -1143,9 +1165,23 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         const uint64_t us = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
                             (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
         // num_records: the run; dword 3: 32-bit data format (raw loads)
-        return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)us, (short)0, nsb * CHUNK, 0x00020000);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)us, (short)0, (WROWS / 16) * nsb * CHUNK, 0x00020000);
     };
     constexpr int kNT = FST_WNT;  // cache policy: non-temporal (streamed once)
+    // MF: lane (n, h) reads row n % 16 of tile n / 16 (the second tile's run
+    // follows the first's), nibble bytes [64h, 64h + 64): region-0 and
+    // region-1 pieces of lane groups 2h and 2h + 1
+    const int mf_n = lane & 31, mf_h = lane >> 5;
+    const int mf_t = (mf_n >> 4) * nsb * CHUNK, mf_r = mf_n & 15;
+    auto load_w2 = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WRaw2 {
+        WRaw2 x;
+        x.h = __builtin_amdgcn_raw_buffer_load_b128(rs, mf_t + 2048 + 16 * mf_r, off, kNT);
+        x.a = __builtin_amdgcn_raw_buffer_load_b128(rs, mf_t + 16 * (32 * mf_h + mf_r), off, kNT);
+        x.b = __builtin_amdgcn_raw_buffer_load_b128(rs, mf_t + 1024 + 16 * (32 * mf_h + mf_r), off, kNT);
+        x.a1 = __builtin_amdgcn_raw_buffer_load_b128(rs, mf_t + 16 * (32 * mf_h + 16 + mf_r), off, kNT);
+        x.b1 = __builtin_amdgcn_raw_buffer_load_b128(rs, mf_t + 1024 + 16 * (32 * mf_h + 16 + mf_r), off, kNT);
+        return x;
+    };
     auto load_w = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WRaw {
         WRaw x;
         // (the header first: issued last, its register was taken by a live
@@ -1168,9 +1204,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
     // and the compiler waits only for the oldest super-block instead of
     // draining the prefetch ring at each step.
     __amdgpu_buffer_rsrc_t wrs = rsrc(wave_base(blockIdx.x));
-    WRaw w[R];
+    using WT = typename std::conditional<MF, WRaw2, WRaw>::type;
+    auto load_any = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WT {
+        if constexpr (MF)
+            return load_w2(rs, off);
+        else
+            return load_w(rs, off);
+    };
+    WT w[R];
 #pragma unroll
-    for (int j = 0; j < PF; ++j) w[j] = load_w(wrs, j * CHUNK);
+    for (int j = 0; j < PF; ++j) w[j] = load_any(wrs, j * CHUNK);
     for (int i = tid; i < 2 * STAGE; i += NT) lds[i] = z4;
 
     // Staging map: chunk q = tid + NT*i of a macro-stage -> (super-block u,
@@ -1282,8 +1325,38 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
         f4_t acc[NGRP];
 #pragma unroll
         for (int q = 0; q < NGRP; ++q) acc[q] = zf;
+        f16v_t acc32 = {};
         const int ngrp_live = (Me + 15) >> 4;
 
+        // 32x32 tiles: 16 MFMAs on the lane's 16 nibble dwords, one for the
+        // min term (sub-block sums of chunks 32 + 2h and 33 + 2h against the
+        // mins of sub-blocks 4h..4h+3)
+        auto compute32 = [&](int sb, const WRaw2& cur) {
+            const int m = sb / MS, u = sb - m * MS;
+            const uint4* st = lds + (m & 1) * STAGE + u * TS + mf_n * kTokStride;
+            Q4kScale S0, S1;
+            q4k_scales(cur.h, 2 * mf_h, q4k_scale_sel(2 * mf_h), S0);
+            q4k_scales(cur.h, 2 * mf_h + 1, q4k_scale_sel(2 * mf_h + 1), S1);
+            const uint32_t Dw[16] = {cur.a.x,  cur.a.y,  cur.a.z,  cur.a.w,  cur.b.x,  cur.b.y,  cur.b.z,  cur.b.w,
+                                     cur.a1.x, cur.a1.y, cur.a1.z, cur.a1.w, cur.b1.x, cur.b1.y, cur.b1.z, cur.b1.w};
+            f16v_t D = {};
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const h8_t b = q4k_bop(Dw[j], j < 8 ? S0 : S1, magic);
+                const h8_t a = __builtin_bit_cast(h8_t, st[16 * mf_h + j]);
+                D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, D, 0, 0, 0);
+            }
+            const h8_t s0 = __builtin_bit_cast(h8_t, st[32 + 2 * mf_h]);
+            const h8_t s1 = __builtin_bit_cast(h8_t, st[33 + 2 * mf_h]);
+            const h8_t am = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+            const h8_t bm = {S0.m[0], S0.m[1], S0.m[2], S0.m[3], S1.m[0], S1.m[1], S1.m[2], S1.m[3]};
+            const f16v_t Dm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, f16v_t{}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                acc32[i] = fmaf(S0.d, D[i], acc32[i]);
+                acc32[i] = fmaf(-S0.dmin, Dm[i], acc32[i]);
+            }
+        };
         auto compute = [&](int sb, const WRaw& cur) {
             const int m = sb / MS, u = sb - m * MS;
             // at a capacity of 8 tokens, MFMA rows 8..15 (discarded) read rows
@@ -1363,11 +1436,14 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                 // one load call site (resource and offset selected first), for
                 // the same reason as the staging loads
                 const bool pnx = pf >= nsb;
-                w[(j + PF) % R] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHUNK);
+                w[(j + PF) % R] = load_any(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHUNK);
                 // keep the prefetches where they are issued (the scheduler
                 // would otherwise sink them next to their use to save registers)
                 __builtin_amdgcn_sched_barrier(0);
-                compute(sb, w[j % R]);
+                if constexpr (MF)
+                    compute32(sb, w[j % R]);
+                else
+                    compute(sb, w[j % R]);
                 if (j % MS == MS - 1) {
                     if (sb / MS + 1 < nms) stage_store(sb / MS + 1);
                     __syncthreads();
@@ -1438,6 +1514,19 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(TOKS
                             ep.h[(size_t)(off + tl) * inter + n] = hv;
                     }
                 }
+            }
+            continue;
+        }
+        if constexpr (MF) {
+            // D layout (32x32): lane (n, h), value i is token row
+            // 8 (i / 4) + 4 h + i % 4 of column n
+            const int row32 = wave_tile(tile) * 16 + mf_n;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int tl = 8 * (i >> 2) + 4 * mf_h + (i & 3);
+                if (tl >= Me) continue;
+                const int pidx = off + tl;
+                out[(size_t)pidx * N + row32] = ldexpf(acc32[i], unscale(pidx));
             }
             continue;
         }
@@ -2027,12 +2116,29 @@ static int linear_waves_per_cu(int M) {
     return 8 * (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1));
 }
 
+static bool mf32_enabled() {
+    static const bool on = getenv("FST_NO_MF32") == nullptr;  // A/B switch for measurements
+    return on;
+}
+
 template <int MODE, int CODEC = 0, int RPER = 0>
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
                               const _Float16* A, const uint4* SX, const int* xs, float* out, const EpiArgs& ep,
                               const RouteArgs& ra = RouteArgs{}) {
 
+    if constexpr (MODE == 0 && CODEC == 0 && RPER == 0) {
+        if (M > 16 && M <= 32 && N % 256 == 0 && mf32_enabled()) {
+            // 32x32 tiles: 8 waves x 32 rows per item, one workgroup per CU (the
+            // tile's accumulators need more than 128 VGPRs)
+            const unsigned items32 = slots * (unsigned)(N / 256);
+            hipLaunchKernelGGL((q4k_linear_kernel<32, 1, 8, MODE, CODEC, RPER, FST_MF32_PF, true>),
+                               dim3(std::min(items32, (unsigned)s.n_cu * (FST_MF32_WPE >= 4 ? 2u : 1u))), dim3(512), 0, st, bank, stride,
+                               mat_off, K, N, s.meta, s.slot_eid, s.slot_M, s.slot_off, a_row, A, SX, xs, out, ep,
+                               ra);
+            return;
+        }
+    }
     const int W = linear_waves(M, N);
     // persistent grid: FST_Q4K_WG_PER_CU workgroups per CU at most
     const unsigned items = slots * (unsigned)(N / (16 * W)) * (unsigned)(MODE == 1 ? std::max(ep.ksplit, 1) : 1);

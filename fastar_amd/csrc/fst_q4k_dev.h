@@ -95,6 +95,11 @@ __device__ __forceinline__ h8_t q4k_bop(uint32_t D, const Q4kScale& S, uint32_t 
 struct WRaw {
     u4v_t h, a, b;
 };
+// The 32x32 tile's lane data: header and four 16-byte nibble pieces.
+struct WRaw2 {
+    u4v_t h, a, b, a1, b1;
+};
+typedef float f16v_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ u4v_t ld_stream(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u4v_t*>(p));
