@@ -586,8 +586,8 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
         fst::launch_moe_fused(st, g, L, M, ctx->s, rq, ctx->fused_epoch, ctx->spin_limit);
         ctx->mark("moe_fused");
         // (a bf16 shared expert ran above; its fp32 rows are the combine's shared term)
-        fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out, d_out_routed,
-                            d_out_shared);
+        fst::launch_combine_tj(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out,
+                               d_out_routed, d_out_shared);
         ctx->mark("combine");
         FST_HIP_TRY(hipGetLastError());
         return FST_OK;

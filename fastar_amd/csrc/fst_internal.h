@@ -330,6 +330,9 @@ bool gemv_supported(const Geometry& g, int M, int tk, int use_shared, const Scra
 int launch_expert_gemv(hipStream_t st, const Geometry& g, const LayerView& L, int M, int tk, const int32_t* eids,
                        const float* wts, int use_shared, const uint16_t* h, const Scratch& s, uint32_t epoch,
                        int spin_limit, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
+// The fused launch's combine: y rows indexed (token, j), j = tk the shared expert.
+void launch_combine_tj(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s, const float* wts,
+                       const float* ys, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
                      const RouteReq& rq, uint32_t epoch, int spin_limit);
 // With o1/o2 (one routed pair per token, no shared expert) it writes

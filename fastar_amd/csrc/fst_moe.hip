@@ -1637,6 +1637,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     __shared__ int s_claim;
     __shared__ int r_meta[META_WORDS], r_seid[RPAIR + 1], r_sM[RPAIR + 1], r_soff[RPAIR + 1];
     __shared__ int r_ptok[RPAIR + kFuT], r_pof[RPAIR], r_psh[kFuT];
+    __shared__ int r_yrow[RPAIR + kFuT];  // pair -> its y row t*(tk+1) + j (shared: j = tk)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     constexpr int hd = HD, inter = INTER;
     const size_t stride = fa.expert_stride;
@@ -1682,6 +1683,13 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             if (ra.use_shared)
                 for (int i = tid; i < ra.M; i += NT) ra.pair_shared[i] = r_psh[i];
         }
+        // y rows by (token, j), so that the combine reads them without the
+        // pair table (one round trip instead of two)
+        for (int i = tid; i < ra.M * ra.tk; i += NT)
+            if (r_pof[i] >= 0) r_yrow[r_pof[i]] = (i / ra.tk) * (ra.tk + 1) + i % ra.tk;
+        if (ra.use_shared)
+            for (int i = tid; i < ra.M; i += NT) r_yrow[r_psh[i]] = i * (ra.tk + 1) + ra.tk;
+        __syncthreads();
     }
     const int ns = r_meta[META_N_SLOTS];
     constexpr int tiles_gu = inter / 64, tiles_dn = hd / 128;
@@ -2046,7 +2054,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tl = 4 * g + i;
-                if (tl < Me) fa.y[(size_t)(off + tl) * hd + row] = ldexpf(acc[i], s_xs2[tl]);
+                if (tl < Me) fa.y[(size_t)r_yrow[off + tl] * hd + row] = ldexpf(acc[i], s_xs2[tl]);
             }
         }
     }
@@ -2329,6 +2337,67 @@ __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int
         a.w = a.w + vs.w;
     }
     put(out, a);
+}
+
+// The combine of the fused launch: y rows by (token, j) (j = tk: the shared
+// expert), so every load is issued at once; same arithmetic as combine_kernel.
+template <int TK>
+__global__ __launch_bounds__(256) void combine_tj_kernel(int M, int hd, int tk, int use_shared,
+                                                         const float* __restrict__ y, const float* __restrict__ ys,
+                                                         const float* __restrict__ wts, uint16_t* __restrict__ out,
+                                                         uint16_t* __restrict__ out_routed,
+                                                         uint16_t* __restrict__ out_shared) {
+    const int t = blockIdx.y;
+    const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (t >= M || n >= hd) return;
+    float w[TK];
+    float4 v[TK];
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+        const int jj = max(min(j, tk - 1), 0);
+        w[j] = tk > 0 ? wts[t * tk + jj] : 0.0f;
+        v[j] = *reinterpret_cast<const float4*>(y + ((size_t)t * (tk + 1) + jj) * hd + n);
+    }
+    const float4 vs = use_shared ? *reinterpret_cast<const float4*>(
+                                       (ys ? ys + (size_t)t * hd : y + ((size_t)t * (tk + 1) + tk) * hd) + n)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+        if (j >= tk) continue;
+        a.x = a.x + w[j] * v[j].x;
+        a.y = a.y + w[j] * v[j].y;
+        a.z = a.z + w[j] * v[j].z;
+        a.w = a.w + w[j] * v[j].w;
+    }
+    auto put = [&](uint16_t* o, const float4& q) {
+        if (!o) return;
+        const uint32_t lo = fst_f32_to_bf16(q.x) | ((uint32_t)fst_f32_to_bf16(q.y) << 16);
+        const uint32_t hi = fst_f32_to_bf16(q.z) | ((uint32_t)fst_f32_to_bf16(q.w) << 16);
+        *reinterpret_cast<uint2*>(o + (size_t)t * hd + n) = make_uint2(lo, hi);
+    };
+    put(out_routed, a);
+    if (use_shared) {
+        put(out_shared, vs);
+        a.x = a.x + vs.x;
+        a.y = a.y + vs.y;
+        a.z = a.z + vs.z;
+        a.w = a.w + vs.w;
+    }
+    put(out, a);
+}
+
+void launch_combine_tj(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s, const float* wts,
+                       const float* ys, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared) {
+    dim3 grid((g.hd / 4 + 255) / 256, M);
+#define FST_COMB(T)                                                                                        \
+    hipLaunchKernelGGL(combine_tj_kernel<T>, grid, dim3(256), 0, st, M, g.hd, g.tk, use_shared, s.y, ys, wts, \
+                       out, out_routed, out_shared)
+    if (g.tk <= 8)
+        FST_COMB(8);
+    else
+        FST_COMB(kMaxTopK);
+#undef FST_COMB
 }
 
 void launch_combine(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
