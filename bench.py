@@ -75,6 +75,31 @@ def measured_traffic(name):
         return None
 
 
+def spin_up(fa, ctx, seconds):
+    """Bring the GPU out of its idle power state before the warm-up steps:
+    `seconds` of back-to-back copies that read the resident expert bank into
+    a scratch buffer (the outputs of no step are computed).  The set-up before
+    this point is mostly host work, during which the GPU idles and lowers its
+    clocks; a handful of warm-up steps (well under a millisecond) does not
+    bring them back, so a short run would otherwise time a GPU in a lower
+    power state than a serving GPU that is never idle."""
+    if seconds <= 0:
+        return
+    import ctypes as C
+    L = fa.lib()
+    L.fst_expert_device_ptr.restype = C.c_void_p
+    n = 256 << 20
+    dst = ctx.dev_alloc(n)
+    base = L.fst_expert_device_ptr(ctx.h, 0, 0)
+    total = ctx.cfg.n_experts * EXPERT_BYTES
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for off in range(0, total - n + 1, n):
+            fa._check(L.fst_device_copy(ctx.h, dst, C.c_void_p(base + off), n))
+        ctx.sync()
+    ctx.dev_free(dst)
+
+
 def step(fa, ctx, bufs, i):
     L = fa.lib()
     hp = bufs["h"] + (i % N_BATCH) * M * HD * 2
@@ -368,6 +393,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--spinup", type=float, default=0.15,
+                    help="seconds of untimed streaming reads before the warm-up steps (0: none)")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="also run N launches of the plain copy kernel (512 MiB) for PMC calibration")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c2mx", "c3", "c4", "c5"],
@@ -388,6 +415,7 @@ def main():
         return
     L = fa.lib()
     ctx, w, hs, logits, draft, bufs = setup(fa)
+    spin_up(fa, ctx, args.spinup)
 
     for i in range(args.warmup):
         step(fa, ctx, bufs, i)
@@ -462,6 +490,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "device_spinup_s": args.spinup,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
