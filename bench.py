@@ -77,8 +77,8 @@ def measured_traffic(name):
 
 def spin_up(fa, ctx, seconds):
     """Bring the GPU out of its idle power state before the warm-up steps:
-    `seconds` of back-to-back copies that read the resident expert bank into
-    a scratch buffer (the outputs of no step are computed).  The set-up before
+    `seconds` of back-to-back 256 MiB device-to-device copies between two
+    scratch buffers (the outputs of no step are computed).  The set-up before
     this point is mostly host work, during which the GPU idles and lowers its
     clocks; a handful of warm-up steps (well under a millisecond) does not
     bring them back, so a short run would otherwise time a GPU in a lower
@@ -87,17 +87,15 @@ def spin_up(fa, ctx, seconds):
         return
     import ctypes as C
     L = fa.lib()
-    L.fst_expert_device_ptr.restype = C.c_void_p
     n = 256 << 20
-    dst = ctx.dev_alloc(n)
-    base = L.fst_expert_device_ptr(ctx.h, 0, 0)
-    total = ctx.cfg.n_experts * EXPERT_BYTES
+    a, b = ctx.dev_alloc(n), ctx.dev_alloc(n)
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        for off in range(0, total - n + 1, n):
-            fa._check(L.fst_device_copy(ctx.h, dst, C.c_void_p(base + off), n))
+        for _ in range(8):
+            fa._check(L.fst_device_copy(ctx.h, b, a, n))
         ctx.sync()
-    ctx.dev_free(dst)
+    ctx.dev_free(a)
+    ctx.dev_free(b)
 
 
 def step(fa, ctx, bufs, i):
@@ -195,7 +193,12 @@ def cpu_baseline(hs, w, min_seconds=8.0, max_steps=400):
 # BASELINE configs other than C2 are parity-test cases; these modes measure
 # them for the record (one JSON line each, not the driver's headline).
 
+SPINUP_S = 0.15  # set from --spinup
+
+
 def timed(ctx, fn, steps, warmup):
+    import fastar_amd as fa
+    spin_up(fa, ctx, SPINUP_S)
     for i in range(warmup):
         fn(i)
     ctx.sync()
@@ -406,6 +409,8 @@ def main():
               "replicated, one all-reduce of the combine per layer). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    global SPINUP_S
+    SPINUP_S = args.spinup
     import fastar_amd as fa
     if args.config != "c2":
         fn = {"c1": bench_c1, "c2mx": bench_c2mx, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config]
