@@ -29,6 +29,22 @@ constexpr int kChunks = 64;
 constexpr int kProbThreads = 1024;
 typedef unsigned __int128 u128;
 
+// Rejection-sampling tail launch (acc_tail_kernel): chunks per sequence,
+// threads, rows (2k + 1 <= 17), elements per thread at most, and the
+// arrival counters: kTailGroups16 groups of 16 chunks, then one top counter,
+// each on its own 256-byte line.
+constexpr int kTailThreads = 512;
+constexpr int kTailChunks = 256;
+constexpr int kTailRows = 17;
+constexpr int kTailPerMax = 2;  // chunk length <= 1024
+constexpr int kTailArrGroups = kTailChunks / 16;
+constexpr int kTailCntStride = 32;  // u64 words between counters
+// [n_seq][kTailChunks][3] chunk sums (residual lo, hi; target E), then
+// [n_seq][kTailArrGroups + 1] counters.
+static size_t tail_words(int n_seq) {
+    return (size_t)n_seq * kTailChunks * 3 + (size_t)n_seq * (kTailArrGroups + 1) * kTailCntStride;
+}
+
 struct AccWs {
     float* part_max;          // [R][kChunks]
     int* part_idx;            // [R][kChunks]
@@ -36,6 +52,7 @@ struct AccWs {
     unsigned long long* part_res;  // [n_seq][kChunks][2] (u128 as lo, hi)
     unsigned long long* dec;       // [n_seq][8]
     unsigned long long* gslot;     // [R][kChunks] greedy chunk partials (zero between calls)
+    float* xsel;                   // [R] each row's logit at its position's draft token (acc_sums_kernel)
     unsigned long long* tail;      // acc_tail_kernel: chunk sums and counters (counters zero between calls)
 };
 
@@ -51,6 +68,7 @@ static AccWs carve(void* ws, int n_seq, int k) {
     w.part_res = (unsigned long long*)p; p += align256(16ull * n_seq * kChunks);
     w.dec = (unsigned long long*)p; p += align256(64ull * n_seq);
     w.gslot = (unsigned long long*)p; p += align256(8ull * R * kChunks);
+    w.xsel = (float*)p; p += align256(sizeof(float) * R);
     w.tail = (unsigned long long*)p;
     return w;
 }
@@ -60,7 +78,7 @@ size_t accept_ws_bytes(int n_seq, int k, int V) {
     const int R = n_seq * (k + 1) + n_seq * k;
     return align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
            align256(8ull * R * kChunks) + align256(16ull * n_seq * kChunks) + align256(64ull * n_seq) +
-           align256(8ull * R * kChunks) + align256(8ull * ((size_t)n_seq * 256 * 3 + n_seq)) + 256;
+           align256(8ull * R * kChunks) + align256(sizeof(float) * R) + align256(8ull * tail_words(n_seq)) + 256;
 }
 
 // Calls f(x, v) for v = v0, v0 + stride, ... < v1 in that order, with the
@@ -175,17 +193,30 @@ __device__ __forceinline__ void wave_row_max_any(const float* part_max, const in
     *any = idx >= 0;
 }
 
-// Chunk sums of E for every row.
+// Chunk sums of E for every row.  With xsel given, the workgroup whose chunk
+// holds the row's draft token (position i of sequence s: draft[s*k + i], for
+// target rows i < k and every draft row) also writes that logit to xsel[r],
+// so that the decisions need no dependent load of it later.
 __global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__ target,
                                                        const float* __restrict__ draft, int n_tgt_rows,
                                                        int V, float inv_t,
                                                        const float* __restrict__ part_max,
                                                        const int* __restrict__ part_idx,
-                                                       unsigned long long* __restrict__ part_sum) {
+                                                       unsigned long long* __restrict__ part_sum,
+                                                       const int32_t* __restrict__ dtok, int k,
+                                                       float* __restrict__ xsel) {
     const int c = blockIdx.x, r = blockIdx.y;
     const float* row = row_ptr(target, draft, n_tgt_rows, r, V);
     const int clen = (V + kChunks - 1) / kChunks;
     const int b0 = c * clen, b1 = min(V, b0 + clen);
+    if (xsel && threadIdx.x == 0 && k > 0) {
+        const int seq = r < n_tgt_rows ? r / (k + 1) : (r - n_tgt_rows) / k;
+        const int pos = r < n_tgt_rows ? r % (k + 1) : (r - n_tgt_rows) % k;
+        if (pos < k) {
+            const int x = dtok[seq * k + pos];
+            if (x >= b0 && x < b1) xsel[r] = row[x];
+        }
+    }
     // the first 8 elements of each thread are loaded before the row maximum
     // is known (they do not depend on it), so both round trips overlap
     constexpr int NB = 8;
@@ -741,43 +772,166 @@ void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k,
 //     of an identically zero residual), writes the sums with device-coherent
 //     stores and counts itself in with one atomic per workgroup;
 //   - the last workgroup of the sequence to arrive (the counter is left at
-//     zero) scans the chunk sums, loads the chosen chunk and picks the token
-//     (as acc_sample_kernel), then writes n_acc and the tokens.
+//     zero) finds the chunk holding the inverse-CDF target, loads it and
+//     picks the token, then writes n_acc and the tokens.
 // No workgroup waits for another, so any grid size is safe.  The arithmetic
 // is the chain's, and the results are identical to it and to the CPU oracle.
+// The two searches ("first index whose inclusive prefix exceeds t") run over
+// LDS: sums of 16-element groups and of 16-group super-groups, then one wave
+// locates the super-group, the group and the element, each level by a
+// ballot over per-lane prefix sums of at most 16 terms (no u128 wave scans).
 #ifdef FST_TRACE
+// per workgroup: wall-clock stamps kept in registers and written at the end
+// (a store per stamp would wait on its own round trip)
 __device__ long long g_tail_trace[1024][8];
-#define TAIL_STAMP(i)                                                  \
-    do {                                                               \
-        if (tid == 0 && blockIdx.x < 1024) {                           \
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");           \
-            g_tail_trace[blockIdx.x][i] = wall_clock64();              \
-        }                                                              \
+#define TAIL_STAMP(i)                                        \
+    do {                                                     \
+        if (tid == 0) tstamp[i] = wall_clock64();            \
+    } while (0)
+#define TAIL_FLUSH(i0, i1)                                                        \
+    do {                                                                          \
+        if (tid == 0 && blockIdx.x < 1024)                                        \
+            for (int q = i0; q < i1; ++q) g_tail_trace[blockIdx.x][q] = tstamp[q]; \
     } while (0)
 #else
 #define TAIL_STAMP(i) \
     do {              \
     } while (0)
+#define TAIL_FLUSH(i0, i1) \
+    do {                   \
+    } while (0)
 #endif
-constexpr int kTailThreads = 512;
-constexpr int kTailChunks = 256;
-constexpr int kTailRows = 17;  // 2k + 1, k <= 8
-constexpr int kTailPer = 2;    // chunk length <= 1024
 constexpr int kTailWaves = kTailThreads / 64;
+constexpr int kTailMaxN = kTailPerMax * kTailThreads;  // longest array searched
+constexpr int kTailGroups = kTailMaxN / 16;            // 16-element groups
+static_assert(kTailChunks <= kTailThreads && kTailGroups <= 64, "search levels");
 
-// [n_seq][kTailChunks][3] chunk sums (residual lo, hi; target E), [n_seq] counters.
-static size_t tail_words(int n_seq) { return (size_t)n_seq * kTailChunks * 3 + (size_t)n_seq; }
 
+// u128 as four 32-bit limbs, each held in 64 bits so that sums over up to
+// 2^32 terms need no carries until recombined.
+struct Limbs {
+    unsigned long long l[4];
+};
+__device__ __forceinline__ Limbs to_limbs(u128 v) {
+    Limbs r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r.l[q] = (uint32_t)(v >> (32 * q));
+    return r;
+}
+__device__ __forceinline__ u128 from_limbs(const Limbs& r) {
+    u128 t = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) t += (u128)r.l[q] << (32 * q);
+    return t;
+}
+// Sum over the 16 lanes of each DPP row, in every lane of the row.
+__device__ __forceinline__ u128 row_sum_u128(u128 v) {
+    Limbs r = to_limbs(v);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        r.l[q] += dpp_u64<0xb1>(r.l[q]);   // quad_perm [1,0,3,2]
+        r.l[q] += dpp_u64<0x4e>(r.l[q]);   // quad_perm [2,3,0,1]
+        r.l[q] += dpp_u64<0x124>(r.l[q]);  // row_ror 4
+        r.l[q] += dpp_u64<0x128>(r.l[q]);  // row_ror 8
+    }
+    return from_limbs(r);
+}
+// Inclusive prefix sum within each DPP row (row_shr 1, 2, 4, 8; lanes
+// without a source add 0).
+__device__ __forceinline__ u128 row_scan_u128(u128 v) {
+    Limbs r = to_limbs(v);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        r.l[q] += dpp_u64<0x111>(r.l[q]);
+        r.l[q] += dpp_u64<0x112>(r.l[q]);
+        r.l[q] += dpp_u64<0x114>(r.l[q]);
+        r.l[q] += dpp_u64<0x118>(r.l[q]);
+    }
+    return from_limbs(r);
+}
+__device__ __forceinline__ u128 readlane_u128(u128 v, int j) {
+    u128 t = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        t |= (u128)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> (32 * q)), j) << (32 * q);
+    return t;
+}
+
+// The search arrays of NU values per thread (value u of thread t is element
+// u*kTailThreads + t, zero at or past n): the elements in a[], the sums of
+// 16-element groups in g[] (a DPP row sum: 16 consecutive threads hold 16
+// consecutive elements) and of 16-group super-groups in sg[] (wave 0).
+// Every thread calls it; a barrier at the start and at the end.
+template <int NU>
+__device__ __forceinline__ void tail_sums(const u128 (&vals)[NU], int n, u128* a, u128* g, u128* sg) {
+    const int tid = threadIdx.x;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        const u128 r = row_sum_u128(vals[u]);
+        const int i = u * kTailThreads + tid;
+        a[i] = vals[u];
+        if ((tid & 15) == 0) g[i >> 4] = r;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int ng = (n + 15) >> 4;
+        const u128 r = row_sum_u128(tid < ng ? g[tid] : (u128)0);
+        if ((tid & 15) == 0) sg[tid >> 4] = r;
+    }
+    __syncthreads();
+}
+
+// One level of the search, called by a whole wave: among v[0..m) (m <= 16),
+// the first j whose running sum, started at run, exceeds t; run becomes the
+// sum before j.  -1 if none.  One LDS load per lane and a DPP row scan.
+__device__ __forceinline__ int tail_level(const u128* v, int m, u128 t, u128& run) {
+    const int lane = threadIdx.x & 63;
+    const u128 own = lane < m ? v[lane] : (u128)0;
+    const u128 pre = row_scan_u128(own) + run;
+    const unsigned long long hit = __ballot(lane < m && pre > t);
+    if (!hit) return -1;
+    const int j = __ffsll((long long)hit) - 1;
+    run = readlane_u128(pre - own, j);
+    return j;
+}
+
+// First index of a[0..n) (n <= 1024) whose inclusive prefix exceeds t
+// (tail_sums done), and in *before the sum of the elements before it; -1 if
+// none.  Called by a whole wave; the results are uniform.
+__device__ __forceinline__ int tail_pick(const u128* a, int n, const u128* g, const u128* sg, u128 t,
+                                         u128* before) {
+    const int ng = (n + 15) >> 4, ns = (ng + 15) >> 4;
+    u128 run = 0;
+    int J = 0;
+    if (ns > 1) {
+        J = tail_level(sg, ns, t, run);
+        if (J < 0) return -1;
+    }
+    const int Q = tail_level(g + J * 16, min(16, ng - J * 16), t, run);
+    if (Q < 0) return -1;
+    const int q = J * 16 + Q;
+    const int e = tail_level(a + q * 16, min(16, n - q * 16), t, run);
+    if (e < 0) return -1;
+    *before = run;
+    return q * 16 + e;
+}
+
+template <int PER>
 __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
     const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V, float inv_t,
     const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base, const float* __restrict__ part_max,
     const int* __restrict__ part_idx, const unsigned long long* __restrict__ part_sum,
-    unsigned long long* __restrict__ tw, int32_t* __restrict__ n_acc, int32_t* __restrict__ tokens) {
+    const float* __restrict__ xsel, unsigned long long* __restrict__ tw, int32_t* __restrict__ n_acc,
+    int32_t* __restrict__ tokens) {
     const int c = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_tgt = n_seq * (k + 1), NR = 2 * k + 1;
     const int clen = (V + kTailChunks - 1) / kTailChunks, b0 = min(V, c * clen), b1 = min(V, b0 + clen);
     unsigned long long* cw = tw + (size_t)s * kTailChunks * 3;  // this sequence's chunk sums
-    int* cnt = reinterpret_cast<int*>(tw + (size_t)n_seq * kTailChunks * 3) + s;
+    // arrival counters: this chunk's group, then the sequence's top counter
+    unsigned long long* cbase = tw + (size_t)n_seq * kTailChunks * 3 + (size_t)s * (kTailArrGroups + 1) * kTailCntStride;
+    int* gcnt = reinterpret_cast<int*>(cbase + (size_t)(c >> 4) * kTailCntStride);
+    int* tcnt = reinterpret_cast<int*>(cbase + (size_t)kTailArrGroups * kTailCntStride);
     auto grow = [&](int rr) { return rr <= k ? s * (k + 1) + rr : n_tgt + s * k + (rr - k - 1); };
     auto rowp = [&](int rr) {
         return rr <= k ? target + (size_t)(s * (k + 1) + rr) * V : draftl + (size_t)(s * k + rr - k - 1) * V;
@@ -785,41 +939,69 @@ __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
     __shared__ float s_M[kTailRows];
     __shared__ int s_any[kTailRows];
     __shared__ unsigned long long s_S[kTailRows];
-    __shared__ int s_n, s_last, s_chunk, s_owner, s_tok, s_mode;
+    __shared__ uint32_t s_U2[kTailRows];
+    __shared__ int s_n, s_last, s_chunk;
     __shared__ u128 s_wtot[kTailWaves], s_rem;
-    __shared__ u128 s_rc[kTailChunks];
-    __shared__ unsigned long long s_ce[kTailChunks];
+    __shared__ unsigned long long s_ew[kTailWaves];
+    // the last workgroup's searches (s_sg padded to one 16-lane level)
+    __shared__ u128 s_a[kTailMaxN], s_g[kTailGroups], s_sg[16];
+#ifdef FST_TRACE
+    long long tstamp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
 
     TAIL_STAMP(0);
-    // ---- loads: the chunk of every row, the draft tokens' logits
-    float xv[kTailRows][kTailPer];
+    // ---- loads, all issued before the first use: the row partials and the
+    // draft tokens' logits first (the decisions wait for these only), then the
+    // chunk of every row (unconditional loads from clamped addresses: no
+    // branch per load; V >= 1)
+    // wave w: rows w, w + 8, w + 16
+    constexpr int kRowsPerWave = (kTailRows + kTailWaves - 1) / kTailWaves;
+    float pm[kRowsPerWave];
+    int pi[kRowsPerWave];
+    unsigned long long ps[kRowsPerWave];
+#pragma unroll
+    for (int q = 0; q < kRowsPerWave; ++q) {
+        const int rr = min(wave + q * kTailWaves, NR - 1);
+        const size_t o = (size_t)grow(rr) * kChunks + lane;
+        pm[q] = part_max[o];
+        pi[q] = part_idx[o];
+        ps[q] = part_sum[o];
+    }
+    float xp = 0.0f, xq = 0.0f;
+    int xt_id = -1;
+    if (wave == 0 && lane < k) {
+        xt_id = draft[s * k + lane];
+        xp = xsel[grow(lane)];
+        xq = xsel[grow(k + 1 + lane)];
+    }
+    float xv[kTailRows][PER];
 #pragma unroll
     for (int rr = 0; rr < kTailRows; ++rr)
 #pragma unroll
-        for (int u = 0; u < kTailPer; ++u) {
+        for (int u = 0; u < PER; ++u) {
             const int v = b0 + tid + u * kTailThreads;
-            xv[rr][u] = (rr < NR && v < b1) ? rowp(rr)[v] : __builtin_nanf("");
+            xv[rr][u] = rowp(min(rr, NR - 1))[min(v, max(b1 - 1, 0))];
+            if (rr >= NR || v >= b1) xv[rr][u] = __builtin_nanf("");
         }
-    float xp = 0.0f, xq = 0.0f;
-    int xok = 0;
-    if (wave == 0 && lane < k) {
-        const int x = draft[s * k + lane];
-        if (x >= 0 && x < V) {
-            xok = 1;
-            xp = rowp(lane)[x];
-            xq = rowp(k + 1 + lane)[x];
-        }
+    // the uniforms (no memory operands: computed while the loads are in
+    // flight): U for the decision at position lane, U2 for a resample at
+    // position lane
+    uint32_t U = 0;
+    if (wave == 0 && lane <= k) {
+        U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 0);
+        s_U2[lane] = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 1);
     }
-    // ---- row maxima and sums from the 64 chunk partials (wave w: rows w, w + 8, ...)
-    for (int rr = wave; rr < NR; rr += kTailWaves) {
-        float mx;
-        int any;
-        wave_row_max_any(part_max, part_idx, grow(rr), &mx, &any);
-        const unsigned long long S = wave_sum_u64(part_sum[(size_t)grow(rr) * kChunks + lane]);
-        if (lane == 0) {
-            s_M[rr] = mx;
-            s_any[rr] = any;
-            s_S[rr] = S;
+#pragma unroll
+    for (int q = 0; q < kRowsPerWave; ++q) {
+        const int rr = wave + q * kTailWaves;
+        if (rr < NR) {
+            wave_argmax(pm[q], pi[q]);
+            const unsigned long long S = wave_sum_u64(ps[q]);
+            if (lane == 0) {
+                s_M[rr] = pm[q];
+                s_any[rr] = pi[q] >= 0;
+                s_S[rr] = S;
+            }
         }
     }
     __syncthreads();
@@ -827,11 +1009,10 @@ __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
     // ---- the decisions (acc_decide_kernel's): lane i < k decides position i
     if (wave == 0) {
         int ok = 0;
-        if (lane < k && xok) {
+        if (lane < k && xt_id >= 0 && xt_id < V) {
             const int rt = lane, rd = k + 1 + lane;
             const unsigned long long P = fixed_prob(xp, inv_t, s_M[rt], s_any[rt]);
             const unsigned long long Q = fixed_prob(xq, inv_t, s_M[rd], s_any[rd]);
-            const uint32_t U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 0);
             const u128 lhs = (u128)U * (u128)Q * (u128)s_S[rt];
             const u128 rhs = ((u128)P * (u128)s_S[rd]) << 24;
             ok = lhs < rhs;
@@ -846,13 +1027,13 @@ __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
     const int ap = s_any[tr], aq = mode0 == 0 ? s_any[dr] : 0;
     // this thread's values of the sampling rows (uniform branches: no
     // dynamic register indexing)
-    float xt[kTailPer], xd[kTailPer];
+    float xt[PER], xd[PER];
 #pragma unroll
-    for (int u = 0; u < kTailPer; ++u) xt[u] = xd[u] = 0.0f;
+    for (int u = 0; u < PER; ++u) xt[u] = xd[u] = 0.0f;
 #pragma unroll
     for (int rr = 0; rr < kTailRows; ++rr)
 #pragma unroll
-        for (int u = 0; u < kTailPer; ++u) {
+        for (int u = 0; u < PER; ++u) {
             if (rr == tr) xt[u] = xv[rr][u];
             if (mode0 == 0 && rr == dr) xd[u] = xv[rr][u];
         }
@@ -860,18 +1041,18 @@ __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
     u128 ra = 0;
     unsigned long long ea = 0;
 #pragma unroll
-    for (int u = 0; u < kTailPer; ++u) {
+    for (int u = 0; u < PER; ++u) {
         ra += res_of(xt[u], xd[u], inv_t, mp, ap, mq, aq, Sp, Sq, mode0);
         ea += fixed_prob(xt[u], inv_t, mp, ap);
     }
     ra = wave_sum_u128(ra);
     ea = wave_sum_u64(ea);
-    __shared__ unsigned long long s_ew[kTailWaves];
     if (lane == 0) {
         s_wtot[wave] = ra;
         s_ew[wave] = ea;
     }
     __syncthreads();
+    TAIL_STAMP(2);
     if (tid == 0) {
         u128 rt = 0;
         unsigned long long et = 0;
@@ -883,101 +1064,99 @@ __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
         st_coherent_u64(cw + (size_t)c * 3 + 1, (unsigned long long)(rt >> 64));
         st_coherent_u64(cw + (size_t)c * 3 + 2, et);
         publish_wait();
-        TAIL_STAMP(2);
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = old == kTailChunks - 1;
-        if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the 16th arrival of a group of 16 chunks counts the group in at the
+        // top; the last group to arrive makes this workgroup the last one
+        // (both counters are left at zero)
+        int last = 0;
+        if (__hip_atomic_fetch_add(gcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 15) {
+            __hip_atomic_store(gcnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = __hip_atomic_fetch_add(tcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kTailArrGroups - 1;
+            if (last) __hip_atomic_store(tcnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_last = last;
     }
     __syncthreads();
     TAIL_STAMP(3);
-    if (!s_last) return;
+    if (!s_last) {
+        TAIL_FLUSH(0, 4);
+        return;
+    }
 
     // ---- the last workgroup: the chunk holding the inverse-CDF target
-    for (int i = tid; i < kTailChunks; i += kTailThreads) {
-        const unsigned long long lo = ld_coherent_u64(cw + (size_t)i * 3), hi = ld_coherent_u64(cw + (size_t)i * 3 + 1);
-        s_rc[i] = ((u128)hi << 64) | (u128)lo;
-        s_ce[i] = ld_coherent_u64(cw + (size_t)i * 3 + 2);
+    // (thread i < kTailChunks holds chunk i's sums)
+    u128 cv[1] = {0};
+    unsigned long long ce = 0;
+    if (tid < kTailChunks) {
+        const unsigned long long lo = ld_coherent_u64(cw + (size_t)tid * 3), hi = ld_coherent_u64(cw + (size_t)tid * 3 + 1);
+        cv[0] = ((u128)hi << 64) | (u128)lo;
+        ce = ld_coherent_u64(cw + (size_t)tid * 3 + 2);
     }
-    __syncthreads();
+    tail_sums(cv, kTailChunks, s_a, s_g, s_sg);
     TAIL_STAMP(4);
+    constexpr int kNs = (kTailChunks + 255) / 256;
+    u128 tot = 0;
+#pragma unroll
+    for (int j = 0; j < kNs; ++j) tot += s_sg[j];
+    int mode = mode0;
+    if (mode == 0 && tot == 0) {
+        // the residual is identically zero: sample from the target row
+        mode = 1;
+        cv[0] = (u128)ce;
+        tail_sums(cv, kTailChunks, s_a, s_g, s_sg);
+        tot = 0;
+#pragma unroll
+        for (int j = 0; j < kNs; ++j) tot += s_sg[j];
+    }
     if (wave == 0) {
-        const uint32_t U2 = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)n, 1);
-        u128 tot = 0;
-        for (int g = 0; g < kTailChunks; g += 64) tot += wave_sum_u128(s_rc[g + lane]);
-        int mode = mode0;
-        if (mode == 0 && tot == 0) {
-            // the residual is identically zero: sample from the target row
-            mode = 1;
-            tot = 0;
-            for (int g = 0; g < kTailChunks; g += 64) tot += wave_sum_u128((u128)s_ce[g + lane]);
-        }
         int chunk = -1;
         u128 rem = 0;
         if (tot != 0) {
-            const u128 tg = ((u128)U2 * tot) >> 24;
-            u128 run = 0;
-            for (int g = 0; g < kTailChunks && chunk < 0; g += 64) {
-                const u128 cs = mode == mode0 ? s_rc[g + lane] : (u128)s_ce[g + lane];
-                const u128 pre = wave_incl_scan_u128(cs) + run;
-                const unsigned long long hit = __ballot(pre > tg);
-                if (hit) {
-                    const int ln = __ffsll((long long)hit) - 1;
-                    chunk = g + ln;
-                    rem = tg - (shfl_u128(pre, ln) - shfl_u128(cs, ln));
-                }
-                run = shfl_u128(pre, 63);
-            }
+            const u128 tg = ((u128)s_U2[n] * tot) >> 24;
+            u128 before;
+            chunk = tail_pick(s_a, kTailChunks, s_g, s_sg, tg, &before);
+            if (chunk >= 0) rem = tg - before;  // tg minus the mass before the chunk
         }
         if (lane == 0) {
             s_chunk = chunk;
             s_rem = rem;
-            s_mode = mode;
-            s_owner = 0x7fffffff;
-            s_tok = 0;  // (as the chain: no crossing in the chunk gives token 0)
         }
     }
     __syncthreads();
+    TAIL_STAMP(5);
     const int cc = s_chunk;
+    int tok = 0;  // (as the chain: no crossing in the chunk gives token 0)
     if (cc >= 0) {
-        // ---- the token: the first v of the chunk (order v = b0 + u*T + tid)
-        // whose inclusive prefix exceeds the remaining target
-        const int mode = s_mode;
+        // ---- the token: the first v of the chunk (index order) whose
+        // inclusive prefix exceeds the remaining target
         const int cb0 = min(V, cc * clen), cb1 = min(V, cb0 + clen);
-        u128 rv[kTailPer];
+        float a[PER], b[PER];
 #pragma unroll
-        for (int u = 0; u < kTailPer; ++u) {
-            const int v = cb0 + tid + u * kTailThreads;
-            const float a = v < cb1 ? rowp(tr)[v] : __builtin_nanf("");
-            const float b = (mode == 0 && v < cb1) ? rowp(dr)[v] : 0.0f;
-            rv[u] = res_of(a, b, inv_t, mp, ap, mq, aq, Sp, Sq, mode);
+        for (int u = 0; u < PER; ++u) {
+            const int v = min(cb0 + tid + u * kTailThreads, cb1 - 1);
+            a[u] = rowp(tr)[v];
+            b[u] = mode == 0 ? rowp(dr)[v] : 0.0f;
         }
-        u128 base = 0;
+        u128 rv[PER];
 #pragma unroll
-        for (int u = 0; u < kTailPer; ++u) {
-            const u128 pre = wave_incl_scan_u128(rv[u]);
-            __syncthreads();
-            if (lane == 63) s_wtot[wave] = pre;
-            __syncthreads();
-            u128 wb = base;
-            for (int w = 0; w < wave; ++w) wb += s_wtot[w];
-            const unsigned long long hit = __ballot(wb + pre > s_rem);
-            if (hit && lane == __ffsll((long long)hit) - 1) atomicMin(&s_owner, tid);
-            __syncthreads();
-            if (s_owner != 0x7fffffff) {
-                if (tid == s_owner) s_tok = cb0 + u * kTailThreads + tid;
-                break;
-            }
-            for (int w = 0; w < kTailWaves; ++w) base += s_wtot[w];
+        for (int u = 0; u < PER; ++u)
+            rv[u] = cb0 + tid + u * kTailThreads < cb1 ? res_of(a[u], b[u], inv_t, mp, ap, mq, aq, Sp, Sq, mode)
+                                                      : (u128)0;
+        tail_sums(rv, cb1 - cb0, s_a, s_g, s_sg);
+        TAIL_STAMP(6);
+        if (wave == 0) {
+            u128 before;
+            const int e = tail_pick(s_a, cb1 - cb0, s_g, s_sg, s_rem, &before);
+            if (e >= 0) tok = cb0 + e;
         }
-        __syncthreads();
     }
     if (tid == 0) {
         for (int i = 0; i < n; ++i) tokens[s * (k + 1) + i] = draft[s * k + i];
-        tokens[s * (k + 1) + n] = cc >= 0 ? s_tok : 0;
+        tokens[s * (k + 1) + n] = tok;
         for (int i = n + 1; i <= k; ++i) tokens[s * (k + 1) + i] = -1;
         n_acc[s] = n;
     }
-    TAIL_STAMP(5);
+    TAIL_STAMP(7);
+    TAIL_FLUSH(0, 8);
 }
 
 #ifdef FST_TRACE
@@ -988,7 +1167,7 @@ int tail_trace_read(void* host, size_t bytes) {
 
 // The tail launch applies when every row's chunk fits the registers.
 static bool tail_fits(int k, int V) {
-    return k >= 0 && 2 * k + 1 <= kTailRows && (V + kTailChunks - 1) / kTailChunks <= kTailPer * kTailThreads;
+    return k >= 0 && 2 * k + 1 <= kTailRows && (V + kTailChunks - 1) / kTailChunks <= kTailPerMax * kTailThreads;
 }
 
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
@@ -998,14 +1177,17 @@ void launch_accept_stochastic(hipStream_t st, const float* target, const float* 
     AccWs w = carve(ws, n_seq, k);
     const int n_tgt = n_seq * (k + 1);
     const int R = n_tgt + n_seq * k;
+    const bool use_tail = tail && tail_fits(k, V);
     hipLaunchKernelGGL(acc_stats_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
                        inv_t, w.part_max, w.part_idx);
     hipLaunchKernelGGL(acc_sums_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
-                       inv_t, w.part_max, w.part_idx, w.part_sum);
-    if (tail && tail_fits(k, V)) {
-        hipLaunchKernelGGL(acc_tail_kernel, dim3(kTailChunks, n_seq), dim3(kTailThreads), 0, st, target,
-                           draft_logits, n_seq, k, V, inv_t, draft, seed, seq_base, w.part_max, w.part_idx,
-                           w.part_sum, w.tail, n_acc, tokens);
+                       inv_t, w.part_max, w.part_idx, w.part_sum, draft, k, use_tail ? w.xsel : nullptr);
+    if (use_tail) {
+        // one element per thread while the chunks fit, else two
+        auto kern = (V + kTailChunks - 1) / kTailChunks <= kTailThreads ? acc_tail_kernel<1> : acc_tail_kernel<2>;
+        hipLaunchKernelGGL(kern, dim3(kTailChunks, n_seq), dim3(kTailThreads), 0, st, target, draft_logits, n_seq,
+                           k, V, inv_t, draft, seed, seq_base, w.part_max, w.part_idx, w.part_sum, w.xsel, w.tail,
+                           n_acc, tokens);
         return;
     }
     hipLaunchKernelGGL(acc_decide_kernel, dim3(n_seq), dim3(64 * kDecideWaves), 0, st, target, draft_logits, n_seq, k, V,

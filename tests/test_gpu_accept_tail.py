@@ -57,7 +57,7 @@ def run_both(fa, ctx, t, d, draft, temp, seed, base):
 
 
 @pytest.mark.parametrize("n_seq,k,V", [(1, 7, 129280), (4, 7, 129280), (2, 3, 1000), (1, 8, 262144),
-                                       (3, 1, 4099), (1, 0, 5000)])
+                                       (3, 1, 4099), (1, 0, 5000), (2, 2, 5), (1, 4, 131072), (1, 4, 131073)])
 def test_fused_rejection_sampling_matches_chain_and_oracle(fa, oracle, acc_ctx, n_seq, k, V):
     ctx = acc_ctx
     t, d, draft = case(fa, 500 + V % 97 + k, n_seq, k, V, special=(V > 4000))
@@ -87,3 +87,22 @@ def test_fused_rejection_sampling_repeated_calls(fa, acc_ctx):
         assert np.array_equal(na, nb)
         for s in range(n_seq):
             assert np.array_equal(ta[s, : na[s] + 1], tb[s, : nb[s] + 1])
+
+
+@pytest.mark.parametrize("V", [129280, 777])
+def test_fused_rejection_sampling_zero_residual(fa, oracle, acc_ctx, V):
+    """Draft rows equal to the target rows and a draft token of zero mass: the
+    first position is rejected and the residual is identically zero, so the
+    token is drawn from the target row instead (both paths and the oracle)."""
+    ctx = acc_ctx
+    k = 3
+    t, _, _ = case(fa, 900 + V % 13, 1, k, V)
+    t[0, 0, 11] = -np.inf
+    d = np.ascontiguousarray(t[:, :k].copy())
+    draft = np.array([[11, 2, 3]], np.int32)
+    for seed in range(3):
+        note("zero residual V=%d seed=%d" % (V, seed))
+        (na, ta), (nb, tb) = run_both(fa, ctx, t, d, draft, 1.0, seed, 7)
+        rn, rt = oracle.accept_stochastic(t[0], d[0], draft[0], 1.0, seed, 7)
+        assert rn == 0 and na[0] == 0 and nb[0] == 0
+        assert np.array_equal(ta[0, :1], rt) and np.array_equal(tb[0, :1], rt)
