@@ -87,6 +87,8 @@ _SIGS = {
     "fst_dequant": (C.c_int, [P, C.c_int, P, SZ, P, P]),
     "fst_set_profiling": (C.c_int, [P, C.c_int]),
     "fst_last_timings": (C.c_int, [P, P]),
+    "fst_kernel_ring": (C.c_int, [P, C.c_int]),
+    "fst_kernel_ring_read": (C.c_int, [P, P, C.c_int, P]),
     "fst_last_active_experts": (C.c_int, [P, P]),
     "fst_device_copy": (C.c_int, [P, P, P, SZ]),
     "fst_upload_norm": (C.c_int, [P, C.c_int, P]),
@@ -458,6 +460,15 @@ class Context:
         t = fst_timings()
         _check(lib().fst_last_timings(self.h, C.byref(t)))
         return [(t.name[i].decode(), t.ms[i]) for i in range(t.n)]
+
+    def kernel_ring(self, capacity):
+        _check(lib().fst_kernel_ring(self.h, int(capacity)))
+
+    def kernel_ring_read(self, max_n=65536):
+        buf = np.zeros(max_n, np.float32)
+        n = C.c_int()
+        _check(lib().fst_kernel_ring_read(self.h, _ptr(buf), max_n, C.byref(n)))
+        return buf[: n.value].copy()
 
     def last_active_experts(self):
         n = C.c_int()

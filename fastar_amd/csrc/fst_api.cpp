@@ -99,6 +99,11 @@ struct fst_ctx {
     std::vector<const char*> ev_names;
     int n_ev = 0;
     fst_timings last{};
+    // kernel ring: start/stop event pairs taken by the dominant launch of
+    // consecutive calls (no synchronisation until read)
+    std::vector<hipEvent_t> kev;
+    int kev_n = 0;
+    bool kring = false;
 
     ~fst_ctx() {
         if (st) (void)hipStreamSynchronize(st);
@@ -115,6 +120,7 @@ struct fst_ctx {
         if (samp_ws) (void)hipFree(samp_ws);
         if (head_logits) (void)hipFree(head_logits);
         for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+        for (hipEvent_t e : kev) (void)hipEventDestroy(e);
         if (st) (void)hipStreamDestroy(st);
     }
 
@@ -351,6 +357,34 @@ int fst_last_timings(fst_ctx* ctx, fst_timings* out) {
     return FST_OK;
 }
 
+int fst_kernel_ring(fst_ctx* ctx, int capacity) {
+    if (!ctx) return fail(FST_EINVAL, "null context");
+    if (capacity < 0 || capacity > 65536) return fail(FST_EINVAL, "capacity must be in [0, 65536]");
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    while ((int)ctx->kev.size() < 2 * capacity) {
+        hipEvent_t e;
+        FST_HIP_TRY(hipEventCreate(&e));
+        ctx->kev.push_back(e);
+    }
+    ctx->kring = capacity > 0;
+    ctx->kev_n = 0;
+    return FST_OK;
+}
+
+int fst_kernel_ring_read(fst_ctx* ctx, float* us, int max_n, int* n) {
+    if (!ctx || !n || (max_n > 0 && !us)) return fail(FST_EINVAL, "null argument");
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    const int cnt = std::min(ctx->kev_n, std::max(max_n, 0));
+    for (int i = 0; i < cnt; ++i) {
+        float ms = 0.0f;
+        FST_HIP_TRY(hipEventElapsedTime(&ms, ctx->kev[2 * i], ctx->kev[2 * i + 1]));
+        us[i] = ms * 1e3f;
+    }
+    *n = cnt;
+    ctx->kev_n = 0;
+    return FST_OK;
+}
+
 int fst_device_copy(fst_ctx* ctx, void* d_dst, const void* d_src, size_t bytes) {
     if (!ctx || !d_dst || !d_src) return fail(FST_EINVAL, "null argument");
     if (bytes % 16) return fail(FST_EINVAL, "bytes must be a multiple of 16");
@@ -583,7 +617,13 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     if (fuse_topk && ctx->fused && use_routed && fst::moe_fused_supported(g, M)) {
         // gate||up and down in one persistent launch, then the combine
         ctx->fused_epoch = ctx->fused_epoch == 0xffffffffu ? 1u : ctx->fused_epoch + 1u;
-        fst::launch_moe_fused(st, g, L, M, ctx->s, rq, ctx->fused_epoch, ctx->spin_limit);
+        hipEvent_t k0 = nullptr, k1 = nullptr;
+        if (ctx->kring && 2 * ctx->kev_n + 1 < (int)ctx->kev.size()) {
+            k0 = ctx->kev[2 * ctx->kev_n];
+            k1 = ctx->kev[2 * ctx->kev_n + 1];
+            ++ctx->kev_n;
+        }
+        fst::launch_moe_fused(st, g, L, M, ctx->s, rq, ctx->fused_epoch, ctx->spin_limit, k0, k1);
         ctx->mark("moe_fused");
         // (a bf16 shared expert ran above; its fp32 rows are the combine's shared term)
         fst::launch_combine_tj(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out,

@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "fst_internal.h"
+#include <hip/hip_ext.h>
 #include "fst_q4k_dev.h"
 #include "../../include/fst_exact_math.h"
 
@@ -2064,7 +2065,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 }
 
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
-                     const RouteReq& rq, uint32_t epoch, int spin_limit) {
+                     const RouteReq& rq, uint32_t epoch, int spin_limit, hipEvent_t ev0, hipEvent_t ev1) {
     const RouteArgs ra = route_args(g, L, M, s.logits, rq.input_ids, rq.use_hash, rq.use_shared, rq.eids, rq.wts, s);
     FusedArgs fa{};
     fa.bank = L.bank;
@@ -2086,7 +2087,11 @@ int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int 
     const unsigned items = (unsigned)s.max_slots * (unsigned)(g.inter / 64 + g.hd / 128);
     const dim3 grid(std::min(items, (unsigned)s.n_cu * 2u));
     fa.singles = (int)grid.x;
-    if (g.hd == 4096 && g.inter == 2048)
+    // with events: they take the dispatch's own start and end times (the
+    // kernel's duration, without the gap to the previous launch)
+    if (g.hd == 4096 && g.inter == 2048 && ev0)
+        hipExtLaunchKernelGGL((moe_fused_kernel<4096, 2048>), grid, dim3(64 * kFuW), 0, st, ev0, ev1, 0, fa, ra);
+    else if (g.hd == 4096 && g.inter == 2048)
         hipLaunchKernelGGL((moe_fused_kernel<4096, 2048>), grid, dim3(64 * kFuW), 0, st, fa, ra);
     else
         return set_error(1, "fused MoE launch: geometry without an instantiation");

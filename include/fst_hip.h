@@ -210,6 +210,13 @@ typedef struct fst_timings {
 } fst_timings;
 int fst_set_profiling(fst_ctx* ctx, int on);
 int fst_last_timings(fst_ctx* ctx, fst_timings* out);
+/* Kernel ring: with capacity > 0, the next `capacity` fused MoE launches
+ * (router-driven calls of at most 8 tokens) record their dispatch's start and
+ * end times in HIP events, with no synchronisation between calls; 0 turns it
+ * off.  fst_kernel_ring_read synchronises the stream, writes up to max_n
+ * kernel durations in microseconds, sets *n and empties the ring. */
+int fst_kernel_ring(fst_ctx* ctx, int capacity);
+int fst_kernel_ring_read(fst_ctx* ctx, float* us, int max_n, int* n);
 /* Plain streaming copy kernel (16-byte vector loads/stores) used to calibrate
  * hardware byte counters against a known traffic volume.  Asynchronous. */
 int fst_device_copy(fst_ctx* ctx, void* d_dst, const void* d_src, size_t bytes);
