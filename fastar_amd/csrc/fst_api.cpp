@@ -1354,8 +1354,9 @@ int fst_verify_forward(fst_ctx* ctx, uint16_t* h, int M, const int32_t* input_id
     const size_t hbytes = (size_t)M * (hc ? 4 : 1) * hd * 2;
     uint16_t* d_res = hc ? ctx->hc_h : ctx->s.h;
     const size_t nlog = (size_t)M * c.vocab_size;
-    float* d_logits = nullptr;
-    FST_HIP_TRY(hipMalloc(&d_logits, nlog * sizeof(float)));
+    // the context's logits buffer (grown once, shared with fst_final_head)
+    if (int rc = grow(ctx->st, (void**)&ctx->head_logits, &ctx->head_logits_cap, nlog * sizeof(float))) return rc;
+    float* d_logits = ctx->head_logits;
     int rc = FST_OK;
     do {
         if (hipMemcpyAsync(d_res, h, hbytes, hipMemcpyHostToDevice, ctx->st) != hipSuccess ||
@@ -1373,7 +1374,6 @@ int fst_verify_forward(fst_ctx* ctx, uint16_t* h, int M, const int32_t* input_id
         rc = check_meta_error(ctx);
     } while (0);
     (void)hipStreamSynchronize(ctx->st);  // (the error, if any, is already in rc)
-    (void)hipFree(d_logits);
     return rc;
 }
 
