@@ -623,7 +623,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
             k1 = ctx->kev[2 * ctx->kev_n + 1];
             ++ctx->kev_n;
         }
-        fst::launch_moe_fused(st, g, L, M, ctx->s, rq, ctx->fused_epoch, ctx->spin_limit, k0, k1);
+        fst::launch_moe_fused(st, g, L, M, ctx->s, rq, ctx->fused_epoch, ctx->spin_limit, d_h, k0, k1);
         ctx->mark("moe_fused");
         // (a bf16 shared expert ran above; its fp32 rows are the combine's shared term)
         fst::launch_combine_tj(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out,

@@ -334,8 +334,8 @@ int launch_expert_gemv(hipStream_t st, const Geometry& g, const LayerView& L, in
 void launch_combine_tj(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s, const float* wts,
                        const float* ys, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
-                     const RouteReq& rq, uint32_t epoch, int spin_limit, hipEvent_t ev0 = nullptr,
-                     hipEvent_t ev1 = nullptr);
+                     const RouteReq& rq, uint32_t epoch, int spin_limit, const uint16_t* h,
+                     hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 // With o1/o2 (one routed pair per token, no shared expert) it writes
 // out = bf16(wts[token] * y) there instead of y, and no combine is needed.
 void launch_q4k_down(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,

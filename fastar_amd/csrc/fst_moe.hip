@@ -1622,9 +1622,15 @@ __device__ __forceinline__ float row16_fmax(float x) {
     return x;
 }
 
-template <int HD, int INTER>
+// CODEC 0: Q4_K experts, fp16 operands with power-of-two prescales, fp16
+// MFMA; 1: MXFP4 experts, bf16 operands (the input rows as they are, h
+// rounded to bf16), bf16 MFMA, as in q4k_linear_kernel's MXFP4 path.
+template <int HD, int INTER, int CODEC>
 __global__ __launch_bounds__(64 * kFuW) __attribute__((amdgpu_waves_per_eu(FST_Q4K_WAVES_PER_EU))) void
 moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
+    constexpr bool MX = CODEC == 1;
+    constexpr int CHK = MX ? 2176 : kFuChunk;     // bytes per 16 rows x 256 weights
+    constexpr int PARTS = MX ? 32 : kFuParts;     // staged chunks per token per super-block
     static_assert(INTER % 1024 == 0 && INTER <= 256 * kFuMaxDnSb && HD % 512 == 0, "fused geometry");
     constexpr int NT = 64 * kFuW;
     constexpr int NS = (kFuNCH + NT - 1) / NT;
@@ -1657,7 +1663,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         uint4 pfv[3];
         const int npf = ra.use_shared ? 3 : 0;
         {
-            const size_t pieces = (size_t)(2 * inter / 16) * (hd >> 8) * (kFuChunk / 16);
+            const size_t pieces = (size_t)(2 * inter / 16) * (hd >> 8) * (CHK / 16);
             const uint4* src = reinterpret_cast<const uint4*>(bank + (size_t)ra.E * stride);
             const size_t step = (size_t)gridDim.x * NT;
 #pragma unroll
@@ -1712,7 +1718,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     const int r = lane & 15, g = lane >> 4;
     constexpr int nsb_gu = hd >> 8, nsb_dn = inter >> 8;
     constexpr int aw = inter / 16;  // amax words per pair
-    constexpr size_t proj = (size_t)inter * (hd / 256) * 144;
+    constexpr size_t proj = (size_t)inter * (hd / 256) * (MX ? 136 : 144);
     const f4_t zf = f4_t{0.f, 0.f, 0.f, 0.f};
     const uint32_t magic = 0x64006400u;
     const uint32_t ssel = q4k_scale_sel(g);
@@ -1754,23 +1760,30 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         if (tt < ngu) {
             const int sl = tt / tiles_gu, ti = tt - sl * tiles_gu;
             const int wt = wave < kFuHalf ? ti * kFuHalf + wave : inter / 16 + ti * kFuHalf + (wave - kFuHalf);
-            return bank + (size_t)r_seid[sl] * stride + (size_t)wt * nsb_gu * kFuChunk;
+            return bank + (size_t)r_seid[sl] * stride + (size_t)wt * nsb_gu * CHK;
         }
         int sl, ti;
         dn_map(tt - ngu, sl, ti);
-        return bank + (size_t)r_seid[sl] * stride + 2 * proj + (size_t)(ti * kFuW + wave) * nsb_dn * kFuChunk;
+        return bank + (size_t)r_seid[sl] * stride + 2 * proj + (size_t)(ti * kFuW + wave) * nsb_dn * CHK;
     };
     auto rsrc = [&](const uint8_t* p, int nsb) -> __amdgpu_buffer_rsrc_t {
         const uint64_t u = (uint64_t)(uintptr_t)p;
         const uint64_t us = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
                             (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
-        return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)us, (short)0, nsb * kFuChunk, 0x00020000);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)us, (short)0, nsb * CHK, 0x00020000);
     };
     auto item_rsrc = [&](int tt) { return rsrc(wave_base(tt), tt < ngu ? nsb_gu : nsb_dn); };
     constexpr int kNT = FST_WNT;
     auto load_w = [&](__amdgpu_buffer_rsrc_t rs, int off) -> WRaw {
         WRaw x;
-        x.h = __builtin_amdgcn_raw_buffer_load_b128(rs, 2048 + 16 * (lane & 15), off, kNT);
+        if constexpr (MX) {
+            // (the scale bytes first, as the Q4_K header, for the same reason)
+            typedef uint32_t u2v_t __attribute__((ext_vector_type(2)));
+            const u2v_t hv = __builtin_amdgcn_raw_buffer_load_b64(rs, 2048 + 8 * (lane & 15), off, kNT);
+            x.h = u4v_t{hv.x, hv.y, 0u, 0u};
+        } else {
+            x.h = __builtin_amdgcn_raw_buffer_load_b128(rs, 2048 + 16 * (lane & 15), off, kNT);
+        }
         x.a = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, off, kNT);
         x.b = __builtin_amdgcn_raw_buffer_load_b128(rs, 1024 + 16 * lane, off, kNT);
         return x;
@@ -1786,8 +1799,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 
     // gate||up staging (one chunk per thread per super-block): chunk tid of a
     // stage -> (token stl, part spart); down items stage nothing here
-    const int stl = tid < kFuNCH ? tid / kFuParts : kFuT;
-    const int spart = tid - (tid / kFuParts) * kFuParts;
+    const int stl = tid < kFuT * PARTS ? tid / PARTS : kFuT;
+    const int spart = tid - (tid / PARTS) * PARTS;
     auto load_row = [&](int tt) -> int {  // operand row of this thread's chunk in item tt (-1: none)
         if (tt >= ngu) return -1;
         const int sl = tt / tiles_gu;
@@ -1822,6 +1835,25 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     // rows at st (row stride rs uint4), accumulated into acc
     auto compute = [&](const uint4* st, const WRaw& cur, f4_t& acc) {
         const uint32_t Dw[8] = {cur.a.x, cur.a.y, cur.a.z, cur.a.w, cur.b.x, cur.b.y, cur.b.z, cur.b.w};
+        if constexpr (MX) {
+            // lane (g, r): blocks 2g (cur.a) and 2g+1 (cur.b) of row r; the
+            // hardware E2M1 conversion applies the block scale exactly
+            const uint32_t sw = g < 2 ? cur.h.x : cur.h.y;
+            const float s0 = e8m0_scale((sw >> ((g & 1) * 16)) & 0xffu);
+            const float s1 = e8m0_scale((sw >> ((g & 1) * 16 + 8)) & 0xffu);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const float sc = c < 4 ? s0 : s1;
+                const auto v0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 0);
+                const auto v1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 1);
+                const auto v2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 2);
+                const auto v3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(Dw[c], sc, 3);
+                const bf8_t b = {v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
+                const bf8_t a = __builtin_bit_cast(bf8_t, st[8 * g + c]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+            }
+            return;
+        }
         Q4kScale S;
         q4k_scales(cur.h, g, ssel, S);
         f4_t D = zf;
@@ -1882,6 +1914,37 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             constexpr int cpr = inter / 8;  // operand chunks per row
             const int nwd = Me * aw;        // maxima words of the slot's rows
             const int nch = Me * cpr;       // operand chunks of the slot's rows
+            if constexpr (MX) {
+                // bf16 operand: the slot's h words rounded to bf16, 8 per chunk
+                // in element order (no prescale, no sub-block sums)
+                for (int spin = 0; stage_op; ++spin) {
+                    int ok = 1;
+                    for (int base = 0; base < nch; base += NT) {
+                        const int qq = base + tid;
+                        const bool live = qq < nch;
+                        const int tl = live ? qq / cpr : 0, q = qq - (qq / cpr) * cpr;
+                        const int sb = q >> 5;
+                        const int rowb = ((off + tl) * inter + sb * 256 + 8 * (q & 31)) * 8;
+                        u4v_t hw[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) hw[i] = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16 * i, 0, 16);
+                        uint32_t o[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            if (live && (hw[i].y != epoch || hw[i].w != epoch)) ok = 0;
+                            o[i] = (uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].x)) |
+                                   ((uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].z)) << 16);
+                        }
+                        if (live) opb[tl * kFuOpStride + sb * 36 + (q & 31)] = make_uint4(o[0], o[1], o[2], o[3]);
+                    }
+                    if (__syncthreads_and(ok)) break;
+                    if (spin >= fa.spin_limit) {
+                        timed_out = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            } else {
             for (int spin = 0; stage_op; ++spin) {
                 int ok = 1;
                 unsigned long long mv[2];
@@ -1964,6 +2027,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 }
                 __builtin_amdgcn_s_sleep(2);
             }
+            }
             if (timed_out && tid == 0) atomicOr(&ra.meta[kMetaTimeout], 1);
             __syncthreads();
 #ifdef FST_TRACE
@@ -1994,7 +2058,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 stage_load(last || dn ? 0 : sb + 1);
                 const int pf = sb + 1;
                 const bool pnx = pf >= nsb;
-                w[(j + 1) & 1] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * kFuChunk);
+                w[(j + 1) & 1] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHK);
                 // gate||up items claim their successor four super-blocks
                 // before the end (issued after this step's loads, so only the
                 // publication one step later waits for it)
@@ -2021,7 +2085,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int tl = 4 * g + i;
-                    xg[(wave * 4 + i) * 64 + lane] = tl < Me ? ldexpf(acc[i], fa.xs[r_ptok[off + tl]]) : 0.0f;
+                    xg[(wave * 4 + i) * 64 + lane] =
+                        tl < Me ? (MX ? acc[i] : ldexpf(acc[i], fa.xs[r_ptok[off + tl]])) : 0.0f;
                 }
             }
             __syncthreads();
@@ -2034,7 +2099,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                     float m = 0.0f;
                     if (tl < Me) {
                         float gv = xg[((wave - kFuHalf) * 4 + i) * 64 + lane];
-                        float uv = ldexpf(acc[i], fa.xs[r_ptok[off + tl]]);
+                        float uv = MX ? acc[i] : ldexpf(acc[i], fa.xs[r_ptok[off + tl]]);
                         if (lim > 0.0f) {
                             gv = fminf(gv, lim);
                             uv = fminf(fmaxf(uv, -lim), lim);
@@ -2044,6 +2109,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                                         ((unsigned long long)epoch << 32) | fst_f32_bits(hv));
                         m = fabsf(hv);
                     }
+                    if (MX) continue;    // bf16 operands: no prescale, no maxima
                     m = row16_fmax(m);  // the 16 rows of this wave
                     if (r == 0 && tl < Me)
                         st_coherent_u64(fa.amaxw + (size_t)(off + tl) * aw + (n >> 4),
@@ -2055,7 +2121,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int tl = 4 * g + i;
-                if (tl < Me) fa.y[(size_t)r_yrow[off + tl] * hd + row] = ldexpf(acc[i], s_xs2[tl]);
+                if (tl < Me) fa.y[(size_t)r_yrow[off + tl] * hd + row] = MX ? acc[i] : ldexpf(acc[i], s_xs2[tl]);
             }
         }
     }
@@ -2065,12 +2131,14 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 }
 
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
-                     const RouteReq& rq, uint32_t epoch, int spin_limit, hipEvent_t ev0, hipEvent_t ev1) {
+                     const RouteReq& rq, uint32_t epoch, int spin_limit, const uint16_t* h, hipEvent_t ev0,
+                     hipEvent_t ev1) {
     const RouteArgs ra = route_args(g, L, M, s.logits, rq.input_ids, rq.use_hash, rq.use_shared, rq.eids, rq.wts, s);
     FusedArgs fa{};
     fa.bank = L.bank;
     fa.expert_stride = L.expert_stride;
-    fa.A = s.x16p;
+    // Q4_K: the fp16 operand the router launch prepared; MXFP4: the bf16 input rows
+    fa.A = g.codec == 1 ? reinterpret_cast<const _Float16*>(h) : s.x16p;
     fa.SX = s.sxp;
     fa.xs = s.xs;
     fa.hbuf = s.hbuf;
@@ -2089,18 +2157,28 @@ int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int 
     fa.singles = (int)grid.x;
     // with events: they take the dispatch's own start and end times (the
     // kernel's duration, without the gap to the previous launch)
-    if (g.hd == 4096 && g.inter == 2048 && ev0)
-        hipExtLaunchKernelGGL((moe_fused_kernel<4096, 2048>), grid, dim3(64 * kFuW), 0, st, ev0, ev1, 0, fa, ra);
+#define FST_FU(C)                                                                                               \
+    do {                                                                                                        \
+        if (ev0)                                                                                                \
+            hipExtLaunchKernelGGL((moe_fused_kernel<4096, 2048, C>), grid, dim3(64 * kFuW), 0, st, ev0, ev1, 0, fa, \
+                                  ra);                                                                          \
+        else                                                                                                    \
+            hipLaunchKernelGGL((moe_fused_kernel<4096, 2048, C>), grid, dim3(64 * kFuW), 0, st, fa, ra);         \
+    } while (0)
+    if (g.hd == 4096 && g.inter == 2048 && g.codec == 1)
+        FST_FU(1);
     else if (g.hd == 4096 && g.inter == 2048)
-        hipLaunchKernelGGL((moe_fused_kernel<4096, 2048>), grid, dim3(64 * kFuW), 0, st, fa, ra);
+        FST_FU(0);
     else
         return set_error(1, "fused MoE launch: geometry without an instantiation");
+#undef FST_FU
     return 0;
 }
 
 bool moe_fused_supported(const Geometry& g, int M) {
     // instantiated for the DeepSeek-V4-Flash-like expert (4096 -> 2048 -> 4096)
-    return g.codec == 0 && M <= kFuT && g.E <= kFusedRouteMaxExperts && g.hd == 4096 && g.inter == 2048;
+    return (g.codec == 0 || g.codec == 1) && M <= kFuT && g.E <= kFusedRouteMaxExperts && g.hd == 4096 &&
+           g.inter == 2048;
 }
 
 // Token capacity of the launch (the call's M bounds every slot's M_e): 8, 16,

@@ -93,3 +93,60 @@ def test_mxfp4_device_synth_matches_host(fa):
         a = ctx.expert_ffn(0, h, np.zeros((8, 1), np.int32), w)
         b = ctx.expert_ffn(0, h, np.ones((8, 1), np.int32), w)
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 8])
+def test_mxfp4_fused_launch_matches_chain(fa, mx_layer, M):
+    """Router-driven MXFP4 calls of at most 8 tokens run gate||up and down in
+    the fused launch (bf16 operands, h rounded to bf16 as the chain's
+    gate||up epilogue does): the same bits as the launch chain, on several
+    batches in a row (the epoch tags of one call must not leak into the
+    next), with the e = 0 / e = 255 blocks of expert 3 in play."""
+    ctx, experts, _ = mx_layer
+    try:
+        for b in range(3):
+            _log("mxfp4 fused vs chain M=%d batch %d" % (M, b))
+            h = fa.synth_normal_bf16(SEED, 500 + 10 * M + b, (M, HD))
+            ctx.set_fused(True)
+            out_f, e_f, w_f = ctx.moe_layer(0, h)
+            ctx.set_fused(False)
+            out_c, e_c, w_c = ctx.moe_layer(0, h)
+            assert np.array_equal(e_f, e_c) and np.array_equal(w_f.view(np.uint32), w_c.view(np.uint32))
+            assert np.array_equal(out_f, out_c)
+    finally:
+        ctx.set_fused(True)
+
+
+def test_mxfp4_c2_layer_fused_vs_chain_and_oracle(fa, oracle):
+    """The C2 shape with MXFP4 experts (256 routed + 1 shared, top-6, 8
+    tokens): the fused launch equals the chain bit for bit over 8 batches in a
+    row, and the first batch matches the oracle."""
+    E2, TK2, M = 256, 6, 8
+    with fa.Context(n_experts=E2, top_k=TK2, max_tokens=64, codec=fa.CODEC_MXFP4) as ctx:
+        ctx.synth_experts(SEED, 0, 0, E2 + 1, 0)
+        w = fa.synth_normal_bf16(SEED, 12, (HD, E2), 0.0, 0.02)
+        ctx.upload_router_bf16(0, w)
+        for b in range(8):
+            _log("mxfp4 C2 fused vs chain batch %d" % b)
+            h = fa.synth_normal_bf16(SEED, 600 + b, (M, HD))
+            ctx.set_fused(True)
+            out_f, e_f, w_f = ctx.moe_layer(0, h)
+            ctx.set_fused(False)
+            out_c, _, _ = ctx.moe_layer(0, h)
+            ctx.set_fused(True)
+            assert np.array_equal(out_f, out_c)
+            if b == 0:
+                e_ref, w_ref, _ = oracle.router(h, w, None, TK2)
+                assert np.array_equal(e_f, e_ref)
+                y = np.zeros((M, TK2, HD), np.float32)
+                for ex in sorted(set(int(v) for v in e_ref.ravel())):
+                    ye = oracle.expert_ffn(1, fa.synth_mxfp4_expert(SEED, ex), h)
+                    for m in range(M):
+                        for j in range(TK2):
+                            if e_ref[m, j] == ex:
+                                y[m, j] = ye[m]
+                ys = oracle.expert_ffn(1, fa.synth_mxfp4_expert(SEED, E2), h)
+                _, ref = oracle.combine(y, ys, w_ref)
+                err = rel_l2(bf16_to_f32(out_f), ref)
+                _log("rel_l2", err)
+                assert err < TOL
