@@ -87,6 +87,7 @@ struct GemvArgs {
     float swiglu_limit;
     uint32_t epoch;
     int spin_limit;
+    int dn_delay;          // s_sleep(8) rounds before the down workgroups' weight loads
 };
 
 __device__ __forceinline__ void st_coherent_f32(float* p, float v) {
@@ -597,6 +598,11 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
 #if defined(FST_GV_EXP) && FST_GV_EXP == 2
     if (!dn) load_weights();  // measurement build: down weights after the poll
 #else
+    // down workgroups start their weight loads after the gate||up ones have
+    // had a head start (dn_delay sleeps), so the gate||up weights, which the
+    // whole launch waits on, do not share the memory bandwidth at first
+    if (dn)
+        for (int i = 0; i < a.dn_delay; ++i) __builtin_amdgcn_s_sleep(8);
     load_weights();
 #endif
 
@@ -823,6 +829,8 @@ int launch_expert_gemv(hipStream_t st, const Geometry& g, const LayerView& L, in
     a.swiglu_limit = g.swiglu_limit;
     a.epoch = epoch;
     a.spin_limit = spin_limit;
+    static const int dn_delay = getenv("FST_GV_DNDELAY") ? atoi(getenv("FST_GV_DNDELAY")) : 9;  // A/B switch
+    a.dn_delay = dn_delay;
     a.ubuf = s.hbuf + (size_t)s.max_pairs * g.inter;
     static const bool valu = getenv("FST_GEMV_VALU") != nullptr;  // A/B switch for measurements
     if (valu)
