@@ -1250,9 +1250,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
         return q0 / (TOKS * PARTS) != q1 / (TOKS * PARTS) ? 0 : (q0 % (TOKS * PARTS)) / PARTS;
     };
     int st_me = 0;  // token count of the item the staging map belongs to
-    const u4v_t* ssrc[NS];
-    int sdst[NS];
-    int sstep[NS];
+    // The map keeps one int per chunk slot: the chunk's offset (16-byte
+    // units) in A (parts 0..31) or SX (parts 32..35) for the item's first
+    // macro-stage, or -1 when the slot has no live row.  Base, step and LDS
+    // destination follow from the slot's (u, token, part), which are fixed
+    // per thread, so they are formed at each use instead of being held in
+    // registers across the super-block loop.
+    int soff[NS];
     u4v_t sv[NS];
     // sbo: the item's first super-block within the row
     auto build_map = [&](const int* ar, int me, int sbo) {
@@ -1260,39 +1264,33 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int u = su[i], part = spart[i];
-            ssrc[i] = reinterpret_cast<const u4v_t*>(MX ? (const void*)A : (const void*)SX);
-            sdst[i] = ar[i] >= 0 ? u * TS + stl[i] * kTokStride + part : -1;
-            sstep[i] = 0;
-            if (ar[i] >= 0) {
-                if (part < 32) {
-                    ssrc[i] = reinterpret_cast<const u4v_t*>(A + (size_t)ar[i] * K) + (sbo + u) * 32 + part;
-                    sstep[i] = 32 * MS;
-                } else {
-                    ssrc[i] = reinterpret_cast<const u4v_t*>(SX + (size_t)ar[i] * nsb_row * 4 + (sbo + u) * 4 +
-                                                               (part - 32));
-                    sstep[i] = 4 * MS;
-                }
-            }
+            soff[i] = ar[i] < 0 ? -1
+                      : part < 32 ? ar[i] * (K / 8) + (sbo + u) * 32 + part
+                                  : (ar[i] * nsb_row + sbo + u) * 4 + (part - 32);
         }
     };
     // past nsb inside a partial macro-stage a chunk re-reads its first
-    // super-block (a valid address; the value is unused)
+    // super-block (a valid address; the value is unused); a slot without a
+    // live row reads the first chunk of its array
     auto stage_load = [&](int m) {
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
 #if FST_SKIP_DEAD_SLOTS
             if (i > 0 && st_me <= slot_minrow(i)) continue;
 #endif
+            const int part = spart[i];
             const bool live = m * MS + su[i] < nsb;
-            const size_t o = live ? (size_t)m * sstep[i] : 0;
-            sv[i] = ssrc[i][o];
+            const int o = soff[i] < 0 ? 0 : soff[i] + (live ? m * (part < 32 ? 32 * MS : 4 * MS) : 0);
+            const u4v_t* base = part < 32 ? reinterpret_cast<const u4v_t*>(A) : reinterpret_cast<const u4v_t*>(SX);
+            sv[i] = base[o];
         }
     };
     auto stage_store = [&](int m) {
         const int base = (m & 1) * STAGE;
 #pragma unroll
         for (int i = 0; i < NS; ++i)
-            if (sdst[i] >= 0) *reinterpret_cast<u4v_t*>(&lds[base + sdst[i]]) = sv[i];
+            if (soff[i] >= 0)
+                *reinterpret_cast<u4v_t*>(&lds[base + su[i] * TS + stl[i] * kTokStride + spart[i]]) = sv[i];
     };
     {
         int ar0[NS];
