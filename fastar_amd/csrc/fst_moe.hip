@@ -1805,26 +1805,20 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         const int Mi = min(r_sM[sl], kFuT), offi = r_soff[sl];
         return stl < Mi ? r_ptok[offi + stl] : -1;
     };
-    const u4v_t* ssrc;
-    int sdst, sstep;
+    // the chunk's 16-byte offset in A (parts 0..31) or SX (32..35) at the
+    // item's first super-block, -1 when this thread stages nothing
+    int soff;
     u4v_t sv;
     auto build_map = [&](int ar) {
-        ssrc = reinterpret_cast<const u4v_t*>(fa.SX);
-        sdst = ar >= 0 ? stl * kTokStride + spart : -1;
-        sstep = 0;
-        if (ar >= 0) {
-            if (spart < 32) {
-                ssrc = reinterpret_cast<const u4v_t*>(fa.A + (size_t)ar * hd) + spart;
-                sstep = 32;
-            } else {
-                ssrc = reinterpret_cast<const u4v_t*>(fa.SX + (size_t)ar * nsb_gu * 4 + (spart - 32));
-                sstep = 4;
-            }
-        }
+        soff = ar < 0 ? -1 : spart < 32 ? ar * (hd / 8) + spart : ar * nsb_gu * 4 + (spart - 32);
     };
-    auto stage_load = [&](int m) { sv = ssrc[(size_t)m * sstep]; };
+    auto stage_load = [&](int m) {
+        const int o = soff < 0 ? 0 : soff + m * (spart < 32 ? 32 : 4);
+        const u4v_t* base = spart < 32 ? reinterpret_cast<const u4v_t*>(fa.A) : reinterpret_cast<const u4v_t*>(fa.SX);
+        sv = base[o];
+    };
     auto stage_store = [&](int m) {
-        if (sdst >= 0) *reinterpret_cast<u4v_t*>(&lds[(m & 1) * kFuTS + sdst]) = sv;
+        if (soff >= 0) *reinterpret_cast<u4v_t*>(&lds[(m & 1) * kFuTS + stl * kTokStride + spart]) = sv;
     };
     build_map(load_row(blockIdx.x));
     stage_load(0);
