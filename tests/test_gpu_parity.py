@@ -135,6 +135,26 @@ def test_invalid_expert_rejected(fa, small_ctx):
     assert ei.value.code == fa.FST_EINVAL
 
 
+def test_token_count_bounds(fa, oracle, small_ctx):
+    """M = 0 and M = max_tokens + 1 are argument errors (the reference's
+    process_expert_ffn divides by M, src/fst_engine.cpp:4070), and a valid
+    call right after them is unaffected."""
+    ctx, experts = small_ctx
+    for M in (0, 65):
+        h = np.zeros((M, HD), np.uint16)
+        note("token bound M", M)
+        with pytest.raises(fa.FstError) as ei:
+            ctx.expert_ffn(0, h, np.zeros((M, 1), np.int32), np.ones((M, 1), np.float32))
+        assert ei.value.code == fa.FST_EINVAL
+        with pytest.raises(fa.FstError) as ei:
+            ctx.shared_expert(0, h)
+        assert ei.value.code == fa.FST_EINVAL
+    h = fa.synth_normal_bf16(5, 1, (1, HD))
+    got = bf16_to_f32(ctx.expert_ffn(0, h, np.array([[2]], np.int32), np.ones((1, 1), np.float32)))
+    ref = oracle.expert_ffn(0, experts[2], h)
+    assert rel_l2(got, ref) < FFN_TOL
+
+
 def test_known_answer_ones(fa, oracle):
     """ones@ones: every weight 1.0 (d=1, sc=1, q=1, dmin=0) and h = 1 gives
     g = u = 4096, act = silu(4096)*4096, y = 2048*act for every output."""
