@@ -103,6 +103,7 @@ struct fst_ctx {
     // consecutive calls (no synchronisation until read)
     std::vector<hipEvent_t> kev;
     int kev_n = 0;
+    int kev_cap = 0;  // launches the ring records (its events may be more)
     bool kring = false;
 
     ~fst_ctx() {
@@ -367,6 +368,7 @@ int fst_kernel_ring(fst_ctx* ctx, int capacity) {
         ctx->kev.push_back(e);
     }
     ctx->kring = capacity > 0;
+    ctx->kev_cap = capacity;
     ctx->kev_n = 0;
     return FST_OK;
 }
@@ -618,7 +620,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
         // gate||up and down in one persistent launch, then the combine
         ctx->fused_epoch = ctx->fused_epoch == 0xffffffffu ? 1u : ctx->fused_epoch + 1u;
         hipEvent_t k0 = nullptr, k1 = nullptr;
-        if (ctx->kring && 2 * ctx->kev_n + 1 < (int)ctx->kev.size()) {
+        if (ctx->kring && ctx->kev_n < ctx->kev_cap) {
             k0 = ctx->kev[2 * ctx->kev_n];
             k1 = ctx->kev[2 * ctx->kev_n + 1];
             ++ctx->kev_n;

@@ -36,3 +36,12 @@ def test_kernel_ring_records_fused_launches(fa, c2_layer):
         ctx.set_fused(True)
         ctx.kernel_ring(0)
     assert np.array_equal(o, ref)  # the two paths agree bit for bit
+    # a smaller capacity after a larger one records only that many launches
+    ctx.kernel_ring(8)
+    ctx.kernel_ring(2)
+    try:
+        for _ in range(4):
+            ctx.moe_layer(0, h)
+        assert len(ctx.kernel_ring_read()) == 2
+    finally:
+        ctx.kernel_ring(0)
