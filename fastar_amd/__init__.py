@@ -83,6 +83,8 @@ _SIGS = {
     "fst_sample_token": (C.c_int, [P, P, C.c_int, C.c_float, C.c_float, U64, U64, P]),
     "fst_sample_token_dev": (C.c_int, [P, P, C.c_int, C.c_int, C.c_float, C.c_float, U64, U64, P]),
     "fst_accept_check": (C.c_int, [P, C.c_int]),
+    "fst_moe_check": (C.c_int, [P]),
+    "fst_device_error_status": (C.c_int, [C.c_int]),
     "fst_accept_greedy_dev_noalloc": (C.c_int, [P, P, C.c_int, C.c_int, C.c_int, P, P, P]),
     "fst_dequant": (C.c_int, [P, C.c_int, P, SZ, P, P]),
     "fst_set_profiling": (C.c_int, [P, C.c_int]),
@@ -336,6 +338,14 @@ class Context:
 
     def set_fused(self, on):
         _check(lib().fst_set_fused(self.h, 1 if on else 0))
+
+    def moe_check(self):
+        """Sticky errors of the stream-ordered MoE calls since the last check
+        (raises FstError; clears them)."""
+        _check(lib().fst_moe_check(self.h))
+
+    def set_wait_limit(self, spins):
+        _check(lib().fst_set_wait_limit(self.h, spins))
 
     def set_small_m(self, on):
         _check(lib().fst_set_small_m(self.h, 1 if on else 0))

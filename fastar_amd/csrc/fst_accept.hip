@@ -780,27 +780,12 @@ void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k,
 // LDS: sums of 16-element groups and of 16-group super-groups, then one wave
 // locates the super-group, the group and the element, each level by a
 // ballot over per-lane prefix sums of at most 16 terms (no u128 wave scans).
-#ifdef FST_TRACE
-// per workgroup: wall-clock stamps kept in registers and written at the end
-// (a store per stamp would wait on its own round trip)
-__device__ long long g_tail_trace[1024][8];
-#define TAIL_STAMP(i)                                        \
-    do {                                                     \
-        if (tid == 0) tstamp[i] = wall_clock64();            \
-    } while (0)
-#define TAIL_FLUSH(i0, i1)                                                        \
-    do {                                                                          \
-        if (tid == 0 && blockIdx.x < 1024)                                        \
-            for (int q = i0; q < i1; ++q) g_tail_trace[blockIdx.x][q] = tstamp[q]; \
-    } while (0)
-#else
 #define TAIL_STAMP(i) \
     do {              \
     } while (0)
 #define TAIL_FLUSH(i0, i1) \
     do {                   \
     } while (0)
-#endif
 constexpr int kTailWaves = kTailThreads / 64;
 constexpr int kTailMaxN = kTailPerMax * kTailThreads;  // longest array searched
 constexpr int kTailGroups = kTailMaxN / 16;            // 16-element groups
@@ -945,9 +930,6 @@ __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
     __shared__ unsigned long long s_ew[kTailWaves];
     // the last workgroup's searches (s_sg padded to one 16-lane level)
     __shared__ u128 s_a[kTailMaxN], s_g[kTailGroups], s_sg[16];
-#ifdef FST_TRACE
-    long long tstamp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#endif
 
     TAIL_STAMP(0);
     // ---- loads, all issued before the first use: the row partials and the
@@ -1159,11 +1141,6 @@ __global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
     TAIL_FLUSH(0, 8);
 }
 
-#ifdef FST_TRACE
-int tail_trace_read(void* host, size_t bytes) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_tail_trace), bytes < sizeof(g_tail_trace) ? bytes : sizeof(g_tail_trace));
-}
-#endif
 
 // The tail launch applies when every row's chunk fits the registers.
 static bool tail_fits(int k, int V) {

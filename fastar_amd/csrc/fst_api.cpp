@@ -248,8 +248,6 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     fst_ctx* x = new fst_ctx();
     x->cfg = c;
     x->max_grid_y = prop.maxGridSize[1] > 0 ? prop.maxGridSize[1] : 65535;
-    x->fused = getenv("FST_NO_FUSED") == nullptr;  // A/B switch for measurements (fst_set_fused at run time)
-    x->gemv = getenv("FST_NO_GEMV") == nullptr;    // likewise (fst_set_small_m)
     int rc = FST_OK;
     auto bail = [&](int code) {
         delete x;
@@ -295,6 +293,10 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
     const int T = c.max_tokens, tk = c.top_k;
     s.max_tokens = T;
     s.n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    // the fused launch's down items wait for gate||up items of other
+    // workgroups, so its grid is only as large as the device holds at once
+    s.fused_per_cu = fst::moe_fused_occupancy(c.codec);
+    if (s.fused_per_cu < 1) x->fused = false;
     s.max_pairs = T * tk + T;
     s.max_slots = std::min(E, T * tk) + 1;
     const int P = s.max_pairs, S = s.max_slots;
@@ -568,8 +570,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     ctx->mark_begin();
     const bool mx = c.codec == FST_CODEC_MXFP4;  // bf16 operands: no fp16 operand prep
     // top-k + bucketing run inside the gate||up launch when the expert count allows
-    static const bool fuse_env = !getenv("FST_SEPARATE_TOPK");  // A/B switch for measurements
-    const bool fuse_topk = fuse_env && do_router && c.n_experts <= fst::kFusedRouteMaxExperts;
+    const bool fuse_topk = do_router && c.n_experts <= fst::kFusedRouteMaxExperts;
     const fst::RouteReq rq{d_ids, use_hash, use_shared && !sh16, d_eids, d_wts};
     if (do_router) {
         // logits and operand prep (Q4_K) in one launch, then (unless fused) top-k + bucketing
@@ -664,15 +665,38 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     return FST_OK;
 }
 
-static int check_meta_error(fst_ctx* ctx) {
-    int m[fst::META_WORDS];
-    FST_HIP_TRY(hipMemcpyAsync(m, ctx->s.meta, sizeof(m), hipMemcpyDeviceToHost, ctx->st));
-    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
-    if (m[fst::META_ERROR] & 1) return fail(FST_EINVAL, "expert id out of range in routing");
-    if (m[fst::META_ERROR] & 2) return fail(FST_EINVAL, "input id out of vocabulary range for hash routing");
-    if (m[5] & 1) return fail(FST_EHIP, "a cross-workgroup hand-off of the fused MoE launch exceeded its spin limit");
+// Status of the sticky error bits of the MoE path (meta[META_STICKY]).
+static int sticky_status(int flags) {
+    // (an input id out of range also leaves its token without valid experts:
+    // the hash message names the cause)
+    if (flags & fst::STICKY_HASH_ID) return fail(FST_EINVAL, "input id out of vocabulary range for hash routing");
+    if (flags & fst::STICKY_EXPERT_ID) return fail(FST_EINVAL, "expert id out of range in routing");
+    if (flags & fst::STICKY_TIMEOUT)
+        return fail(FST_EHIP, "a cross-workgroup hand-off of the MoE launch exceeded its spin limit");
     return FST_OK;
 }
+
+// Waits for the context's stream, reads the sticky error bits every MoE
+// launch since the last read ORed in, clears them, and turns them into a
+// status.
+static int check_meta_error(fst_ctx* ctx) {
+    int flags = 0;
+    FST_HIP_TRY(hipMemcpyAsync(&flags, ctx->s.meta + fst::META_STICKY, sizeof(int), hipMemcpyDeviceToHost, ctx->st));
+    FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    if (flags) {
+        const int zero = 0;
+        FST_HIP_TRY(hipMemcpyAsync(ctx->s.meta + fst::META_STICKY, &zero, sizeof(int), hipMemcpyHostToDevice, ctx->st));
+        FST_HIP_TRY(hipStreamSynchronize(ctx->st));
+    }
+    return sticky_status(flags);
+}
+
+int fst_moe_check(fst_ctx* ctx) {
+    if (!ctx) return fail(FST_EINVAL, "fst_moe_check: null context");
+    return check_meta_error(ctx);
+}
+
+int fst_device_error_status(int flags) { return sticky_status(flags); }
 
 // Device activation / logits buffers are read with 16-byte loads (null
 // pointers, i.e. absent optional buffers, pass).
@@ -858,7 +882,7 @@ int fst_accept_greedy_dev_noalloc(fst_ctx* ctx, const float* d_target, int n_seq
 
 int fst_set_fused(fst_ctx* ctx, int on) {
     if (!ctx) return fail(FST_EINVAL, "null context");
-    ctx->fused = on != 0;
+    ctx->fused = on != 0 && ctx->s.fused_per_cu > 0;
     return FST_OK;
 }
 
@@ -942,15 +966,6 @@ int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_
     return accept_host(ctx, target, draft_logits, n_seq, k, V, draft, temperature, seed, seq_base, n_acc, tokens, 1);
 }
 
-#ifdef FST_TRACE
-extern "C++" {
-namespace fst { int trace_read(void* host, size_t bytes); int gemv_trace_read(void* host, size_t bytes);
-                int tail_trace_read(void* host, size_t bytes); }
-}
-int fst_debug_trace_tail(void* host, size_t bytes) { return fst::tail_trace_read(host, bytes); }
-int fst_debug_trace(void* host, size_t bytes) { return fst::trace_read(host, bytes); }
-int fst_debug_trace_gemv(void* host, size_t bytes) { return fst::gemv_trace_read(host, bytes); }
-#endif
 
 // ------------------------------------------------------------ sample_token
 

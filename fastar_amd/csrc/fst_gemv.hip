@@ -1,41 +1,41 @@
 // fst_gemv.hip — the small-M expert FFN: caller-given routing (process_expert_ffn,
 // src/fst_engine.cpp:4068-4371, with process_shared_expert :4373-4489 as one more
 // slot and the combine :4196-4201, :2851-2852) for calls of at most two tokens, in
-// ONE launch with VALU dot products instead of MFMA tiles.
+// ONE launch.
 //
-// At one or two tokens a 16x16x32 MFMA uses one or two of its 16 token rows,
-// and the launch chain of the MFMA path (bucketing + operand prep, gate||up,
-// h prep, down) is four dependent launches, each a few microseconds of
-// dispatch and memory latency around a sub-microsecond stream of one expert's
-// 14 MB.  Here every workgroup finds the call's slots itself, and the work is
-// cut so that one expert spreads over the whole chip:
+// At one or two tokens the launch chain of the MFMA path (bucketing + operand
+// prep, gate||up, h prep, down) is four dependent launches, each a few
+// microseconds of dispatch and memory latency around a sub-microsecond stream
+// of one expert's 14 MB.  Here every workgroup finds the call's slots itself,
+// and the work is cut so that one expert spreads over the whole chip:
 //
-//   workgroups [0, S*inter/16): gate||up, one (slot, 16-row tile): 8 waves
-//     split K (super-blocks w, w+8, ...) over the gate and the up rows of the
-//     tile, partials summed across the 4 lanes of a row (row-pair and half
-//     swaps) and across the waves through LDS in wave order; h = silu(g)*u goes
-//     out as 64-bit words {epoch, h bits} with device-coherent stores.
-//   workgroups [S*inter/16, +S*hd/16): down, one (slot, 16-row tile): the
-//     weights are loaded first, then the slot's h words are polled (the epoch
-//     marks this call's words) into LDS as fp32, and the same dot runs over
-//     K = inter.  The down rows then go out with device-coherent stores, and
-//     the last slot's workgroup to finish a row tile (a per-tile counter,
-//     left at zero) sums the tile in the reference's order: routed pairs in
-//     slot order j = 0..tk-1, weighted, then the shared term; one RNE bf16
-//     rounding (the combine kernel's arithmetic).
+//   workgroups [0, S*2*inter/16): (slot, gate or up, 16-row tile): each of the
+//     8 waves takes two super-blocks of K, stages its own fp16 operand (per
+//     (token, super-block) a power-of-two prescale, k-interleaved, sub-block
+//     sums split hi+lo) and runs 8 v_mfma_f32_16x16x32_f16 over the exact fp16
+//     sc*q decode of the weights plus one for the min term; partials are summed
+//     across the waves through LDS in wave order, and the rows go out as 64-bit
+//     words {epoch, value} with device-coherent stores.
+//   workgroups [S*2*inter/16, +S*hd/16): (slot, 16-row down tile): the weights
+//     are loaded first, then each wave waits for its super-block of the gate
+//     and up words (the epoch marks this call's words), forms h = silu(g)*u and
+//     runs the same tile.  The down rows then go out with device-coherent
+//     stores, and the last slot's workgroup to finish a row tile (a per-tile
+//     counter, left at zero) sums the tile in the reference's order: routed
+//     pairs in slot order j = 0..tk-1, weighted, then the shared term; one RNE
+//     bf16 rounding (the combine kernel's arithmetic).
 //
 // Weight tile layout (16 rows x one super-block, 2304 bytes): lane 16g+r holds
 // bytes [32g, 32g+16) and [32g+16, 32g+32) of row r's nibbles, so its 64 weights
 // are sub-block 2g (low nibbles) and 2g+1 (high nibbles), and the headers
-// (fp16 d, fp16 dmin, 12 scale bytes) follow at byte 2048 + 16r.  Per sub-block
-// j the dot is d*sc_j*sum(q*x) - dmin*m_j*sum(x), with q*x in fp32 FMAs
-// (kernels/fst_dequant_q4k_kernel.cc:40-100 for the block decode) and the
-// sub-block sums of x precomputed once per workgroup.
+// (fp16 d, fp16 dmin, 12 scale bytes) follow at byte 2048 + 16r
+// (kernels/fst_dequant_q4k_kernel.cc:40-100 for the block decode).
 //
 // Waits: a down workgroup waits only for gate||up workgroups, which have lower
 // ids and never wait; workgroups are dispatched in id order on each XCD, so
 // every awaited workgroup is resident or done.  The wait is bounded by the
-// context's spin limit (past it: meta word 5 bit 0, and the call completes).
+// context's spin limit (past it: the sticky timeout bit of the meta words,
+// and the call completes).
 #include <algorithm>
 #include <cstdlib>
 #include "fst_internal.h"
@@ -52,24 +52,15 @@ constexpr int kGvMaxM = 2;          // tokens per call
 constexpr int kGvMaxK = 4096;       // hd and inter bounds (LDS)
 constexpr int kGvMaxPairs = kGvMaxM * kMaxTopK;
 constexpr int kGvMaxSlots = kGvMaxPairs + 1;
-constexpr int kMetaTimeoutWord = 5;
 #ifndef FST_GV_SLEEP
 #define FST_GV_SLEEP 4
 #endif
 
-#ifdef FST_TRACE
-// Timeline probe (measurement builds only): per workgroup, the wall clock
-// (100 MHz) at entry, after the slot list, when the weights are in, when the
-// operand is ready, and at exit.
-constexpr int kGvTraceWG = 1024;
-__device__ long long g_gv_trace[kGvTraceWG][16];
-#endif
 
-// fp32 activations in LDS with 4 floats of padding after every 64, so that
-// the 16-byte reads of the 4 lane groups (64 elements apart) fall in
-// different banks.
-__device__ __forceinline__ int xpad(int k) { return k + ((k >> 6) << 2); }
-constexpr int kGvXStride = kGvMaxK + (kGvMaxK >> 6) * 4;
+// s_sleep(8) rounds before the down workgroups' first weight loads, so that
+// the gate||up weights, which every down workgroup waits for, get the memory
+// bandwidth first (measured best at 8-10 rounds).
+constexpr int kGvDnDelay = 9;
 
 struct GemvArgs {
     const uint8_t* bank;
@@ -97,142 +88,6 @@ __device__ __forceinline__ void st_coherent_f32(float* p, float v) {
 __device__ __forceinline__ float ld_coherent_f32(const float* p) {
     return fst_bits_f32(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT));
-}
-
-// Sum of x over the 4 lanes r, r+16, r+32, r+48 (rows 0+1, then halves), in
-// every lane.
-__device__ __forceinline__ float row4_sum(float x) {
-    const uint32_t u = fst_f32_bits(x);
-    const auto p16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    x = fst_bits_f32((uint32_t)p16[0]) + fst_bits_f32((uint32_t)p16[1]);
-    const uint32_t v = fst_f32_bits(x);
-    const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return fst_bits_f32((uint32_t)p32[0]) + fst_bits_f32((uint32_t)p32[1]);
-}
-
-// One 2304-byte tile as one lane holds it.
-struct Tile {
-    uint4 lo, hi, hdr;
-};
-__device__ __forceinline__ Tile load_tile(const uint8_t* chunk, int lane) {
-    const uint4* c = reinterpret_cast<const uint4*>(chunk);
-    Tile t;
-    t.lo = c[lane];
-    t.hi = c[64 + lane];
-    t.hdr = c[128 + (lane & 15)];
-    return t;
-}
-
-// 6-bit scale and min of sub-block j from the 12 scale bytes (bytes 4..15 of
-// the header): the get_scale_min_k4 packing of the Q4_K block.
-__device__ __forceinline__ void scale_min(const uint4& hdr, int j, int& sc, int& m) {
-    // bytes 0-3 of the scales are hdr.y, 4-7 hdr.z, 8-11 hdr.w
-    const int sh = 8 * (j & 3);
-    const uint32_t by = hdr.y >> sh, bz = hdr.z >> sh, bw = hdr.w >> sh;
-    if (j < 4) {
-        sc = (int)(by & 63u);
-        m = (int)(bz & 63u);
-    } else {
-        sc = (int)((bw & 15u) | ((by >> 2) & 48u));
-        m = (int)(((bw >> 4) & 15u) | ((bz >> 2) & 48u));
-    }
-}
-
-// This lane's share of one tile's dot with NT token rows (LDS, padded fp32)
-// and their sub-block sums: sub-blocks 2g (low nibbles) and 2g+1 (high
-// nibbles) of super-block sb.  Each weight is converted once for all rows.
-template <int NT>
-__device__ __forceinline__ void tile_dot(const Tile& t, const float* const* xs, const float* const* sx, int sb, int g,
-                                         float* out) {
-    const int base = sb * 256 + 64 * g;
-    const uint32_t q[8] = {t.lo.x, t.lo.y, t.lo.z, t.lo.w, t.hi.x, t.hi.y, t.hi.z, t.hi.w};
-    float dl[NT], dh[NT];
-#pragma unroll
-    for (int n = 0; n < NT; ++n) dl[n] = dh[n] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t lo = q[k] & 0x0f0f0f0fu, hi = (q[k] >> 4) & 0x0f0f0f0fu;
-        const float l0 = (float)(lo & 0xffu), l1 = (float)((lo >> 8) & 0xffu), l2 = (float)((lo >> 16) & 0xffu),
-                    l3 = (float)(lo >> 24);
-        const float h0 = (float)(hi & 0xffu), h1 = (float)((hi >> 8) & 0xffu), h2 = (float)((hi >> 16) & 0xffu),
-                    h3 = (float)(hi >> 24);
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            const float4 xl = *reinterpret_cast<const float4*>(xs[n] + xpad(base + 4 * k));
-            const float4 xh = *reinterpret_cast<const float4*>(xs[n] + xpad(base + 32 + 4 * k));
-            dl[n] = fmaf(l0, xl.x, dl[n]);
-            dl[n] = fmaf(l1, xl.y, dl[n]);
-            dl[n] = fmaf(l2, xl.z, dl[n]);
-            dl[n] = fmaf(l3, xl.w, dl[n]);
-            dh[n] = fmaf(h0, xh.x, dh[n]);
-            dh[n] = fmaf(h1, xh.y, dh[n]);
-            dh[n] = fmaf(h2, xh.z, dh[n]);
-            dh[n] = fmaf(h3, xh.w, dh[n]);
-        }
-        // one dword at a time: the sums of this dword are complete before
-        // the later LDS reads issue (else all 64 x values of a row are live)
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-            if (k & 1) asm volatile("" : "+v"(dl[n]), "+v"(dh[n])::"memory");
-    }
-    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.hdr.x & 0xffffu));
-    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(t.hdr.x >> 16));
-    int sc0, m0, sc1, m1;
-    scale_min(t.hdr, 2 * g, sc0, m0);
-    scale_min(t.hdr, 2 * g + 1, sc1, m1);
-    const int j0 = sb * 8 + 2 * g;
-    const float ds0 = d * (float)sc0, ds1 = d * (float)sc1, dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-        const float pos = fmaf(ds0, dl[n], ds1 * dh[n]);
-        const float neg = fmaf(dm0, sx[n][j0], dm1 * sx[n][j0 + 1]);
-        out[n] += pos - neg;
-    }
-}
-
-// The dot of one lane's tiles (two super-blocks) with the slot's token rows
-// (mask: bit t = token t uses the slot), summed over the row's 4 lanes.
-template <int NTILE>
-__device__ __forceinline__ void tiles_dot(const Tile* tl, int nsb, int wave, int g, int mask, float (*xs)[kGvXStride],
-                                          float (*sx)[kGvMaxK / 32], float* res) {
-    float acc[2] = {0.0f, 0.0f};
-    if (mask == 3) {
-        const float* xp[2] = {xs[0], xs[1]};
-        const float* sp[2] = {sx[0], sx[1]};
-#pragma unroll
-        for (int i = 0; i < NTILE; ++i) {
-            const int sb = wave + kGvW * i;
-            if (sb < nsb) tile_dot<2>(tl[i], xp, sp, sb, g, acc);
-        }
-    } else {
-        const int t = mask == 2 ? 1 : 0;
-        const float* xp[1] = {xs[t]};
-        const float* sp[1] = {sx[t]};
-#pragma unroll
-        for (int i = 0; i < NTILE; ++i) {
-            const int sb = wave + kGvW * i;
-            if (sb < nsb) tile_dot<1>(tl[i], xp, sp, sb, g, acc + t);
-        }
-    }
-    res[0] = row4_sum(acc[0]);
-    res[1] = row4_sum(acc[1]);
-}
-
-// Sub-block sums of a row held in LDS: thread i sums elements [8i, 8i+8) in
-// order, then the 4 lanes of a 32-element sub-block add pairwise.
-__device__ __forceinline__ void subblock_sums(const float* xs, float* sx, int K, int tid) {
-    for (int i0 = 0; i0 < K / 8; i0 += kGvNT) {
-        const int i = i0 + tid;
-        float s = 0.0f;
-        if (i < K / 8) {
-            const float4 a = *reinterpret_cast<const float4*>(xs + xpad(8 * i));
-            const float4 b = *reinterpret_cast<const float4*>(xs + xpad(8 * i + 4));
-            s = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-        }
-        s = s + fdpp<0xb1>(s);  // quad_perm [1,0,3,2]
-        s = s + fdpp<0x4e>(s);  // quad_perm [2,3,0,1]
-        if (i < K / 8 && (i & 3) == 0) sx[i >> 2] = s;
-    }
 }
 
 // The call's slots as every workgroup derives them: distinct valid experts in
@@ -273,7 +128,8 @@ __device__ __forceinline__ void gemv_slots(const GemvArgs& a, GvSlots& S, int ti
         S.ns = ns;
         if (blockIdx.x == 0) {
             a.meta[META_ERROR] = err;
-            a.meta[kMetaTimeoutWord] = 0;
+            a.meta[META_TIMEOUT] = 0;
+            sticky_or(a.meta, err);
         }
     }
     __syncthreads();
@@ -340,183 +196,6 @@ __device__ __forceinline__ float swiglu(float gv, float uv, float lim) {
     return (gv / (1.0f + expf(-gv))) * uv;
 }
 
-__global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void expert_gemv_valu_kernel(GemvArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r = lane & 15, g = lane >> 4;
-    const int hd = a.hd, inter = a.inter, M = a.M, tk = a.tk;
-    __shared__ __attribute__((aligned(16))) float xs[kGvMaxM][kGvXStride];
-    __shared__ float sx[kGvMaxM][kGvMaxK / 32];
-    __shared__ float red[2][kGvW][kGvMaxM][16];
-    __shared__ GvSlots S;
-    __shared__ float ystage[kGvMaxM][16];
-
-#ifdef FST_TRACE
-    long long* trc = blockIdx.x < kGvTraceWG ? g_gv_trace[blockIdx.x] : nullptr;
-    if (trc && tid == 0) trc[0] = wall_clock64();
-#endif
-    gemv_slots(a, S, tid);
-#ifdef FST_TRACE
-    if (trc && tid == 0) trc[1] = wall_clock64();
-#endif
-    const int ns = __builtin_amdgcn_readfirstlane(S.ns);
-    const int tiles_gu = inter / 16, tiles_dn = hd / 16;
-    const int ngu = a.smax * tiles_gu;
-    const bool dn = (int)blockIdx.x >= ngu;
-    const int b = dn ? (int)blockIdx.x - ngu : (int)blockIdx.x;
-    const int slot = dn ? b / tiles_dn : b / tiles_gu;
-    const int rt = dn ? b - slot * tiles_dn : b - slot * tiles_gu;
-    const size_t proj = (size_t)inter * (hd / 256) * 144;
-
-    if (ns == 0) {
-        // no valid expert and no shared one: the combine's result is zero
-        if (dn && slot == 0 && tid < M * 16) {
-            const size_t o = (size_t)(tid >> 4) * hd + rt * 16 + (tid & 15);
-            if (a.out) a.out[o] = 0;
-            if (a.out_routed) a.out_routed[o] = 0;
-        }
-        return;
-    }
-    if (slot >= ns) return;
-    const int mask = __builtin_amdgcn_readfirstlane(S.slot_mask[slot]);
-    const uint8_t* ex = a.bank + (size_t)__builtin_amdgcn_readfirstlane(S.slot_e[slot]) * a.expert_stride;
-
-    if (!dn) {
-        // ---------------- gate||up: rows [16 rt, 16 rt + 16) of both
-        const int nsb = hd >> 8;
-        const uint8_t* wg = ex + (size_t)rt * nsb * 2304;
-        const uint8_t* wu = wg + proj;
-        // this wave's super-blocks w, w+8, ... (two tiles of each in flight)
-        Tile tg[2], tu[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int sb = wave + kGvW * i;
-            if (sb < nsb) {
-                tg[i] = load_tile(wg + (size_t)sb * 2304, lane);
-                tu[i] = load_tile(wu + (size_t)sb * 2304, lane);
-            }
-        }
-        // the token rows, bf16 -> fp32 into LDS, and their sub-block sums
-        for (int t = 0; t < M; ++t) {
-            for (int i = tid; i < hd / 8; i += kGvNT) {
-                const uint4 v = reinterpret_cast<const uint4*>(a.h + (size_t)t * hd)[i];
-                float4 p0, p1;
-                p0.x = fst_bits_f32(v.x << 16);
-                p0.y = fst_bits_f32(v.x & 0xffff0000u);
-                p0.z = fst_bits_f32(v.y << 16);
-                p0.w = fst_bits_f32(v.y & 0xffff0000u);
-                p1.x = fst_bits_f32(v.z << 16);
-                p1.y = fst_bits_f32(v.z & 0xffff0000u);
-                p1.z = fst_bits_f32(v.w << 16);
-                p1.w = fst_bits_f32(v.w & 0xffff0000u);
-                *reinterpret_cast<float4*>(&xs[t][xpad(8 * i)]) = p0;
-                *reinterpret_cast<float4*>(&xs[t][xpad(8 * i + 4)]) = p1;
-            }
-        }
-        __syncthreads();
-        for (int t = 0; t < M; ++t) subblock_sums(xs[t], sx[t], hd, tid);
-        __syncthreads();
-#ifdef FST_TRACE
-        if (trc && tid == 0) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            trc[2] = wall_clock64();
-        }
-#endif
-        {
-            float rg_[2], ru_[2];
-            tiles_dot<2>(tg, nsb, wave, g, mask, xs, sx, rg_);
-            tiles_dot<2>(tu, nsb, wave, g, mask, xs, sx, ru_);
-            if (g == 0) {
-                for (int t = 0; t < M; ++t) {
-                    red[0][wave][t][r] = rg_[t];
-                    red[1][wave][t][r] = ru_[t];
-                }
-            }
-        }
-        __syncthreads();
-        if (tid < M * 16) {
-            const int t = tid >> 4, rr = tid & 15;
-            if ((mask >> t) & 1) {
-                float gv = 0.0f, uv = 0.0f;
-                for (int w = 0; w < kGvW; ++w) {
-                    gv += red[0][w][t][rr];
-                    uv += red[1][w][t][rr];
-                }
-                const float hv = swiglu(gv, uv, a.swiglu_limit);
-                st_coherent_u64(a.hbuf + (size_t)(slot * M + t) * inter + rt * 16 + rr,
-                                ((unsigned long long)a.epoch << 32) | fst_f32_bits(hv));
-            }
-        }
-#ifdef FST_TRACE
-        if (trc && tid == 0) trc[4] = wall_clock64();
-#endif
-        return;
-    }
-
-    // ---------------- down: rows [16 rt, 16 rt + 16) of the slot's down matrix
-    const int nsb = inter >> 8;
-    const uint8_t* wd = ex + 2 * proj + (size_t)rt * nsb * 2304;
-    Tile td[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int sb = wave + kGvW * i;
-        if (sb < nsb) td[i] = load_tile(wd + (size_t)sb * 2304, lane);
-    }
-    // the slot's h rows: poll the words of this call's epoch into LDS
-    int timed_out = 0;
-    for (int spin = 0;; ++spin) {
-        int ok = 1;
-        for (int t = 0; t < M; ++t) {
-            if (!((mask >> t) & 1)) continue;
-            const unsigned long long* hw = a.hbuf + (size_t)(slot * M + t) * inter;
-            for (int i = tid; i < inter / 4; i += kGvNT) {
-                unsigned long long v[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) v[k] = ld_coherent_u64(hw + 4 * i + k);
-                float4 f;
-                f.x = fst_bits_f32((uint32_t)v[0]);
-                f.y = fst_bits_f32((uint32_t)v[1]);
-                f.z = fst_bits_f32((uint32_t)v[2]);
-                f.w = fst_bits_f32((uint32_t)v[3]);
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if ((uint32_t)(v[k] >> 32) != a.epoch) ok = 0;
-                *reinterpret_cast<float4*>(&xs[t][xpad(4 * i)]) = f;
-            }
-        }
-        if (__syncthreads_and(ok)) break;
-        if (spin >= a.spin_limit) {
-            timed_out = 1;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-    if (timed_out && tid == 0) atomicOr(&a.meta[kMetaTimeoutWord], 1);
-#ifdef FST_TRACE
-    if (trc && tid == 0) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        trc[3] = wall_clock64();
-    }
-#endif
-    for (int t = 0; t < M; ++t)
-        if ((mask >> t) & 1) subblock_sums(xs[t], sx[t], inter, tid);
-    __syncthreads();
-    {
-        float rd_[2];
-        tiles_dot<2>(td, nsb, wave, g, mask, xs, sx, rd_);
-        if (g == 0)
-            for (int t = 0; t < M; ++t) red[0][wave][t][r] = rd_[t];
-    }
-    __syncthreads();
-    float v = 0.0f;
-    if (tid < M * 16)
-        for (int w = 0; w < kGvW; ++w) v += red[0][w][tid >> 4][tid & 15];
-    gemv_tile_out(a, S, ystage, ns, slot, mask, rt, tid, v);
-#ifdef FST_TRACE
-    if (trc && tid == 0) trc[4] = wall_clock64();
-#endif
-}
-
 
 // 16 lanes' max (DPP within the row), then the row pair's (rows 0+1, 2+3).
 __device__ __forceinline__ float max32(float x) {
@@ -532,7 +211,7 @@ __device__ __forceinline__ float max32(float x) {
 constexpr int kGvMaxSb = kGvMaxK / 256;
 constexpr int kGvOpSb = 36;  // 32 operand chunks + 4 sub-block-sum chunks per super-block
 
-// MFMA variant: the same work split and hand-off, with each wave staging its
+// The launch: each wave stages its
 // own super-blocks' operand (no workgroup barrier before the dot products):
 // per (token, super-block) a power-of-two prescale from the 256 values' max,
 // the fp16 operand k-interleaved to match q4k_bop, and the sub-block sums
@@ -550,14 +229,7 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
     __shared__ GvSlots S;
     __shared__ float ystage[kGvMaxM][16];
 
-#ifdef FST_TRACE
-    long long* trc = blockIdx.x < kGvTraceWG ? g_gv_trace[blockIdx.x] : nullptr;
-    if (trc && tid == 0) trc[0] = wall_clock64();
-#endif
     gemv_slots(a, S, tid);
-#ifdef FST_TRACE
-    if (trc && tid == 0) trc[1] = wall_clock64();
-#endif
     const int ns = __builtin_amdgcn_readfirstlane(S.ns);
     // workgroups: (slot, gate or up, 16-row tile), then (slot, down tile)
     const int tiles_gu = inter / 16, tiles_dn = hd / 16;
@@ -595,16 +267,12 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
             if (sb < nsb) w0[i] = load_wraw(wbase + (size_t)sb * 2304, lane);
         }
     };
-#if defined(FST_GV_EXP) && FST_GV_EXP == 2
-    if (!dn) load_weights();  // measurement build: down weights after the poll
-#else
     // down workgroups start their weight loads after the gate||up ones have
     // had a head start (dn_delay sleeps), so the gate||up weights, which the
     // whole launch waits on, do not share the memory bandwidth at first
     if (dn)
         for (int i = 0; i < a.dn_delay; ++i) __builtin_amdgcn_s_sleep(8);
     load_weights();
-#endif
 
     // ---- this wave's operand: (token, super-block) pairs, two per pass
     // (lanes 0-31 and 32-63), lane q = 8 gq + c builds chunk (gq, c)
@@ -613,13 +281,16 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
     const int np = nT * nsw;
     const int q = lane & 31, gq = q >> 3, c = q & 7;
     int timed_out = 0;
+    // polls of this wave so far: the one-lane pre-poll and every later poll
+    // draw on one budget of spin_limit polls
+    int spent = 0;
     if (dn && np > 0) {
         // first wait on one word (the last row of the last gate and up tiles
         // of this wave's first super-block) with one lane: device-coherent
         // loads from every lane (or from one lane per source tile) slow the
         // gate||up weight streams measurably for the whole wait
         const size_t wo = (size_t)(slot * M + t0) * inter + wave * 256 + 255;
-        for (int spin = 0; spin < a.spin_limit; ++spin) {
+        for (; spent < a.spin_limit; ++spent) {
             int ready = 1;
             if (lane == 0) {
                 const unsigned long long gv = ld_coherent_u64(a.hbuf + wo), uv = ld_coherent_u64(a.ubuf + wo);
@@ -657,7 +328,7 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
             const unsigned long long* gw = a.hbuf + wo;
             const unsigned long long* uw = a.ubuf + wo;
             unsigned long long gv[8], uv[8];
-            for (int spin = 0;; ++spin) {
+            for (;;) {
                 int ok = 1;
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
@@ -669,7 +340,7 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
                 for (int k = 0; k < 8; ++k)
                     if ((uint32_t)(gv[k] >> 32) != a.epoch || (uint32_t)(uv[k] >> 32) != a.epoch) ok = 0;
                 if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
-                if (spin >= a.spin_limit) {
+                if (++spent > a.spin_limit) {
                     timed_out = 1;
                     break;
                 }
@@ -711,7 +382,7 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
             if (q == 0) s_exp[t][sb] = se;
         }
     }
-    if (timed_out && lane == 0) atomicOr(&a.meta[kMetaTimeoutWord], 1);
+    if (timed_out && lane == 0) sticky_or(a.meta, STICKY_TIMEOUT);
 #if defined(FST_GV_EXP) && FST_GV_EXP == 2
     if (dn) load_weights();
 #endif
@@ -720,14 +391,6 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_wave_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-#ifdef FST_TRACE
-    if (trc && lane == 0) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const long long tnow = wall_clock64();
-        trc[8 + wave] = tnow;
-        if (wave == 0) trc[dn ? 3 : 2] = tnow;
-    }
-#endif
 
     // ---- dot products: rows r of the tile for token rows 0..M-1 (A rows r
     // read token r & (M-1): broadcast reads; rows >= M are discarded)
@@ -774,27 +437,16 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
                                 ((unsigned long long)a.epoch << 32) | fst_f32_bits(v));
             }
         }
-#ifdef FST_TRACE
-        if (trc && tid == 0) trc[4] = wall_clock64();
-#endif
         return;
     }
     float v = 0.0f;
     if (tid < M * 16)
         for (int w = 0; w < kGvW; ++w) v += red[0][w][tid >> 4][tid & 15];
     gemv_tile_out(a, S, ystage, ns, slot, mask, rt, tid, v);
-#ifdef FST_TRACE
-    if (trc && tid == 0) trc[4] = wall_clock64();
-#endif
 }
 
 }  // namespace
 
-#ifdef FST_TRACE
-int gemv_trace_read(void* host, size_t bytes) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_gv_trace), bytes < sizeof(g_gv_trace) ? bytes : sizeof(g_gv_trace));
-}
-#endif
 
 bool gemv_supported(const Geometry& g, int M, int tk, int use_shared, const Scratch& s) {
     if (g.codec != 0 || M < 1 || M > kGvMaxM || tk < 0 || tk > kMaxTopK) return false;
@@ -829,16 +481,10 @@ int launch_expert_gemv(hipStream_t st, const Geometry& g, const LayerView& L, in
     a.swiglu_limit = g.swiglu_limit;
     a.epoch = epoch;
     a.spin_limit = spin_limit;
-    static const int dn_delay = getenv("FST_GV_DNDELAY") ? atoi(getenv("FST_GV_DNDELAY")) : 9;  // A/B switch
-    a.dn_delay = dn_delay;
+    a.dn_delay = kGvDnDelay;
     a.ubuf = s.hbuf + (size_t)s.max_pairs * g.inter;
-    static const bool valu = getenv("FST_GEMV_VALU") != nullptr;  // A/B switch for measurements
-    if (valu)
-        hipLaunchKernelGGL(expert_gemv_valu_kernel, dim3((unsigned)a.smax * (unsigned)(g.inter / 16 + g.hd / 16)),
-                           dim3(kGvNT), 0, st, a);
-    else
-        hipLaunchKernelGGL(expert_gemv_mfma_kernel, dim3((unsigned)a.smax * (unsigned)(2 * g.inter / 16 + g.hd / 16)),
-                           dim3(kGvNT), 0, st, a);
+    hipLaunchKernelGGL(expert_gemv_mfma_kernel, dim3((unsigned)a.smax * (unsigned)(2 * g.inter / 16 + g.hd / 16)),
+                       dim3(kGvNT), 0, st, a);
     return 0;
 }
 

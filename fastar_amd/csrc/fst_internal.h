@@ -28,13 +28,30 @@ enum MetaIdx {
     META_N_PAIRS = 2,      // (token, expert) pairs incl. shared
     META_ERROR = 3,        // nonzero: invalid expert id seen
     META_N_ROUTED_PAIRS = 4,
+    META_TIMEOUT = 5,      // this call: a cross-workgroup hand-off wait gave up
+    META_STICKY = 6,       // kernels only OR into it; only the host clears it
     META_WORDS = 8
 };
+// Bits of meta[META_STICKY]: every error a launch of the MoE path detects on
+// the device, kept until the host reads and clears it (fst_moe_check and the
+// host-pointer entry points), so that an error of an earlier stream-ordered
+// call is not overwritten by the calls after it.
+enum StickyBits {
+    STICKY_EXPERT_ID = 1,  // an expert id out of range in the routing
+    STICKY_HASH_ID = 2,    // an input id out of the vocabulary for hash routing
+    STICKY_TIMEOUT = 4     // a hand-off wait gave up (spin limit)
+};
+// ORs a routing error word (META_ERROR bits 1 and 2) and a timeout flag into
+// the sticky word; meta may be any address space the caller holds.
+__device__ __forceinline__ void sticky_or(int* meta, int bits) {
+    if (bits) atomicOr(&meta[META_STICKY], bits);
+}
 
 // Device scratch owned by a context, sized for max_tokens.
 struct Scratch {
     int max_tokens, max_pairs, max_slots;
     int n_cu;              // compute units of the device (persistent grids)
+    int fused_per_cu;      // workgroups of the fused MoE launch resident per CU (0: launch unused)
     uint16_t* h;           // bf16 [T][hd] staging for host-pointer calls
     uint16_t* out;         // bf16 [T][hd]
     uint16_t* out_routed;  // bf16 [T][hd]
@@ -324,6 +341,9 @@ void launch_prep_act_split(hipStream_t st, const float* part, int S, int rows, f
 // with topk = 0; y rows go to s.y for launch_combine.  epoch: a new nonzero
 // value per call (tags the h words); spin_limit bounds each hand-off wait.
 bool moe_fused_supported(const Geometry& g, int M);
+// Workgroups of the fused MoE launch (codec's instantiation) that one CU holds
+// at once, by the occupancy calculator, capped at 2 (0 on error).
+int moe_fused_occupancy(int codec);
 // Small-M expert FFN with caller-given routing (M <= 2, Q4_K): one launch
 // from the eids to the combined bf16 rows.
 bool gemv_supported(const Geometry& g, int M, int tk, int use_shared, const Scratch& s);

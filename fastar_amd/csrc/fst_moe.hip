@@ -34,14 +34,6 @@
 
 namespace fst {
 
-#ifdef FST_TRACE
-// Timeline probe (measurement builds only): per workgroup of the linear
-// kernels, the wall clock (100 MHz) at launch entry, after routing, and at
-// the start / end of each work item.
-constexpr int kTraceWG = 1024, kTraceSlots = 32;
-__device__ long long g_trace[2][kTraceWG][kTraceSlots];
-__device__ int g_trace_kernel;
-#endif
 
 // Sum of the 64 lanes' values in the canonical halving-tree order, as lane 0
 // sees it: p[j] += p[j + off] for off = 32, 16, ..., 1.  The cross-row steps
@@ -256,6 +248,7 @@ __device__ void bucket_block(int M, int E, int tk, int use_shared, const int* ei
         meta[META_N_ROUTED_PAIRS] = pair_base - p0;
         meta[META_N_PAIRS] = pair_base;
         meta[META_ERROR] = err | topk_err;
+        sticky_or(meta, err | topk_err);
     }
 }
 
@@ -1101,6 +1094,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
             const int ns = r_meta[META_N_SLOTS], np = r_meta[META_N_PAIRS];
             const int t = threadIdx.x;
             if (t <= META_N_ROUTED_PAIRS) ra.meta[t] = r_meta[t];
+            if (t == 0) sticky_or(ra.meta, r_meta[META_ERROR]);
             for (int i = t; i < ns; i += 64 * WAVES) {
                 ra.slot_eid[i] = r_seid[i];
                 ra.slot_M[i] = r_sM[i];
@@ -1112,15 +1106,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
                 for (int i = t; i < ra.M; i += 64 * WAVES) ra.pair_shared[i] = r_psh[i];
         }
     }
-#ifdef FST_TRACE
-    const int tk_id = MODE == 2 ? 1 : 0;
-    long long* trc = blockIdx.x < kTraceWG ? g_trace[tk_id][blockIdx.x] : nullptr;
-    int trn = 2;
-    if (trc && threadIdx.x == 0) {
-        trc[0] = wall_clock64();
-        for (int i = 2; i < kTraceSlots; ++i) trc[i] = 0;
-    }
-#endif
     const int* meta = RPER > 0 ? r_meta : meta_g;
     const int* slot_eid = RPER > 0 ? r_seid : slot_eid_g;
     const int* slot_M = RPER > 0 ? r_sM : slot_M_g;
@@ -1300,13 +1285,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
     }
     const int nms = nsb / MS;
 
-#ifdef FST_TRACE
-    if (trc && threadIdx.x == 0) trc[1] = wall_clock64();
-#endif
     for (int t = blockIdx.x; t < total; t += gridDim.x) {
-#ifdef FST_TRACE
-        if (trc && threadIdx.x == 0 && trn < kTraceSlots) trc[trn++] = wall_clock64();
-#endif
         const int slot = t / (tiles * S);
         const int tile = (t - slot * tiles * S) / S;
         const int ks = t % S;
@@ -1551,9 +1530,6 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
             }
         }
     }
-#ifdef FST_TRACE
-    if (trc && threadIdx.x == 0 && trn < kTraceSlots) trc[trn] = -wall_clock64();  // negative: the exit
-#endif
 }
 
 // --------------------------------------------- fused gate||up + down launch
@@ -1581,8 +1557,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 // indices) before it reaches a down item, and the grid never exceeds the
 // workgroups the device holds at once (two per CU), so every item a down
 // item waits for is processed.  The waits are still bounded: past
-// spin_limit polls a workgroup sets meta[kMetaTimeout] and carries on (the
-// host-pointer entry points turn that into FST_EHIP).
+// spin_limit polls a workgroup sets meta[META_TIMEOUT] and the sticky
+// timeout bit and carries on (fst_moe_check and the host-pointer entry
+// points turn that into FST_EHIP).
 constexpr int kFuT = 8;                           // token capacity
 constexpr int kFuW = 8;                           // waves per workgroup
 constexpr int kFuHalf = kFuW / 2;
@@ -1592,7 +1569,6 @@ constexpr int kFuTS = kFuT * kTokStride;          // one gate||up stage (one sup
 constexpr int kFuNCH = kFuT * kFuParts;           // staged chunks per stage
 constexpr int kFuMaxDnSb = 8;                     // down K (inter) <= 2048
 constexpr int kFuOpStride = kFuMaxDnSb * 36 + 1;  // down operand row in LDS, uint4
-constexpr int kMetaTimeout = 5;                   // meta word: a hand-off wait gave up
 
 struct FusedArgs {
     const uint8_t* bank;
@@ -1677,7 +1653,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         if (blockIdx.x == 0) {
             const int ns = r_meta[META_N_SLOTS], np = r_meta[META_N_PAIRS];
             if (tid <= META_N_ROUTED_PAIRS) ra.meta[tid] = r_meta[tid];
-            if (tid == kMetaTimeout) ra.meta[kMetaTimeout] = 0;
+            if (tid == 0) sticky_or(ra.meta, r_meta[META_ERROR]);
+            if (tid == META_TIMEOUT) ra.meta[META_TIMEOUT] = 0;
             for (int i = tid; i < ns; i += NT) {
                 ra.slot_eid[i] = r_seid[i];
                 ra.slot_M[i] = r_sM[i];
@@ -1698,20 +1675,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     }
     const int ns = r_meta[META_N_SLOTS];
     constexpr int tiles_gu = inter / 64, tiles_dn = hd / 128;
-#ifdef FST_FUSED_GU_ONLY
-    const int ngu = ns * tiles_gu, total = ngu;  // measurement build: gate||up items only
-#else
     const int ngu = ns * tiles_gu, total = ngu + ns * tiles_dn;
-#endif
     const int ndn = total - ngu;
-#ifdef FST_TRACE
-    long long* trc = blockIdx.x < kTraceWG ? g_trace[0][blockIdx.x] : nullptr;
-    int trn = 2;
-    if (trc && threadIdx.x == 0) {
-        trc[1] = wall_clock64();
-        for (int i = 2; i < kTraceSlots; ++i) trc[i] = 0;
-    }
-#endif
     if ((int)blockIdx.x >= total) return;
     const int r = lane & 15, g = lane >> 4;
     constexpr int nsb_gu = hd >> 8, nsb_dn = inter >> 8;
@@ -1869,21 +1834,11 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     int claimed = 0;    // thread 0: the item its last claim returned
     for (int t = blockIdx.x, tn = total; t < total; t = tn) {
         const bool dn = t >= ngu;
-#ifdef FST_TRACE
-        if (trc && tid == 0 && trn + 1 < kTraceSlots) {
-            trc[trn] = dn ? -wall_clock64() : wall_clock64();  // negative: a down item
-            g_trace[1][blockIdx.x][trn] = t;
-            trn += 2;
-        }
-#endif
         __syncthreads();  // the previous item's readers of the LDS are done
         const int nsb = dn ? nsb_dn : nsb_gu;
         int slot = t / tiles_gu, tile = t - slot * tiles_gu;
         if (dn) dn_map(t - ngu, slot, tile);
         const int Me = min(r_sM[slot], kFuT), off = r_soff[slot];
-#ifdef FST_TRACE
-        if (trc && tid == 0 && trn - 1 < kTraceSlots) g_trace[1][blockIdx.x][trn - 1] = slot * 16 + Me;
-#endif
         // the item that follows: the second half of this down pair, or claimed
         const bool pair1 = dyn && dn && t - ngu < D1 && ((t - ngu) & 1) == 0;
         const bool claims = dyn && !pair1;
@@ -2020,11 +1975,11 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 __builtin_amdgcn_s_sleep(2);
             }
             }
-            if (timed_out && tid == 0) atomicOr(&ra.meta[kMetaTimeout], 1);
+            if (timed_out && tid == 0) {
+                atomicOr(&ra.meta[META_TIMEOUT], 1);
+                sticky_or(ra.meta, STICKY_TIMEOUT);
+            }
             __syncthreads();
-#ifdef FST_TRACE
-            if (trc && tid == 0 && trn - 1 < kTraceSlots) trc[trn - 1] = wall_clock64();  // operand ready
-#endif
         }
         // One super-block loop for both kinds (one copy of the loop keeps the
         // register budget of the gate||up path), U = 2 per iteration: weight
@@ -2117,9 +2072,6 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             }
         }
     }
-#ifdef FST_TRACE
-    if (trc && tid == 0) trc[0] = wall_clock64();  // exit
-#endif
 }
 
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
@@ -2137,15 +2089,15 @@ int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int 
     fa.amaxw = s.amaxw;
     fa.hbuf_bytes = (size_t)s.max_pairs * g.inter * 8;
     fa.y = s.y;
-    static const bool no_claim = getenv("FST_FUSED_STATIC") != nullptr;  // A/B switch for measurements
-    fa.claim = no_claim ? nullptr : s.fused_claim;
+    fa.claim = s.fused_claim;
     fa.swiglu_limit = g.swiglu_limit;
     fa.epoch = epoch;
     fa.spin_limit = spin_limit;
-    // two workgroups per CU, all resident at once (the down items' waits
-    // rely on it; the kernel's VGPR and LDS budget allows two per CU)
+    // as many workgroups per CU as the occupancy calculator says fit (two:
+    // the kernel's VGPR and LDS budget allows two), all resident at once
+    // (the down items' waits rely on it)
     const unsigned items = (unsigned)s.max_slots * (unsigned)(g.inter / 64 + g.hd / 128);
-    const dim3 grid(std::min(items, (unsigned)s.n_cu * 2u));
+    const dim3 grid(std::min(items, (unsigned)s.n_cu * (unsigned)std::max(1, s.fused_per_cu)));
     fa.singles = (int)grid.x;
     // with events: they take the dispatch's own start and end times (the
     // kernel's duration, without the gap to the previous launch)
@@ -2165,6 +2117,15 @@ int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int 
         return set_error(1, "fused MoE launch: geometry without an instantiation");
 #undef FST_FU
     return 0;
+}
+
+int moe_fused_occupancy(int codec) {
+    int n = 0;
+    const hipError_t e =
+        codec == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, moe_fused_kernel<4096, 2048, 1>, 64 * kFuW, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, moe_fused_kernel<4096, 2048, 0>, 64 * kFuW, 0);
+    if (e != hipSuccess) return 0;
+    return std::min(n, 2);
 }
 
 bool moe_fused_supported(const Geometry& g, int M) {
@@ -2199,11 +2160,6 @@ static int linear_waves_per_cu(int M) {
     return 8 * (M <= 8 ? FST_Q4K_WG_PER_CU : (M <= 32 && FST_Q4K_WPE_MID >= 4 ? 2 : 1));
 }
 
-static bool mf32_enabled() {
-    static const bool on = getenv("FST_NO_MF32") == nullptr;  // A/B switch for measurements
-    return on;
-}
-
 template <int MODE, int CODEC = 0, int RPER = 0>
 static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8_t* bank, size_t stride,
                               size_t mat_off, int K, int N, const Scratch& s, const int* a_row,
@@ -2211,7 +2167,7 @@ static void launch_q4k_linear(hipStream_t st, int M, unsigned slots, const uint8
                               const RouteArgs& ra = RouteArgs{}) {
 
     if constexpr (MODE == 0 && CODEC == 0 && RPER == 0) {
-        if (M > 16 && M <= 32 && N % 256 == 0 && mf32_enabled()) {
+        if (M > 16 && M <= 32 && N % 256 == 0) {
             // 32x32 tiles: 8 waves x 32 rows per item, one workgroup per CU (the
             // tile's accumulators need more than 128 VGPRs)
             const unsigned items32 = slots * (unsigned)(N / 256);
@@ -2346,11 +2302,6 @@ void launch_q4k_dense(hipStream_t st, const uint8_t* W, int M, int K, int N, con
     launch_q4k_linear<0>(st, M, 1u, W, 0, 0, K, N, t, nullptr, s.x16p, s.sxp, s.xs, out, EpiArgs{});
 }
 
-#ifdef FST_TRACE
-int trace_read(void* host, size_t bytes) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes < sizeof(g_trace) ? bytes : sizeof(g_trace));
-}
-#endif
 
 // ------------------------------------------------------------------ combine
 

@@ -133,6 +133,24 @@ int fst_moe_layer_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const i
 int fst_moe_ffn_dev(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_eids,
                     const float* d_wts, int use_shared, uint16_t* d_out,
                     uint16_t* d_out_routed, uint16_t* d_out_shared);
+/* Errors of the asynchronous MoE calls (fst_moe_layer_dev, fst_moe_ffn_dev,
+ * fst_verify_forward_dev).  The reference raises a failed or stuck NPU
+ * dispatch as an exception per dispatch (npu_run_wait, flush_pending_runs,
+ * src/fst_engine.cpp:200-223).  Here every MoE launch ORs what it detects on
+ * the device into a sticky error word of the context: an expert id out of
+ * range (FST_EINVAL), an input id out of the vocabulary for hash routing
+ * (FST_EINVAL), a cross-workgroup hand-off wait that gave up at the spin
+ * limit (FST_EHIP; that call's output rows are wrong).  Kernels only set
+ * bits; fst_moe_check waits for the context's stream, returns the status of
+ * the bits set since the last check (FST_OK when none), and clears them.
+ * The host-pointer entry points (fst_moe_layer, fst_router, fst_expert_ffn,
+ * fst_shared_expert, fst_verify_forward) run the same check before they
+ * return, so an error of any layer of a verify forward is reported. */
+int fst_moe_check(fst_ctx* ctx);
+/* The status fst_moe_check returns for a given word of sticky bits (1: expert
+ * id, 2: hash input id, 4: hand-off timeout), for callers that read the word
+ * themselves; sets fst_last_error like any failing call. */
+int fst_device_error_status(int flags);
 
 /* ---- acceptance (src/fst_engine.cpp:6021-6063) ---- */
 /* target: [n_seq][k+1][V] fp32, draft: [n_seq][k] int32,
@@ -155,19 +173,23 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
  * wait that gives up writes n_acc[s] = -1 and tokens -1 for its sequence
  * (the host-pointer entry points then return FST_EHIP); after an asynchronous
  * *_dev call, fst_accept_check on the copied-back n_acc does the same. */
-int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default; also bounds the fused MoE launch's waits */
+int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default; also bounds the MoE launches' waits (fst_moe_check) */
 /* Router-driven MoE calls (fst_moe_layer[_dev], the verify forward) of at
  * most 8 tokens run gate||up and down as one persistent launch, and
  * rejection sampling runs its decisions, residual sums and pick as one
  * launch (default; k <= 8, V <= 262144); on = 0 selects the separate launch
- * chains.  Both give bit-identical results.  A fused launch whose hand-off wait exceeds the spin limit makes
- * the host-pointer entry points return FST_EHIP. */
+ * chains.  Both give bit-identical results.  A fused launch whose hand-off wait exceeds the spin limit sets
+ * the sticky timeout bit (fst_moe_check and the host-pointer entry points
+ * return FST_EHIP). */
 int fst_set_fused(fst_ctx* ctx, int on);
 /* Caller-routed calls (fst_moe_ffn_dev, fst_expert_ffn, fst_shared_expert) of
  * one or two tokens over Q4_K experts (hidden and intermediate sizes <= 4096)
- * run as one launch with fp32 VALU dot products (default); on = 0 selects the
- * MFMA launch chain.  The two agree to fp32 rounding, not bit for bit.  Its
- * hand-off wait is bounded like the fused launch's. */
+ * run as one launch (default): gate||up and down as fp16 MFMA tiles over the
+ * exact fp16 decode of the weights, with each token's activations prescaled
+ * by a power of two per 256-element super-block and rounded to fp16.  on = 0
+ * selects the launch chain, whose prescale is per row: the two agree within
+ * the fp16 operand rounding, not bit for bit.  Its hand-off wait is bounded
+ * like the fused launch's. */
 int fst_set_small_m(fst_ctx* ctx, int on);
 int fst_accept_check(const int32_t* n_acc, int n_seq);  /* host memory; FST_EHIP if any n_acc < 0 */
 /* fst_accept_greedy_dev without any allocation.  No counterpart in the

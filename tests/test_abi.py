@@ -95,3 +95,20 @@ def test_accept_check_flags_abandoned_sequences(fa):
     assert b"sequence 1" in L.fst_last_error()
     assert L.fst_accept_check(None, 3) == fa.FST_EINVAL
     assert L.fst_accept_check(fa._ptr(ok), 0) == fa.FST_EINVAL
+
+
+def test_device_error_status_decoding(fa):
+    # the sticky error bits of the MoE launches and the status each maps to
+    L = fa.lib()
+    assert L.fst_device_error_status(0) == fa.FST_OK
+    assert L.fst_device_error_status(1) == fa.FST_EINVAL
+    assert b"expert id" in L.fst_last_error()
+    assert L.fst_device_error_status(2) == fa.FST_EINVAL
+    assert b"hash" in L.fst_last_error()
+    assert L.fst_device_error_status(4) == fa.FST_EHIP
+    assert b"spin limit" in L.fst_last_error()
+    # an id error outranks a timeout seen in the same calls
+    assert L.fst_device_error_status(4 | 2) == fa.FST_EINVAL
+    assert L.fst_device_error_status(1 | 2) == fa.FST_EINVAL
+    assert b"hash" in L.fst_last_error()
+    assert L.fst_moe_check(None) == fa.FST_EINVAL

@@ -134,6 +134,11 @@ def test_small_m_invalid_expert_id(fa, oracle, c2_layer):
     note("small-M invalid id, device entry")
     out, _, _ = run_dev(fa, ctx, h, eids, wts, 0)
     c_out, _, _ = run_dev(fa, ctx, h, eids, wts, 0, small_m=False)
+    # both device calls left the sticky expert-id bit; one check reports it
+    with pytest.raises(fa.FstError) as ei:
+        ctx.moe_check()
+    assert ei.value.code == fa.FST_EINVAL
+    ctx.moe_check()
     assert rel_l2(bf16_to_f32(out), bf16_to_f32(c_out)) < CHAIN_TOL
     valid = eids.copy()
     keep = (eids >= 0) & (eids < E)
