@@ -1384,8 +1384,11 @@ size_t sample_ws_bytes(int n_rows, int V) { return (size_t)n_rows * V * 8 + 256;
 // (hipGetSymbolAddress, with that device current) and only that address is
 // handed to kernels: in host code the array's name is not a device address.
 // Every call on a device shares the array; calls that overlap on one device
-// race.  Each call takes the next epoch of the device, so no clearing is
-// needed between calls (zero-initialised words carry epoch 0, never used).
+// race.  Each call takes the next epoch of the device (1..4095), so no
+// clearing is needed between calls (zero-initialised words carry epoch 0,
+// never used); the array is cleared with a fill kernel before each call
+// that takes epoch 1, so that late words of a timed-out call cannot match
+// a reused epoch.
 static __device__ __align__(256) unsigned long long scratch[kStaticGreedyRows * kGreedyChunks];
 
 namespace {
@@ -1411,6 +1414,15 @@ void* accept_scratch_ptr(int device) {
     if (device < 0 || device >= kMaxDevices) return nullptr;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     return g_scratch_ptr[device];
+}
+
+__global__ __launch_bounds__(256) void fill_zero_u64_kernel(unsigned long long* __restrict__ p, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0ull;
+}
+
+void accept_scratch_clear(hipStream_t st, void* words) {
+    constexpr int n = kStaticGreedyRows * kGreedyChunks;
+    hipLaunchKernelGGL(fill_zero_u64_kernel, dim3(64), dim3(256), 0, st, static_cast<unsigned long long*>(words), n);
 }
 
 uint32_t accept_scratch_epoch(int device) {

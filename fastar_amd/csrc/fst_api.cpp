@@ -873,8 +873,10 @@ int fst_accept_greedy_dev_noalloc(fst_ctx* ctx, const float* d_target, int n_seq
     void* words = fst::accept_scratch_ptr(ctx->cfg.device);
     if (!words) return fail(FST_EHIP, "scratch address of the device was not set up");
     ctx->mark_begin();
-    fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens, words,
-                              fst::accept_scratch_epoch(ctx->cfg.device), ctx->spin_limit);
+    const uint32_t epoch = fst::accept_scratch_epoch(ctx->cfg.device);
+    if (epoch == 1) fst::accept_scratch_clear(ctx->st, words);
+    fst::launch_accept_greedy(ctx->st, d_target, n_seq, k, V, d_draft, d_n_acc, d_tokens, words, epoch,
+                              ctx->spin_limit);
     ctx->mark("accept_greedy");
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;

@@ -406,6 +406,12 @@ constexpr int kStaticGreedyRows = 2048;
 int accept_scratch_init(int device);
 void* accept_scratch_ptr(int device);
 uint32_t accept_scratch_epoch(int device);
+// Zeroes the whole fixed greedy array of the device with a fill kernel on st
+// (no memset node, so the call stays capturable).  Run before the call that
+// takes epoch 1 again: words a timed-out call wrote after its owner left
+// carry that call's epoch and may sit at offsets later shapes do not
+// rewrite; clearing at every wrap keeps them from matching a reused epoch.
+void accept_scratch_clear(hipStream_t st, void* words);
 // Rejection sampling: row maxima and sums, then (tail, when the rows' chunks
 // fit) one launch for the decisions, residual and pick, else three.
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,

@@ -85,3 +85,27 @@ def test_draw_follows_truncated_softmax(oracle):
     assert set(draws.tolist()) == {0, 3}
     frac3 = np.mean(draws == 3)
     assert abs(frac3 - p[3] / (p[3] + p[0])) < 0.03
+
+
+def test_kept_sets_beyond_the_reference_sort_window(oracle):
+    # the reference sorts only the first min(V, 10000) candidates
+    # (std::partial_sort, src/fst_engine.cpp:4509-4510) and leaves the order of
+    # the rest unspecified; this build orders the whole vocabulary (E
+    # descending, then index).  At V = 129,280 with flat logits the kept set is
+    # larger than 10,000: its size still matches the float64 restatement of the
+    # reference's cumulative rule, and its first 10,000 members are the
+    # reference's sorted window.
+    rng = np.random.default_rng(4)
+    V = 129280
+    x = rng.normal(0, 0.5, V).astype(np.float32)
+    for top_p in (0.5, 0.9):
+        l = x.astype(np.float64)
+        p = np.exp(l - l.max())
+        p /= p.sum()
+        order = np.lexsort((np.arange(V), -p))
+        c = np.cumsum(p[order])
+        n64 = int(np.searchsorted(c, top_p)) + 1
+        t, n = oracle.sample_token(x, 1.0, top_p, 5, 0)
+        assert n > 10000
+        assert abs(n - n64) <= 1
+        assert t in set(order[:n].tolist())
