@@ -1542,9 +1542,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 // separate gate||up launch, and no operand-prep launch runs between them.
 //  - routing: every workgroup computes the call's top-k and bucketing into
 //    LDS first (topk_bucket_block), as the gate||up launch does;
-//  - gate||up items: as q4k_linear_kernel MODE 1 (8 tokens, 8 waves: 64
-//    gate rows in waves 0..3 paired with the same up rows in waves 4..7); the
-//    up waves write h = silu(g)*u as 64-bit words {epoch, h bits} with
+//  - gate||up items: the arithmetic of q4k_linear_kernel MODE 1 (8 tokens,
+//    8 waves: 64 gate rows in waves 0..3 paired with the same up rows in
+//    waves 4..7), with the item's whole operand copied into LDS once at its
+//    start (a slot of more than 4 tokens: in two halves of K), so that the
+//    super-block loop has no staging loads and no per-super-block barrier;
+//    the up waves write h = silu(g)*u as 64-bit words {epoch, h bits} with
 //    device-coherent stores, and per 16 rows the largest |h| of each token
 //    in the same form (the down operand's prescale needs the row maximum);
 //  - down items: wait until the slot's maxima and h words carry this call's
@@ -1565,10 +1568,9 @@ constexpr int kFuW = 8;                           // waves per workgroup
 constexpr int kFuHalf = kFuW / 2;
 constexpr int kFuChunk = 2304;                    // Q4_K bytes per 16 rows x 256 weights
 constexpr int kFuParts = 36;                      // staged chunks per token per super-block
-constexpr int kFuTS = kFuT * kTokStride;          // one gate||up stage (one super-block)
-constexpr int kFuNCH = kFuT * kFuParts;           // staged chunks per stage
 constexpr int kFuMaxDnSb = 8;                     // down K (inter) <= 2048
 constexpr int kFuOpStride = kFuMaxDnSb * 36 + 1;  // down operand row in LDS, uint4
+constexpr int kFuOpStride16 = 16 * 36 + 1;        // gate||up operand row of <= 4 tokens x 16 super-blocks
 
 struct FusedArgs {
     const uint8_t* bank;
@@ -1607,11 +1609,10 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     constexpr int PARTS = MX ? 32 : kFuParts;     // staged chunks per token per super-block
     static_assert(INTER % 1024 == 0 && INTER <= 256 * kFuMaxDnSb && HD % 512 == 0, "fused geometry");
     constexpr int NT = 64 * kFuW;
-    constexpr int NS = (kFuNCH + NT - 1) / NT;
-    static_assert(NS == 1, "one staged chunk per thread");
+    static_assert(4 * kFuOpStride16 <= kFuT * kFuOpStride && HD == 4096, "gate||up operand of 4 tokens fits opb");
     constexpr int RPER = 4;
     constexpr int RPAIR = kFuT * kMaxTopK;
-    __shared__ uint4 lds[2 * kFuTS];
+    __shared__ float xg[kFuHalf * 4 * 64];  // gate rows handed to the up waves
     __shared__ uint4 opb[kFuT * kFuOpStride];
     __shared__ float s_amax[kFuT][2];
     __shared__ int s_xs2[kFuT];
@@ -1758,35 +1759,41 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     __amdgpu_buffer_rsrc_t wrs = item_rsrc(blockIdx.x);
     WRaw w[2];
     w[0] = load_w(wrs, 0);
-    for (int i = tid; i < 2 * kFuTS; i += NT) lds[i] = make_uint4(0u, 0u, 0u, 0u);
-
-    // gate||up staging (one chunk per thread per super-block): chunk tid of a
-    // stage -> (token stl, part spart); down items stage nothing here
-    const int stl = tid < kFuT * PARTS ? tid / PARTS : kFuT;
-    const int spart = tid - (tid / PARTS) * PARTS;
-    auto load_row = [&](int tt) -> int {  // operand row of this thread's chunk in item tt (-1: none)
-        if (tt >= ngu) return -1;
-        const int sl = tt / tiles_gu;
-        const int Mi = min(r_sM[sl], kFuT), offi = r_soff[sl];
-        return stl < Mi ? r_ptok[offi + stl] : -1;
+    // The gate||up operand of an item, copied once from the call's prepared
+    // rows (A: fp16 operand chunks, SX: sub-block sums) into opb: for a slot
+    // of at most 4 tokens all nsb_gu super-blocks at once (row stride
+    // kFuOpStride16), else 8 super-blocks per phase (row stride kFuOpStride,
+    // the down operand's layout).  Per token row and super-block 36 chunks,
+    // 32 operand chunks then the 4 sum chunks (MXFP4: the 32 chunks of bf16
+    // input only).  Rows past the slot's tokens are left as they are: their
+    // MFMA rows are discarded.
+    // (NB loads per thread in flight: fewer inside the super-block loop,
+    // where the weight ring holds registers)
+    auto gu_build = [&](auto nbc, int Me, int off, int sbase, int nph, int ostr) {
+        constexpr int NB = decltype(nbc)::value;
+        const int per = nph * PARTS, n = Me * per;
+        const u4v_t* A4 = reinterpret_cast<const u4v_t*>(fa.A);
+        const u4v_t* SX4 = reinterpret_cast<const u4v_t*>(fa.SX);
+        for (int q0 = tid; q0 < n; q0 += NB * NT) {
+            u4v_t v[NB];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int q = min(q0 + u * NT, n - 1);
+                const int tl = q / per, rem = q - tl * per, sbl = rem / PARTS, part = rem - sbl * PARTS;
+                const int tok = r_ptok[off + tl];
+                v[u] = part < 32 ? A4[tok * (hd / 8) + (sbase + sbl) * 32 + part]
+                                 : SX4[tok * nsb_gu * 4 + (sbase + sbl) * 4 + (part - 32)];
+            }
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const int q = q0 + u * NT;
+                if (q < n) {
+                    const int tl = q / per, rem = q - tl * per, sbl = rem / PARTS, part = rem - sbl * PARTS;
+                    *reinterpret_cast<u4v_t*>(&opb[tl * ostr + sbl * 36 + part]) = v[u];
+                }
+            }
+        }
     };
-    // the chunk's 16-byte offset in A (parts 0..31) or SX (32..35) at the
-    // item's first super-block, -1 when this thread stages nothing
-    int soff;
-    u4v_t sv;
-    auto build_map = [&](int ar) {
-        soff = ar < 0 ? -1 : spart < 32 ? ar * (hd / 8) + spart : ar * nsb_gu * 4 + (spart - 32);
-    };
-    auto stage_load = [&](int m) {
-        const int o = soff < 0 ? 0 : soff + m * (spart < 32 ? 32 : 4);
-        const u4v_t* base = spart < 32 ? reinterpret_cast<const u4v_t*>(fa.A) : reinterpret_cast<const u4v_t*>(fa.SX);
-        sv = base[o];
-    };
-    auto stage_store = [&](int m) {
-        if (soff >= 0) *reinterpret_cast<u4v_t*>(&lds[(m & 1) * kFuTS + stl * kTokStride + spart]) = sv;
-    };
-    build_map(load_row(blockIdx.x));
-    stage_load(0);
 
     // one 16-row x 256-weight step: Q4_K decode + MFMA against the operand
     // rows at st (row stride rs uint4), accumulated into acc
@@ -1830,7 +1837,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     };
     const int rsel = r & (kFuT - 1);  // MFMA rows 8..15 (discarded) read rows 0..7
 
-    int opb_slot = -1;  // slot whose down operand opb holds
+    int opb_key = -1;  // what opb holds: slot (gate||up, one phase), slot | 2^20 (down), -1: neither
     int claimed = 0;    // thread 0: the item its last claim returned
     for (int t = blockIdx.x, tn = total; t < total; t = tn) {
         const bool dn = t >= ngu;
@@ -1842,12 +1849,15 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         // the item that follows: the second half of this down pair, or claimed
         const bool pair1 = dyn && dn && t - ngu < D1 && ((t - ngu) & 1) == 0;
         const bool claims = dyn && !pair1;
-        if (claims && dn && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
         __amdgpu_buffer_rsrc_t nrs = wrs;
-        int ar_next = -1;
-        stage_store(0);
         f4_t acc = zf;
+        // gate||up operand layout: all super-blocks (at most 4 tokens) or two phases
+        const bool g2 = !dn && Me > 4;
+        const int ostr = dn || g2 ? kFuOpStride : kFuOpStride16;
         if (!dn) {
+            const int key = g2 ? -1 : slot;
+            if (key < 0 || key != opb_key) gu_build(std::integral_constant<int, 5>{}, Me, off, 0, g2 ? 8 : nsb_gu, ostr);
+            opb_key = key;
             __syncthreads();
         } else {
             // ---- the slot's down operand, built in LDS from the h words
@@ -1856,8 +1866,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             // first pass of h loads together, so a slot of one or two tokens
             // (most routed slots) costs one round trip when its words are in.
             int timed_out = 0;
-            const bool stage_op = slot != opb_slot;
-            opb_slot = slot;
+            const bool stage_op = (slot | 0x100000) != opb_key;
+            opb_key = slot | 0x100000;
             constexpr int cpr = inter / 8;  // operand chunks per row
             const int nwd = Me * aw;        // maxima words of the slot's rows
             const int nch = Me * cpr;       // operand chunks of the slot's rows
@@ -1981,14 +1991,12 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             }
             __syncthreads();
         }
-        // One super-block loop for both kinds (one copy of the loop keeps the
-        // register budget of the gate||up path), U = 2 per iteration: weight
-        // ring slot j, the staging of the next super-block (gate||up: from
-        // the stage ring, the next item's first at the last one; down: a
-        // dummy reload until the last, where the next item's first stage is
-        // loaded), one barrier per super-block for gate||up only (down reads
-        // its whole operand from opb).
-        const uint4* opr = dn ? opb + rsel * kFuOpStride : lds + rsel * kTokStride;
+        // One super-block loop for both kinds, U = 2 per iteration (weight
+        // ring slot j), with the whole operand in opb: no staging and no
+        // barrier inside it except the one that publishes the claimed next
+        // item (and, for a two-phase gate||up operand, the rebuild after
+        // super-block 7).
+        const uint4* opr = opb + (dn || g2 ? rsel : (r & 3)) * ostr;
         for (int sb0 = 0; sb0 < nsb; sb0 += 2) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -1999,25 +2007,24 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                     tn = pair1 ? t + 1 : (dyn ? s_claim : t + G);
                     tn = tn < total ? tn : total;
                     if (tn < total) nrs = item_rsrc(tn);
-                    ar_next = load_row(tn < total ? tn : t);
-                    build_map(ar_next);
                 }
-                stage_load(last || dn ? 0 : sb + 1);
                 const int pf = sb + 1;
                 const bool pnx = pf >= nsb;
                 w[(j + 1) & 1] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHK);
-                // gate||up items claim their successor four super-blocks
-                // before the end (issued after this step's loads, so only the
+                // each item claims its successor four super-blocks before
+                // the end (issued after this step's loads, so only the
                 // publication one step later waits for it)
-                if (claims && !dn && sb == nsb - 4 && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
+                if (claims && sb == nsb - 4 && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
                 __builtin_amdgcn_sched_barrier(0);
-                compute(opr + (dn ? sb * 36 : (sb & 1) * kFuTS), w[j], acc);
-                if (sb == nsb - 3 && tid == 0) s_claim = claimed;
-                if (!dn) {
-                    if (!last) stage_store(sb + 1);
-                    __syncthreads();
-                } else if (sb == nsb - 3) {
+                compute(opr + (g2 ? (sb & 7) : sb) * 36, w[j], acc);
+                if (sb == nsb - 3) {
+                    if (tid == 0) s_claim = claimed;
                     __syncthreads();  // publishes s_claim
+                }
+                if (g2 && sb == 7) {
+                    __syncthreads();
+                    gu_build(std::integral_constant<int, 1>{}, Me, off, 8, 8, ostr);
+                    __syncthreads();
                 }
             }
         }
@@ -2025,9 +2032,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 
         // D layout: lane holds token rows 4g+i (i = 0..3), column r
         if (!dn) {
-            // gate waves hand their rows to the up waves through LDS (the
-            // staging ring is free: the loop ended on a barrier)
-            float* xg = reinterpret_cast<float*>(lds);
+            // gate waves hand their rows to the up waves through LDS
             if (wave < kFuHalf) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
