@@ -1610,9 +1610,12 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     static_assert(INTER % 1024 == 0 && INTER <= 256 * kFuMaxDnSb && HD % 512 == 0, "fused geometry");
     constexpr int NT = 64 * kFuW;
     static_assert(4 * kFuOpStride16 <= kFuT * kFuOpStride && HD == 4096, "gate||up operand of 4 tokens fits opb");
+    static_assert(HD / 8 == NT, "one operand chunk per thread for a one-token prefetch");
     constexpr int RPER = 4;
     constexpr int RPAIR = kFuT * kMaxTopK;
     __shared__ float xg[kFuHalf * 4 * 64];  // gate rows handed to the up waves
+    __shared__ int s_xs[kFuT];              // prescale exponents of the token rows
+    __shared__ uint4 opn[kFuOpStride16];    // the next item's one-token gate||up operand
     __shared__ uint4 opb[kFuT * kFuOpStride];
     __shared__ float s_amax[kFuT][2];
     __shared__ int s_xs2[kFuT];
@@ -1672,6 +1675,10 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             if (r_pof[i] >= 0) r_yrow[r_pof[i]] = (i / ra.tk) * (ra.tk + 1) + i % ra.tk;
         if (ra.use_shared)
             for (int i = tid; i < ra.M; i += NT) r_yrow[r_psh[i]] = i * (ra.tk + 1) + ra.tk;
+        // the tokens' operand prescale exponents, read in LDS by the gate||up
+        // epilogue (a global load there would wait, in the in-order count,
+        // behind the next item's weight prefetch)
+        if (!MX && tid < ra.M) s_xs[tid] = fa.xs[tid];
         __syncthreads();
     }
     const int ns = r_meta[META_N_SLOTS];
@@ -1838,6 +1845,17 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     const int rsel = r & (kFuT - 1);  // MFMA rows 8..15 (discarded) read rows 0..7
 
     int opb_key = -1;  // what opb holds: slot (gate||up, one phase), slot | 2^20 (down), -1: neither
+    // A gate||up item of a one-token slot gets its operand chunks loaded into
+    // registers (pv: chunk tid = 32 sb + part, the 32 operand chunks of each
+    // super-block) one super-block before the end of the item before it, and
+    // written to opn with the sub-block sums (computed from the same fp16
+    // values in prep_row's order) once that item's readers are done: no load
+    // latency at its start.  The loads are issued for every item on one
+    // straight path (loads on two paths merge into register copies that wait
+    // for them), before the weight prefetch of the next item's first
+    // super-block, so waiting for them waits for nothing else.
+    bool pre = false;  // this item's operand arrives in pv
+    u4v_t pv = u4v_t{0u, 0u, 0u, 0u};
     int claimed = 0;    // thread 0: the item its last claim returned
     for (int t = blockIdx.x, tn = total; t < total; t = tn) {
         const bool dn = t >= ngu;
@@ -1855,9 +1873,31 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         const bool g2 = !dn && Me > 4;
         const int ostr = dn || g2 ? kFuOpStride : kFuOpStride16;
         if (!dn) {
-            const int key = g2 ? -1 : slot;
-            if (key < 0 || key != opb_key) gu_build(std::integral_constant<int, 5>{}, Me, off, 0, g2 ? 8 : nsb_gu, ostr);
-            opb_key = key;
+            if (pre) {
+                const int sbl = tid >> 5, part = tid & 31;
+                *reinterpret_cast<u4v_t*>(&opn[sbl * 36 + part]) = pv;
+                if constexpr (!MX) {
+                    const h8_t v = __builtin_bit_cast(h8_t, pv);
+                    float s0 = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+                    float s1 = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
+                    s0 = s0 + fdpp<0xb1>(s0);  // quad_perm [1,0,3,2]
+                    s1 = s1 + fdpp<0xb1>(s1);
+                    s0 = s0 + fdpp<0x4e>(s0);  // quad_perm [2,3,0,1]
+                    s1 = s1 + fdpp<0x4e>(s1);
+                    s0 = s0 + fdpp<0x104>(s0);  // row_shl 4
+                    s1 = s1 + fdpp<0x104>(s1);
+                    if ((part & 7) == 0) {
+                        const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
+                        const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
+                        const _Float16 z = (_Float16)0.0f;
+                        opn[sbl * 36 + 32 + (part >> 3)] = __builtin_bit_cast(uint4, h8_t{h0, h1, l0, l1, z, z, z, z});
+                    }
+                }
+            } else {
+                const int key = g2 ? -1 : slot;
+                if (key < 0 || key != opb_key) gu_build(std::integral_constant<int, 5>{}, Me, off, 0, g2 ? 8 : nsb_gu, ostr);
+                opb_key = key;
+            }
             __syncthreads();
         } else {
             // ---- the slot's down operand, built in LDS from the h words
@@ -1996,38 +2036,49 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         // barrier inside it except the one that publishes the claimed next
         // item (and, for a two-phase gate||up operand, the rebuild after
         // super-block 7).
-        const uint4* opr = opb + (dn || g2 ? rsel : (r & 3)) * ostr;
-        for (int sb0 = 0; sb0 < nsb; sb0 += 2) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int sb = sb0 + j;
-                const bool last = sb + 1 >= nsb;
-                if (last) {
-                    // the next item (published three super-blocks earlier)
-                    tn = pair1 ? t + 1 : (dyn ? s_claim : t + G);
-                    tn = tn < total ? tn : total;
-                    if (tn < total) nrs = item_rsrc(tn);
-                }
-                const int pf = sb + 1;
-                const bool pnx = pf >= nsb;
-                w[(j + 1) & 1] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHK);
-                // each item claims its successor four super-blocks before
-                // the end (issued after this step's loads, so only the
-                // publication one step later waits for it)
-                if (claims && sb == nsb - 4 && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
-                __builtin_amdgcn_sched_barrier(0);
-                compute(opr + (g2 ? (sb & 7) : sb) * 36, w[j], acc);
-                if (sb == nsb - 3) {
-                    if (tid == 0) s_claim = claimed;
-                    __syncthreads();  // publishes s_claim
-                }
-                if (g2 && sb == 7) {
-                    __syncthreads();
-                    gu_build(std::integral_constant<int, 1>{}, Me, off, 8, 8, ostr);
-                    __syncthreads();
-                }
+        const uint4* opr = pre && !dn ? opn : opb + (dn || g2 ? rsel : (r & 3)) * ostr;
+        // one super-block step; j: the weight ring slot
+        auto step = [&](int sb, auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const int pf = sb + 1;
+            const bool pnx = pf >= nsb;
+            w[(j + 1) & 1] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHK);
+            // each item claims its successor four super-blocks before its
+            // end (issued after this step's loads, so only the publication
+            // one step later waits for it)
+            if (claims && sb == nsb - 4 && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(opr + (g2 ? (sb & 7) : sb) * 36, w[j], acc);
+            if (sb == nsb - 3) {
+                if (tid == 0) s_claim = claimed;
+                __syncthreads();  // publishes s_claim
             }
+            if (g2 && sb == 7) {
+                __syncthreads();
+                gu_build(std::integral_constant<int, 1>{}, Me, off, 8, 8, ostr);
+                __syncthreads();
+            }
+        };
+        using J0 = std::integral_constant<int, 0>;
+        using J1 = std::integral_constant<int, 1>;
+        for (int sb0 = 0; sb0 < nsb - 2; sb0 += 2) {
+            step(sb0, J0{});
+            step(sb0 + 1, J1{});
         }
+        step(nsb - 2, J0{});
+        // the next item (published two super-blocks earlier) and the operand
+        // prefetch of a one-token gate||up item
+        tn = pair1 ? t + 1 : (dyn ? s_claim : t + G);
+        tn = tn < total ? tn : total;
+        if (tn < total) nrs = item_rsrc(tn);
+        {
+            const int nsl = tn < ngu ? tn / tiles_gu : 0;
+            pre = tn < ngu && r_sM[nsl] == 1;
+            const int tok = r_ptok[r_soff[nsl]];
+            pv = reinterpret_cast<const u4v_t*>(fa.A)[tok * (hd / 8) + tid];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        step(nsb - 1, J1{});
         wrs = nrs;
 
         // D layout: lane holds token rows 4g+i (i = 0..3), column r
@@ -2038,7 +2089,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 for (int i = 0; i < 4; ++i) {
                     const int tl = 4 * g + i;
                     xg[(wave * 4 + i) * 64 + lane] =
-                        tl < Me ? (MX ? acc[i] : ldexpf(acc[i], fa.xs[r_ptok[off + tl]])) : 0.0f;
+                        tl < Me ? (MX ? acc[i] : ldexpf(acc[i], s_xs[r_ptok[off + tl]])) : 0.0f;
                 }
             }
             __syncthreads();
@@ -2051,7 +2102,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                     float m = 0.0f;
                     if (tl < Me) {
                         float gv = xg[((wave - kFuHalf) * 4 + i) * 64 + lane];
-                        float uv = MX ? acc[i] : ldexpf(acc[i], fa.xs[r_ptok[off + tl]]);
+                        float uv = MX ? acc[i] : ldexpf(acc[i], s_xs[r_ptok[off + tl]]);
                         if (lim > 0.0f) {
                             gv = fminf(gv, lim);
                             uv = fminf(fmaxf(uv, -lim), lim);
