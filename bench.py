@@ -285,28 +285,42 @@ def bench_c4(fa, args):
         t = timed(ctx, lambda i: fa._check(L.fst_moe_ffn_dev(ctx.h, 0, dh, M, de[i % N_BATCH], dw[i % N_BATCH], 1,
                                                              do, None, None)), args.steps, args.warmup)
         byts = (distinct + 1) * EXPERT_BYTES
-        # MFMA work of the gate|up launch per routing batch: each 16-row x
-        # 256-weight chunk issues 9 fp16 16x16x32 MFMAs (16,384 flops) per
-        # live 16-token group of its expert; useful = 2 x pairs x K x N
+        # MFMA work per routing batch: each 16-row x 256-weight chunk issues 9
+        # fp16 16x16x32 MFMAs (16,384 flops) per token group of its expert
+        # (fused launch: groups of 16 tokens for gate|up, 8 for down; launch
+        # chain: the gate|up launch, groups of 16); useful = 2 x pairs x K x N
         ctx.set_profiling(True)
-        issued, useful, t_gu = [], [], []
+        issued, useful, t_k = [], [], []
+        fused = False
         for b, (eids, _) in enumerate(batches):
             fa._check(L.fst_moe_ffn_dev(ctx.h, 0, dh, M, de[b], dw[b], 1, do, None, None))
-            t_gu.append(dict(ctx.last_timings())["q4k_gate_up"] * 1e-3)
+            tm = dict(ctx.last_timings())
+            fused = "moe_fused" in tm
+            t_k.append(tm["moe_fused" if fused else "q4k_gate_up"] * 1e-3)
             counts = np.bincount(eids.ravel(), minlength=E)
-            groups = int(np.sum((counts[counts > 0] + 15) // 16)) + (M + 15) // 16  # routed + shared
-            issued.append(groups * (2 * INTER // 16) * (HD // 256) * 9 * 16384.0)
-            useful.append(2.0 * (M * TK + M) * HD * 2 * INTER)
+            live = counts[counts > 0]
+            gu_groups = int(np.sum((live + 15) // 16)) + (M + 15) // 16  # routed + shared
+            gu = gu_groups * (2 * INTER // 16) * (HD // 256) * 9 * 16384.0
+            if fused:
+                dn_groups = int(np.sum((live + 7) // 8)) + (M + 7) // 8
+                issued.append(gu + dn_groups * (HD // 16) * (INTER // 256) * 9 * 16384.0)
+                useful.append(2.0 * (M * TK + M) * HD * 3 * INTER)
+            else:
+                issued.append(gu)
+                useful.append(2.0 * (M * TK + M) * HD * 2 * INTER)
         ctx.set_profiling(False)
-        iss = float(np.mean(np.array(issued) / np.array(t_gu))) / 1e12
-        use = float(np.mean(np.array(useful) / np.array(t_gu))) / 1e12
-        out["M%d" % M] = {"tokens_per_s": round(M / t, 1), "us_per_step": round(t * 1e6, 2),
-                          "mean_distinct_routed": round(distinct, 2),
-                          "packed_weight_GBps": round(byts / t / 1e9, 1),
-                          "gate_up_us": round(float(np.mean(t_gu)) * 1e6, 2),
-                          "mfma_gate_up": {"issued_tflops": round(iss, 1), "useful_tflops": round(use, 1),
-                                           "peak_tflops": MFMA_F16_PEAK_TFLOPS,
-                                           "util": round(iss / MFMA_F16_PEAK_TFLOPS, 4)}}
+        iss = float(np.mean(np.array(issued) / np.array(t_k))) / 1e12
+        use = float(np.mean(np.array(useful) / np.array(t_k))) / 1e12
+        kb = byts if fused else (distinct + 1) * 2 * PROJ_BYTES
+        rec = {"tokens_per_s": round(M / t, 1), "us_per_step": round(t * 1e6, 2),
+               "mean_distinct_routed": round(distinct, 2),
+               "packed_weight_GBps": round(byts / t / 1e9, 1),
+               "kernel": "moe_fused (gate|up + down)" if fused else "q4k_gate_up",
+               "kernel_us": round(float(np.mean(t_k)) * 1e6, 2),
+               "kernel_GBps": round(kb / float(np.mean(t_k)) / 1e9, 1),
+               "mfma": {"issued_tflops": round(iss, 1), "useful_tflops": round(use, 1),
+                        "peak_tflops": MFMA_F16_PEAK_TFLOPS, "util": round(iss / MFMA_F16_PEAK_TFLOPS, 4)}}
+        out["M%d" % M] = rec
     ctx.close()
     return {"metric": "C4 Zipf-routed MoE verify throughput", "value": out["M32"]["tokens_per_s"],
             "unit": "tokens/s", "higher_is_better": True, "blocks": out,
@@ -412,6 +426,8 @@ def main():
                     help="time the fused launch in the profiling pass only (no replay of the timed steps)")
     ap.add_argument("--calib-copy", type=int, default=0,
                     help="also run N launches of the plain copy kernel (512 MiB) for PMC calibration")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the C1 and C3 figures that the headline line carries under 'secondary'")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c2mx", "c3", "c4", "c5"],
                     help="c2 (default) is the headline; the others print their own record line")
     args = ap.parse_args()
@@ -576,8 +592,23 @@ def main():
         "accepted_len_step": n_acc,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    if not args.no_secondary:
+        # the cheap secondary configs, timed in the same process after the
+        # headline (their own contexts; 200 timed calls each): C1 one expert
+        # at M = 1, C3 greedy and stochastic acceptance
+        sec_args = argparse.Namespace(steps=200, warmup=20)
+        c1 = bench_c1(fa, sec_args)
+        c3 = bench_c3(fa, sec_args)
+        res["secondary"] = {
+            "c1_us_per_expert": c1["value"],
+            "c1_packed_weight_GBps": c1["packed_weight_GBps"],
+            "c1_kernel_us": c1["kernel_us"],
+            "c3_greedy_us": c3["greedy_us"],
+            "c3_stochastic_us": c3["stochastic_us"],
+            "timing": "wall clock over 200 back-to-back calls after 20 warm-up calls, inputs resident",
+        }
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":

@@ -571,7 +571,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     const bool mx = c.codec == FST_CODEC_MXFP4;  // bf16 operands: no fp16 operand prep
     // top-k + bucketing run inside the gate||up launch when the expert count allows
     const bool fuse_topk = do_router && c.n_experts <= fst::kFusedRouteMaxExperts;
-    const fst::RouteReq rq{d_ids, use_hash, use_shared && !sh16, d_eids, d_wts};
+    const fst::RouteReq rq{d_ids, use_hash, use_shared && !sh16, d_eids, d_wts, do_router ? 0 : 1};
     if (do_router) {
         // logits and operand prep (Q4_K) in one launch, then (unless fused) top-k + bucketing
         fst::launch_route(st, g, L, d_h, M, mx ? 0 : 1, d_ids, use_hash, use_shared && !sh16, d_eids, d_wts,
@@ -617,7 +617,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
         ctx->mark("bucket_prep");
     }
     const int sh_q = use_shared && !sh16 ? 1 : 0;  // the shared expert runs as slot 0
-    if (fuse_topk && ctx->fused && use_routed && fst::moe_fused_supported(g, M)) {
+    if ((fuse_topk || !do_router) && !direct && ctx->fused && use_routed && fst::moe_fused_supported(g, M)) {
         // gate||up and down in one persistent launch, then the combine
         ctx->fused_epoch = ctx->fused_epoch == 0xffffffffu ? 1u : ctx->fused_epoch + 1u;
         hipEvent_t k0 = nullptr, k1 = nullptr;
@@ -628,9 +628,15 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
         }
         fst::launch_moe_fused(st, g, L, M, ctx->s, rq, ctx->fused_epoch, ctx->spin_limit, d_h, k0, k1);
         ctx->mark("moe_fused");
-        // (a bf16 shared expert ran above; its fp32 rows are the combine's shared term)
-        fst::launch_combine_tj(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out,
-                               d_out_routed, d_out_shared);
+        // (a bf16 shared expert ran above; its fp32 rows are the combine's
+        // shared term).  Router-driven calls: y rows by (token, j); caller
+        // routing: y rows by pair, through the pair tables
+        if (do_router)
+            fst::launch_combine_tj(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out,
+                                   d_out_routed, d_out_shared);
+        else
+            fst::launch_combine(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out,
+                                d_out_routed, d_out_shared);
         ctx->mark("combine");
         FST_HIP_TRY(hipGetLastError());
         return FST_OK;

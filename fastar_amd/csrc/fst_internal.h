@@ -279,6 +279,7 @@ struct RouteReq {
     int use_hash, use_shared;
     int32_t* eids;
     float* wts;
+    int given;  // eids/wts are the caller's routing (no router)
 };
 // Largest expert count the in-launch routing handles (4 experts per lane).
 constexpr int kFusedRouteMaxExperts = 256;

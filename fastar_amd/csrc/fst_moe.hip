@@ -284,6 +284,7 @@ struct RouteArgs {
     int* pair_tok;
     int* pair_of;
     int* pair_shared;
+    const int32_t* given;  // caller-given eids [M][tk] (process_expert_ffn): no top-k, no eids/wts written
 };
 
 // One workgroup of NT threads: wave w selects the top-k of tokens w, w+NT/64,
@@ -310,6 +311,13 @@ __device__ void topk_bucket_block(const RouteArgs& ra, bool gw = true) {
     const float zero_score = ra.score_func == 0 ? fst_sigmoidf(0.0f) : fst_sqrtsoftplusf(0.0f);
     if (tid == 0) s_err = 0;
     __syncthreads();
+    if (ra.given) {
+        for (int i = tid; i < M * tk; i += NT) s_eids[i] = ra.given[i];
+        __syncthreads();
+        bucket_block<NT, (PER * 64 < kMaxExperts ? PER * 64 : kMaxExperts)>(M, E, tk, ra.use_shared, s_eids, 0, ra.meta,
+                         ra.slot_eid, ra.slot_M, ra.slot_off, ra.pair_tok, ra.pair_of, ra.pair_shared);
+        return;
+    }
     for (int t = wave; t < M; t += NW) {
         const float* row = scores + (size_t)t * E;
         if (hash) {
@@ -433,7 +441,7 @@ static RouteArgs route_args(const Geometry& g, const LayerView& L, int M, const 
                      use_hash ? L.hash : nullptr, input_ids, g.vocab, use_shared,
                      eids,       wts,         s.meta,     s.slot_eid,
                      s.slot_M,   s.slot_off,  s.pair_tok, s.pair_of,
-                     s.pair_shared};
+                     s.pair_shared, nullptr};
 }
 
 void launch_bucket(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
@@ -653,6 +661,8 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
 __global__ __launch_bounds__(kRouteThreads) void bucket_prep_kernel(
     int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids, Scratch s, const uint16_t* h, int K,
     uint16_t* o1, uint16_t* o2, int hd, int nprep, const uint4* __restrict__ pf, size_t pf_pieces) {
+    // the fused launch that may follow claims work from this counter
+    if (blockIdx.x == 0 && threadIdx.x == 0) *s.fused_claim = 0;
     if ((int)blockIdx.x > nprep) {
         // workgroups past the prep rows read pf (the shared expert's gate||up
         // weights, streamed first by the next launch) into the device-wide
@@ -1563,7 +1573,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 // spin_limit polls a workgroup sets meta[META_TIMEOUT] and the sticky
 // timeout bit and carries on (fst_moe_check and the host-pointer entry
 // points turn that into FST_EHIP).
-constexpr int kFuT = 8;                           // token capacity
+constexpr int kFuT = 16;                          // token rows of a gate||up slot (the MFMA's 16 rows)
+constexpr int kFuTD = 8;                          // token rows of a down slot
+constexpr int kFuMaxM = 32;                       // tokens of one call
+constexpr int kFuMaxPairs = 256;                  // routed (token, expert) pairs of one call
+// slots of one call: every routed pair its own expert, the shared expert,
+// and the extra slots of experts split into groups of kFuT tokens
+constexpr int kFuMaxSlots = kFuMaxPairs + 1 + (kFuMaxPairs + kFuMaxM) / kFuTD;
 constexpr int kFuW = 8;                           // waves per workgroup
 constexpr int kFuHalf = kFuW / 2;
 constexpr int kFuChunk = 2304;                    // Q4_K bytes per 16 rows x 256 weights
@@ -1571,6 +1587,8 @@ constexpr int kFuParts = 36;                      // staged chunks per token per
 constexpr int kFuMaxDnSb = 8;                     // down K (inter) <= 2048
 constexpr int kFuOpStride = kFuMaxDnSb * 36 + 1;  // down operand row in LDS, uint4
 constexpr int kFuOpStride16 = 16 * 36 + 1;        // gate||up operand row of <= 4 tokens x 16 super-blocks
+constexpr int kFuOpStride4 = 4 * 36 + 1;          // operand row of 9..16 tokens, 4 super-blocks per phase
+constexpr int kFuOpb = 16 * kFuOpStride4 > 8 * kFuOpStride ? 16 * kFuOpStride4 : 8 * kFuOpStride;
 
 struct FusedArgs {
     const uint8_t* bank;
@@ -1609,20 +1627,22 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     constexpr int PARTS = MX ? 32 : kFuParts;     // staged chunks per token per super-block
     static_assert(INTER % 1024 == 0 && INTER <= 256 * kFuMaxDnSb && HD % 512 == 0, "fused geometry");
     constexpr int NT = 64 * kFuW;
-    static_assert(4 * kFuOpStride16 <= kFuT * kFuOpStride && HD == 4096, "gate||up operand of 4 tokens fits opb");
+    static_assert(4 * kFuOpStride16 <= kFuOpb && HD == 4096, "gate||up operand of 4 tokens fits opb");
     static_assert(HD / 8 == NT, "one operand chunk per thread for a one-token prefetch");
     constexpr int RPER = 4;
-    constexpr int RPAIR = kFuT * kMaxTopK;
     __shared__ float xg[kFuHalf * 4 * 64];  // gate rows handed to the up waves
-    __shared__ int s_xs[kFuT];              // prescale exponents of the token rows
+    __shared__ int s_xs[kFuMaxM];           // prescale exponents of the token rows
     __shared__ uint4 opn[kFuOpStride16];    // the next item's one-token gate||up operand
-    __shared__ uint4 opb[kFuT * kFuOpStride];
-    __shared__ float s_amax[kFuT][2];
-    __shared__ int s_xs2[kFuT];
+    __shared__ uint4 opb[kFuOpb];
+    __shared__ float s_amax[kFuTD][1];
+    __shared__ int s_xs2[kFuTD];
     __shared__ int s_claim;
-    __shared__ int r_meta[META_WORDS], r_seid[RPAIR + 1], r_sM[RPAIR + 1], r_soff[RPAIR + 1];
-    __shared__ int r_ptok[RPAIR + kFuT], r_pof[RPAIR], r_psh[kFuT];
-    __shared__ int r_yrow[RPAIR + kFuT];  // pair -> its y row t*(tk+1) + j (shared: j = tk)
+    __shared__ int s_vn[kFuW];              // slot split: the waves' counts
+    __shared__ int r_meta[META_WORDS], r_seid[kFuMaxSlots], r_sM[kFuMaxSlots], r_soff[kFuMaxSlots];
+    __shared__ int d_seid[kFuMaxSlots], d_sM[kFuMaxSlots], d_soff[kFuMaxSlots];  // down slots
+    __shared__ int s_nds;
+    __shared__ int r_ptok[kFuMaxPairs + kFuMaxM], r_pof[kFuMaxPairs], r_psh[kFuMaxM];
+    __shared__ int r_yrow[kFuMaxPairs + kFuMaxM];  // pair -> its y row t*(tk+1) + j (shared: j = tk)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     constexpr int hd = HD, inter = INTER;
     const size_t stride = fa.expert_stride;
@@ -1650,7 +1670,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 pfv[i] = i < npf ? src[q < pieces ? q : 0] : make_uint4(0u, 0u, 0u, 0u);
             }
         }
-        topk_bucket_block<RPER, NT, kFuT>(la, blockIdx.x == 0);
+        topk_bucket_block<RPER, NT, kFuMaxM>(la, blockIdx.x == 0);
 #pragma unroll
         for (int i = 0; i < 3; ++i) asm volatile("" ::"v"(pfv[i].x));
         __syncthreads();
@@ -1670,20 +1690,79 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 for (int i = tid; i < ra.M; i += NT) ra.pair_shared[i] = r_psh[i];
         }
         // y rows by (token, j), so that the combine reads them without the
-        // pair table (one round trip instead of two)
+        // pair table (one round trip instead of two); the rows of pairs
+        // without a valid expert are zeros (workgroup 0 writes them), which
+        // the combine adds as the chain's combine skips them
+        // (caller-given routing may name one expert twice for a token: two
+        // (token, j) share one pair there, so y stays indexed by pair and the
+        // pair-table combine follows)
+        if (ra.given) {
+            for (int i = tid; i < kFuMaxPairs + kFuMaxM; i += NT) r_yrow[i] = i;
+        } else {
         for (int i = tid; i < ra.M * ra.tk; i += NT)
             if (r_pof[i] >= 0) r_yrow[r_pof[i]] = (i / ra.tk) * (ra.tk + 1) + i % ra.tk;
-        if (ra.use_shared)
+        }
+        if (blockIdx.x == 0 && r_meta[META_ERROR] && !ra.given)
+            for (int i = 0; i < ra.M * ra.tk; ++i)
+                if (r_pof[i] < 0) {
+                    float4* yz = reinterpret_cast<float4*>(fa.y + (size_t)((i / ra.tk) * (ra.tk + 1) + i % ra.tk) * hd);
+                    for (int q = tid; q < hd / 4; q += NT) yz[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+        if (ra.use_shared && !ra.given)
             for (int i = tid; i < ra.M; i += NT) r_yrow[r_psh[i]] = i * (ra.tk + 1) + ra.tk;
         // the tokens' operand prescale exponents, read in LDS by the gate||up
         // epilogue (a global load there would wait, in the in-order count,
         // behind the next item's weight prefetch)
         if (!MX && tid < ra.M) s_xs[tid] = fa.xs[tid];
         __syncthreads();
+        // Slots of more than kFuT tokens become several gate||up slots of at
+        // most kFuT consecutive pairs each, and slots of more than kFuTD tokens
+        // several down slots of at most kFuTD (the expert's matrix streamed
+        // once per group).  Each thread reads its slot, the waves count the
+        // new slots (shuffle prefix), and every slot writes its groups.
+        {
+            const int ns0 = r_meta[META_N_SLOTS];
+            int e0 = 0, m0 = 0, o0 = 0;
+            if (tid < ns0) {
+                e0 = r_seid[tid];
+                m0 = r_sM[tid];
+                o0 = r_soff[tid];
+            }
+            auto split = [&](int cap, int* se, int* sm, int* so, int* count) {
+                const int nv = tid < ns0 ? (m0 + cap - 1) / cap : 0;
+                int x = nv;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int y = __shfl_up(x, d, 64);
+                    if (lane >= d) x += y;
+                }
+                if (lane == 63) s_vn[wave] = x;
+                __syncthreads();
+                int before = 0, total_v = 0;
+#pragma unroll
+                for (int w2 = 0; w2 < kFuW; ++w2) {
+                    const int c = s_vn[w2];
+                    if (w2 < wave) before += c;
+                    total_v += c;
+                }
+                const int first = before + x - nv;
+                __syncthreads();
+                for (int v = 0; v < nv; ++v) {
+                    se[first + v] = e0;
+                    sm[first + v] = min(cap, m0 - v * cap);
+                    so[first + v] = o0 + v * cap;
+                }
+                if (tid == 0) *count = total_v;
+            };
+            // (ns0 <= kFuMaxPairs + 1 <= NT: one slot per thread)
+            split(kFuTD, d_seid, d_sM, d_soff, &s_nds);
+            if (__syncthreads_or(m0 > kFuT)) split(kFuT, r_seid, r_sM, r_soff, &r_meta[META_N_SLOTS]);
+            __syncthreads();
+        }
     }
-    const int ns = r_meta[META_N_SLOTS];
+    const int ns = r_meta[META_N_SLOTS], nds = s_nds;
     constexpr int tiles_gu = inter / 64, tiles_dn = hd / 128;
-    const int ngu = ns * tiles_gu, total = ngu + ns * tiles_dn;
+    const int ngu = ns * tiles_gu, total = ngu + nds * tiles_dn;
     const int ndn = total - ngu;
     if ((int)blockIdx.x >= total) return;
     const int r = lane & 15, g = lane >> 4;
@@ -1735,7 +1814,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         }
         int sl, ti;
         dn_map(tt - ngu, sl, ti);
-        return bank + (size_t)r_seid[sl] * stride + 2 * proj + (size_t)(ti * kFuW + wave) * nsb_dn * CHK;
+        return bank + (size_t)d_seid[sl] * stride + 2 * proj + (size_t)(ti * kFuW + wave) * nsb_dn * CHK;
     };
     auto rsrc = [&](const uint8_t* p, int nsb) -> __amdgpu_buffer_rsrc_t {
         const uint64_t u = (uint64_t)(uintptr_t)p;
@@ -1762,6 +1841,10 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     // h words of the call, read with device-coherent 16-byte loads (sc1)
     const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
         fa.hbuf, (short)0, (int)(fa.hbuf_bytes < 0x7fffffffull ? fa.hbuf_bytes : 0x7fffffffull), 0x00020000);
+    // the row maxima words, likewise
+    static_assert(aw == 128, "one wave's 64 lanes x 2 words cover a row's maxima");
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        fa.amaxw, (short)0, (int)(fa.hbuf_bytes / 16 < 0x7fffffffull ? fa.hbuf_bytes / 16 : 0x7fffffffull), 0x00020000);
 
     __amdgpu_buffer_rsrc_t wrs = item_rsrc(blockIdx.x);
     WRaw w[2];
@@ -1799,6 +1882,119 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                     *reinterpret_cast<u4v_t*>(&opb[tl * ostr + sbl * 36 + part]) = v[u];
                 }
             }
+        }
+    };
+
+    // The down operand of a down slot's rows (at most kFuTD), all nsb_dn
+    // super-blocks, built in LDS from the gate||up items' h words: poll until
+    // the words and the row maxima words carry this call's epoch
+    // (device-coherent loads, bounded), then convert.  Each polling round issues the
+    // maxima loads (Me*aw words) and the first pass of h loads together, so a
+    // slot of one or two tokens (most routed slots) costs one round trip when
+    // its words are in.  Q4_K: the fp16 operand, prescaled, k-interleaved and
+    // with the sub-block sums split hi+lo exactly as prep_row builds it;
+    // MXFP4: the h words rounded to bf16, 8 per chunk in element order.
+    auto dn_build = [&](int Me, int off) {
+        constexpr int cpr = nsb_dn * 32;  // operand chunks per row
+        constexpr int ostr = kFuOpStride;
+        const int nwd = Me * aw;      // maxima words of the slot's rows
+        const int nch = Me * cpr;     // operand chunks of the slot's rows
+        int timed_out = 0;
+        for (int spin = 0;; ++spin) {
+            int ok = 1;
+            // maxima words: two per thread and load (16 bytes), so that the
+            // 128 words of a row are one wave's (aw == 128)
+            static_assert(kFuTD * aw <= 2 * NT, "one 16-byte maxima load per thread");
+            u4v_t mv;
+            if constexpr (!MX) {
+                const int i = 2 * tid;
+                mv = __builtin_amdgcn_raw_buffer_load_b128(ars, (off * aw + (i < nwd ? i : 0)) * 8, 0, 16);
+            }
+            for (int base = 0; base < nch; base += NT) {
+                const int qq = base + tid;
+                const bool live = qq < nch;
+                const int tl = live ? qq / cpr : 0, q = qq - (qq / cpr) * cpr;
+                const int sbl = q >> 5, sb = sbl;
+                if constexpr (MX) {
+                    const int rowb = ((off + tl) * inter + sb * 256 + 8 * (q & 31)) * 8;
+                    u4v_t hw[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) hw[i] = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16 * i, 0, 16);
+                    uint32_t o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (live && (hw[i].y != epoch || hw[i].w != epoch)) ok = 0;
+                        o[i] = (uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].x)) |
+                               ((uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].z)) << 16);
+                    }
+                    if (live) opb[tl * ostr + sbl * 36 + (q & 31)] = make_uint4(o[0], o[1], o[2], o[3]);
+                } else {
+                    const int gg = (q >> 3) & 3, c = q & 7;
+                    const int e0 = sb * 256 + 64 * gg + 4 * c;
+                    const int rowb = ((off + tl) * inter + e0) * 8;
+                    const u4v_t lo0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb, 0, 16);
+                    const u4v_t lo1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16, 0, 16);
+                    const u4v_t hi0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 256, 0, 16);
+                    const u4v_t hi1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 272, 0, 16);
+                    if (base == 0) {
+                        // the row maxima -> prescale exponents (the 128 words
+                        // of a row are one wave's)
+                        const int i = 2 * tid;
+                        float m = 0.0f;
+                        if (i < nwd) {
+                            // words {max bits, epoch}
+                            if (mv.y != epoch || mv.w != epoch)
+                                ok = 0;
+                            else
+                                m = fmaxf(fst_bits_f32(mv.x), fst_bits_f32(mv.z));
+                        }
+                        m = wave_fmax(m);
+                        if (lane == 0 && i < nwd) s_amax[i / aw][0] = m;
+                        __syncthreads();
+                        if (tid < Me) s_xs2[tid] = prescale_exp(s_amax[tid][0]);
+                        __syncthreads();
+                    }
+                    // words {h bits, epoch}: .y / .w hold the tags
+                    if (live && (lo0.y != epoch || lo0.w != epoch || lo1.y != epoch || lo1.w != epoch ||
+                                 hi0.y != epoch || hi0.w != epoch || hi1.y != epoch || hi1.w != epoch))
+                        ok = 0;
+                    const int sx = s_xs2[tl];
+                    h8_t v;
+                    v[0] = (_Float16)ldexpf(fst_bits_f32(lo0.x), -sx);
+                    v[1] = (_Float16)ldexpf(fst_bits_f32(lo1.x), -sx);
+                    v[2] = (_Float16)ldexpf(fst_bits_f32(lo0.z), -sx);
+                    v[3] = (_Float16)ldexpf(fst_bits_f32(lo1.z), -sx);
+                    v[4] = (_Float16)ldexpf(fst_bits_f32(hi0.x), -sx);
+                    v[5] = (_Float16)ldexpf(fst_bits_f32(hi1.x), -sx);
+                    v[6] = (_Float16)ldexpf(fst_bits_f32(hi0.z), -sx);
+                    v[7] = (_Float16)ldexpf(fst_bits_f32(hi1.z), -sx);
+                    if (live) opb[tl * ostr + sbl * 36 + (q & 31)] = __builtin_bit_cast(uint4, v);
+                    float s0 = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+                    float s1 = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
+                    s0 = s0 + fdpp<0xb1>(s0);  // quad_perm [1,0,3,2]
+                    s1 = s1 + fdpp<0xb1>(s1);
+                    s0 = s0 + fdpp<0x4e>(s0);  // quad_perm [2,3,0,1]
+                    s1 = s1 + fdpp<0x4e>(s1);
+                    s0 = s0 + fdpp<0x104>(s0);  // row_shl 4
+                    s1 = s1 + fdpp<0x104>(s1);
+                    if (live && c == 0) {
+                        const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
+                        const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
+                        const _Float16 z = (_Float16)0.0f;
+                        opb[tl * ostr + sbl * 36 + 32 + gg] = __builtin_bit_cast(uint4, h8_t{h0, h1, l0, l1, z, z, z, z});
+                    }
+                }
+            }
+            if (__syncthreads_and(ok)) break;
+            if (spin >= fa.spin_limit) {
+                timed_out = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (timed_out && tid == 0) {
+            atomicOr(&ra.meta[META_TIMEOUT], 1);
+            sticky_or(ra.meta, STICKY_TIMEOUT);
         }
     };
 
@@ -1842,7 +2038,6 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             acc[i] = fmaf(-S.dmin, Dm[i], acc[i]);
         }
     };
-    const int rsel = r & (kFuT - 1);  // MFMA rows 8..15 (discarded) read rows 0..7
 
     int opb_key = -1;  // what opb holds: slot (gate||up, one phase), slot | 2^20 (down), -1: neither
     // A gate||up item of a one-token slot gets its operand chunks loaded into
@@ -1863,15 +2058,30 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         const int nsb = dn ? nsb_dn : nsb_gu;
         int slot = t / tiles_gu, tile = t - slot * tiles_gu;
         if (dn) dn_map(t - ngu, slot, tile);
-        const int Me = min(r_sM[slot], kFuT), off = r_soff[slot];
+        const int Me = dn ? d_sM[slot] : r_sM[slot], off = dn ? d_soff[slot] : r_soff[slot];
         // the item that follows: the second half of this down pair, or claimed
         const bool pair1 = dyn && dn && t - ngu < D1 && ((t - ngu) & 1) == 0;
         const bool claims = dyn && !pair1;
         __amdgpu_buffer_rsrc_t nrs = wrs;
         f4_t acc = zf;
-        // gate||up operand layout: all super-blocks (at most 4 tokens) or two phases
-        const bool g2 = !dn && Me > 4;
-        const int ostr = dn || g2 ? kFuOpStride : kFuOpStride16;
+        // the operand layout of the item: nph super-blocks in opb at once
+        // (all of them, or phases rebuilt inside the super-block loop), the
+        // row stride, and the operand row a lane's MFMA row reads
+        int nph, ostr, rs;
+        if (Me <= 4 && !dn) {
+            nph = nsb_gu;
+            ostr = kFuOpStride16;
+            rs = r & 3;
+        } else if (Me <= 8) {  // (every down slot)
+            nph = 8;
+            ostr = kFuOpStride;
+            rs = r & 7;
+        } else {
+            nph = 4;
+            ostr = kFuOpStride4;
+            rs = r;
+        }
+        const bool multi = nph < nsb;
         if (!dn) {
             if (pre) {
                 const int sbl = tid >> 5, part = tid & 31;
@@ -1894,149 +2104,19 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                     }
                 }
             } else {
-                const int key = g2 ? -1 : slot;
-                if (key < 0 || key != opb_key) gu_build(std::integral_constant<int, 5>{}, Me, off, 0, g2 ? 8 : nsb_gu, ostr);
+                const int key = multi ? -1 : slot;
+                if (key < 0 || key != opb_key) gu_build(std::integral_constant<int, 5>{}, Me, off, 0, nph, ostr);
                 opb_key = key;
             }
             __syncthreads();
         } else {
-            // ---- the slot's down operand, built in LDS from the h words
-            // unless the previous item built it for the same slot.
-            // Each polling round issues the maxima loads (Me*aw words) and the
-            // first pass of h loads together, so a slot of one or two tokens
-            // (most routed slots) costs one round trip when its words are in.
-            int timed_out = 0;
-            const bool stage_op = (slot | 0x100000) != opb_key;
-            opb_key = slot | 0x100000;
-            constexpr int cpr = inter / 8;  // operand chunks per row
-            const int nwd = Me * aw;        // maxima words of the slot's rows
-            const int nch = Me * cpr;       // operand chunks of the slot's rows
-            if constexpr (MX) {
-                // bf16 operand: the slot's h words rounded to bf16, 8 per chunk
-                // in element order (no prescale, no sub-block sums)
-                for (int spin = 0; stage_op; ++spin) {
-                    int ok = 1;
-                    for (int base = 0; base < nch; base += NT) {
-                        const int qq = base + tid;
-                        const bool live = qq < nch;
-                        const int tl = live ? qq / cpr : 0, q = qq - (qq / cpr) * cpr;
-                        const int sb = q >> 5;
-                        const int rowb = ((off + tl) * inter + sb * 256 + 8 * (q & 31)) * 8;
-                        u4v_t hw[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) hw[i] = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16 * i, 0, 16);
-                        uint32_t o[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            if (live && (hw[i].y != epoch || hw[i].w != epoch)) ok = 0;
-                            o[i] = (uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].x)) |
-                                   ((uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].z)) << 16);
-                        }
-                        if (live) opb[tl * kFuOpStride + sb * 36 + (q & 31)] = make_uint4(o[0], o[1], o[2], o[3]);
-                    }
-                    if (__syncthreads_and(ok)) break;
-                    if (spin >= fa.spin_limit) {
-                        timed_out = 1;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(2);
-                }
-            } else {
-            for (int spin = 0; stage_op; ++spin) {
-                int ok = 1;
-                unsigned long long mv[2];
-#pragma unroll
-                for (int k = 0; k < 2; ++k) {  // kFuT * aw <= 2 * NT
-                    const int i = k * NT + tid;
-                    const int ii = i < nwd ? i : 0;
-                    mv[k] = ld_coherent_u64(fa.amaxw + (size_t)(off + ii / aw) * aw + (ii - (ii / aw) * aw));
-                }
-                for (int base = 0; base < nch; base += NT) {
-                    const int qq = base + tid;
-                    const bool live = qq < nch;
-                    const int tl = live ? qq / cpr : 0, q = qq - (qq / cpr) * cpr;
-                    const int sb = q >> 5, gg = (q >> 3) & 3, c = q & 7;
-                    const int e0 = sb * 256 + 64 * gg + 4 * c;
-                    const int rowb = ((off + tl) * inter + e0) * 8;
-                    const u4v_t lo0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb, 0, 16);
-                    const u4v_t lo1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16, 0, 16);
-                    const u4v_t hi0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 256, 0, 16);
-                    const u4v_t hi1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 272, 0, 16);
-                    if (base == 0) {
-                        // the row maxima -> prescale exponents (the 64 words of a
-                        // wave belong to one row: aw is a multiple of 64)
-#pragma unroll
-                        for (int k = 0; k < 2; ++k) {
-                            const int i = k * NT + tid;
-                            float m = 0.0f;
-                            if (i < nwd) {
-                                if ((uint32_t)(mv[k] >> 32) != epoch)
-                                    ok = 0;
-                                else
-                                    m = fst_bits_f32((uint32_t)mv[k]);
-                            }
-                            m = wave_fmax(m);
-                            if (lane == 0 && i < nwd) s_amax[i / aw][(i - (i / aw) * aw) >> 6] = m;
-                        }
-                        __syncthreads();
-                        if (tid < Me) {
-                            float a = s_amax[tid][0];
-                            if (aw > 64) a = fmaxf(a, s_amax[tid][1]);
-                            s_xs2[tid] = prescale_exp(a);
-                        }
-                        __syncthreads();
-                    }
-                    // words {h bits, epoch}: .y / .w hold the tags
-                    if (live && (lo0.y != epoch || lo0.w != epoch || lo1.y != epoch || lo1.w != epoch ||
-                                 hi0.y != epoch || hi0.w != epoch || hi1.y != epoch || hi1.w != epoch))
-                        ok = 0;
-                    const int s = s_xs2[tl];
-                    h8_t v;
-                    v[0] = (_Float16)ldexpf(fst_bits_f32(lo0.x), -s);
-                    v[1] = (_Float16)ldexpf(fst_bits_f32(lo1.x), -s);
-                    v[2] = (_Float16)ldexpf(fst_bits_f32(lo0.z), -s);
-                    v[3] = (_Float16)ldexpf(fst_bits_f32(lo1.z), -s);
-                    v[4] = (_Float16)ldexpf(fst_bits_f32(hi0.x), -s);
-                    v[5] = (_Float16)ldexpf(fst_bits_f32(hi1.x), -s);
-                    v[6] = (_Float16)ldexpf(fst_bits_f32(hi0.z), -s);
-                    v[7] = (_Float16)ldexpf(fst_bits_f32(hi1.z), -s);
-                    if (live) opb[tl * kFuOpStride + sb * 36 + (q & 31)] = __builtin_bit_cast(uint4, v);
-                    float s0 = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
-                    float s1 = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
-                    s0 = s0 + fdpp<0xb1>(s0);  // quad_perm [1,0,3,2]
-                    s1 = s1 + fdpp<0xb1>(s1);
-                    s0 = s0 + fdpp<0x4e>(s0);  // quad_perm [2,3,0,1]
-                    s1 = s1 + fdpp<0x4e>(s1);
-                    s0 = s0 + fdpp<0x104>(s0);  // row_shl 4
-                    s1 = s1 + fdpp<0x104>(s1);
-                    if (live && c == 0) {
-                        const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
-                        const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
-                        const _Float16 z = (_Float16)0.0f;
-                        opb[tl * kFuOpStride + sb * 36 + 32 + gg] =
-                            __builtin_bit_cast(uint4, h8_t{h0, h1, l0, l1, z, z, z, z});
-                    }
-                }
-                if (__syncthreads_and(ok)) break;
-                if (spin >= fa.spin_limit) {
-                    timed_out = 1;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-            }
-            }
-            if (timed_out && tid == 0) {
-                atomicOr(&ra.meta[META_TIMEOUT], 1);
-                sticky_or(ra.meta, STICKY_TIMEOUT);
-            }
+            // the slot's down operand, unless the previous item built it
+            const int key = slot | 0x100000;
+            if (key != opb_key) dn_build(Me, off);
+            opb_key = key;
             __syncthreads();
         }
-        // One super-block loop for both kinds, U = 2 per iteration (weight
-        // ring slot j), with the whole operand in opb: no staging and no
-        // barrier inside it except the one that publishes the claimed next
-        // item (and, for a two-phase gate||up operand, the rebuild after
-        // super-block 7).
-        const uint4* opr = pre && !dn ? opn : opb + (dn || g2 ? rsel : (r & 3)) * ostr;
+        const uint4* opr = pre && !dn ? opn : opb + rs * ostr;
         // one super-block step; j: the weight ring slot
         auto step = [&](int sb, auto jc) {
             constexpr int j = decltype(jc)::value;
@@ -2048,20 +2128,22 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             // one step later waits for it)
             if (claims && sb == nsb - 4 && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
             __builtin_amdgcn_sched_barrier(0);
-            compute(opr + (g2 ? (sb & 7) : sb) * 36, w[j], acc);
+            compute(opr + (sb & (nph - 1)) * 36, w[j], acc);
             if (sb == nsb - 3) {
                 if (tid == 0) s_claim = claimed;
                 __syncthreads();  // publishes s_claim
-            }
-            if (g2 && sb == 7) {
-                __syncthreads();
-                gu_build(std::integral_constant<int, 1>{}, Me, off, 8, 8, ostr);
-                __syncthreads();
             }
         };
         using J0 = std::integral_constant<int, 0>;
         using J1 = std::integral_constant<int, 1>;
         for (int sb0 = 0; sb0 < nsb - 2; sb0 += 2) {
+            if (multi && sb0 > 0 && (sb0 & (nph - 1)) == 0) {
+                // the operand's next phase (nph is even: the phases start at
+                // even super-blocks, before the last two)
+                __syncthreads();
+                gu_build(std::integral_constant<int, 1>{}, Me, off, sb0, nph, ostr);
+                __syncthreads();
+            }
             step(sb0, J0{});
             step(sb0 + 1, J1{});
         }
@@ -2133,7 +2215,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,
                      const RouteReq& rq, uint32_t epoch, int spin_limit, const uint16_t* h, hipEvent_t ev0,
                      hipEvent_t ev1) {
-    const RouteArgs ra = route_args(g, L, M, s.logits, rq.input_ids, rq.use_hash, rq.use_shared, rq.eids, rq.wts, s);
+    RouteArgs ra = route_args(g, L, M, s.logits, rq.input_ids, rq.use_hash, rq.use_shared, rq.eids, rq.wts, s);
+    if (rq.given) ra.given = rq.eids;
     FusedArgs fa{};
     fa.bank = L.bank;
     fa.expert_stride = L.expert_stride;
@@ -2186,8 +2269,8 @@ int moe_fused_occupancy(int codec) {
 
 bool moe_fused_supported(const Geometry& g, int M) {
     // instantiated for the DeepSeek-V4-Flash-like expert (4096 -> 2048 -> 4096)
-    return (g.codec == 0 || g.codec == 1) && M <= kFuT && g.E <= kFusedRouteMaxExperts && g.hd == 4096 &&
-           g.inter == 2048;
+    return (g.codec == 0 || g.codec == 1) && M <= kFuMaxM && M * g.tk <= kFuMaxPairs &&
+           g.E <= kFusedRouteMaxExperts && g.hd == 4096 && g.inter == 2048;
 }
 
 // Token capacity of the launch (the call's M bounds every slot's M_e): 8, 16,

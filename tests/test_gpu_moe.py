@@ -100,9 +100,9 @@ def test_repeated_calls_changing_M(fa, oracle, c2_layer):
             assert rel_l2(bf16_to_f32(out), ref) < TOL
 
 
-@pytest.mark.parametrize("M", [1, 2, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 16, 32])
 def test_fused_launch_matches_launch_chain(fa, c2_layer, M):
-    """The fused gate||up + down launch (router-driven calls of at most 8
+    """The fused gate||up + down launch (router-driven calls of at most 32
     tokens) gives the same bits as the separate launch chain: same routing,
     same fp16 operands (the down operand built in LDS from the epoch-tagged h
     words), same MFMA order.  Several batches in a row, so the epoch tags of
