@@ -1754,13 +1754,23 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 }
                 if (tid == 0) *count = total_v;
             };
-            // (ns0 <= kFuMaxPairs + 1 <= NT: one slot per thread)
-            split(kFuTD, d_seid, d_sM, d_soff, &s_nds);
-            if (__syncthreads_or(m0 > kFuT)) split(kFuT, r_seid, r_sM, r_soff, &r_meta[META_N_SLOTS]);
+            // (ns0 <= kFuMaxPairs + 1 <= NT: one slot per thread; without
+            // large slots, the down items read the gate||up table)
+            const int big = __syncthreads_or(m0 > kFuTD);
+            if (big) {
+                split(kFuTD, d_seid, d_sM, d_soff, &s_nds);
+                if (__syncthreads_or(m0 > kFuT)) split(kFuT, r_seid, r_sM, r_soff, &r_meta[META_N_SLOTS]);
+            } else if (tid == 0) {
+                s_nds = -1;
+            }
             __syncthreads();
         }
     }
-    const int ns = r_meta[META_N_SLOTS], nds = s_nds;
+    const int ns = r_meta[META_N_SLOTS], nds = s_nds < 0 ? ns : s_nds;
+    // the down slot table: its own when slots were split for the down items
+    const int* dtab_e = s_nds < 0 ? r_seid : d_seid;
+    const int* dtab_m = s_nds < 0 ? r_sM : d_sM;
+    const int* dtab_o = s_nds < 0 ? r_soff : d_soff;
     constexpr int tiles_gu = inter / 64, tiles_dn = hd / 128;
     const int ngu = ns * tiles_gu, total = ngu + nds * tiles_dn;
     const int ndn = total - ngu;
@@ -1814,7 +1824,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         }
         int sl, ti;
         dn_map(tt - ngu, sl, ti);
-        return bank + (size_t)d_seid[sl] * stride + 2 * proj + (size_t)(ti * kFuW + wave) * nsb_dn * CHK;
+        return bank + (size_t)dtab_e[sl] * stride + 2 * proj + (size_t)(ti * kFuW + wave) * nsb_dn * CHK;
     };
     auto rsrc = [&](const uint8_t* p, int nsb) -> __amdgpu_buffer_rsrc_t {
         const uint64_t u = (uint64_t)(uintptr_t)p;
@@ -2058,7 +2068,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         const int nsb = dn ? nsb_dn : nsb_gu;
         int slot = t / tiles_gu, tile = t - slot * tiles_gu;
         if (dn) dn_map(t - ngu, slot, tile);
-        const int Me = dn ? d_sM[slot] : r_sM[slot], off = dn ? d_soff[slot] : r_soff[slot];
+        const int Me = dn ? dtab_m[slot] : r_sM[slot], off = dn ? dtab_o[slot] : r_soff[slot];
         // the item that follows: the second half of this down pair, or claimed
         const bool pair1 = dyn && dn && t - ngu < D1 && ((t - ngu) & 1) == 0;
         const bool claims = dyn && !pair1;
