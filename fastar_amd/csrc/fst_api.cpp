@@ -595,7 +595,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     }
     if (!do_router && !mx && !sh16 && ctx->gemv && fst::gemv_supported(g, M, g.tk, use_shared, ctx->s)) {
         // at one or two tokens: one launch from the caller's routing to the
-        // combined rows (VALU dot products; every workgroup finds the slots)
+        // combined rows (every workgroup finds the slots)
         ctx->fused_epoch = ctx->fused_epoch == 0xffffffffu ? 1u : ctx->fused_epoch + 1u;
         fst::launch_expert_gemv(st, g, L, M, g.tk, d_eids, d_wts, use_shared, d_h, ctx->s, ctx->fused_epoch,
                                 ctx->spin_limit, d_out, d_out_routed, d_out_shared);
@@ -606,7 +606,17 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
     // one routed pair per token and no shared expert: the down launch writes
     // the bf16 result itself (the combine of one term), no combine launch
     const bool direct = use_routed && g.tk == 1 && !use_shared;
-    if (!do_router) {
+    // gate||up and down as one persistent launch (which routes or buckets the
+    // call itself), or the launch chain
+    const bool fused_path =
+        (fuse_topk || !do_router) && !direct && ctx->fused && use_routed && fst::moe_fused_supported(g, M);
+    if (!do_router && fused_path) {
+        // the fused launch buckets the given ids itself (and streams the
+        // shared expert first): only the token rows' operand (Q4_K) and the
+        // launch's claim counter are prepared
+        fst::launch_bucket_prep(st, g, M, 0, d_eids, ctx->s, mx ? nullptr : d_h, nullptr, nullptr, nullptr, 0, false);
+        ctx->mark("prep");
+    } else if (!do_router) {
         // the shared expert's gate||up weights (Q4_K) are read into the
         // device-wide cache during this latency-bound launch
         const size_t gu_bytes = (size_t)2 * c.inter_dim * (c.hidden_dim / 256) * 144;
@@ -617,7 +627,7 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
         ctx->mark("bucket_prep");
     }
     const int sh_q = use_shared && !sh16 ? 1 : 0;  // the shared expert runs as slot 0
-    if ((fuse_topk || !do_router) && !direct && ctx->fused && use_routed && fst::moe_fused_supported(g, M)) {
+    if (fused_path) {
         // gate||up and down in one persistent launch, then the combine
         ctx->fused_epoch = ctx->fused_epoch == 0xffffffffu ? 1u : ctx->fused_epoch + 1u;
         hipEvent_t k0 = nullptr, k1 = nullptr;

@@ -292,9 +292,11 @@ void launch_prep_bf16(hipStream_t st, const uint16_t* x, int rows, int K, _Float
 // launch; o1/o2: the outputs the down launch will write directly (their
 // rows of tokens with an invalid expert id are zeroed here); pf/pf_bytes
 // (optional): weights read into the device-wide cache by extra workgroups.
+// bucket = false: no bucketing (the fused launch buckets the ids itself).
+// Also zeroes the fused launch's claim counter.
 void launch_bucket_prep(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
                         const Scratch& s, const uint16_t* h, uint16_t* o1, uint16_t* o2, const void* pf = nullptr,
-                        size_t pf_bytes = 0);
+                        size_t pf_bytes = 0, bool bucket = true);
 // Residual add + RMSNorm per token row (see resid_norm_kernel); optional
 // outputs: h_out (x), normed (bf16), the fp16 operand in prep->x16p/sxp/xs,
 // and a one-slot table for launch_q4k_dense in slot_tab (META_WORDS + 3 ints).

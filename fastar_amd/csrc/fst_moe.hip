@@ -660,7 +660,7 @@ __global__ __launch_bounds__(256) void prep_kernel(Src src, const int* __restric
 // invalid, which the combine would have written as zeros.
 __global__ __launch_bounds__(kRouteThreads) void bucket_prep_kernel(
     int M, int E, int tk, int use_shared, const int32_t* __restrict__ eids, Scratch s, const uint16_t* h, int K,
-    uint16_t* o1, uint16_t* o2, int hd, int nprep, const uint4* __restrict__ pf, size_t pf_pieces) {
+    uint16_t* o1, uint16_t* o2, int hd, int nprep, const uint4* __restrict__ pf, size_t pf_pieces, int bucket) {
     // the fused launch that may follow claims work from this counter
     if (blockIdx.x == 0 && threadIdx.x == 0) *s.fused_claim = 0;
     if ((int)blockIdx.x > nprep) {
@@ -680,6 +680,7 @@ __global__ __launch_bounds__(kRouteThreads) void bucket_prep_kernel(
         prep_row<kRouteThreads>(SrcBf16{h}, blockIdx.x - 1, K, xv, s.x16p, s.sxp, s.xs);
         return;
     }
+    if (!bucket) return;
     __shared__ int s_eids[kMaxTokens * kMaxTopK];
     for (int i = threadIdx.x; i < M * tk; i += kRouteThreads) s_eids[i] = eids[i];
     __syncthreads();
@@ -698,12 +699,12 @@ __global__ __launch_bounds__(kRouteThreads) void bucket_prep_kernel(
 
 void launch_bucket_prep(hipStream_t st, const Geometry& g, int M, int use_shared, const int32_t* eids,
                         const Scratch& s, const uint16_t* h, uint16_t* o1, uint16_t* o2, const void* pf,
-                        size_t pf_bytes) {
+                        size_t pf_bytes, bool bucket) {
     const int nprep = h ? M : 0;
     const int extra = pf ? 32 : 0;  // 1024-thread prefetch workgroups
     hipLaunchKernelGGL(bucket_prep_kernel, dim3(1 + nprep + extra), dim3(kRouteThreads), 0, st, M, g.E, g.tk,
                        use_shared, eids, s, h, g.hd, o1, o2, g.hd, nprep, static_cast<const uint4*>(pf),
-                       pf_bytes / 16);
+                       pf_bytes / 16, bucket ? 1 : 0);
 }
 
 // The routing front of a layer call in one launch: workgroups [0, nrb) compute
