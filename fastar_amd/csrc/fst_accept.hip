@@ -1,17 +1,19 @@
 // fst_accept.hip — greedy and rejection-sampling acceptance for gfx950.
 //
 // Rows: target rows r = s*(k+1)+i (i = 0..k) of n_seq sequences, then (for
-// rejection sampling) draft rows n_seq*(k+1) + s*k + i.  Each row of V logits
-// is split into kChunks chunks processed by one workgroup each.
+// rejection sampling) draft rows n_seq*(k+1) + s*k + i.
 //
 // Greedy (src/fst_engine.cpp:6021-6063): argmax per target row with the
 // reference's sequential semantics (first maximum wins, NaN skipped, a NaN at
 // index 0 pins the result to 0), then the longest matching prefix and bonus.
 //
-// Rejection sampling: probabilities in exact 2^-32 fixed point
-// E = floor(exp(l - max) * 2^32) with the shared fst_expf, integer sums, and
-// 128-bit integer comparisons/prefix sums, so the accept decisions and the
-// resampled token are identical to the CPU oracle for identical logits.
+// Rejection sampling (defined by this build; the reference is greedy-only):
+// each row's softmax (max, sum) in binary32 with a fixed chunking and
+// summation order, u < p/q decided as u*q < p, and the resampled (or bonus)
+// token drawn by an exponential race (argmin of -log(u_v)/r_v over the
+// residual r = p - q > 0, per-element Philox uniforms), as Gumbel-max
+// sampling draws; every operation is the CPU oracle's, in the same order, so
+// the accepted lengths and tokens are identical to it for identical logits.
 #include <atomic>
 #include <mutex>
 #include <string>
@@ -22,39 +24,30 @@
 
 namespace fst {
 
-constexpr int kChunks = 64;
-// threads of the per-sequence residual and sampling workgroups (two
-// exponentials and 128-bit products per element, few workgroups: compute
-// bound per thread; the per-row sums keep 256, their grid is large)
-constexpr int kProbThreads = 1024;
 typedef unsigned __int128 u128;
 
-// Rejection-sampling tail launch (acc_tail_kernel): chunks per sequence,
-// threads, rows (2k + 1 <= 17), elements per thread at most, and the
-// arrival counters: kTailGroups16 groups of 16 chunks, then one top counter,
-// each on its own 256-byte line.
-constexpr int kTailThreads = 512;
-constexpr int kTailChunks = 256;
-constexpr int kTailRows = 17;
-constexpr int kTailPerMax = 2;  // chunk length <= 1024
-constexpr int kTailArrGroups = kTailChunks / 16;
-constexpr int kTailCntStride = 32;  // u64 words between counters
-// [n_seq][kTailChunks][3] chunk sums (residual lo, hi; target E), then
-// [n_seq][kTailArrGroups + 1] counters.
-static size_t tail_words(int n_seq) {
-    return (size_t)n_seq * kTailChunks * 3 + (size_t)n_seq * (kTailArrGroups + 1) * kTailCntStride;
+// Rejection sampling: softmax-statistics chunks per row, race chunks per
+// sequence (the tail launch's workgroups), threads of the tail launch, and
+// the tail's arrival counters: kRsArrGroups groups of 16 race chunks, then
+// one top counter, each on its own 256-byte line.
+constexpr int kRsChunks = 64;
+constexpr int kRsRaceChunks = 256;
+constexpr int kRsTailThreads = 512;
+constexpr int kRsArrGroups = kRsRaceChunks / 16;
+constexpr int kRsCntStride = 32;  // u64 words between counters
+constexpr int kRsMaxRows = 2 * 63 + 1;  // rows of one sequence (k <= 63)
+// [n_seq][kRsRaceChunks][2] chunk race results, then [n_seq][kRsArrGroups + 1] counters.
+static size_t rs_tail_words(int n_seq) {
+    return (size_t)n_seq * kRsRaceChunks * 2 + (size_t)n_seq * (kRsArrGroups + 1) * kRsCntStride;
 }
 
 struct AccWs {
-    float* part_max;          // [R][kChunks]
-    int* part_idx;            // [R][kChunks]
-    unsigned long long* part_sum;  // [R][kChunks]
-    unsigned long long* part_res;  // [n_seq][kChunks][2] (u128 as lo, hi)
-    unsigned long long* dec;       // [n_seq][8]
-    unsigned long long* gslot;     // [R][kChunks] greedy chunk partials (zero between calls)
-    float* xsel;                   // [R] each row's logit at its position's draft token (acc_sums_kernel)
-    unsigned long long* tail;      // acc_tail_kernel: chunk sums and counters (counters zero between calls)
+    unsigned long long* gslot;     // [R][kGreedySlots] greedy chunk words (zero between calls)
+    float2* rs_part;               // [R][kRsChunks] rejection sampling: chunk (max, sum)
+    float* xsel;                   // [R] each row's scaled logit at its position's draft token
+    unsigned long long* tail;      // acc_rs_tail_kernel: chunk race results and counters (counters zero between calls)
 };
+constexpr int kGreedySlots = 64;   // >= the greedy launch's chunks per row
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -62,12 +55,8 @@ static AccWs carve(void* ws, int n_seq, int k) {
     const int R = n_seq * (k + 1) + n_seq * k;
     char* p = (char*)ws;
     AccWs w;
-    w.part_max = (float*)p; p += align256(sizeof(float) * R * kChunks);
-    w.part_idx = (int*)p; p += align256(sizeof(int) * R * kChunks);
-    w.part_sum = (unsigned long long*)p; p += align256(8ull * R * kChunks);
-    w.part_res = (unsigned long long*)p; p += align256(16ull * n_seq * kChunks);
-    w.dec = (unsigned long long*)p; p += align256(64ull * n_seq);
-    w.gslot = (unsigned long long*)p; p += align256(8ull * R * kChunks);
+    w.gslot = (unsigned long long*)p; p += align256(8ull * R * kGreedySlots);
+    w.rs_part = (float2*)p; p += align256(8ull * R * kRsChunks);
     w.xsel = (float*)p; p += align256(sizeof(float) * R);
     w.tail = (unsigned long long*)p;
     return w;
@@ -76,9 +65,8 @@ static AccWs carve(void* ws, int n_seq, int k) {
 size_t accept_ws_bytes(int n_seq, int k, int V) {
     (void)V;
     const int R = n_seq * (k + 1) + n_seq * k;
-    return align256(sizeof(float) * R * kChunks) + align256(sizeof(int) * R * kChunks) +
-           align256(8ull * R * kChunks) + align256(16ull * n_seq * kChunks) + align256(64ull * n_seq) +
-           align256(8ull * R * kChunks) + align256(sizeof(float) * R) + align256(8ull * tail_words(n_seq)) + 256;
+    return align256(8ull * R * kGreedySlots) + align256(8ull * R * kRsChunks) + align256(sizeof(float) * R) +
+           align256(8ull * rs_tail_words(n_seq)) + 256;
 }
 
 // Calls f(x, v) for v = v0, v0 + stride, ... < v1 in that order, with the
@@ -96,485 +84,6 @@ __device__ __forceinline__ void for_strided(const float* __restrict__ p, int v0,
             if (base + u * stride < v1) f(x[u], base + u * stride);
     }
 }
-// Two rows at once (the same indices of p and q).
-template <int NB, typename F>
-__device__ __forceinline__ void for_strided2(const float* __restrict__ p, const float* __restrict__ q, int v0,
-                                             int v1, int stride, F&& f) {
-    for (int base = v0; base < v1; base += NB * stride) {
-        float x[NB], y[NB];
-#pragma unroll
-        for (int u = 0; u < NB; ++u) {
-            const int v = min(base + u * stride, v1 - 1);
-            x[u] = p[v];
-            y[u] = q ? q[v] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < NB; ++u)
-            if (base + u * stride < v1) f(x[u], y[u], base + u * stride);
-    }
-}
-
-__device__ __forceinline__ const float* row_ptr(const float* target, const float* draft, int n_tgt_rows,
-                                                int r, int V) {
-    return r < n_tgt_rows ? target + (size_t)r * V : draft + (size_t)(r - n_tgt_rows) * V;
-}
-
-// (max over non-NaN of x*inv_t, lowest index attaining it) per (row, chunk).
-__global__ __launch_bounds__(256) void acc_stats_kernel(const float* __restrict__ target,
-                                                        const float* __restrict__ draft, int n_tgt_rows,
-                                                        int V, float inv_t, float* __restrict__ part_max,
-                                                        int* __restrict__ part_idx) {
-    const int c = blockIdx.x, r = blockIdx.y;
-    const float* row = row_ptr(target, draft, n_tgt_rows, r, V);
-    const int clen = (V + kChunks - 1) / kChunks;
-    const int b0 = c * clen, b1 = min(V, b0 + clen);
-    float best = 0.0f;
-    int bi = 0x7fffffff;
-    for_strided<8>(row, b0 + (int)threadIdx.x, b1, 256, [&](float x, int v) {
-        const float l = x * inv_t;
-        if (l != l) return;
-        if (bi == 0x7fffffff || l > best) { best = l; bi = v; }
-    });
-    if (bi == 0x7fffffff) bi = -1;
-    wave_argmax(best, bi);
-    __shared__ float sm[4];
-    __shared__ int si[4];
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        sm[wave] = best;
-        si[wave] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int q = 1; q < 4; ++q) argmax_merge(best, bi, sm[q], si[q]);
-        part_max[(size_t)r * kChunks + c] = best;
-        part_idx[(size_t)r * kChunks + c] = bi;
-    }
-}
-
-// Wave-parallel reduction of the kChunks (= 64) chunk partials of row r: lane
-// c reads chunk c.  Returns (max, lowest index attaining it, -1 if the row
-// has no number) in every lane.
-__device__ __forceinline__ void wave_row_argmax(const float* part_max, const int* part_idx, int r, float* mx,
-                                                int* idx) {
-    const int lane = threadIdx.x & 63;
-    float m = part_max[(size_t)r * kChunks + lane];
-    int i = part_idx[(size_t)r * kChunks + lane];
-    wave_argmax(m, i);
-    *mx = m;
-    *idx = i;
-}
-
-__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) { return wave_sum_u64_dpp(v); }
-
-// Wave-wide sum of a u128 as four 32-bit limbs summed exactly in u64, then
-// recombined (result in every lane).
-__device__ __forceinline__ u128 wave_sum_u128(u128 v) {
-    u128 t = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) t += (u128)wave_sum_u64_dpp((uint32_t)(v >> (32 * k))) << (32 * k);
-    return t;
-}
-
-
-__device__ __forceinline__ unsigned long long fixed_prob(float x, float inv_t, float mx, int any) {
-    const float l = x * inv_t;
-    if (!any || l != l) return 0ull;
-    if (l == mx) return 4294967296ull;
-    const float d = l - mx;
-    if (d != d) return 0ull;
-    return (unsigned long long)fst_prob_fixed(d);
-}
-
-__device__ __forceinline__ void wave_row_max_any(const float* part_max, const int* part_idx, int r, float* mx,
-                                                 int* any) {
-    int idx;
-    wave_row_argmax(part_max, part_idx, r, mx, &idx);
-    *any = idx >= 0;
-}
-
-// Chunk sums of E for every row.  With xsel given, the workgroup whose chunk
-// holds the row's draft token (position i of sequence s: draft[s*k + i], for
-// target rows i < k and every draft row) also writes that logit to xsel[r],
-// so that the decisions need no dependent load of it later.
-__global__ __launch_bounds__(256) void acc_sums_kernel(const float* __restrict__ target,
-                                                       const float* __restrict__ draft, int n_tgt_rows,
-                                                       int V, float inv_t,
-                                                       const float* __restrict__ part_max,
-                                                       const int* __restrict__ part_idx,
-                                                       unsigned long long* __restrict__ part_sum,
-                                                       const int32_t* __restrict__ dtok, int k,
-                                                       float* __restrict__ xsel) {
-    const int c = blockIdx.x, r = blockIdx.y;
-    const float* row = row_ptr(target, draft, n_tgt_rows, r, V);
-    const int clen = (V + kChunks - 1) / kChunks;
-    const int b0 = c * clen, b1 = min(V, b0 + clen);
-    if (xsel && threadIdx.x == 0 && k > 0) {
-        const int seq = r < n_tgt_rows ? r / (k + 1) : (r - n_tgt_rows) / k;
-        const int pos = r < n_tgt_rows ? r % (k + 1) : (r - n_tgt_rows) % k;
-        if (pos < k) {
-            const int x = dtok[seq * k + pos];
-            if (x >= b0 && x < b1) xsel[r] = row[x];
-        }
-    }
-    // the first 8 elements of each thread are loaded before the row maximum
-    // is known (they do not depend on it), so both round trips overlap
-    constexpr int NB = 8;
-    const int v0 = b0 + (int)threadIdx.x;
-    float x0[NB];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) x0[u] = row[max(min(v0 + u * 256, b1 - 1), 0)];
-    __shared__ float s_mx;
-    __shared__ int s_any;
-    if (threadIdx.x < 64) {
-        float mx;
-        int any;
-        wave_row_max_any(part_max, part_idx, r, &mx, &any);
-        if (threadIdx.x == 0) {
-            s_mx = mx;
-            s_any = any;
-        }
-    }
-    __syncthreads();
-    const float mx = s_mx;
-    const int any = s_any;
-    unsigned long long acc = 0;
-#pragma unroll
-    for (int u = 0; u < NB; ++u)
-        if (v0 + u * 256 < b1) acc += fixed_prob(x0[u], inv_t, mx, any);
-    for_strided<8>(row, v0 + NB * 256, b1, 256, [&](float x, int) { acc += fixed_prob(x, inv_t, mx, any); });
-    // integer sums: any order gives the same total
-    __shared__ unsigned long long sm[256 / 64];
-    acc = wave_sum_u64_dpp(acc);
-    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long t = 0;
-        for (int w = 0; w < 256 / 64; ++w) t += sm[w];
-        part_sum[(size_t)r * kChunks + c] = t;
-    }
-}
-
-// dec layout per sequence: [0] n_acc, [1] sampling target row, [2] mode
-// (0: residual vs draft row, 1: sample from target row), [3] U', [4] Sp, [5] Sq,
-// [6] draft row, [7] unused.
-// One workgroup per sequence; wave w decides positions w, w+NW, ... in
-// parallel (each decision is independent given the logits and uniforms).
-constexpr int kDecideWaves = 8;
-__global__ __launch_bounds__(64 * kDecideWaves) void acc_decide_kernel(
-    const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
-    float inv_t, const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base,
-    const float* __restrict__ part_max, const int* __restrict__ part_idx,
-    const unsigned long long* __restrict__ part_sum, unsigned long long* __restrict__ dec,
-    int32_t* __restrict__ n_acc, int32_t* __restrict__ tokens) {
-    const int s = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n_tgt = n_seq * (k + 1);
-    __shared__ int accept[64];
-    __shared__ unsigned long long Sp_s[65], Sq_s[64];
-    for (int i = wave; i <= k; i += kDecideWaves) {
-        const int rt = s * (k + 1) + i;
-        const unsigned long long Sp = wave_sum_u64(part_sum[(size_t)rt * kChunks + lane]);
-        if (i == k) {
-            if (lane == 0) Sp_s[k] = Sp;
-            continue;
-        }
-        const int rd = n_tgt + s * k + i;
-        const unsigned long long Sq = wave_sum_u64(part_sum[(size_t)rd * kChunks + lane]);
-        float mp, mq;
-        int ap, aq;
-        wave_row_max_any(part_max, part_idx, rt, &mp, &ap);
-        wave_row_max_any(part_max, part_idx, rd, &mq, &aq);
-        if (lane == 0) {
-            const int x = draft[s * k + i];
-            int ok = 0;
-            if (x >= 0 && x < V) {
-                const unsigned long long P = fixed_prob(target[(size_t)rt * V + x], inv_t, mp, ap);
-                const unsigned long long Q = fixed_prob(draftl[(size_t)(rd - n_tgt) * V + x], inv_t, mq, aq);
-                const uint32_t U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)i, 0);
-                const u128 lhs = (u128)U * (u128)Q * (u128)Sp;
-                const u128 rhs = ((u128)P * (u128)Sq) << 24;
-                ok = lhs < rhs;
-            }
-            accept[i] = ok;
-            Sp_s[i] = Sp;
-            Sq_s[i] = Sq;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int n = 0;
-        while (n < k && accept[n]) ++n;
-        unsigned long long* d = dec + (size_t)s * 8;
-        d[0] = (unsigned long long)n;
-        d[1] = (unsigned long long)(s * (k + 1) + n);
-        d[3] = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)n, 1);
-        d[4] = Sp_s[n];
-        if (n < k) {
-            d[2] = 0;
-            d[5] = Sq_s[n];
-            d[6] = (unsigned long long)(n_tgt + s * k + n);
-        } else {
-            d[2] = 1;
-            d[5] = 0;
-            d[6] = 0;
-        }
-        for (int i = 0; i < n; ++i) tokens[s * (k + 1) + i] = draft[s * k + i];
-        for (int i = n; i <= k; ++i) tokens[s * (k + 1) + i] = -1;
-        n_acc[s] = n;
-    }
-}
-
-// Residual weight of one element from its target (xt) and draft (xd) logits.
-__device__ __forceinline__ u128 res_of(float xt, float xd, float inv_t, float mp, int ap, float mq, int aq,
-                                       unsigned long long Sp, unsigned long long Sq, int mode) {
-    const unsigned long long P = fixed_prob(xt, inv_t, mp, ap);
-    if (mode) return (u128)P;
-    const unsigned long long Q = fixed_prob(xd, inv_t, mq, aq);
-    const u128 a = (u128)P * Sq, b = (u128)Q * Sp;
-    return a > b ? a - b : (u128)0;
-}
-__device__ __forceinline__ u128 res_value(const float* trow, const float* drow, int v, float inv_t,
-                                          float mp, int ap, float mq, int aq, unsigned long long Sp,
-                                          unsigned long long Sq, int mode) {
-    return res_of(trow[v], mode ? 0.0f : drow[v], inv_t, mp, ap, mq, aq, Sp, Sq, mode);
-}
-
-struct RowCtx {
-    const float* trow;
-    const float* drow;
-    float mp, mq;
-    int ap, aq, mode;
-    unsigned long long Sp, Sq;
-};
-
-// Called by all lanes of the first wave; lane 0 stores the context.
-__device__ void load_rowctx_wave(const float* target, const float* draftl, int n_tgt, int V,
-                                 const float* part_max, const int* part_idx, const unsigned long long* d,
-                                 RowCtx& rc) {
-    const int rt = (int)d[1];
-    const int mode = (int)d[2];
-    float mp, mq = 0.0f;
-    int ap, aq = 0;
-    wave_row_max_any(part_max, part_idx, rt, &mp, &ap);
-    const int rd = (int)d[6];
-    if (mode == 0) wave_row_max_any(part_max, part_idx, rd, &mq, &aq);
-    if ((threadIdx.x & 63) == 0) {
-        rc.mode = mode;
-        rc.Sp = d[4];
-        rc.Sq = d[5];
-        rc.trow = target + (size_t)rt * V;
-        rc.drow = mode == 0 ? draftl + (size_t)(rd - n_tgt) * V : nullptr;
-        rc.mp = mp;
-        rc.ap = ap;
-        rc.mq = mq;
-        rc.aq = aq;
-    }
-}
-
-// Residual (or target) chunk sums for the one sampling row of each sequence.
-__global__ __launch_bounds__(kProbThreads) void acc_res_chunks_kernel(
-    const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
-    float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
-    const unsigned long long* __restrict__ dec, unsigned long long* __restrict__ part_res) {
-    const int c = blockIdx.x, s = blockIdx.y;
-    const unsigned long long* d = dec + (size_t)s * 8;
-    const int clen = (V + kChunks - 1) / kChunks;
-    const int b0 = c * clen, b1 = min(V, b0 + clen);
-    // the thread's first elements are loaded as soon as the sampling rows are
-    // known, before their maxima (round trips overlap)
-    constexpr int NB = 2;
-    const int v0 = b0 + (int)threadIdx.x;
-    const int mode0 = (int)d[2];
-    const float* trow0 = target + (size_t)d[1] * V;
-    const float* drow0 = mode0 == 0 ? draftl + ((size_t)d[6] - (size_t)n_seq * (k + 1)) * V : trow0;
-    float xt0[NB], xd0[NB];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) {
-        const int v = max(min(v0 + u * kProbThreads, b1 - 1), 0);
-        xt0[u] = trow0[v];
-        xd0[u] = drow0[v];
-    }
-    __shared__ RowCtx rc;
-    if (threadIdx.x < 64) load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
-    __syncthreads();
-    u128 acc = 0;
-#pragma unroll
-    for (int u = 0; u < NB; ++u)
-        if (v0 + u * kProbThreads < b1)
-            acc += res_of(xt0[u], rc.mode ? 0.0f : xd0[u], inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
-    for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, v0 + NB * kProbThreads, b1, kProbThreads,
-                    [&](float xt, float xd, int) {
-                        acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
-                    });
-    // integer sums: any order gives the same total
-    __shared__ u128 sm[kProbThreads / 64];
-    acc = wave_sum_u128(acc);
-    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        u128 tot = 0;
-        for (int w = 0; w < kProbThreads / 64; ++w) tot += sm[w];
-        unsigned long long* o = part_res + ((size_t)s * kChunks + c) * 2;
-        o[0] = (unsigned long long)tot;
-        o[1] = (unsigned long long)(tot >> 64);
-    }
-}
-
-__device__ __forceinline__ u128 shfl_u128(u128 v, int src) {
-    const uint64_t lo = (uint64_t)v, hi = (uint64_t)(v >> 64);
-    const uint32_t a = __shfl((uint32_t)lo, src, 64), b = __shfl((uint32_t)(lo >> 32), src, 64);
-    const uint32_t c = __shfl((uint32_t)hi, src, 64), d = __shfl((uint32_t)(hi >> 32), src, 64);
-    return ((u128)(((uint64_t)d << 32) | c) << 64) | (u128)(((uint64_t)b << 32) | a);
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave (exact, unsigned 128-bit).
-__device__ __forceinline__ u128 wave_incl_scan_u128(u128 v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const u128 o = shfl_u128(v, max(lane - off, 0));
-        if (lane >= off) v += o;
-    }
-    return v;
-}
-
-// Inverse-CDF pick: the first v whose inclusive prefix exceeds
-// target = (U' * total) >> 24.  Chunk sums are scanned by one wave (lane c
-// = chunk c), then the chosen chunk by the whole workgroup (thread t owns a
-// contiguous run), and only the owning thread walks its few elements.
-__global__ __launch_bounds__(kProbThreads) void acc_sample_kernel(
-    const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V,
-    float inv_t, const float* __restrict__ part_max, const int* __restrict__ part_idx,
-    const unsigned long long* __restrict__ part_sum, unsigned long long* __restrict__ dec,
-    const unsigned long long* __restrict__ part_res, int32_t* __restrict__ tokens) {
-    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ RowCtx rc;
-    __shared__ u128 s_target, s_before;
-    __shared__ int s_chunk;
-    __shared__ u128 wtot[kProbThreads / 64];
-    __shared__ int s_owner;
-    __shared__ u128 s_run;
-    __shared__ int s_tok;
-    unsigned long long* d = dec + (size_t)s * 8;
-    // the chunk totals do not depend on the row context: load them first so
-    // that both round trips overlap
-    unsigned long long o0 = 0, o1 = 0;
-    if (tid < 64) {
-        const unsigned long long* o = part_res + ((size_t)s * kChunks + lane) * 2;
-        o0 = o[0];
-        o1 = o[1];
-        load_rowctx_wave(target, draftl, n_seq * (k + 1), V, part_max, part_idx, d, rc);
-    }
-    __syncthreads();
-    if (tid < 64) {
-        const unsigned long long U2 = d[3];
-        u128 cs = ((u128)o1 << 64) | (u128)o0;
-        u128 pre = wave_incl_scan_u128(cs);
-        u128 tot = shfl_u128(pre, 63);
-        int mode = rc.mode;
-        if (mode == 0 && tot == 0) {
-            // residual is identically zero: sample from the target row instead
-            mode = 1;
-            cs = (u128)part_sum[(size_t)((int)d[1]) * kChunks + lane];
-            pre = wave_incl_scan_u128(cs);
-            tot = shfl_u128(pre, 63);
-        }
-        int chunk = -1;
-        u128 tg = 0;
-        if (tot != 0) {
-            tg = ((u128)U2 * tot) >> 24;
-            const unsigned long long hit = __ballot(pre > tg);
-            chunk = hit ? __ffsll((long long)hit) - 1 : -1;
-        }
-        const u128 before = chunk > 0 ? shfl_u128(pre, chunk - 1) : (u128)0;
-        if (lane == 0) {
-            rc.mode = mode;
-            s_chunk = chunk;
-            s_target = tg;
-            s_before = before;
-            s_tok = 0;
-        }
-    }
-    __syncthreads();
-    const int c = s_chunk;
-    if (c >= 0) {
-        const int clen = (V + kChunks - 1) / kChunks;
-        const int b0 = c * clen, b1 = min(V, b0 + clen);
-        const int per = (clen + kProbThreads - 1) / kProbThreads;
-        const int v0 = b0 + tid * per, v1 = min(b1, v0 + per);
-        // the thread's residual values stay in registers for the owner's walk
-        // (runs of up to kCache elements; longer ones are recomputed there)
-        constexpr int kCache = 16;
-        u128 cache[kCache];
-        u128 acc = 0;
-        if (per <= kCache) {
-            // slots past the run length `per` (uniform) are skipped, not
-            // computed and discarded: each slot costs two exponentials and
-            // 128-bit products
-            float xt[kCache], xd[kCache];
-#pragma unroll
-            for (int u = 0; u < kCache; ++u) {
-                if (u >= per) break;
-                const int v = max(min(v0 + u, v1 - 1), 0);
-                xt[u] = rc.trow[v];
-                xd[u] = rc.mode ? 0.0f : rc.drow[v];
-            }
-#pragma unroll
-            for (int u = 0; u < kCache; ++u) {
-                cache[u] = 0;
-                if (u >= per) continue;
-                if (v0 + u < v1)
-                    cache[u] = res_of(xt[u], xd[u], inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
-                acc += cache[u];
-            }
-        } else {
-            for_strided2<8>(rc.trow, rc.mode ? nullptr : rc.drow, v0, v1, 1, [&](float xt, float xd, int) {
-                acc += res_of(xt, xd, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq, rc.mode);
-            });
-        }
-        const u128 pre = wave_incl_scan_u128(acc);
-        if (lane == 63) wtot[wave] = pre;
-        if (tid == 0) s_owner = 0x7fffffff;
-        __syncthreads();
-        u128 base = s_before;
-        for (int w2 = 0; w2 < wave; ++w2) base += wtot[w2];
-        const unsigned long long hit = __ballot(base + pre > s_target);
-        if (hit && lane == __ffsll((long long)hit) - 1) atomicMin(&s_owner, tid);
-        __syncthreads();
-        if (tid == s_owner) s_run = base + pre - acc;  // prefix before this thread's run
-        __syncthreads();
-        if (tid == s_owner) {
-            u128 run = s_run;
-            int tok = v1 - 1;
-            if (per <= kCache) {
-#pragma unroll
-                for (int u = 0; u < kCache; ++u) {
-                    if (v0 + u >= v1) break;
-                    run += cache[u];
-                    if (run > s_target) {
-                        tok = v0 + u;
-                        break;
-                    }
-                }
-            } else {
-                for (int v = v0; v < v1; ++v) {
-                    run += res_value(rc.trow, rc.drow, v, inv_t, rc.mp, rc.ap, rc.mq, rc.aq, rc.Sp, rc.Sq,
-                                     rc.mode);
-                    if (run > s_target) {
-                        tok = v;
-                        break;
-                    }
-                }
-            }
-            s_tok = tok;
-        }
-        __syncthreads();
-        if (tid == 0) tokens[s * (k + 1) + (int)d[0]] = s_owner == 0x7fffffff ? 0 : s_tok;
-    } else if (tid == 0) {
-        tokens[s * (k + 1) + (int)d[0]] = 0;
-    }
-}
-
 // Greedy acceptance in one launch, without counters.  Every (row, chunk)
 // workgroup reduces its chunk to (max, lowest index) and publishes it as one
 // 64-bit word {tag, max bits}, tag = epoch << 20 | (index + 1): a word is
@@ -761,419 +270,375 @@ void launch_accept_greedy(hipStream_t st, const float* target, int n_seq, int k,
 }
 
 
-// ------------------------------- rejection sampling: decide, residual, pick
+// ------------------------------------------------- rejection sampling
 //
-// The last three steps of the chain in one launch.  Workgroup (c, s) of
-// kTailChunks chunks per sequence:
-//   - loads chunk c of every row of sequence s, the draft tokens' logits and
-//     the row partials of the maxima and sums launches, all at once;
-//   - takes the accept decisions (every workgroup alike, as acc_decide_kernel);
-//   - sums the residual of its chunk (and the target row's E, for the case
-//     of an identically zero residual), writes the sums with device-coherent
-//     stores and counts itself in with one atomic per workgroup;
-//   - the last workgroup of the sequence to arrive (the counter is left at
-//     zero) finds the chunk holding the inverse-CDF target, loads it and
-//     picks the token, then writes n_acc and the tokens.
-// No workgroup waits for another, so any grid size is safe.  The arithmetic
-// is the chain's, and the results are identical to it and to the CPU oracle.
-// The two searches ("first index whose inclusive prefix exceeds t") run over
-// LDS: sums of 16-element groups and of 16-group super-groups, then one wave
-// locates the super-group, the group and the element, each level by a
-// ballot over per-lane prefix sums of at most 16 terms (no u128 wave scans).
-#define TAIL_STAMP(i) \
-    do {              \
-    } while (0)
-#define TAIL_FLUSH(i0, i1) \
-    do {                   \
-    } while (0)
-constexpr int kTailWaves = kTailThreads / 64;
-constexpr int kTailMaxN = kTailPerMax * kTailThreads;  // longest array searched
-constexpr int kTailGroups = kTailMaxN / 16;            // 16-element groups
-static_assert(kTailChunks <= kTailThreads && kTailGroups <= 64, "search levels");
+// Two launches per call, with the CPU oracle's arithmetic in its order
+// (fo_rs_row_stats, fo_rs_race, fo_accept_stochastic):
+//   acc_rs_stats_kernel  workgroup (c, r): chunk c of row r (kRsChunks chunks
+//                        of L = ceil(V/64) rounded up to 4 elements) reduced
+//                        to its softmax partial (m_c, s_c): thread t adds
+//                        e(x | m_c) over elements b0 + 4t + 1024i + {0..3}
+//                        in that order, the waves' partials by the halving
+//                        tree, the four wave sums left to right; the
+//                        workgroup whose chunk holds the row's draft token
+//                        also stores that scaled logit (xsel);
+//   acc_rs_tail_kernel   workgroup (c, s): every workgroup merges the
+//                        sequence's row partials into (M, S) per row (the
+//                        halving tree over the 64 chunks), takes the accept
+//                        decisions (wave 0, one lane per position), runs the
+//                        exponential race over race chunk c of the first
+//                        rejected position (or the bonus row), publishes the
+//                        chunk's two minimum keys with device-coherent stores
+//                        and counts itself in (the 16th arrival of a group of
+//                        16 chunks counts the group in at a top counter, each
+//                        on its own line); the last workgroup takes the
+//                        minimum over the chunks and writes n_acc and the
+//                        tokens.  With at most 16 rows per sequence (k <= 7)
+//                        and short race chunks, every row's chunk is loaded
+//                        with the partials, so the race does not wait for a
+//                        second round trip after the decisions.
+// No workgroup waits for another, so any grid is safe; the counters are
+// left at zero by their last arrival.
+__device__ __forceinline__ int rs_chunk_len(int V) { return ((V + kRsChunks - 1) / kRsChunks + 3) & ~3; }
 
+// e(x | M) of a scaled logit: 0 for NaN, -inf, or a row with no number
+__device__ __forceinline__ float rs_e(float x, float M) {
+    if (x != x || M == fst_bits_f32(0xff800000u)) return 0.0f;
+    return fst_rel_exp(x, M);
+}
 
-// u128 as four 32-bit limbs, each held in 64 bits so that sums over up to
-// 2^32 terms need no carries until recombined.
-struct Limbs {
-    unsigned long long l[4];
-};
-__device__ __forceinline__ Limbs to_limbs(u128 v) {
-    Limbs r;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) r.l[q] = (uint32_t)(v >> (32 * q));
-    return r;
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long x) { return ~wave_max_u64(~x); }
+
+// fst_softmax_merge with one exponential: the larger maximum's weight is
+// exactly 1 and s*1 = s, so a = s1*w1, b = s2*w2, a + b come out bit for bit.
+__device__ __forceinline__ void rs_merge(float& m1, float& s1, float m2, float s2) {
+    const float ninf = fst_bits_f32(0xff800000u);
+    const bool first = m1 >= m2 || m2 != m2;
+    const float M = first ? m1 : m2;
+    const float lo = first ? m2 : m1, slo = first ? s2 : s1, shi = first ? s1 : s2;
+    const float w = lo == M ? 1.0f : fst_expf(lo - M);
+    const float b = slo * w;
+    s1 = M == ninf ? 0.0f : shi + b;
+    m1 = M;
 }
-__device__ __forceinline__ u128 from_limbs(const Limbs& r) {
-    u128 t = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) t += (u128)r.l[q] << (32 * q);
-    return t;
-}
-// Sum over the 16 lanes of each DPP row, in every lane of the row.
-__device__ __forceinline__ u128 row_sum_u128(u128 v) {
-    Limbs r = to_limbs(v);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        r.l[q] += dpp_u64<0xb1>(r.l[q]);   // quad_perm [1,0,3,2]
-        r.l[q] += dpp_u64<0x4e>(r.l[q]);   // quad_perm [2,3,0,1]
-        r.l[q] += dpp_u64<0x124>(r.l[q]);  // row_ror 4
-        r.l[q] += dpp_u64<0x128>(r.l[q]);  // row_ror 8
+// Two rows' merges in one wave, each the halving tree over its 64 chunk
+// partials: lanes 0..31 hold row A's chunks j and j + 32 (tree level 32 is
+// their local merge), lanes 32..63 row B's; levels 16..1 then run in both
+// halves at once (the row-pair swap and DPP row shifts stay inside a half).
+// Results in lanes 0 (row A) and 32 (row B).
+__device__ __forceinline__ void rs_tree_merge2(float& m, float& s, float m_hi, float s_hi) {
+    auto take = [&](float om, float os) { rs_merge(m, s, om, os); };
+    take(m_hi, s_hi);
+    {
+        const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m), false, false);
+        const auto b = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, s), __builtin_bit_cast(uint32_t, s), false, false);
+        take(__builtin_bit_cast(float, (uint32_t)a[1]), __builtin_bit_cast(float, (uint32_t)b[1]));
     }
-    return from_limbs(r);
-}
-// Inclusive prefix sum within each DPP row (row_shr 1, 2, 4, 8; lanes
-// without a source add 0).
-__device__ __forceinline__ u128 row_scan_u128(u128 v) {
-    Limbs r = to_limbs(v);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        r.l[q] += dpp_u64<0x111>(r.l[q]);
-        r.l[q] += dpp_u64<0x112>(r.l[q]);
-        r.l[q] += dpp_u64<0x114>(r.l[q]);
-        r.l[q] += dpp_u64<0x118>(r.l[q]);
-    }
-    return from_limbs(r);
-}
-__device__ __forceinline__ u128 readlane_u128(u128 v, int j) {
-    u128 t = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        t |= (u128)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> (32 * q)), j) << (32 * q);
-    return t;
+    take(fdpp<0x108>(m), fdpp<0x108>(s));  // row_shl 8
+    take(fdpp<0x104>(m), fdpp<0x104>(s));  // row_shl 4
+    take(fdpp<0x102>(m), fdpp<0x102>(s));  // row_shl 2
+    take(fdpp<0x101>(m), fdpp<0x101>(s));  // row_shl 1
 }
 
-// The search arrays of NU values per thread (value u of thread t is element
-// u*kTailThreads + t, zero at or past n): the elements in a[], the sums of
-// 16-element groups in g[] (a DPP row sum: 16 consecutive threads hold 16
-// consecutive elements) and of 16-group super-groups in sg[] (wave 0).
-// Every thread calls it; a barrier at the start and at the end.
-template <int NU>
-__device__ __forceinline__ void tail_sums(const u128 (&vals)[NU], int n, u128* a, u128* g, u128* sg) {
+// Chunk partial of thread-ordered values xv (NaN: no element), rounds of 4.
+template <int NI>
+__device__ __forceinline__ float rs_thread_sum(const float (&xv)[NI][4], float m, float acc) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x = xv[i][e];
+            if (x == x) acc = acc + fst_rel_exp(x, m);
+        }
+    return acc;
+}
+
+// Loads rounds [i0, i0 + NI) of this thread's elements of [b0, b1), scaled;
+// NaN past b1.
+template <int NI>
+__device__ __forceinline__ void rs_load_rounds(const float* __restrict__ row, int V, int b0, int b1, int i0,
+                                               float inv_t, float (&xv)[NI][4]) {
     const int tid = threadIdx.x;
-    __syncthreads();
+    const float nan = __builtin_nanf("");
+    if ((V & 3) == 0) {
+        // 16-byte loads, all issued before any is used (b1 - 4 >= 0: V >= 4)
+        float4 q[NI];
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        const u128 r = row_sum_u128(vals[u]);
-        const int i = u * kTailThreads + tid;
-        a[i] = vals[u];
-        if ((tid & 15) == 0) g[i >> 4] = r;
+        for (int i = 0; i < NI; ++i)
+            q[i] = *reinterpret_cast<const float4*>(row + min(b0 + 4 * tid + 1024 * (i0 + i), b1 - 4));
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int v = b0 + 4 * tid + 1024 * (i0 + i);
+            xv[i][0] = v < b1 ? q[i].x * inv_t : nan;
+            xv[i][1] = v + 1 < b1 ? q[i].y * inv_t : nan;
+            xv[i][2] = v + 2 < b1 ? q[i].z * inv_t : nan;
+            xv[i][3] = v + 3 < b1 ? q[i].w * inv_t : nan;
+        }
+    } else {
+        float q[NI][4];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[i][e] = row[min(b0 + 4 * tid + 1024 * (i0 + i) + e, V - 1)];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[i][e] = b0 + 4 * tid + 1024 * (i0 + i) + e < b1 ? q[i][e] * inv_t : nan;
     }
+}
+
+// REG: the chunk fits the registers (L <= 4096: four rounds), one pass over
+// memory; else two passes (maximum, then the sum from the device cache).
+template <bool REG>
+__global__ __launch_bounds__(256) void acc_rs_stats_kernel(const float* __restrict__ target,
+                                                           const float* __restrict__ draftl, int n_seq, int k,
+                                                           int V, float inv_t, const int32_t* __restrict__ draft,
+                                                           float2* __restrict__ part, float* __restrict__ xsel) {
+    const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n_tgt = n_seq * (k + 1);
+    const float* row = r < n_tgt ? target + (size_t)r * V : draftl + (size_t)(r - n_tgt) * V;
+    int di = r - n_tgt;  // this row's draft token: draft[di] (draft rows s*k+i, target rows s*(k+1)+i, i < k)
+    if (r < n_tgt) {
+        const int s = r / (k + 1), i = r - s * (k + 1);
+        di = i < k ? s * k + i : -1;
+    }
+    const int x_id = di >= 0 ? draft[di] : -1;
+    const int L = rs_chunk_len(V), b0 = min(V, c * L), b1 = min(V, b0 + L);
+    const int nrounds = (L + 1023) / 1024;
+    __shared__ float s_m[4], s_s[4];
+    float m = fst_bits_f32(0xff800000u), acc = 0.0f;
+    constexpr int NI = 4;
+    float xv[NI][4];
+    if (REG) rs_load_rounds<NI>(row, V, b0, b1, 0, inv_t, xv);
+    for (int i0 = 0; i0 < (REG ? NI : nrounds); i0 += NI) {
+        if (!REG) rs_load_rounds<NI>(row, V, b0, b1, i0, inv_t, xv);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, xv[i][e]);  // fmaxf skips NaN
+    }
+    m = wave_fmax(m);
+    if (lane == 0) s_m[wave] = m;
     __syncthreads();
-    if (tid < 64) {
-        const int ng = (n + 15) >> 4;
-        const u128 r = row_sum_u128(tid < ng ? g[tid] : (u128)0);
-        if ((tid & 15) == 0) sg[tid >> 4] = r;
+    m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    if (REG) {
+        acc = rs_thread_sum<NI>(xv, m, acc);
+    } else {
+        for (int i0 = 0; i0 < nrounds; i0 += NI) {
+            rs_load_rounds<NI>(row, V, b0, b1, i0, inv_t, xv);
+            acc = rs_thread_sum<NI>(xv, m, acc);
+        }
     }
+    acc = tree_sum64(acc);
+    if (lane == 0) s_s[wave] = acc;
     __syncthreads();
-}
-
-// One level of the search, called by a whole wave: among v[0..m) (m <= 16),
-// the first j whose running sum, started at run, exceeds t; run becomes the
-// sum before j.  -1 if none.  One LDS load per lane and a DPP row scan.
-__device__ __forceinline__ int tail_level(const u128* v, int m, u128 t, u128& run) {
-    const int lane = threadIdx.x & 63;
-    const u128 own = lane < m ? v[lane] : (u128)0;
-    const u128 pre = row_scan_u128(own) + run;
-    const unsigned long long hit = __ballot(lane < m && pre > t);
-    if (!hit) return -1;
-    const int j = __ffsll((long long)hit) - 1;
-    run = readlane_u128(pre - own, j);
-    return j;
-}
-
-// First index of a[0..n) (n <= 1024) whose inclusive prefix exceeds t
-// (tail_sums done), and in *before the sum of the elements before it; -1 if
-// none.  Called by a whole wave; the results are uniform.
-__device__ __forceinline__ int tail_pick(const u128* a, int n, const u128* g, const u128* sg, u128 t,
-                                         u128* before) {
-    const int ng = (n + 15) >> 4, ns = (ng + 15) >> 4;
-    u128 run = 0;
-    int J = 0;
-    if (ns > 1) {
-        J = tail_level(sg, ns, t, run);
-        if (J < 0) return -1;
+    if (tid == 0) {
+        part[(size_t)r * kRsChunks + c] = make_float2(m, ((s_s[0] + s_s[1]) + s_s[2]) + s_s[3]);
+        if (x_id >= b0 && x_id < b1) xsel[r] = row[x_id] * inv_t;
     }
-    const int Q = tail_level(g + J * 16, min(16, ng - J * 16), t, run);
-    if (Q < 0) return -1;
-    const int q = J * 16 + Q;
-    const int e = tail_level(a + q * 16, min(16, n - q * 16), t, run);
-    if (e < 0) return -1;
-    *before = run;
-    return q * 16 + e;
 }
 
-template <int PER>
-__global__ __launch_bounds__(kTailThreads) void acc_tail_kernel(
+// PRE: every row's race chunk is loaded with the partials (at most kPreRows
+// rows per sequence, race chunks of at most kRsTailThreads elements).
+constexpr int kPreRows = 16;
+template <bool PRE>
+__global__ __launch_bounds__(kRsTailThreads) void acc_rs_tail_kernel(
     const float* __restrict__ target, const float* __restrict__ draftl, int n_seq, int k, int V, float inv_t,
-    const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base, const float* __restrict__ part_max,
-    const int* __restrict__ part_idx, const unsigned long long* __restrict__ part_sum,
+    const int32_t* __restrict__ draft, uint64_t seed, uint64_t seq_base, const float2* __restrict__ part,
     const float* __restrict__ xsel, unsigned long long* __restrict__ tw, int32_t* __restrict__ n_acc,
     int32_t* __restrict__ tokens) {
+    constexpr int NW = kRsTailThreads / 64;
     const int c = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n_tgt = n_seq * (k + 1), NR = 2 * k + 1;
-    const int clen = (V + kTailChunks - 1) / kTailChunks, b0 = min(V, c * clen), b1 = min(V, b0 + clen);
-    unsigned long long* cw = tw + (size_t)s * kTailChunks * 3;  // this sequence's chunk sums
-    // arrival counters: this chunk's group, then the sequence's top counter
-    unsigned long long* cbase = tw + (size_t)n_seq * kTailChunks * 3 + (size_t)s * (kTailArrGroups + 1) * kTailCntStride;
-    int* gcnt = reinterpret_cast<int*>(cbase + (size_t)(c >> 4) * kTailCntStride);
-    int* tcnt = reinterpret_cast<int*>(cbase + (size_t)kTailArrGroups * kTailCntStride);
+    const uint64_t seq = seq_base + (uint64_t)s;
+    unsigned long long* cw = tw + (size_t)s * kRsRaceChunks * 2;  // this sequence's chunk results
+    unsigned long long* cbase =
+        tw + (size_t)n_seq * kRsRaceChunks * 2 + (size_t)s * (kRsArrGroups + 1) * kRsCntStride;
+    int* gcnt = reinterpret_cast<int*>(cbase + (size_t)(c >> 4) * kRsCntStride);
+    int* tcnt = reinterpret_cast<int*>(cbase + (size_t)kRsArrGroups * kRsCntStride);
     auto grow = [&](int rr) { return rr <= k ? s * (k + 1) + rr : n_tgt + s * k + (rr - k - 1); };
-    auto rowp = [&](int rr) {
+    auto rowp = [&](int rr) -> const float* {
         return rr <= k ? target + (size_t)(s * (k + 1) + rr) * V : draftl + (size_t)(s * k + rr - k - 1) * V;
     };
-    __shared__ float s_M[kTailRows];
-    __shared__ int s_any[kTailRows];
-    __shared__ unsigned long long s_S[kTailRows];
-    __shared__ uint32_t s_U2[kTailRows];
-    __shared__ int s_n, s_last, s_chunk;
-    __shared__ u128 s_wtot[kTailWaves], s_rem;
-    __shared__ unsigned long long s_ew[kTailWaves];
-    // the last workgroup's searches (s_sg padded to one 16-lane level)
-    __shared__ u128 s_a[kTailMaxN], s_g[kTailGroups], s_sg[16];
+    __shared__ float s_M[kRsMaxRows], s_S[kRsMaxRows];
+    __shared__ int s_n, s_last;
+    __shared__ unsigned long long s_kr[NW], s_kp[NW];
+    const int Lr = (V + kRsRaceChunks - 1) / kRsRaceChunks, b0 = min(V, c * Lr), b1 = min(V, b0 + Lr);
 
-    TAIL_STAMP(0);
-    // ---- loads, all issued before the first use: the row partials and the
-    // draft tokens' logits first (the decisions wait for these only), then the
-    // chunk of every row (unconditional loads from clamped addresses: no
-    // branch per load; V >= 1)
-    // wave w: rows w, w + 8, w + 16
-    constexpr int kRowsPerWave = (kTailRows + kTailWaves - 1) / kTailWaves;
-    float pm[kRowsPerWave];
-    int pi[kRowsPerWave];
-    unsigned long long ps[kRowsPerWave];
-#pragma unroll
-    for (int q = 0; q < kRowsPerWave; ++q) {
-        const int rr = min(wave + q * kTailWaves, NR - 1);
-        const size_t o = (size_t)grow(rr) * kChunks + lane;
-        pm[q] = part_max[o];
-        pi[q] = part_idx[o];
-        ps[q] = part_sum[o];
-    }
+    // the decision inputs (wave 0, lane i < k: position i), loaded first
+    int x_id = -1;
     float xp = 0.0f, xq = 0.0f;
-    int xt_id = -1;
     if (wave == 0 && lane < k) {
-        xt_id = draft[s * k + lane];
+        x_id = draft[s * k + lane];
         xp = xsel[grow(lane)];
         xq = xsel[grow(k + 1 + lane)];
     }
-    float xv[kTailRows][PER];
+    // every row's (M, S): wave w merges rows 2w and 2w + 1, then 2w + 16, ...
+    // (lane j < 32: chunks j and j + 32 of the first row, lane 32 + j those
+    // of the second), the first pass's loads issued before the row values
+    const int hrow = lane >> 5, hl = lane & 31;
+    float2 pa[2];
+    {
+        const int rr = min(2 * wave + hrow, NR - 1);
+        pa[0] = part[(size_t)grow(rr) * kRsChunks + hl];
+        pa[1] = part[(size_t)grow(rr) * kRsChunks + hl + 32];
+    }
+    // PRE: this thread's element of race chunk c in every row
+    float pre[PRE ? kPreRows : 1];
+    if constexpr (PRE) {
+        const int v = min(b0 + tid, V - 1);
 #pragma unroll
-    for (int rr = 0; rr < kTailRows; ++rr)
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int v = b0 + tid + u * kTailThreads;
-            xv[rr][u] = rowp(min(rr, NR - 1))[min(v, max(b1 - 1, 0))];
-            if (rr >= NR || v >= b1) xv[rr][u] = __builtin_nanf("");
+        for (int rr = 0; rr < kPreRows; ++rr) pre[rr] = rowp(min(rr, NR - 1))[v];
+    }
+    for (int rr0 = 2 * wave; rr0 < NR; rr0 += 2 * NW) {
+        if (rr0 != 2 * wave) {
+            const int rr = min(rr0 + hrow, NR - 1);
+            pa[0] = part[(size_t)grow(rr) * kRsChunks + hl];
+            pa[1] = part[(size_t)grow(rr) * kRsChunks + hl + 32];
         }
-    // the uniforms (no memory operands: computed while the loads are in
-    // flight): U for the decision at position lane, U2 for a resample at
-    // position lane
+        float m = pa[0].x, sm = pa[0].y;
+        rs_tree_merge2(m, sm, pa[1].x, pa[1].y);
+        const int rr = rr0 + hrow;
+        if (hl == 0 && rr < NR) {
+            s_M[rr] = m;
+            s_S[rr] = sm;
+        }
+    }
     uint32_t U = 0;
-    if (wave == 0 && lane <= k) {
-        U = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 0);
-        s_U2[lane] = fst_uniform24(seed, seq_base + (uint64_t)s, (uint32_t)lane, 1);
-    }
-#pragma unroll
-    for (int q = 0; q < kRowsPerWave; ++q) {
-        const int rr = wave + q * kTailWaves;
-        if (rr < NR) {
-            wave_argmax(pm[q], pi[q]);
-            const unsigned long long S = wave_sum_u64(ps[q]);
-            if (lane == 0) {
-                s_M[rr] = pm[q];
-                s_any[rr] = pi[q] >= 0;
-                s_S[rr] = S;
-            }
-        }
-    }
+    if (wave == 0 && lane < k) U = fst_uniform24(seed, seq, (uint32_t)lane, 0);
     __syncthreads();
-    TAIL_STAMP(1);
-    // ---- the decisions (acc_decide_kernel's): lane i < k decides position i
+    // the decisions: lane i < k decides position i; n = the first reject
     if (wave == 0) {
         int ok = 0;
-        if (lane < k && xt_id >= 0 && xt_id < V) {
-            const int rt = lane, rd = k + 1 + lane;
-            const unsigned long long P = fixed_prob(xp, inv_t, s_M[rt], s_any[rt]);
-            const unsigned long long Q = fixed_prob(xq, inv_t, s_M[rd], s_any[rd]);
-            const u128 lhs = (u128)U * (u128)Q * (u128)s_S[rt];
-            const u128 rhs = ((u128)P * (u128)s_S[rd]) << 24;
+        if (lane < k && x_id >= 0 && x_id < V) {
+            const float St = s_S[lane], Sd = s_S[k + 1 + lane];
+            const float et = rs_e(xp, s_M[lane]), ed = rs_e(xq, s_M[k + 1 + lane]);
+            const float u = (float)U * 5.9604644775390625e-8f;
+            const float lhs = (u * ed) * St, rhs = et * Sd;
             ok = lhs < rhs;
         }
         const unsigned long long rej = __ballot(lane < k && !ok);
         if (lane == 0) s_n = rej ? __ffsll((long long)rej) - 1 : k;
     }
     __syncthreads();
-    const int n = s_n, mode0 = n < k ? 0 : 1, tr = n, dr = min(k + 1 + n, NR - 1);
-    const unsigned long long Sp = s_S[tr], Sq = mode0 == 0 ? s_S[dr] : 0ull;
-    const float mp = s_M[tr], mq = mode0 == 0 ? s_M[dr] : 0.0f;
-    const int ap = s_any[tr], aq = mode0 == 0 ? s_any[dr] : 0;
-    // this thread's values of the sampling rows (uniform branches: no
-    // dynamic register indexing)
-    float xt[PER], xd[PER];
+    const int n = s_n;
+    const bool has_d = n < k;
+    const float Mt = s_M[n], St = s_S[n];
+    const float Md = has_d ? s_M[k + 1 + n] : 0.0f, Sd = has_d ? s_S[k + 1 + n] : 0.0f;
+    const float* trow = rowp(n);
+    const float* drow = has_d ? rowp(k + 1 + n) : trow;
+    // the race over chunk c: keys (bits of E/r << 32 | v) over r > 0 and
+    // (fallback) E/e_t over e_t > 0
+    unsigned long long kr = ~0ull, kp = ~0ull;
+    for (int v = b0 + tid; v < b1; v += kRsTailThreads) {
+        float tv, dv;
+        if constexpr (PRE) {
+            // (uniform selects: no dynamic register indexing)
+            tv = dv = 0.0f;
 #pragma unroll
-    for (int u = 0; u < PER; ++u) xt[u] = xd[u] = 0.0f;
-#pragma unroll
-    for (int rr = 0; rr < kTailRows; ++rr)
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            if (rr == tr) xt[u] = xv[rr][u];
-            if (mode0 == 0 && rr == dr) xd[u] = xv[rr][u];
+            for (int rr = 0; rr < kPreRows; ++rr) {
+                if (rr == n) tv = pre[rr];
+                if (has_d && rr == k + 1 + n) dv = pre[rr];
+            }
+        } else {
+            tv = trow[v];
+            dv = drow[v];
         }
-    // ---- the chunk's residual and target-E sums (exact, any order)
-    u128 ra = 0;
-    unsigned long long ea = 0;
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-        ra += res_of(xt[u], xd[u], inv_t, mp, ap, mq, aq, Sp, Sq, mode0);
-        ea += fixed_prob(xt[u], inv_t, mp, ap);
+        const float et = rs_e(tv * inv_t, Mt);
+        float r = et;
+        if (has_d) {
+            const float ed = rs_e(dv * inv_t, Md);
+            const float a = et * Sd, b = ed * St;
+            r = a - b;
+        }
+        fst_philox_ctr ctr;
+        ctr.v[0] = (uint32_t)v;
+        ctr.v[1] = 0x52430000u ^ (uint32_t)n;
+        ctr.v[2] = (uint32_t)seq;
+        ctr.v[3] = (uint32_t)(seq >> 32);
+        const fst_philox_ctr w = fst_philox4x32_10(ctr, (uint32_t)seed, (uint32_t)(seed >> 32));
+        const float u = (float)(2u * (w.v[0] >> 9) + 1u) * 5.9604644775390625e-8f;
+        const float E = -fst_logf(u);
+        if (r > 0.0f) {
+            const unsigned long long key = ((unsigned long long)fst_f32_bits(E / r) << 32) | (uint32_t)v;
+            kr = key < kr ? key : kr;
+        }
+        if (et > 0.0f) {
+            const unsigned long long key = ((unsigned long long)fst_f32_bits(E / et) << 32) | (uint32_t)v;
+            kp = key < kp ? key : kp;
+        }
     }
-    ra = wave_sum_u128(ra);
-    ea = wave_sum_u64(ea);
+    kr = wave_min_u64(kr);
+    kp = wave_min_u64(kp);
     if (lane == 0) {
-        s_wtot[wave] = ra;
-        s_ew[wave] = ea;
+        s_kr[wave] = kr;
+        s_kp[wave] = kp;
     }
     __syncthreads();
-    TAIL_STAMP(2);
+    // publish the chunk's keys and count in
     if (tid == 0) {
-        u128 rt = 0;
-        unsigned long long et = 0;
-        for (int w = 0; w < kTailWaves; ++w) {
-            rt += s_wtot[w];
-            et += s_ew[w];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            kr = s_kr[w] < kr ? s_kr[w] : kr;
+            kp = s_kp[w] < kp ? s_kp[w] : kp;
         }
-        st_coherent_u64(cw + (size_t)c * 3, (unsigned long long)rt);
-        st_coherent_u64(cw + (size_t)c * 3 + 1, (unsigned long long)(rt >> 64));
-        st_coherent_u64(cw + (size_t)c * 3 + 2, et);
+        st_coherent_u64(cw + 2 * c, kr);
+        st_coherent_u64(cw + 2 * c + 1, kp);
         publish_wait();
-        // the 16th arrival of a group of 16 chunks counts the group in at the
-        // top; the last group to arrive makes this workgroup the last one
-        // (both counters are left at zero)
         int last = 0;
         if (__hip_atomic_fetch_add(gcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 15) {
             __hip_atomic_store(gcnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = __hip_atomic_fetch_add(tcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kTailArrGroups - 1;
+            last = __hip_atomic_fetch_add(tcnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kRsArrGroups - 1;
             if (last) __hip_atomic_store(tcnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         s_last = last;
     }
     __syncthreads();
-    TAIL_STAMP(3);
-    if (!s_last) {
-        TAIL_FLUSH(0, 4);
-        return;
+    if (!s_last) return;
+    // the last workgroup: the minimum keys over the chunks give the token
+    unsigned long long a = ~0ull, b = ~0ull;
+    if (tid < kRsRaceChunks) {
+        a = ld_coherent_u64(cw + 2 * tid);
+        b = ld_coherent_u64(cw + 2 * tid + 1);
     }
-
-    // ---- the last workgroup: the chunk holding the inverse-CDF target
-    // (thread i < kTailChunks holds chunk i's sums)
-    u128 cv[1] = {0};
-    unsigned long long ce = 0;
-    if (tid < kTailChunks) {
-        const unsigned long long lo = ld_coherent_u64(cw + (size_t)tid * 3), hi = ld_coherent_u64(cw + (size_t)tid * 3 + 1);
-        cv[0] = ((u128)hi << 64) | (u128)lo;
-        ce = ld_coherent_u64(cw + (size_t)tid * 3 + 2);
-    }
-    tail_sums(cv, kTailChunks, s_a, s_g, s_sg);
-    TAIL_STAMP(4);
-    constexpr int kNs = (kTailChunks + 255) / 256;
-    u128 tot = 0;
-#pragma unroll
-    for (int j = 0; j < kNs; ++j) tot += s_sg[j];
-    int mode = mode0;
-    if (mode == 0 && tot == 0) {
-        // the residual is identically zero: sample from the target row
-        mode = 1;
-        cv[0] = (u128)ce;
-        tail_sums(cv, kTailChunks, s_a, s_g, s_sg);
-        tot = 0;
-#pragma unroll
-        for (int j = 0; j < kNs; ++j) tot += s_sg[j];
-    }
-    if (wave == 0) {
-        int chunk = -1;
-        u128 rem = 0;
-        if (tot != 0) {
-            const u128 tg = ((u128)s_U2[n] * tot) >> 24;
-            u128 before;
-            chunk = tail_pick(s_a, kTailChunks, s_g, s_sg, tg, &before);
-            if (chunk >= 0) rem = tg - before;  // tg minus the mass before the chunk
-        }
-        if (lane == 0) {
-            s_chunk = chunk;
-            s_rem = rem;
-        }
+    a = wave_min_u64(a);
+    b = wave_min_u64(b);
+    __syncthreads();
+    if (lane == 0) {
+        s_kr[wave] = a;
+        s_kp[wave] = b;
     }
     __syncthreads();
-    TAIL_STAMP(5);
-    const int cc = s_chunk;
-    int tok = 0;  // (as the chain: no crossing in the chunk gives token 0)
-    if (cc >= 0) {
-        // ---- the token: the first v of the chunk (index order) whose
-        // inclusive prefix exceeds the remaining target
-        const int cb0 = min(V, cc * clen), cb1 = min(V, cb0 + clen);
-        float a[PER], b[PER];
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int v = min(cb0 + tid + u * kTailThreads, cb1 - 1);
-            a[u] = rowp(tr)[v];
-            b[u] = mode == 0 ? rowp(dr)[v] : 0.0f;
-        }
-        u128 rv[PER];
-#pragma unroll
-        for (int u = 0; u < PER; ++u)
-            rv[u] = cb0 + tid + u * kTailThreads < cb1 ? res_of(a[u], b[u], inv_t, mp, ap, mq, aq, Sp, Sq, mode)
-                                                      : (u128)0;
-        tail_sums(rv, cb1 - cb0, s_a, s_g, s_sg);
-        TAIL_STAMP(6);
-        if (wave == 0) {
-            u128 before;
-            const int e = tail_pick(s_a, cb1 - cb0, s_g, s_sg, s_rem, &before);
-            if (e >= 0) tok = cb0 + e;
-        }
-    }
     if (tid == 0) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            a = s_kr[w] < a ? s_kr[w] : a;
+            b = s_kp[w] < b ? s_kp[w] : b;
+        }
+        const int tok = a != ~0ull ? (int)(uint32_t)a : (b != ~0ull ? (int)(uint32_t)b : 0);
         for (int i = 0; i < n; ++i) tokens[s * (k + 1) + i] = draft[s * k + i];
         tokens[s * (k + 1) + n] = tok;
         for (int i = n + 1; i <= k; ++i) tokens[s * (k + 1) + i] = -1;
         n_acc[s] = n;
     }
-    TAIL_STAMP(7);
-    TAIL_FLUSH(0, 8);
-}
-
-
-// The tail launch applies when every row's chunk fits the registers.
-static bool tail_fits(int k, int V) {
-    return k >= 0 && 2 * k + 1 <= kTailRows && (V + kTailChunks - 1) / kTailChunks <= kTailPerMax * kTailThreads;
 }
 
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
                               int n_seq, int k, int V, const int32_t* draft, float inv_t,
-                              uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,
-                              void* ws, bool tail) {
+                              uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens, void* ws) {
     AccWs w = carve(ws, n_seq, k);
-    const int n_tgt = n_seq * (k + 1);
-    const int R = n_tgt + n_seq * k;
-    const bool use_tail = tail && tail_fits(k, V);
-    hipLaunchKernelGGL(acc_stats_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
-                       inv_t, w.part_max, w.part_idx);
-    hipLaunchKernelGGL(acc_sums_kernel, dim3(kChunks, R), dim3(256), 0, st, target, draft_logits, n_tgt, V,
-                       inv_t, w.part_max, w.part_idx, w.part_sum, draft, k, use_tail ? w.xsel : nullptr);
-    if (use_tail) {
-        // one element per thread while the chunks fit, else two
-        auto kern = (V + kTailChunks - 1) / kTailChunks <= kTailThreads ? acc_tail_kernel<1> : acc_tail_kernel<2>;
-        hipLaunchKernelGGL(kern, dim3(kTailChunks, n_seq), dim3(kTailThreads), 0, st, target, draft_logits, n_seq,
-                           k, V, inv_t, draft, seed, seq_base, w.part_max, w.part_idx, w.part_sum, w.xsel, w.tail,
-                           n_acc, tokens);
-        return;
-    }
-    hipLaunchKernelGGL(acc_decide_kernel, dim3(n_seq), dim3(64 * kDecideWaves), 0, st, target, draft_logits, n_seq, k, V,
-                       inv_t, draft, seed, seq_base, w.part_max, w.part_idx, w.part_sum, w.dec, n_acc,
-                       tokens);
-    hipLaunchKernelGGL(acc_res_chunks_kernel, dim3(kChunks, n_seq), dim3(kProbThreads), 0, st, target, draft_logits,
-                       n_seq, k, V, inv_t, w.part_max, w.part_idx, w.dec, w.part_res);
-    hipLaunchKernelGGL(acc_sample_kernel, dim3(n_seq), dim3(kProbThreads), 0, st, target, draft_logits, n_seq, k, V,
-                       inv_t, w.part_max, w.part_idx, w.part_sum, w.dec, w.part_res, tokens);
+    const int R = n_seq * (2 * k + 1);
+    const int L = ((V + kRsChunks - 1) / kRsChunks + 3) & ~3;
+    if (L <= 4096)
+        hipLaunchKernelGGL(acc_rs_stats_kernel<true>, dim3(kRsChunks, R), dim3(256), 0, st, target, draft_logits,
+                           n_seq, k, V, inv_t, draft, w.rs_part, w.xsel);
+    else
+        hipLaunchKernelGGL(acc_rs_stats_kernel<false>, dim3(kRsChunks, R), dim3(256), 0, st, target, draft_logits,
+                           n_seq, k, V, inv_t, draft, w.rs_part, w.xsel);
+    const bool pre = 2 * k + 1 <= kPreRows && (V + kRsRaceChunks - 1) / kRsRaceChunks <= kRsTailThreads;
+    auto tail = pre ? acc_rs_tail_kernel<true> : acc_rs_tail_kernel<false>;
+    hipLaunchKernelGGL(tail, dim3(kRsRaceChunks, n_seq), dim3(kRsTailThreads), 0, st, target, draft_logits, n_seq,
+                       k, V, inv_t, draft, seed, seq_base, w.rs_part, w.xsel, w.tail, n_acc, tokens);
 }
 
 // ---------------------------------------------------------- sample_token
@@ -1192,6 +657,16 @@ void launch_accept_stochastic(hipStream_t st, const float* target, const float* 
 // E = 2^32 (the maxima) first, then 4 levels of 8-bit digits with LDS
 // histograms of the digit's mass, then the rank among equal values in index
 // order.  Integer sums: any reduction order gives the same result.
+// E = floor(exp(x*inv_t - max) * 2^32) of one logit (0 for NaN or a row
+// without numbers), the fixed-point mass of sample_token.
+__device__ __forceinline__ unsigned long long fixed_prob(float x, float inv_t, float mx, int any) {
+    const float l = x * inv_t;
+    if (!any || l != l) return 0ull;
+    if (l == mx) return 4294967296ull;
+    const float d = l - mx;
+    if (d != d) return 0ull;
+    return (unsigned long long)fst_prob_fixed(d);
+}
 constexpr int kSampleThreads = 1024;
 constexpr unsigned long long kOne32 = 4294967296ull;
 

@@ -936,7 +936,7 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
     const float inv_t = 1.0f / temperature;
     ctx->mark_begin();
     fst::launch_accept_stochastic(ctx->st, d_target, d_draft_logits, n_seq, k, V, d_draft, inv_t, seed, seq_base,
-                                  d_n_acc, d_tokens, ctx->acc_ws, ctx->fused);
+                                  d_n_acc, d_tokens, ctx->acc_ws);
     ctx->mark("accept_stochastic");
     FST_HIP_TRY(hipGetLastError());
     return FST_OK;

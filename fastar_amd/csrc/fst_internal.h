@@ -164,6 +164,25 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
     return min(min(a, b), min(c, d));
 }
 
+// Sum of the 64 lanes' values in the canonical halving-tree order, as lane 0
+// sees it: p[j] += p[j + off] for off = 32, 16, ..., 1.  The cross-row steps
+// use gfx950's permlane32/16 swaps (lanes j < 32 read lane j + 32; lanes of
+// even rows read the next row), the in-row steps DPP row shifts (lane j reads
+// lane j + off).  Only lane 0's result is meaningful.
+__device__ __forceinline__ float tree_sum64(float acc) {
+    const uint32_t a = __builtin_bit_cast(uint32_t, acc);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+    acc = acc + __builtin_bit_cast(float, (uint32_t)s32[1]);
+    const uint32_t b = __builtin_bit_cast(uint32_t, acc);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    acc = acc + __builtin_bit_cast(float, (uint32_t)s16[1]);
+    acc = acc + __builtin_bit_cast(float, dpp<0x108>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 8
+    acc = acc + __builtin_bit_cast(float, dpp<0x104>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 4
+    acc = acc + __builtin_bit_cast(float, dpp<0x102>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 2
+    acc = acc + __builtin_bit_cast(float, dpp<0x101>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 1
+    return acc;
+}
+
 // Wave-wide max of a uint64 held by every lane, in every lane: DPP within
 // each row of 16 lanes, then gfx950's row-pair and half swaps (with both
 // operands x, permlane16_swap returns {x of the even row, x of the odd row}
@@ -415,11 +434,11 @@ uint32_t accept_scratch_epoch(int device);
 // carry that call's epoch and may sit at offsets later shapes do not
 // rewrite; clearing at every wrap keeps them from matching a reused epoch.
 void accept_scratch_clear(hipStream_t st, void* words);
-// Rejection sampling: row maxima and sums, then (tail, when the rows' chunks
-// fit) one launch for the decisions, residual and pick, else three.
+// Rejection sampling in two launches: every row's chunk softmax partials,
+// then the decisions, the exponential race and the token.
 void launch_accept_stochastic(hipStream_t st, const float* target, const float* draft_logits,
                               int n_seq, int k, int V, const int32_t* draft, float inv_t,
                               uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens,
-                              void* ws, bool tail);
+                              void* ws);
 
 }  // namespace fst

@@ -35,25 +35,6 @@
 namespace fst {
 
 
-// Sum of the 64 lanes' values in the canonical halving-tree order, as lane 0
-// sees it: p[j] += p[j + off] for off = 32, 16, ..., 1.  The cross-row steps
-// use gfx950's permlane32/16 swaps (lanes j < 32 read lane j + 32; lanes of
-// even rows read the next row), the in-row steps DPP row shifts (lane j reads
-// lane j + off).  Only lane 0's result is meaningful.
-__device__ __forceinline__ float tree_sum64(float acc) {
-    const uint32_t a = __builtin_bit_cast(uint32_t, acc);
-    const auto s32 = __builtin_amdgcn_permlane32_swap(a, a, false, false);
-    acc = acc + __builtin_bit_cast(float, (uint32_t)s32[1]);
-    const uint32_t b = __builtin_bit_cast(uint32_t, acc);
-    const auto s16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-    acc = acc + __builtin_bit_cast(float, (uint32_t)s16[1]);
-    acc = acc + __builtin_bit_cast(float, dpp<0x108>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 8
-    acc = acc + __builtin_bit_cast(float, dpp<0x104>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 4
-    acc = acc + __builtin_bit_cast(float, dpp<0x102>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 2
-    acc = acc + __builtin_bit_cast(float, dpp<0x101>(__builtin_bit_cast(uint32_t, acc)));  // row_shl 1
-    return acc;
-}
-
 // ---------------------------------------------------------------- router
 
 // Router logits: one wave per (expert, TPW tokens); lane j owns the

@@ -164,12 +164,48 @@ FST_HD fst_philox_ctr fst_philox4x32_10(fst_philox_ctr c, uint32_t k0, uint32_t 
 
 /* 24-bit uniform integer U (u = U / 2^24 in [0,1)) for acceptance sampling.
  * Counter = (position, stream, seq_lo, seq_hi), key = (seed_lo, seed_hi).
- * stream 0: accept/reject uniform u_i; stream 1: resampling uniform u'_i. */
+ * stream 0: the accept/reject uniform u_i; stream 2: sample_token's draw. */
 FST_HD uint32_t fst_uniform24(uint64_t seed, uint64_t seq, uint32_t pos, uint32_t stream) {
     fst_philox_ctr c;
     c.v[0] = pos; c.v[1] = stream; c.v[2] = (uint32_t)seq; c.v[3] = (uint32_t)(seq >> 32);
     fst_philox_ctr r = fst_philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
     return r.v[0] >> 8;
+}
+
+/* ---- rejection sampling: softmax partials and the exponential race ----
+ * e(x | m): the softmax weight of x relative to a maximum m: 0 for x = -inf,
+ * exactly 1 at the maximum, fst_expf(x - m) otherwise (callers skip NaN). */
+FST_HD float fst_rel_exp(float x, float m) {
+    const float ninf = fst_bits_f32(0xff800000u);
+    return x == ninf ? 0.0f : (x == m ? 1.0f : fst_expf(x - m));
+}
+/* Merge of two softmax partials (m = maximum, s = sum of e(x | m)):
+ * M = max(m1, m2), S = s1*e(m1 | M) + s2*e(m2 | M), two rounded products
+ * and one rounded sum (symmetric in its arguments, bit for bit); both
+ * empty (-inf) stays (-inf, 0). */
+FST_HD void fst_softmax_merge(float* m1, float* s1, float m2, float s2) {
+    const float ninf = fst_bits_f32(0xff800000u);
+    const float M = *m1 > m2 ? *m1 : m2;
+    if (M == ninf) {
+        *m1 = ninf;
+        *s1 = 0.0f;
+        return;
+    }
+    const float w1 = *m1 == M ? 1.0f : fst_expf(*m1 - M);
+    const float w2 = m2 == M ? 1.0f : fst_expf(m2 - M);
+    const float a = *s1 * w1, b = s2 * w2;
+    *m1 = M;
+    *s1 = a + b;
+}
+/* Uniform in (0, 1) for element v of the exponential race at position pos:
+ * Philox counter (v, 0x52430000 ^ pos, seq_lo, seq_hi), key (seed_lo,
+ * seed_hi), first word w; u = (2*(w >> 9) + 1) * 2^-24, exact in binary32
+ * (distinct from fst_uniform24's counters, whose second word is < 3). */
+FST_HD float fst_race_uniform(uint64_t seed, uint64_t seq, uint32_t pos, uint32_t v) {
+    fst_philox_ctr c;
+    c.v[0] = v; c.v[1] = 0x52430000u ^ pos; c.v[2] = (uint32_t)seq; c.v[3] = (uint32_t)(seq >> 32);
+    fst_philox_ctr r = fst_philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    return (float)(2u * (r.v[0] >> 9) + 1u) * 5.9604644775390625e-8f;
 }
 
 /* Fixed-point probability mass: E = floor(exp(l - max) * 2^32), l - max <= 0.

@@ -18,10 +18,15 @@
  *                       float64 restatement on small shapes.
  *   fo_router           brute-force tie/bias/hash cases; logits vs float64 sum
  *                       (within fp32 error); top-k vs numpy lexsort.
- *   fo_accept_*         planted accepted lengths 0..k, argmax ties and NaN,
- *                       brute-force rational arithmetic for the stochastic
- *                       decision and residual sampling on small vocabularies;
- *                       Philox known-answer vectors from Salmon et al.
+ *   fo_accept_greedy    planted accepted lengths 0..k, argmax ties and NaN.
+ *   fo_accept_stochastic closed forms (p = q accepts every draft; q(x) = 0
+ *                       accepts iff p(x) > 0; p(x) = 0 always rejects; a
+ *                       residual with one positive entry draws it), row
+ *                       statistics vs float64 softmax, the decision against
+ *                       a float64 u < p/q away from ties, and chi-square tests
+ *                       of the accept rate min(1, p/q) and of the drawn
+ *                       tokens against norm(max(0, p - q)) and p; Philox
+ *                       known-answer vectors from Salmon et al.
  */
 #include "fst_oracle.h"
 #include "../include/fst_exact_math.h"
@@ -364,17 +369,6 @@ static uint64_t fo_softmax_fixed(const float* row, int V, float inv_t, uint64_t*
     return s;
 }
 
-static int fo_sample_fixed(const uint64_t* E, uint64_t S, int V, uint32_t U) {
-    if (S == 0) return 0;
-    u128 target = ((u128)U * (u128)S) >> 24;
-    u128 c = 0;
-    for (int v = 0; v < V; ++v) {
-        c += E[v];
-        if (c > target) return v;
-    }
-    return V - 1;
-}
-
 /* Speculative rejection sampling (Leviathan et al. 2023; Chen et al. 2023).
  * The reference has no stochastic acceptance (its only sampler draws from an
  * unseeded mt19937, src/fst_engine.cpp:4522-4523), so this build defines it:
@@ -386,51 +380,146 @@ static int fo_sample_fixed(const uint64_t* E, uint64_t S, int V, uint32_t U) {
  *   by inverse CDF with target = (U'_i * sum) >> 24, U'_i from stream 1
  *   (if that residual is all zero, sample from p_i instead);
  *   if all k accepted, the bonus is sampled from p_k with U'_k. */
+/* Rejection-sampling softmax statistics of one row of logits l (x = l*inv_t),
+ * in the device's fixed order: the row is cut into FO_RS_CHUNKS = 64 chunks of
+ * L = ceil(V/64) rounded up to a multiple of 4 elements; a chunk's maximum
+ * m_c (NaN skipped) and s_c = sum e(x | m_c), summed by 256 "threads" (thread
+ * t adds elements b0 + 4t + 1024i + {0,1,2,3}, i = 0, 1, ..., in that order),
+ * the 64 partials of each group of 64 threads by the halving tree p[j] +=
+ * p[j+off] (off = 32..1), then the four group sums left to right; the row's
+ * (M, S) merges the 64 chunk partials (fst_softmax_merge) by the same
+ * halving tree. */
+#define FO_RS_CHUNKS 64
+static int fo_rs_chunk_len(int V) { return ((V + FO_RS_CHUNKS - 1) / FO_RS_CHUNKS + 3) & ~3; }
+
+static void fo_rs_chunk(const float* row, int V, float inv_t, int c, float* m_out, float* s_out) {
+    const int L = fo_rs_chunk_len(V);
+    const int b0 = c * L < V ? c * L : V, b1 = b0 + L < V ? b0 + L : V;
+    float m = -INFINITY;
+    for (int v = b0; v < b1; ++v) {
+        const float x = row[v] * inv_t;
+        if (x == x && x > m) m = x;
+    }
+    float part[256];
+    for (int t = 0; t < 256; ++t) {
+        float acc = 0.0f;
+        for (int base = b0 + 4 * t; base < b1; base += 1024)
+            for (int e = 0; e < 4; ++e) {
+                const int v = base + e;
+                if (v >= b1) break;
+                const float x = row[v] * inv_t;
+                if (x == x) acc = acc + fst_rel_exp(x, m);
+            }
+        part[t] = acc;
+    }
+    float ws[4];
+    for (int w = 0; w < 4; ++w) {
+        float a[64];
+        for (int j = 0; j < 64; ++j) a[j] = part[64 * w + j];
+        for (int off = 32; off >= 1; off >>= 1)
+            for (int j = 0; j < off; ++j) a[j] = a[j] + a[j + off];
+        ws[w] = a[0];
+    }
+    *m_out = m;
+    *s_out = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+}
+
+void fo_rs_row_stats(const float* row, int V, float inv_t, float* M, float* S) {
+    float lm[FO_RS_CHUNKS], ls[FO_RS_CHUNKS];
+    for (int c = 0; c < FO_RS_CHUNKS; ++c) fo_rs_chunk(row, V, inv_t, c, &lm[c], &ls[c]);
+    for (int off = 32; off >= 1; off >>= 1)
+        for (int j = 0; j < off; ++j) fst_softmax_merge(&lm[j], &ls[j], lm[j + off], ls[j + off]);
+    *M = lm[0];
+    *S = ls[0];
+}
+
+/* e(x | M) of a scaled logit (0 for NaN, -inf, or a row with no number):
+ * the softmax numerator, p(x) = e / S. */
+static float fo_rs_e(float x, float M) {
+    if (x != x || M == -INFINITY) return 0.0f;
+    return fst_rel_exp(x, M);
+}
+
+float fo_race_uniform(uint64_t seed, uint64_t seq, uint32_t pos, uint32_t v) {
+    return fst_race_uniform(seed, seq, pos, v);
+}
+
+/* The exponential race at position pos over the residual in numerator form,
+ * r_v = e_t(v)*S_d - e_d(v)*S_t = (p_v - q_v)*S_t*S_d (two rounded products,
+ * one rounded difference; for the bonus position r_v = e_t(v)): the token is
+ * the v minimising E_v / r_v over r_v > 0 (E_v = -log u_v, u_v =
+ * fst_race_uniform(seed, seq, pos, v); ties to the lower index), i.e. a draw
+ * from norm(max(0, p - q)); with no r_v > 0, the race over e_t(v) > 0 (a draw
+ * from p); with neither, token 0.  Keys compare as (float bits << 32 | v),
+ * which orders non-negative floats, then indices. */
+int fo_rs_race(const float* trow, const float* drow, int V, float inv_t, float Mt, float St, float Md, float Sd,
+               uint64_t seed, uint64_t seq, uint32_t pos) {
+    uint64_t best_r = ~0ull, best_p = ~0ull;
+    for (int v = 0; v < V; ++v) {
+        const float et = fo_rs_e(trow[v] * inv_t, Mt);
+        float r = et;
+        if (drow) {
+            const float ed = fo_rs_e(drow[v] * inv_t, Md);
+            const float a = et * Sd, b = ed * St;
+            r = a - b;
+        }
+        const float E = -fst_logf(fst_race_uniform(seed, seq, pos, (uint32_t)v));
+        if (r > 0.0f) {
+            const uint64_t key = ((uint64_t)fst_f32_bits(E / r) << 32) | (uint32_t)v;
+            if (key < best_r) best_r = key;
+        }
+        if (et > 0.0f) {
+            const uint64_t key = ((uint64_t)fst_f32_bits(E / et) << 32) | (uint32_t)v;
+            if (key < best_p) best_p = key;
+        }
+    }
+    if (best_r != ~0ull) return (int)(uint32_t)best_r;
+    if (best_p != ~0ull) return (int)(uint32_t)best_p;
+    return 0;
+}
+
+/* Speculative rejection sampling (Leviathan et al. 2023; Chen et al. 2023).
+ * The reference has no stochastic acceptance (its only sampler draws from an
+ * unseeded mt19937, src/fst_engine.cpp:4522-4523; its HF script samples by
+ * Gumbel-max, scripts/hf_gen_ref.py:632-639), so this build defines it:
+ *   p_i = softmax(t_i/T), q_i = softmax(d_i/T) from the rows' (M, S)
+ *   (fo_rs_row_stats) and numerators e(x | M);
+ *   u_i = U_i / 2^24, U_i = fst_uniform24(seed, seq, i, 0);
+ *   accept x_i iff (u_i * e_d(x_i)) * S_t < e_t(x_i) * S_d, i.e. u < p/q
+ *   with both sides multiplied by S_t*S_d (a draft row with no number
+ *   rejects);
+ *   on the first reject at i, the token is drawn from norm(max(0, p_i - q_i))
+ *   by the exponential race fo_rs_race(pos = i) (from p_i if that residual is
+ *   all zero); if all k are accepted, the bonus is the race over p_k. */
 int fo_accept_stochastic(const float* target, const float* draft_logits, int k, int V,
                          const int32_t* draft, float temperature, uint64_t seed, uint64_t seq,
                          int32_t* n_acc, int32_t* tokens) {
     if (!(temperature > 0.0f)) return 1;
-    float inv_t = 1.0f / temperature;
-    uint64_t* P = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
-    uint64_t* Q = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
+    const float inv_t = 1.0f / temperature;
     int n = 0;
     for (; n < k; ++n) {
-        uint64_t Sp = fo_softmax_fixed(target + (size_t)n * V, V, inv_t, P);
-        uint64_t Sq = fo_softmax_fixed(draft_logits + (size_t)n * V, V, inv_t, Q);
-        int x = draft[n];
-        if (x < 0 || x >= V) { free(P); free(Q); return 1; }
-        uint32_t U = fst_uniform24(seed, seq, (uint32_t)n, 0);
-        u128 lhs = (u128)U * (u128)Q[x] * (u128)Sp;
-        u128 rhs = ((u128)P[x] * (u128)Sq) << 24;
-        if (lhs < rhs) { tokens[n] = x; continue; }
-        /* reject: residual resample */
-        uint32_t U2 = fst_uniform24(seed, seq, (uint32_t)n, 1);
-        u128 R = 0;
-        for (int v = 0; v < V; ++v) {
-            u128 a = (u128)P[v] * Sq, b = (u128)Q[v] * Sp;
-            if (a > b) R += a - b;
+        const int x = draft[n];
+        if (x < 0 || x >= V) return 1;
+        float Mt, St, Md, Sd;
+        fo_rs_row_stats(target + (size_t)n * V, V, inv_t, &Mt, &St);
+        fo_rs_row_stats(draft_logits + (size_t)n * V, V, inv_t, &Md, &Sd);
+        const float et = fo_rs_e(target[(size_t)n * V + x] * inv_t, Mt);
+        const float ed = fo_rs_e(draft_logits[(size_t)n * V + x] * inv_t, Md);
+        const float u = (float)fst_uniform24(seed, seq, (uint32_t)n, 0) * 5.9604644775390625e-8f;
+        const float lhs = (u * ed) * St, rhs = et * Sd;
+        if (lhs < rhs) {
+            tokens[n] = x;
+            continue;
         }
-        int tok;
-        if (R == 0) tok = fo_sample_fixed(P, Sp, V, U2);
-        else {
-            u128 tgt = ((u128)U2 * R) >> 24;
-            u128 c = 0;
-            tok = V - 1;
-            for (int v = 0; v < V; ++v) {
-                u128 a = (u128)P[v] * Sq, b = (u128)Q[v] * Sp;
-                if (a > b) c += a - b;
-                if (c > tgt) { tok = v; break; }
-            }
-        }
-        tokens[n] = tok;
+        tokens[n] = fo_rs_race(target + (size_t)n * V, draft_logits + (size_t)n * V, V, inv_t, Mt, St, Md, Sd,
+                               seed, seq, (uint32_t)n);
         *n_acc = n;
-        free(P); free(Q);
         return 0;
     }
-    uint64_t Sp = fo_softmax_fixed(target + (size_t)k * V, V, inv_t, P);
-    tokens[k] = fo_sample_fixed(P, Sp, V, fst_uniform24(seed, seq, (uint32_t)k, 1));
+    float Mt, St;
+    fo_rs_row_stats(target + (size_t)k * V, V, inv_t, &Mt, &St);
+    tokens[k] = fo_rs_race(target + (size_t)k * V, NULL, V, inv_t, Mt, St, 0.0f, 0.0f, seed, seq, (uint32_t)k);
     *n_acc = k;
-    free(P); free(Q);
     return 0;
 }
 

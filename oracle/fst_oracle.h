@@ -56,6 +56,12 @@ int fo_accept_greedy(const float* target, int k, int V, const int32_t* draft,
 int fo_accept_stochastic(const float* target, const float* draft_logits, int k, int V,
                          const int32_t* draft, float temperature, uint64_t seed, uint64_t seq,
                          int32_t* n_acc, int32_t* tokens);
+/* Rejection sampling's pieces, for pinning tests: a row's softmax (M, S) in the
+ * device's fixed order, and the exponential race of one position. */
+void fo_rs_row_stats(const float* row, int V, float inv_t, float* M, float* S);
+int fo_rs_race(const float* trow, const float* drow /* nullable */, int V, float inv_t, float Mt, float St,
+               float Md, float Sd, uint64_t seed, uint64_t seq, uint32_t pos);
+float fo_race_uniform(uint64_t seed, uint64_t seq, uint32_t pos, uint32_t v);
 
 /* RMSNorm (src/fst_engine.cpp:89-91 with RNE): out = bf16((x * r) * w),
  * r = (float)(1/sqrt(ss/d + eps)), ss in double in the fixed order of fst_oracle.c. */

@@ -45,6 +45,10 @@ def lib():
         "fo_sample_token": (C.c_int, [P, C.c_int, C.c_float, C.c_float, C.c_uint64, C.c_uint64, P]),
         "fo_accept_greedy": (C.c_int, [P, C.c_int, C.c_int, P, P, P]),
         "fo_accept_stochastic": (C.c_int, [P, P, C.c_int, C.c_int, P, C.c_float, C.c_uint64, C.c_uint64, P, P]),
+        "fo_rs_row_stats": (None, [P, C.c_int, C.c_float, P, P]),
+        "fo_rs_race": (C.c_int, [P, P, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float,
+                                 C.c_uint64, C.c_uint64, C.c_uint32]),
+        "fo_race_uniform": (C.c_float, [C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint32]),
         "fo_rmsnorm": (None, [P, P, C.c_int, C.c_int, C.c_float, P]),
         "fo_q4k_linear": (C.c_int, [P, C.c_int, C.c_int, P, C.c_int, P]),
         "fo_hc_mix": (None, [P, P, C.c_int, C.c_int, P]),
@@ -183,6 +187,25 @@ def accept_stochastic(target, draft_logits, draft, temperature, seed, seq):
                                     C.byref(n), _p(tok))
     assert rc == 0
     return n.value, tok[: n.value + 1]
+
+
+def rs_row_stats(row, inv_t=1.0):
+    """fo_rs_row_stats: a row's softmax (max, sum) in the device's fixed order."""
+    row = np.ascontiguousarray(row, np.float32)
+    M, S = C.c_float(), C.c_float()
+    lib().fo_rs_row_stats(_p(row), row.shape[-1], inv_t, C.byref(M), C.byref(S))
+    return M.value, S.value
+
+
+def rs_race(trow, drow, inv_t, seed, seq, pos):
+    """fo_rs_race with the rows' statistics computed by rs_row_stats (drow None: the bonus race)."""
+    trow = np.ascontiguousarray(trow, np.float32)
+    Mt, St = rs_row_stats(trow, inv_t)
+    if drow is None:
+        return lib().fo_rs_race(_p(trow), None, trow.shape[-1], inv_t, Mt, St, 0.0, 0.0, seed, seq, pos)
+    drow = np.ascontiguousarray(drow, np.float32)
+    Md, Sd = rs_row_stats(drow, inv_t)
+    return lib().fo_rs_race(_p(trow), _p(drow), trow.shape[-1], inv_t, Mt, St, Md, Sd, seed, seq, pos)
 
 
 def rmsnorm(x, w, eps=1e-6):

@@ -3,7 +3,6 @@ closed forms, independent implementations and brute force.  No GPU needed."""
 import json
 import math
 import os
-from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -275,63 +274,144 @@ def test_argmax_reference_semantics(oracle):
     assert oracle.argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
 
 
-def _fixed_probs(oracle, row, inv_t):
-    l = (row.astype(np.float32) * np.float32(inv_t)).astype(np.float32)
-    mx = np.max(l)
-    E = []
-    for v in l:
-        if v == mx:
-            E.append(2 ** 32)
-        else:
-            e = np.float32(oracle.lib().fo_expf(float(np.float32(v - mx))))
-            E.append(int(np.float32(e * np.float32(4294967296.0))))
-    return E
+def _softmax64(row, inv_t=1.0):
+    x = (np.asarray(row, np.float32) * np.float32(inv_t)).astype(np.float64)
+    x = np.where(np.isnan(x), -np.inf, x)
+    e = np.exp(x - x.max())
+    return e / e.sum()
 
 
-@pytest.mark.parametrize("seed", range(40))
-def test_stochastic_bruteforce_small_vocab(oracle, seed):
-    """Rational-arithmetic restatement of the decision and the residual draw."""
+@pytest.mark.parametrize("V", [1, 5, 1000, 129280, 262147])
+def test_rs_row_stats_vs_float64(oracle, V):
+    """(M, S): M is the row's exact maximum, S = sum exp(x - M) within fp32
+    summation error of the float64 sum, at vocabularies that leave chunks
+    empty (V < 256), partial (V % 4 != 0) and several float4s long."""
+    rng = np.random.default_rng(V)
+    row = rng.normal(0, 2, V).astype(np.float32)
+    for inv_t in (1.0, 0.5):
+        M, S = oracle.rs_row_stats(row, inv_t)
+        x = (row * np.float32(inv_t)).astype(np.float32)
+        assert M == float(x.max())
+        ref = np.exp(x.astype(np.float64) - float(x.max())).sum()
+        assert abs(S - ref) <= 2e-6 * ref, (S, ref)
+
+
+def test_rs_row_stats_special_values(oracle):
+    row = np.array([1.0, np.nan, -np.inf, 2.0, np.nan], np.float32)
+    M, S = oracle.rs_row_stats(row)
+    assert M == 2.0 and abs(S - (1.0 + math.exp(-1.0))) < 1e-6
+    M, S = oracle.rs_row_stats(np.full(7, np.nan, np.float32))
+    assert M == -math.inf and S == 0.0
+    M, S = oracle.rs_row_stats(np.array([0.0, np.inf, 3.0, np.inf], np.float32))
+    assert M == math.inf and S == 2.0                  # each +inf weighs 1, the rest 0
+    M, S = oracle.rs_row_stats(np.zeros(1000, np.float32))
+    assert M == 0.0 and S == 1000.0                    # exact: 1000 ones in any order
+
+
+def test_race_uniform_range_and_mean(oracle):
+    u = np.array([oracle.lib().fo_race_uniform(9, 3, 2, v) for v in range(20000)])
+    assert u.min() > 0.0 and u.max() < 1.0
+    assert abs(u.mean() - 0.5) < 0.01
+    # a different position or sequence gives other uniforms
+    assert oracle.lib().fo_race_uniform(9, 3, 2, 5) != oracle.lib().fo_race_uniform(9, 3, 3, 5)
+    assert oracle.lib().fo_race_uniform(9, 3, 2, 5) != oracle.lib().fo_race_uniform(9, 4, 2, 5)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_stochastic_closed_forms(oracle, seed):
     rng = np.random.default_rng(seed)
-    k, V = 3, 5
-    t = rng.normal(0, 1.5, (k + 1, V)).astype(np.float32)
-    d = rng.normal(0, 1.5, (k, V)).astype(np.float32)
+    k, V = 5, 300
+    t = rng.normal(0, 2, (k + 1, V)).astype(np.float32)
     draft = rng.integers(0, V, k).astype(np.int32)
-    n, tok = oracle.accept_stochastic(t, d, draft, 1.0, seed, 5)
-    emitted = []
-    for i in range(k + 1):
-        P = _fixed_probs(oracle, t[i], 1.0)
-        Sp = sum(P)
-        if i == k:
-            u2 = oracle.uniform24(seed, 5, i, 1)
-            target = (u2 * Sp) >> 24
-            c = 0
-            for v in range(V):
-                c += P[v]
-                if c > target:
-                    emitted.append(v)
-                    break
-            break
-        Q = _fixed_probs(oracle, d[i], 1.0)
-        Sq = sum(Q)
-        x = int(draft[i])
-        u = Fraction(oracle.uniform24(seed, 5, i, 0), 2 ** 24)
-        if u * Fraction(Q[x], Sq) < Fraction(P[x], Sp):
-            emitted.append(x)
+    # p == q: u < 1 = p/q accepts every draft; the bonus is the race over p_k
+    n, tok = oracle.accept_stochastic(t, t[:k], draft, 1.0, seed, 3)
+    assert n == k and list(tok[:k]) == list(draft)
+    assert tok[k] == oracle.rs_race(t[k], None, 1.0, seed, 3, k)
+    # q(x) = 0 (draft logit -inf at x): accepted whenever p(x) > 0
+    d = t[:k].copy()
+    d[np.arange(k), draft] = -np.inf
+    n, tok = oracle.accept_stochastic(t, d, draft, 1.0, seed, 4)
+    assert n == k
+    # p(x) = 0 at position 2 (target logit -inf): rejected there, and the
+    # resampled token has p > q
+    d = rng.normal(0, 2, (k, V)).astype(np.float32)
+    t2 = t.copy()
+    t2[:2] = d[:2]                                    # positions 0, 1: p == q, accepted
+    t2[2, draft[2]] = -np.inf
+    n, tok = oracle.accept_stochastic(t2, d, draft, 1.0, seed, 5)
+    assert n == 2 and tok[2] != draft[2]
+    p, q = _softmax64(t2[2]), _softmax64(d[2])
+    assert p[tok[2]] > q[tok[2]]
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_race_single_positive_residual(oracle, seed):
+    """Only v* has p > q (the target raises one logit of the draft row), so
+    norm(max(0, p - q)) is the point mass at v*, whatever the uniforms."""
+    rng = np.random.default_rng(100 + seed)
+    V = 1000
+    d = rng.normal(0, 2, V).astype(np.float32)
+    vs = int(rng.integers(0, V))
+    t = d.copy()
+    t[vs] += 3.0
+    for pos in range(4):
+        assert oracle.rs_race(t, d, 1.0, seed, 7, pos) == vs
+    # an identically zero residual falls back to the race over p
+    assert oracle.rs_race(d, d, 1.0, seed, 7, 1) == oracle.rs_race(d, None, 1.0, seed, 7, 1)
+
+
+def test_stochastic_decision_vs_float64(oracle):
+    """The accept decision u*q(x) < p(x) agrees with float64 u < p/q wherever
+    the two sides are not within float rounding of each other."""
+    rng = np.random.default_rng(5)
+    V, checked = 2000, 0
+    for s in range(300):
+        t = rng.normal(0, 1, (2, V)).astype(np.float32)
+        d = rng.normal(0, 1, (1, V)).astype(np.float32)
+        x = int(rng.integers(0, V))
+        n, tok = oracle.accept_stochastic(t, d, np.array([x], np.int32), 1.0, s, 0)
+        p, q = _softmax64(t[0])[x], _softmax64(d[0])[x]
+        u = oracle.uniform24(s, 0, 0, 0) / 2 ** 24
+        if abs(u * q - p) <= 1e-5 * p:
             continue
-        R = [max(0, P[v] * Sq - Q[v] * Sp) for v in range(V)]
-        u2 = oracle.uniform24(seed, 5, i, 1)
-        tot = sum(R) if sum(R) > 0 else Sp
-        vals = R if sum(R) > 0 else P
-        target = (u2 * tot) >> 24
-        c = 0
-        for v in range(V):
-            c += vals[v]
-            if c > target:
-                emitted.append(v)
-                break
-        break
-    assert n == len(emitted) - 1
-    assert list(tok) == emitted
+        checked += 1
+        assert (n == 1) == (u * q < p)
+    assert checked > 250
+
+
+def test_race_draws_the_normalized_residual(oracle):
+    """Chi-square of 6000 races (different sequence numbers) against
+    norm(max(0, p - q)) on V = 6."""
+    p = np.array([0.30, 0.05, 0.25, 0.10, 0.20, 0.10])
+    q = np.array([0.10, 0.20, 0.10, 0.30, 0.05, 0.25])
+    t, d = np.log(p).astype(np.float32), np.log(q).astype(np.float32)
+    r = np.maximum(p - q, 0)
+    r /= r.sum()
+    counts = np.zeros(6)
+    for s in range(6000):
+        counts[oracle.rs_race(t, d, 1.0, 11, s, 0)] += 1
+    assert counts[r == 0].sum() == 0
+    exp = 6000 * r[r > 0]
+    chi2 = float(((counts[r > 0] - exp) ** 2 / exp).sum())
+    assert chi2 < 16.0, (counts, chi2)        # 2 degrees of freedom
+
+
+def test_accept_rate_is_sum_of_min(oracle):
+    """With x ~ q the first draft is accepted with probability sum_x min(p, q)."""
+    V = 5
+    p = np.array([0.35, 0.05, 0.2, 0.3, 0.1])
+    q = np.array([0.1, 0.3, 0.2, 0.15, 0.25])
+    t = np.log(np.stack([p, p])).astype(np.float32)
+    d = np.log(q)[None, :].astype(np.float32)
+    rng = np.random.default_rng(1)
+    n_acc = 0
+    N = 6000
+    for s in range(N):
+        x = int(rng.choice(V, p=q))
+        n, _ = oracle.accept_stochastic(t, d, np.array([x], np.int32), 1.0, 500 + s, 0)
+        n_acc += n
+    a = float(np.minimum(p, q).sum())
+    assert abs(n_acc / N - a) < 4 * math.sqrt(a * (1 - a) / N), (n_acc / N, a)
 
 
 def test_speculative_sampling_preserves_target_distribution(oracle):
