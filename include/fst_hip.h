@@ -158,7 +158,12 @@ int fst_device_error_status(int flags);
 int fst_accept_greedy(fst_ctx* ctx, const float* target, int n_seq, int k, int V,
                       const int32_t* draft, int32_t* n_acc, int32_t* tokens);
 /* Rejection sampling (defined by this build; the reference is greedy-only):
- * draft_logits [n_seq][k][V]; Philox uniforms keyed by (seed, seq_base + s). */
+ * draft_logits [n_seq][k][V]; p = softmax(target/T), q = softmax(draft/T)
+ * from each row's (max, sum) in binary32 in a fixed order; draft x_i is
+ * accepted iff u_i*q(x_i) < p(x_i) (compared as (u*e_q)*S_p < e_p*S_q); the
+ * first rejected position draws from norm(max(0, p - q)), and the bonus
+ * position from p, by an exponential race (argmin of -log(u_v)/r_v, Gumbel-max
+ * sampling); Philox uniforms keyed by (seed, seq_base + s, position). */
 int fst_accept_stochastic(fst_ctx* ctx, const float* target, const float* draft_logits,
                           int n_seq, int k, int V, const int32_t* draft, float temperature,
                           uint64_t seed, uint64_t seq_base, int32_t* n_acc, int32_t* tokens);
@@ -174,13 +179,13 @@ int fst_accept_stochastic_dev(fst_ctx* ctx, const float* d_target, const float* 
  * (the host-pointer entry points then return FST_EHIP); after an asynchronous
  * *_dev call, fst_accept_check on the copied-back n_acc does the same. */
 int fst_set_wait_limit(fst_ctx* ctx, int spins);  /* 0: the default; also bounds the MoE launches' waits (fst_moe_check) */
-/* Router-driven MoE calls (fst_moe_layer[_dev], the verify forward) of at
- * most 8 tokens run gate||up and down as one persistent launch, and
- * rejection sampling runs its decisions, residual sums and pick as one
- * launch (default; k <= 8, V <= 262144); on = 0 selects the separate launch
- * chains.  Both give bit-identical results.  A fused launch whose hand-off wait exceeds the spin limit sets
- * the sticky timeout bit (fst_moe_check and the host-pointer entry points
- * return FST_EHIP). */
+/* MoE calls of at most 32 tokens and 256 routed pairs over 4096 -> 2048 ->
+ * 4096 experts (router-driven or caller-routed) run gate||up and down as one
+ * persistent launch (default); on = 0 selects the
+ * separate launch chain.  Both give the same results (bit for bit where the
+ * chain does not split the gate||up sums over K).  A fused launch whose
+ * hand-off wait exceeds the spin limit sets the sticky timeout bit
+ * (fst_moe_check and the host-pointer entry points return FST_EHIP). */
 int fst_set_fused(fst_ctx* ctx, int on);
 /* Caller-routed calls (fst_moe_ffn_dev, fst_expert_ffn, fst_shared_expert) of
  * one or two tokens over Q4_K experts (hidden and intermediate sizes <= 4096)
