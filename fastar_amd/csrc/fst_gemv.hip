@@ -52,9 +52,8 @@ constexpr int kGvMaxM = 2;          // tokens per call
 constexpr int kGvMaxK = 4096;       // hd and inter bounds (LDS)
 constexpr int kGvMaxPairs = kGvMaxM * kMaxTopK;
 constexpr int kGvMaxSlots = kGvMaxPairs + 1;
-#ifndef FST_GV_SLEEP
-#define FST_GV_SLEEP 4
-#endif
+// s_sleep argument between the down waves' one-lane polls
+constexpr int kGvPollSleep = 4;
 
 
 // s_sleep(8) rounds before the down workgroups' first weight loads, so that
@@ -255,9 +254,6 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
     const int K = dn ? inter : hd, nsb = K >> 8;
     const uint8_t* wbase = ex + (dn ? 2 * proj : up * proj) + (size_t)rt * nsb * 2304;
 
-#if defined(FST_GV_EXP) && FST_GV_EXP == 1
-    if (dn) return;  // measurement build: gate||up workgroups only
-#endif
     // ---- this wave's weight tiles (super-blocks wave, wave + 8)
     WRaw w0[2];
     auto load_weights = [&]() {
@@ -297,7 +293,7 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
                 ready = (uint32_t)(gv >> 32) == a.epoch && (uint32_t)(uv >> 32) == a.epoch;
             }
             if (__builtin_amdgcn_readfirstlane(ready)) break;
-            __builtin_amdgcn_s_sleep(FST_GV_SLEEP);
+            __builtin_amdgcn_s_sleep(kGvPollSleep);
         }
     }
     for (int p0 = 0; p0 < np; p0 += 2) {
@@ -383,9 +379,6 @@ __global__ __launch_bounds__(kGvNT) __attribute__((amdgpu_waves_per_eu(4))) void
         }
     }
     if (timed_out && lane == 0) sticky_or(a.meta, STICKY_TIMEOUT);
-#if defined(FST_GV_EXP) && FST_GV_EXP == 2
-    if (dn) load_weights();
-#endif
     // the wave reads back only what it wrote: LDS keeps one wave's accesses
     // in order, the compiler must too
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
