@@ -56,7 +56,8 @@ def check(oracle, t, d, draft, temp, seed, base, na, ta):
 
 @pytest.mark.parametrize("n_seq,k,V", [(1, 7, 129280), (4, 7, 129280), (2, 3, 1000), (1, 8, 262144),
                                        (3, 1, 4099), (1, 0, 5000), (2, 2, 5), (1, 4, 131072), (1, 4, 131073),
-                                       (2, 15, 3000), (1, 63, 301), (1, 2, (1 << 20) - 2)])
+                                       (2, 15, 3000), (1, 63, 301), (1, 2, (1 << 20) - 2), (64, 7, 5000),
+                                       (16, 31, 777)])
 def test_rejection_sampling_matches_oracle(fa, oracle, acc_ctx, n_seq, k, V):
     ctx = acc_ctx
     t, d, draft = case(fa, 500 + V % 97 + k, n_seq, k, V, special=(V > 4000))
