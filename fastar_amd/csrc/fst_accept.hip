@@ -316,7 +316,7 @@ __device__ __forceinline__ void rs_merge(float& m1, float& s1, float m2, float s
     const bool first = m1 >= m2 || m2 != m2;
     const float M = first ? m1 : m2;
     const float lo = first ? m2 : m1, slo = first ? s2 : s1, shi = first ? s1 : s2;
-    const float w = lo == M ? 1.0f : fst_expf(lo - M);
+    const float w = lo == M ? 1.0f : fst_exp_nonpos(lo - M);
     const float b = slo * w;
     s1 = M == ninf ? 0.0f : shi + b;
     m1 = M;

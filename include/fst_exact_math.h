@@ -102,6 +102,35 @@ FST_HD float fst_expf(float x) {
     return (x != x) ? x : res;
 }
 
+/* e^x for x <= 0 (a logit minus its row's maximum): fst_expf's operations
+ * without its overflow path, so for every x <= 0 (and -inf, and NaN) the
+ * result is fst_expf(x) bit for bit: x below LO gives 0, otherwise the
+ * exponent n = round(x*log2e) lies in [-126, 0] and the scaling is fst_expf's
+ * "mid" product. */
+FST_HD float fst_exp_nonpos(float x) {
+    const float LO = -87.33654022216797f;
+    const float LOG2E = 1.44269502162933349609f;
+    const float LN2_HI = 0.693145751953125f;
+    const float LN2_LO = 1.42860676533018704504e-06f;
+    const float SHIFT = 12582912.0f;
+    const float xc = x < LO ? LO : x;  /* NaN passes through */
+    float t = fmaf(xc, LOG2E, SHIFT);
+    float n = t - SHIFT;
+    float r = fmaf(-n, LN2_HI, xc);
+    r = fmaf(-n, LN2_LO, r);
+    float p = 1.98412698412698412526e-04f;
+    p = fmaf(p, r, 1.38888888888888894189e-03f);
+    p = fmaf(p, r, 8.33333333333333321769e-03f);
+    p = fmaf(p, r, 4.16666666666666643537e-02f);
+    p = fmaf(p, r, 1.66666666666666657415e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (n == n) ? (int)n : 0;
+    const float res = p * fst_pow2i(ni);
+    return (x != x) ? x : (x < LO ? 0.0f : res);
+}
+
 FST_HD float fst_logf(float x) {
     if (x != x) return x;
     if (x < 0.0f) return fst_bits_f32(0x7fc00000u);
@@ -177,7 +206,7 @@ FST_HD uint32_t fst_uniform24(uint64_t seed, uint64_t seq, uint32_t pos, uint32_
  * exactly 1 at the maximum, fst_expf(x - m) otherwise (callers skip NaN). */
 FST_HD float fst_rel_exp(float x, float m) {
     const float ninf = fst_bits_f32(0xff800000u);
-    return x == ninf ? 0.0f : (x == m ? 1.0f : fst_expf(x - m));
+    return x == ninf ? 0.0f : (x == m ? 1.0f : fst_exp_nonpos(x - m));
 }
 /* Merge of two softmax partials (m = maximum, s = sum of e(x | m)):
  * M = max(m1, m2), S = s1*e(m1 | M) + s2*e(m2 | M), two rounded products
@@ -191,8 +220,8 @@ FST_HD void fst_softmax_merge(float* m1, float* s1, float m2, float s2) {
         *s1 = 0.0f;
         return;
     }
-    const float w1 = *m1 == M ? 1.0f : fst_expf(*m1 - M);
-    const float w2 = m2 == M ? 1.0f : fst_expf(m2 - M);
+    const float w1 = *m1 == M ? 1.0f : fst_exp_nonpos(*m1 - M);
+    const float w2 = m2 == M ? 1.0f : fst_exp_nonpos(m2 - M);
     const float a = *s1 * w1, b = s2 * w2;
     *m1 = M;
     *s1 = a + b;

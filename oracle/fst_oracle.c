@@ -54,6 +54,13 @@ int fo_get_threads(void) {
 float fo_fp16_to_f32(uint16_t h) { return fst_fp16_to_f32(h); }
 uint16_t fo_f32_to_bf16(float f) { return fst_f32_to_bf16(f); }
 float fo_expf(float x) { return fst_expf(x); }
+/* fst_exp_nonpos over n values (for the bit-for-bit check against fst_expf). */
+void fo_exp_nonpos_n(const float* x, int n, float* out) {
+    for (int i = 0; i < n; ++i) out[i] = fst_exp_nonpos(x[i]);
+}
+void fo_expf_n(const float* x, int n, float* out) {
+    for (int i = 0; i < n; ++i) out[i] = fst_expf(x[i]);
+}
 float fo_logf(float x) { return fst_logf(x); }
 float fo_sigmoidf(float x) { return fst_sigmoidf(x); }
 float fo_sqrtsoftplusf(float x) { return fst_sqrtsoftplusf(x); }

@@ -85,6 +85,8 @@ void fo_hc_head(const uint16_t* h_hc, const uint16_t* fnT, float scale, const fl
 
 /* exact-math passthroughs for pinning tests */
 float fo_expf(float x);
+void fo_exp_nonpos_n(const float* x, int n, float* out);
+void fo_expf_n(const float* x, int n, float* out);
 float fo_logf(float x);
 float fo_sigmoidf(float x);
 float fo_sqrtsoftplusf(float x);

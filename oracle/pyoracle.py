@@ -57,6 +57,8 @@ def lib():
         "fo_hc_post": (None, [P, P, P, P, C.c_int, C.c_int, P]),
         "fo_hc_head": (None, [P, P, C.c_float, P, C.c_int, C.c_int, C.c_float, P]),
         "fo_expf": (C.c_float, [C.c_float]),
+        "fo_exp_nonpos_n": (None, [P, C.c_int, P]),
+        "fo_expf_n": (None, [P, C.c_int, P]),
         "fo_logf": (C.c_float, [C.c_float]),
         "fo_sigmoidf": (C.c_float, [C.c_float]),
         "fo_sqrtsoftplusf": (C.c_float, [C.c_float]),

@@ -51,6 +51,31 @@ def test_expf_within_2ulp(oracle):
     assert math.isinf(oracle.lib().fo_expf(100.0))
 
 
+def test_exp_nonpos_equals_expf_bit_for_bit(oracle):
+    """fst_exp_nonpos (the softmax weights of rejection sampling) is fst_expf
+    without its overflow path: identical bits for every x <= 0, checked on
+    every float in [-2^-20, 0], around the flush boundary -87.3365 and the
+    2^-126 results, on 4M random values in [-100, 0], and on -0, -inf, NaN."""
+    import ctypes as C
+    rng = np.random.default_rng(11)
+    lo = np.float32(-87.33654022216797)
+    parts = [
+        -rng.random(4_000_000, dtype=np.float32) * np.float32(100.0),
+        np.arange(0x80000000, 0x80000000 + (1 << 20) + 1, dtype=np.uint64).astype(np.uint32).view(np.float32)[:-1],
+        (lo.view(np.uint32) + np.arange(-50000, 50000).astype(np.int64)).astype(np.uint32).view(np.float32),
+        np.linspace(-88.0, -86.5, 200_000, dtype=np.float32),
+        np.array([0.0, -0.0, -np.inf, np.nan, -1e-45, -1e-30, -103.0], np.float32),
+    ]
+    x = np.ascontiguousarray(np.concatenate(parts).astype(np.float32))
+    x = x[(x <= 0) | np.isnan(x)]
+    a = np.empty_like(x)
+    b = np.empty_like(x)
+    P = C.c_void_p
+    oracle.lib().fo_exp_nonpos_n(x.ctypes.data_as(P), x.size, a.ctypes.data_as(P))
+    oracle.lib().fo_expf_n(x.ctypes.data_as(P), x.size, b.ctypes.data_as(P))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_logf_within_2ulp(oracle):
     xs = np.concatenate([np.geomspace(1e-38, 3e38, 100001), np.linspace(0.5, 2.0, 20001)]).astype(np.float32)
     got = np.array([oracle.lib().fo_logf(float(v)) for v in xs], np.float32)
