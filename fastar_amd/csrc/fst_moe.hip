@@ -1545,7 +1545,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 //  - down items: wait until the slot's maxima and h words carry this call's
 //    epoch (coherent loads, bounded polling), then build the slot's whole
 //    fp16 operand (prescale, k-interleave and sub-block sums exactly as
-//    prep_row) in LDS once per item, and stream the down weights with no
+//    prep_row) in LDS once per item (a slot of more than 8 tokens: in two
+//    halves of K), and stream the down weights with no
 //    staging or barrier inside the super-block loop; y rows go out in fp32
 //    for the combine launch.
 // Deadlock freedom: every workgroup finishes its gate||up items (lower
@@ -1555,8 +1556,14 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 // spin_limit polls a workgroup sets meta[META_TIMEOUT] and the sticky
 // timeout bit and carries on (fst_moe_check and the host-pointer entry
 // points turn that into FST_EHIP).
+#ifndef FST_FU_NB
+#define FST_FU_NB 5
+#endif
+#ifndef FST_FU_TD
+#define FST_FU_TD 16
+#endif
 constexpr int kFuT = 16;                          // token rows of a gate||up slot (the MFMA's 16 rows)
-constexpr int kFuTD = 8;                          // token rows of a down slot
+constexpr int kFuTD = FST_FU_TD;                          // token rows of a down slot
 constexpr int kFuMaxM = 32;                       // tokens of one call
 constexpr int kFuMaxPairs = 256;                  // routed (token, expert) pairs of one call
 // slots of one call: every routed pair its own expert, the shared expert,
@@ -1877,8 +1884,9 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         }
     };
 
-    // The down operand of a down slot's rows (at most kFuTD), all nsb_dn
-    // super-blocks, built in LDS from the gate||up items' h words: poll until
+    // The down operand of a down slot's rows (at most kFuTD): all nsb_dn
+    // super-blocks for a slot of at most 8 tokens, else nph super-blocks from
+    // sbase per call (the row maxima read with the first phase), built in LDS from the gate||up items' h words: poll until
     // the words and the row maxima words carry this call's epoch
     // (device-coherent loads, bounded), then convert.  Each polling round issues the
     // maxima loads (Me*aw words) and the first pass of h loads together, so a
@@ -1886,27 +1894,31 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     // its words are in.  Q4_K: the fp16 operand, prescaled, k-interleaved and
     // with the sub-block sums split hi+lo exactly as prep_row builds it;
     // MXFP4: the h words rounded to bf16, 8 per chunk in element order.
-    auto dn_build = [&](int Me, int off) {
-        constexpr int cpr = nsb_dn * 32;  // operand chunks per row
-        constexpr int ostr = kFuOpStride;
-        const int nwd = Me * aw;      // maxima words of the slot's rows
+    auto dn_build = [&](int Me, int off, int sbase, int nph, int ostr) {
+        const int cpr = nph * 32;     // operand chunks per row of this phase
+        const int nwd = sbase == 0 ? Me * aw : 0;  // maxima words of the slot's rows (first phase)
         const int nch = Me * cpr;     // operand chunks of the slot's rows
         int timed_out = 0;
         for (int spin = 0;; ++spin) {
             int ok = 1;
             // maxima words: two per thread and load (16 bytes), so that the
             // 128 words of a row are one wave's (aw == 128)
-            static_assert(kFuTD * aw <= 2 * NT, "one 16-byte maxima load per thread");
-            u4v_t mv;
+            static_assert(kFuTD * aw <= 4 * NT, "two 16-byte maxima loads per thread");
+            u4v_t mv[2];
             if constexpr (!MX) {
-                const int i = 2 * tid;
-                mv = __builtin_amdgcn_raw_buffer_load_b128(ars, (off * aw + (i < nwd ? i : 0)) * 8, 0, 16);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int i = 2 * tid + 2 * NT * k;
+                    mv[k] = (k == 0 || kFuTD * aw > 2 * NT)
+                                ? __builtin_amdgcn_raw_buffer_load_b128(ars, (off * aw + (i < nwd ? i : 0)) * 8, 0, 16)
+                                : u4v_t{0u, 0u, 0u, 0u};
+                }
             }
             for (int base = 0; base < nch; base += NT) {
                 const int qq = base + tid;
                 const bool live = qq < nch;
                 const int tl = live ? qq / cpr : 0, q = qq - (qq / cpr) * cpr;
-                const int sbl = q >> 5, sb = sbl;
+                const int sbl = q >> 5, sb = sbase + sbl;
                 if constexpr (MX) {
                     const int rowb = ((off + tl) * inter + sb * 256 + 8 * (q & 31)) * 8;
                     u4v_t hw[4];
@@ -1931,20 +1943,26 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                     if (base == 0) {
                         // the row maxima -> prescale exponents (the 128 words
                         // of a row are one wave's)
-                        const int i = 2 * tid;
-                        float m = 0.0f;
-                        if (i < nwd) {
-                            // words {max bits, epoch}
-                            if (mv.y != epoch || mv.w != epoch)
-                                ok = 0;
-                            else
-                                m = fmaxf(fst_bits_f32(mv.x), fst_bits_f32(mv.z));
+                        if (sbase == 0) {
+#pragma unroll
+                            for (int k = 0; k < 2; ++k) {
+                                if (k == 1 && kFuTD * aw <= 2 * NT) break;
+                                const int i = 2 * tid + 2 * NT * k;
+                                float m = 0.0f;
+                                if (i < nwd) {
+                                    // words {max bits, epoch}
+                                    if (mv[k].y != epoch || mv[k].w != epoch)
+                                        ok = 0;
+                                    else
+                                        m = fmaxf(fst_bits_f32(mv[k].x), fst_bits_f32(mv[k].z));
+                                }
+                                m = wave_fmax(m);
+                                if (lane == 0 && i < nwd) s_amax[i / aw][0] = m;
+                            }
+                            __syncthreads();
+                            if (tid < Me) s_xs2[tid] = prescale_exp(s_amax[tid][0]);
+                            __syncthreads();
                         }
-                        m = wave_fmax(m);
-                        if (lane == 0 && i < nwd) s_amax[i / aw][0] = m;
-                        __syncthreads();
-                        if (tid < Me) s_xs2[tid] = prescale_exp(s_amax[tid][0]);
-                        __syncthreads();
                     }
                     // words {h bits, epoch}: .y / .w hold the tags
                     if (live && (lo0.y != epoch || lo0.w != epoch || lo1.y != epoch || lo1.w != epoch ||
@@ -2064,7 +2082,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             nph = nsb_gu;
             ostr = kFuOpStride16;
             rs = r & 3;
-        } else if (Me <= 8) {  // (every down slot)
+        } else if (Me <= 8) {  // (every down slot of at most 8 tokens)
             nph = 8;
             ostr = kFuOpStride;
             rs = r & 7;
@@ -2103,8 +2121,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             __syncthreads();
         } else {
             // the slot's down operand, unless the previous item built it
-            const int key = slot | 0x100000;
-            if (key != opb_key) dn_build(Me, off);
+            const int key = multi ? -1 : slot | 0x100000;
+            if (key < 0 || key != opb_key) dn_build(Me, off, 0, nph, ostr);
             opb_key = key;
             __syncthreads();
         }
@@ -2133,7 +2151,10 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 // the operand's next phase (nph is even: the phases start at
                 // even super-blocks, before the last two)
                 __syncthreads();
-                gu_build(std::integral_constant<int, 1>{}, Me, off, sb0, nph, ostr);
+                if (dn)
+                    dn_build(Me, off, sb0, nph, ostr);
+                else
+                    gu_build(std::integral_constant<int, FST_FU_NB>{}, Me, off, sb0, nph, ostr);
                 __syncthreads();
             }
             step(sb0, J0{});
