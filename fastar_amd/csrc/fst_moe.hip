@@ -688,18 +688,15 @@ void launch_bucket_prep(hipStream_t st, const Geometry& g, int M, int use_shared
                        pf_bytes / 16, bucket ? 1 : 0);
 }
 
-// The routing front of a layer call in one launch: workgroups [0, nrb) compute
-// the router logits (router_block), workgroups [nrb, nrb + nprep) prepare the
-// expert operand of each token row (prep_row; Q4_K only), and the router
-// workgroup that finishes last runs the top-k and bucketing of the call
-// (topk_bucket_block) on the logits the others published with device-coherent
-// stores.  `done` counts finished router workgroups; the last one re-arms it.
 // Router logits (workgroups [0, nrb), router_block) and the fp16 expert
 // operand of each token row (workgroups [nrb, nrb + nprep), prep_row; Q4_K
-// only) in one launch; the top-k and bucketing of the call follow in
-// topk_bucket_kernel.  (A single launch whose last router workgroup runs the
-// top-k was measured slower: the hand-off through device-coherent stores and
-// a contended completion counter costs more than the kernel boundary.)
+// only) in one launch.  The top-k and bucketing of the call follow in the
+// gate||up launch's prologue (the fused launch, or the chain's gate||up launch:
+// every workgroup routes the call into LDS), or in topk_bucket_kernel when the
+// layer has more experts than that prologue handles.  (A single launch whose last router
+// workgroup runs the top-k was measured slower: the hand-off through
+// device-coherent stores and a contended completion counter costs more than
+// the kernel boundary.)
 template <int NV, int TPW>
 __global__ __launch_bounds__(256) void router_prep_kernel(const uint4* __restrict__ w_il,
                                                           const uint16_t* __restrict__ h, int M, int K, int E,
