@@ -74,6 +74,12 @@ struct fst_ctx {
     bool nested = false;                     // inside verify_forward: no per-kernel marks
     fst::Scratch s{};
     uint32_t fused_epoch = 0;                // fused MoE launches issued (tags of their h words)
+    // verify forward: the next layer's residual + RMSNorm folded into this
+    // layer's combine (run_moe sets folded when it did so)
+    uint16_t* fold_h = nullptr;
+    const uint16_t* fold_w = nullptr;
+    uint16_t* fold_mn = nullptr;
+    bool folded = false;
     bool fused = true;                       // use the fused launch where it applies
     bool gemv = true;                        // use the small-M launch where it applies
     std::vector<void*> allocs;
@@ -315,13 +321,15 @@ int fst_create(const fst_config* cfg, fst_ctx** out) {
         (rc = x->dalloc(&s.sh_h16, (size_t)T * c.inter_dim)) || (rc = x->dalloc(&s.ys, (size_t)T * hd)) ||
         (rc = x->dalloc(&s.hbuf, (size_t)2 * P * inter)) ||
         (rc = x->dalloc(&s.amaxw, (size_t)P * (inter / 16))) || (rc = x->dalloc(&s.fused_claim, 64)) ||
-        (rc = x->dalloc(&s.gemv_cnt, hd / 16 + 1)))
+        (rc = x->dalloc(&s.gemv_cnt, hd / 16 + 1)) || (rc = x->dalloc(&s.norm_part, (size_t)T * 64)) ||
+        (rc = x->dalloc(&s.norm_cnt, T)))
         return bail(rc);
     if (hipMemsetAsync(s.hbuf, 0, sizeof(unsigned long long) * (size_t)2 * P * inter, x->st) != hipSuccess ||
         hipMemsetAsync(s.amaxw, 0, sizeof(unsigned long long) * (size_t)P * (inter / 16), x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(hand-off words) failed"));
     if (hipMemsetAsync(s.meta, 0, sizeof(int) * fst::META_WORDS, x->st) != hipSuccess ||
-        hipMemsetAsync(s.gemv_cnt, 0, sizeof(int) * (hd / 16 + 1), x->st) != hipSuccess)
+        hipMemsetAsync(s.gemv_cnt, 0, sizeof(int) * (hd / 16 + 1), x->st) != hipSuccess ||
+        hipMemsetAsync(s.norm_cnt, 0, sizeof(int) * T, x->st) != hipSuccess)
         return bail(fail(FST_EHIP, "hipMemsetAsync(meta) failed"));
     x->ev.resize(17);
     x->ev_names.assign(17, "");
@@ -547,6 +555,8 @@ int fst_upload_hash_table(fst_ctx* ctx, int lid, const int32_t* tid2eid) {
 
 // ------------------------------------------------------------ MoE chain
 
+static constexpr float kNormEps = 1e-6f;  // rms_cpu default and the NPU rmsnorm (src/fst_engine.cpp:89)
+
 static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int32_t* d_ids, int do_router,
                    int32_t* d_eids, float* d_wts, int tk, int use_routed, int use_shared, uint16_t* d_out,
                    uint16_t* d_out_routed, uint16_t* d_out_shared) {
@@ -641,7 +651,12 @@ static int run_moe(fst_ctx* ctx, int lid, const uint16_t* d_h, int M, const int3
         // (a bf16 shared expert ran above; its fp32 rows are the combine's
         // shared term).  Router-driven calls: y rows by (token, j); caller
         // routing: y rows by pair, through the pair tables
-        if (do_router)
+        if (do_router && ctx->fold_w && !d_out_routed && !d_out_shared && fst::combine_norm_supported(g)) {
+            // the verify forward's next residual add + RMSNorm in the same launch
+            fst::launch_combine_norm_tj(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, ctx->fold_h,
+                                        ctx->fold_w, kNormEps, ctx->fold_mn);
+            ctx->folded = true;
+        } else if (do_router)
             fst::launch_combine_tj(st, g, M, use_shared, ctx->s, d_wts, sh16 ? ctx->s.ys : nullptr, d_out,
                                    d_out_routed, d_out_shared);
         else
@@ -1059,7 +1074,6 @@ int fst_dequant(fst_ctx* ctx, int codec, const void* blocks, size_t nblocks, flo
 
 // ------------------------------------------------ verify forward (C5 path)
 
-static constexpr float kNormEps = 1e-6f;  // rms_cpu default and the NPU rmsnorm (src/fst_engine.cpp:89)
 
 int fst_upload_norm(fst_ctx* ctx, int lid, const uint16_t* w) {
     if (!ctx) return fail(FST_EINVAL, "null context");
@@ -1356,16 +1370,30 @@ int fst_verify_forward_dev(fst_ctx* ctx, uint16_t* d_h, int M, const int32_t* d_
                                ctx->hc_sb + (size_t)l * 27 + 3, M, hd, ctx->hc_cur, ctx->hc_post, ctx->hc_comb);
             fst::launch_resid_norm(ctx->st, ctx->hc_cur, nullptr, ctx->norms + (size_t)l * hd, M, hd, kNormEps,
                                    nullptr, ctx->mn, nullptr, nullptr);
-        } else {
+        } else if (!ctx->folded) {
             // h += y (previous layer), mn = RMSNorm_l(h); y = MoE_l(mn)
             fst::launch_resid_norm(ctx->st, d_h, l > 0 ? ctx->s.out : nullptr, ctx->norms + (size_t)l * hd, M, hd,
                                    kNormEps, l > 0 ? d_h : nullptr, ctx->mn, nullptr, nullptr);
         }
+        // (the previous layer's combine did this layer's h += y and norm when folded)
+        ctx->folded = false;
+        if (!hc && l + 1 < c.n_layers) {
+            ctx->fold_h = d_h;
+            ctx->fold_w = ctx->norms + (size_t)(l + 1) * hd;
+            ctx->fold_mn = ctx->mn;
+        }
         rc = run_moe(ctx, l, ctx->mn, M, d_input_ids, 1, ctx->s.eids, ctx->s.wts, c.top_k, 1, c.has_shared,
                      ctx->s.out, nullptr, nullptr);
+        ctx->fold_h = nullptr;
+        ctx->fold_w = nullptr;
+        ctx->fold_mn = nullptr;
         if (hc && rc == FST_OK) fst::launch_hc_post(ctx->st, ctx->s.out, d_h, ctx->hc_post, ctx->hc_comb, M, hd);
     }
     ctx->nested = false;
+    ctx->folded = false;
+    ctx->fold_h = nullptr;
+    ctx->fold_w = nullptr;
+    ctx->fold_mn = nullptr;
     if (rc) return rc;
     ctx->mark("layers", true);
     if (hc) {

@@ -83,6 +83,9 @@ struct Scratch {
     unsigned long long* amaxw;  // [P][inter/16]
     int* fused_claim;           // down-pair counter of the fused launch (zeroed by the router launch)
     int* gemv_cnt;              // [hd/16] arrival counters of the small-M launch (zero between calls)
+    // combine with the next layer's residual + RMSNorm folded in (verify forward)
+    unsigned long long* norm_part;  // [T][64] double sums of squares of the row's lane chunks
+    int* norm_cnt;                  // [T] arrival counters (zero between calls)
 };
 
 // Device expert bank: n_layers x (n_experts + 1) packed experts.
@@ -373,6 +376,13 @@ int launch_expert_gemv(hipStream_t st, const Geometry& g, const LayerView& L, in
                        const float* wts, int use_shared, const uint16_t* h, const Scratch& s, uint32_t epoch,
                        int spin_limit, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 // The fused launch's combine: y rows indexed (token, j), j = tk the shared expert.
+// The combine of a verify-forward layer with the next layer's h += out and
+// RMSNorm (weights w) folded in: h is updated in place and normed written,
+// bit-identical to launch_combine_tj followed by launch_resid_norm.
+bool combine_norm_supported(const Geometry& g);
+void launch_combine_norm_tj(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
+                            const float* wts, const float* ys, uint16_t* h, const uint16_t* w, float eps,
+                            uint16_t* normed);
 void launch_combine_tj(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s, const float* wts,
                        const float* ys, uint16_t* out, uint16_t* out_routed, uint16_t* out_shared);
 int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int M, const Scratch& s,

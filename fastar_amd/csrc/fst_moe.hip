@@ -2516,6 +2516,33 @@ __global__ __launch_bounds__(256) void combine_kernel(int M, int hd, int tk, int
 
 // The combine of the fused launch: y rows by (token, j) (j = tk: the shared
 // expert), so every load is issued at once; same arithmetic as combine_kernel.
+// Columns n..n+3 of token t: a = the routed pairs' weighted sum (slot order
+// j = 0..tk-1), vs = the shared term.
+template <int TK>
+__device__ __forceinline__ void combine_tj_cols(int t, int n, int hd, int tk, int use_shared,
+                                                const float* __restrict__ y, const float* __restrict__ ys,
+                                                const float* __restrict__ wts, float4& a, float4& vs) {
+    float w[TK];
+    float4 v[TK];
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+        const int jj = max(min(j, tk - 1), 0);
+        w[j] = tk > 0 ? wts[t * tk + jj] : 0.0f;
+        v[j] = *reinterpret_cast<const float4*>(y + ((size_t)t * (tk + 1) + jj) * hd + n);
+    }
+    vs = use_shared ? *reinterpret_cast<const float4*>((ys ? ys + (size_t)t * hd : y + ((size_t)t * (tk + 1) + tk) * hd) + n)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < TK; ++j) {
+        if (j >= tk) continue;
+        a.x = a.x + w[j] * v[j].x;
+        a.y = a.y + w[j] * v[j].y;
+        a.z = a.z + w[j] * v[j].z;
+        a.w = a.w + w[j] * v[j].w;
+    }
+}
+
 template <int TK>
 __global__ __launch_bounds__(256) void combine_tj_kernel(int M, int hd, int tk, int use_shared,
                                                          const float* __restrict__ y, const float* __restrict__ ys,
@@ -2525,26 +2552,8 @@ __global__ __launch_bounds__(256) void combine_tj_kernel(int M, int hd, int tk, 
     const int t = blockIdx.y;
     const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (t >= M || n >= hd) return;
-    float w[TK];
-    float4 v[TK];
-#pragma unroll
-    for (int j = 0; j < TK; ++j) {
-        const int jj = max(min(j, tk - 1), 0);
-        w[j] = tk > 0 ? wts[t * tk + jj] : 0.0f;
-        v[j] = *reinterpret_cast<const float4*>(y + ((size_t)t * (tk + 1) + jj) * hd + n);
-    }
-    const float4 vs = use_shared ? *reinterpret_cast<const float4*>(
-                                       (ys ? ys + (size_t)t * hd : y + ((size_t)t * (tk + 1) + tk) * hd) + n)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int j = 0; j < TK; ++j) {
-        if (j >= tk) continue;
-        a.x = a.x + w[j] * v[j].x;
-        a.y = a.y + w[j] * v[j].y;
-        a.z = a.z + w[j] * v[j].z;
-        a.w = a.w + w[j] * v[j].w;
-    }
+    float4 a, vs;
+    combine_tj_cols<TK>(t, n, hd, tk, use_shared, y, ys, wts, a, vs);
     auto put = [&](uint16_t* o, const float4& q) {
         if (!o) return;
         const uint32_t lo = fst_f32_to_bf16(q.x) | ((uint32_t)fst_f32_to_bf16(q.y) << 16);
@@ -2560,6 +2569,114 @@ __global__ __launch_bounds__(256) void combine_tj_kernel(int M, int hd, int tk, 
         a.w = a.w + vs.w;
     }
     put(out, a);
+}
+
+// The combine of a verify-forward layer with the next layer's residual add
+// and RMSNorm folded in (process_layer's order, include/fst_engine.h:308:
+// h += out, then mn = RMSNorm(h) for the next layer).  Grid (hd / 1024, M):
+// workgroup c of token t combines columns [1024c, 1024c + 1024) as
+// combine_tj_kernel does, rounds out to bf16, forms x = bf16(h + out) as
+// resid_norm_kernel does, writes x back to h (device-coherent 8-byte stores)
+// and the double sums of squares of its hd/64-element lane chunks (lanes
+// 1024c/(hd/64) on; each chunk summed in order, as resid_norm_kernel's lane
+// does) to npart.  The token's last workgroup to arrive (ncnt, left at zero)
+// runs resid_norm_kernel's halving tree over the 64 partials and writes
+// mn = bf16((x * r) * w) for the whole row: the same bits as combine_tj_kernel
+// followed by resid_norm_kernel.
+template <int TK>
+__global__ __launch_bounds__(256) void combine_norm_tj_kernel(int M, int hd, int tk, int use_shared,
+                                                              const float* __restrict__ y,
+                                                              const float* __restrict__ ys,
+                                                              const float* __restrict__ wts, uint16_t* h,
+                                                              const uint16_t* __restrict__ w, float eps,
+                                                              uint16_t* __restrict__ normed,
+                                                              unsigned long long* npart, int* ncnt) {
+    __shared__ float xl[1024 + 1024 / 64];  // this workgroup's x, one pad word per 64
+    __shared__ int s_last;
+    __shared__ float s_r;
+    auto xi = [](int e) { return e + (e >> 6); };
+    const int t = blockIdx.y, tid = threadIdx.x;
+    const int n = blockIdx.x * 1024 + tid * 4;
+    float4 a, vs;
+    combine_tj_cols<TK>(t, n, hd, tk, use_shared, y, ys, wts, a, vs);
+    if (use_shared) {
+        a.x = a.x + vs.x;
+        a.y = a.y + vs.y;
+        a.z = a.z + vs.z;
+        a.w = a.w + vs.w;
+    }
+    const float av[4] = {a.x, a.y, a.z, a.w};
+    unsigned long long* hrow = reinterpret_cast<unsigned long long*>(h + (size_t)t * hd);
+    const unsigned long long hv = hrow[n / 4];
+    unsigned long long xw = 0ull;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float o = fst_bf16_to_f32(fst_f32_to_bf16(av[k]));
+        const uint16_t xb = fst_f32_to_bf16(fst_bf16_to_f32((uint16_t)(hv >> (16 * k))) + o);
+        xl[xi(4 * tid + k)] = fst_bf16_to_f32(xb);
+        xw |= (unsigned long long)xb << (16 * k);
+    }
+    st_coherent_u64(hrow + n / 4, xw);
+    __syncthreads();
+    const int C = hd / 64, nl = 1024 / C;  // elements per lane chunk, chunks of this workgroup
+    if (tid < nl) {
+        double s = 0.0;
+        for (int i = 0; i < C; ++i) {
+            const double v = (double)xl[xi(tid * C + i)];
+            s = __dadd_rn(s, __dmul_rn(v, v));
+        }
+        st_coherent_u64(npart + (size_t)t * 64 + blockIdx.x * nl + tid, (unsigned long long)__double_as_longlong(s));
+    }
+    publish_wait();
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(ncnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == (int)gridDim.x - 1;
+        if (s_last) __hip_atomic_store(ncnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid < 64) {
+        double s = __longlong_as_double((long long)ld_coherent_u64(npart + (size_t)t * 64 + tid));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) s = s + __shfl_down(s, off, 64);
+        if (tid == 0) s_r = (float)(1.0 / sqrt(s / (double)hd + (double)eps));
+    }
+    __syncthreads();
+    const float r = s_r;
+    for (int q = tid; q < hd / 4; q += 256) {
+        const unsigned long long xq = ld_coherent_u64(hrow + q);
+        const uint2 wq = reinterpret_cast<const uint2*>(w)[q];
+        const uint32_t ww[2] = {wq.x, wq.y};
+        uint32_t o[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t o2 = 0u;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const float x = fst_bf16_to_f32((uint16_t)(xq >> (32 * i + 16 * hh)));
+                o2 |= (uint32_t)fst_f32_to_bf16((x * r) * fst_bf16_to_f32((uint16_t)(ww[i] >> (16 * hh)))) << (16 * hh);
+            }
+            o[i] = o2;
+        }
+        reinterpret_cast<uint2*>(normed + (size_t)t * hd)[q] = make_uint2(o[0], o[1]);
+    }
+}
+
+bool combine_norm_supported(const Geometry& g) { return g.hd % 1024 == 0 && 65536 % g.hd == 0; }
+
+void launch_combine_norm_tj(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s,
+                            const float* wts, const float* ys, uint16_t* h, const uint16_t* w, float eps,
+                            uint16_t* normed) {
+    dim3 grid(g.hd / 1024, M);
+#define FST_CN(T)                                                                                              \
+    hipLaunchKernelGGL(combine_norm_tj_kernel<T>, grid, dim3(256), 0, st, M, g.hd, g.tk, use_shared, s.y, ys, wts, \
+                       h, w, eps, normed, s.norm_part, s.norm_cnt)
+    if (g.tk <= 8)
+        FST_CN(8);
+    else
+        FST_CN(kMaxTopK);
+#undef FST_CN
 }
 
 void launch_combine_tj(hipStream_t st, const Geometry& g, int M, int use_shared, const Scratch& s, const float* wts,
