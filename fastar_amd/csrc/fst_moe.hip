@@ -1540,7 +1540,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 //    device-coherent stores, and per 16 rows the largest |h| of each token
 //    in the same form (the down operand's prescale needs the row maximum);
 //  - down items: wait until the slot's maxima and h words carry this call's
-//    epoch (coherent loads, bounded polling), then build the slot's whole
+//    epoch (coherent loads, bounded polling; for a one-token slot the first
+//    poll's words are loaded during the last super-block of the item before),
+//    then build the slot's whole
 //    fp16 operand (prescale, k-interleave and sub-block sums exactly as
 //    prep_row) in LDS once per item (a slot of more than 8 tokens: in two
 //    halves of K), and stream the down weights with no
@@ -1891,13 +1893,34 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     // its words are in.  Q4_K: the fp16 operand, prescaled, k-interleaved and
     // with the sub-block sums split hi+lo exactly as prep_row builds it;
     // MXFP4: the h words rounded to bf16, 8 per chunk in element order.
-    auto dn_build = [&](int Me, int off, int sbase, int nph, int ostr) {
+    // Each round covers 512 operand chunks as two sub-rounds of 256: thread
+    // tid takes chunk base + 256u + (tid & 255) of sub-round u and half
+    // tid >> 8 of it (the chunk's elements e0..e0+3, or e0+32..e0+35: two
+    // 16-byte h loads), so a one-token slot (256 chunks per row) spreads over
+    // all 512 threads.  Chunk q's 8 lanes of a sub-block sit in consecutive
+    // lanes of one wave, as the sub-block sums' butterflies need.  `pf`: the
+    // first poll of a one-token slot takes sub-round 0's words (pd) and the
+    // maxima (pm) that the item before loaded.
+    u4v_t pd[2] = {u4v_t{0u, 0u, 0u, 0u}, u4v_t{0u, 0u, 0u, 0u}};
+    u4v_t pm = u4v_t{0u, 0u, 0u, 0u};
+    // byte offsets of the two h loads of chunk q (chunk-row tl) and half hf
+    auto h_off = [&](int off, int tl, int q, int sb, int hf) -> int {
+        if constexpr (MX) {
+            return ((off + tl) * inter + sb * 256 + 8 * (q & 31)) * 8 + 32 * hf;
+        } else {
+            const int gg = (q >> 3) & 3, c = q & 7;
+            return ((off + tl) * inter + sb * 256 + 64 * gg + 4 * c) * 8 + 256 * hf;
+        }
+    };
+    auto dn_build = [&](int Me, int off, int sbase, int nph, int ostr, bool pf) {
         const int cpr = nph * 32;     // operand chunks per row of this phase
         const int nwd = sbase == 0 ? Me * aw : 0;  // maxima words of the slot's rows (first phase)
         const int nch = Me * cpr;     // operand chunks of the slot's rows
+        const int hf = tid >> 8, ql = tid & 255;
         int timed_out = 0;
         for (int spin = 0;; ++spin) {
             int ok = 1;
+            const bool use_pf = pf && spin == 0;
             // maxima words: two per thread and load (16 bytes), so that the
             // 128 words of a row are one wave's (aw == 128)
             static_assert(kFuTD * aw <= 4 * NT, "two 16-byte maxima loads per thread");
@@ -1910,85 +1933,87 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                                 ? __builtin_amdgcn_raw_buffer_load_b128(ars, (off * aw + (i < nwd ? i : 0)) * 8, 0, 16)
                                 : u4v_t{0u, 0u, 0u, 0u};
                 }
+                if (use_pf) mv[0] = pm;
             }
-            for (int base = 0; base < nch; base += NT) {
-                const int qq = base + tid;
-                const bool live = qq < nch;
-                const int tl = live ? qq / cpr : 0, q = qq - (qq / cpr) * cpr;
-                const int sbl = q >> 5, sb = sbase + sbl;
-                if constexpr (MX) {
-                    const int rowb = ((off + tl) * inter + sb * 256 + 8 * (q & 31)) * 8;
-                    u4v_t hw[4];
+            for (int base = 0; base < nch; base += 2 * 256) {
+                u4v_t hw[2][2];
+                int tlu[2], qu[2];
+                bool liveu[2];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) hw[i] = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16 * i, 0, 16);
-                    uint32_t o[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (live && (hw[i].y != epoch || hw[i].w != epoch)) ok = 0;
-                        o[i] = (uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].x)) |
-                               ((uint32_t)fst_f32_to_bf16(fst_bits_f32(hw[i].z)) << 16);
-                    }
-                    if (live) opb[tl * ostr + sbl * 36 + (q & 31)] = make_uint4(o[0], o[1], o[2], o[3]);
-                } else {
-                    const int gg = (q >> 3) & 3, c = q & 7;
-                    const int e0 = sb * 256 + 64 * gg + 4 * c;
-                    const int rowb = ((off + tl) * inter + e0) * 8;
-                    const u4v_t lo0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb, 0, 16);
-                    const u4v_t lo1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 16, 0, 16);
-                    const u4v_t hi0 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 256, 0, 16);
-                    const u4v_t hi1 = __builtin_amdgcn_raw_buffer_load_b128(hrs, rowb + 272, 0, 16);
-                    if (base == 0) {
+                for (int u = 0; u < 2; ++u) {
+                    const int qq = base + 256 * u + ql;
+                    liveu[u] = qq < nch;
+                    tlu[u] = liveu[u] ? qq / cpr : 0;
+                    qu[u] = qq - (qq / cpr) * cpr;
+                    const int o = h_off(off, tlu[u], qu[u], sbase + (qu[u] >> 5), hf);
+                    hw[u][0] = __builtin_amdgcn_raw_buffer_load_b128(hrs, o, 0, 16);
+                    hw[u][1] = __builtin_amdgcn_raw_buffer_load_b128(hrs, o + 16, 0, 16);
+                }
+                if (use_pf && base == 0) {
+                    hw[0][0] = pd[0];
+                    hw[0][1] = pd[1];
+                }
+                if constexpr (!MX) {
+                    if (base == 0 && sbase == 0) {
                         // the row maxima -> prescale exponents (the 128 words
                         // of a row are one wave's)
-                        if (sbase == 0) {
 #pragma unroll
-                            for (int k = 0; k < 2; ++k) {
-                                if (k == 1 && kFuTD * aw <= 2 * NT) break;
-                                const int i = 2 * tid + 2 * NT * k;
-                                float m = 0.0f;
-                                if (i < nwd) {
-                                    // words {max bits, epoch}
-                                    if (mv[k].y != epoch || mv[k].w != epoch)
-                                        ok = 0;
-                                    else
-                                        m = fmaxf(fst_bits_f32(mv[k].x), fst_bits_f32(mv[k].z));
-                                }
-                                m = wave_fmax(m);
-                                if (lane == 0 && i < nwd) s_amax[i / aw][0] = m;
+                        for (int k = 0; k < 2; ++k) {
+                            if (k == 1 && kFuTD * aw <= 2 * NT) break;
+                            const int i = 2 * tid + 2 * NT * k;
+                            float m = 0.0f;
+                            if (i < nwd) {
+                                // words {max bits, epoch}
+                                if (mv[k].y != epoch || mv[k].w != epoch)
+                                    ok = 0;
+                                else
+                                    m = fmaxf(fst_bits_f32(mv[k].x), fst_bits_f32(mv[k].z));
                             }
-                            __syncthreads();
-                            if (tid < Me) s_xs2[tid] = prescale_exp(s_amax[tid][0]);
-                            __syncthreads();
+                            m = wave_fmax(m);
+                            if (lane == 0 && i < nwd) s_amax[i / aw][0] = m;
                         }
+                        __syncthreads();
+                        if (tid < Me) s_xs2[tid] = prescale_exp(s_amax[tid][0]);
+                        __syncthreads();
                     }
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const bool live = liveu[u];
+                    const int tl = tlu[u], q = qu[u], sbl = q >> 5;
+                    const u4v_t a = hw[u][0], b = hw[u][1];
                     // words {h bits, epoch}: .y / .w hold the tags
-                    if (live && (lo0.y != epoch || lo0.w != epoch || lo1.y != epoch || lo1.w != epoch ||
-                                 hi0.y != epoch || hi0.w != epoch || hi1.y != epoch || hi1.w != epoch))
-                        ok = 0;
-                    const int sx = s_xs2[tl];
-                    h8_t v;
-                    v[0] = (_Float16)ldexpf(fst_bits_f32(lo0.x), -sx);
-                    v[1] = (_Float16)ldexpf(fst_bits_f32(lo1.x), -sx);
-                    v[2] = (_Float16)ldexpf(fst_bits_f32(lo0.z), -sx);
-                    v[3] = (_Float16)ldexpf(fst_bits_f32(lo1.z), -sx);
-                    v[4] = (_Float16)ldexpf(fst_bits_f32(hi0.x), -sx);
-                    v[5] = (_Float16)ldexpf(fst_bits_f32(hi1.x), -sx);
-                    v[6] = (_Float16)ldexpf(fst_bits_f32(hi0.z), -sx);
-                    v[7] = (_Float16)ldexpf(fst_bits_f32(hi1.z), -sx);
-                    if (live) opb[tl * ostr + sbl * 36 + (q & 31)] = __builtin_bit_cast(uint4, v);
-                    float s0 = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
-                    float s1 = ((float)v[4] + (float)v[5]) + ((float)v[6] + (float)v[7]);
-                    s0 = s0 + fdpp<0xb1>(s0);  // quad_perm [1,0,3,2]
-                    s1 = s1 + fdpp<0xb1>(s1);
-                    s0 = s0 + fdpp<0x4e>(s0);  // quad_perm [2,3,0,1]
-                    s1 = s1 + fdpp<0x4e>(s1);
-                    s0 = s0 + fdpp<0x104>(s0);  // row_shl 4
-                    s1 = s1 + fdpp<0x104>(s1);
-                    if (live && c == 0) {
-                        const _Float16 h0 = (_Float16)s0, h1 = (_Float16)s1;
-                        const _Float16 l0 = (_Float16)(s0 - (float)h0), l1 = (_Float16)(s1 - (float)h1);
-                        const _Float16 z = (_Float16)0.0f;
-                        opb[tl * ostr + sbl * 36 + 32 + gg] = __builtin_bit_cast(uint4, h8_t{h0, h1, l0, l1, z, z, z, z});
+                    if (live && (a.y != epoch || a.w != epoch || b.y != epoch || b.w != epoch)) ok = 0;
+                    uint2* dst = reinterpret_cast<uint2*>(&opb[tl * ostr + sbl * 36 + (q & 31)]) + hf;
+                    if constexpr (MX) {
+                        const uint32_t o0 = (uint32_t)fst_f32_to_bf16(fst_bits_f32(a.x)) |
+                                            ((uint32_t)fst_f32_to_bf16(fst_bits_f32(a.z)) << 16);
+                        const uint32_t o1 = (uint32_t)fst_f32_to_bf16(fst_bits_f32(b.x)) |
+                                            ((uint32_t)fst_f32_to_bf16(fst_bits_f32(b.z)) << 16);
+                        if (live) *dst = make_uint2(o0, o1);
+                    } else {
+                        const int gg = (q >> 3) & 3, c = q & 7;
+                        const int sx = s_xs2[tl];
+                        typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+                        h4_t v;
+                        v[0] = (_Float16)ldexpf(fst_bits_f32(a.x), -sx);
+                        v[1] = (_Float16)ldexpf(fst_bits_f32(b.x), -sx);
+                        v[2] = (_Float16)ldexpf(fst_bits_f32(a.z), -sx);
+                        v[3] = (_Float16)ldexpf(fst_bits_f32(b.z), -sx);
+                        if (live) *dst = __builtin_bit_cast(uint2, v);
+                        float sm = ((float)v[0] + (float)v[1]) + ((float)v[2] + (float)v[3]);
+                        sm = sm + fdpp<0xb1>(sm);  // quad_perm [1,0,3,2]
+                        sm = sm + fdpp<0x4e>(sm);  // quad_perm [2,3,0,1]
+                        sm = sm + fdpp<0x104>(sm);  // row_shl 4
+                        if (live && c == 0) {
+                            // the sum chunk {h0, h1, l0, l1, 0, 0, 0, 0}: half 0
+                            // holds sub-block 2gg's sum (h0, l0), half 1 the other
+                            _Float16* sc = reinterpret_cast<_Float16*>(&opb[tl * ostr + sbl * 36 + 32 + gg]);
+                            const _Float16 hs = (_Float16)sm;
+                            sc[hf] = hs;
+                            sc[2 + hf] = (_Float16)(sm - (float)hs);
+                            if (hf == 0) *reinterpret_cast<uint2*>(sc + 4) = make_uint2(0u, 0u);
+                        }
                     }
                 }
             }
@@ -2058,6 +2083,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     // super-block, so waiting for them waits for nothing else.
     bool pre = false;  // this item's operand arrives in pv
     u4v_t pv = u4v_t{0u, 0u, 0u, 0u};
+    bool pdn = false;  // this down item's first h words and maxima arrive in pd, pm
     int claimed = 0;    // thread 0: the item its last claim returned
     for (int t = blockIdx.x, tn = total; t < total; t = tn) {
         const bool dn = t >= ngu;
@@ -2119,7 +2145,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
         } else {
             // the slot's down operand, unless the previous item built it
             const int key = multi ? -1 : slot | 0x100000;
-            if (key < 0 || key != opb_key) dn_build(Me, off, 0, nph, ostr);
+            if (key < 0 || key != opb_key) dn_build(Me, off, 0, nph, ostr, pdn);
             opb_key = key;
             __syncthreads();
         }
@@ -2149,7 +2175,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 // even super-blocks, before the last two)
                 __syncthreads();
                 if (dn)
-                    dn_build(Me, off, sb0, nph, ostr);
+                    dn_build(Me, off, sb0, nph, ostr, false);
                 else
                     gu_build(std::integral_constant<int, FST_FU_NB>{}, Me, off, sb0, nph, ostr);
                 __syncthreads();
@@ -2168,6 +2194,18 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             pre = tn < ngu && r_sM[nsl] == 1;
             const int tok = r_ptok[r_soff[nsl]];
             pv = reinterpret_cast<const u4v_t*>(fa.A)[tok * (hd / 8) + tid];
+            // a one-token down item of another slot: its first poll's words
+            // (one straight path: clamped to word 0 otherwise)
+            int dsl = 0, dti = 0;
+            if (tn >= ngu && tn < total) dn_map(tn - ngu, dsl, dti);
+            const bool nd = tn >= ngu && tn < total && !(dn && dsl == slot) && dtab_m[dsl] == 1;
+            const int doff = nd ? dtab_o[dsl] : 0;
+            const int ql = tid & 255;
+            const int ho = nd ? h_off(doff, 0, ql, ql >> 5, tid >> 8) : 0;
+            pd[0] = __builtin_amdgcn_raw_buffer_load_b128(hrs, ho, 0, 16);
+            pd[1] = __builtin_amdgcn_raw_buffer_load_b128(hrs, nd ? ho + 16 : 0, 0, 16);
+            if constexpr (!MX) pm = __builtin_amdgcn_raw_buffer_load_b128(ars, nd && 2 * tid < aw ? (doff * aw + 2 * tid) * 8 : 0, 0, 16);
+            pdn = nd;
         }
         __builtin_amdgcn_sched_barrier(0);
         step(nsb - 1, J1{});
