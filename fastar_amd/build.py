@@ -28,6 +28,15 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
+# per-source flags.  fst_moe.hip: no wave-aggregated expansion of atomics.
+# Its atomics run on one lane, and the expansion reads the returned value at
+# once, so the fused launch's work claim (whose value is used one
+# super-block later) would wait there for every load in flight, the weight
+# prefetch included.
+EXTRA_FLAGS = {
+    "fst_moe.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
 
 def _hipcc():
     for c in ("/opt/rocm/bin/hipcc", "hipcc"):
@@ -51,7 +60,7 @@ def build_lib(verbose=False):
     objs = []
     for src in SOURCES:
         obj = os.path.join(objdir, src.replace(".", "_") + ".o")
-        cmd = [_hipcc(), *HIPCC_FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
         out = _run(cmd)
         if verbose and out.strip():
             print(out)

@@ -2084,7 +2084,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     bool pre = false;  // this item's operand arrives in pv
     u4v_t pv = u4v_t{0u, 0u, 0u, 0u};
     bool pdn = false;  // this down item's first h words and maxima arrive in pd, pm
-    int claimed = 0;    // thread 0: the item its last claim returned
+    int claimed = 0;    // thread 0: the counter value its last claim returned
     for (int t = blockIdx.x, tn = total; t < total; t = tn) {
         const bool dn = t >= ngu;
         __syncthreads();  // the previous item's readers of the LDS are done
@@ -2157,13 +2157,14 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             const bool pnx = pf >= nsb;
             w[(j + 1) & 1] = load_w(pnx ? nrs : wrs, (pnx ? pf - nsb : pf) * CHK);
             // each item claims its successor four super-blocks before its
-            // end (issued after this step's loads, so only the publication
-            // one step later waits for it)
-            if (claims && sb == nsb - 4 && tid == 0) claimed = claim_item(G + atomicAdd(fa.claim, 1));
+            // end (issued after this step's loads; its value is first used
+            // at the publication one step later, so the wait for it there
+            // leaves the next step's weight loads in flight)
+            if (claims && sb == nsb - 4 && tid == 0) claimed = atomicAdd(fa.claim, 1);
             __builtin_amdgcn_sched_barrier(0);
             compute(opr + (sb & (nph - 1)) * 36, w[j], acc);
             if (sb == nsb - 3) {
-                if (tid == 0) s_claim = claimed;
+                if (tid == 0) s_claim = claim_item(G + claimed);
                 __syncthreads();  // publishes s_claim
             }
         };
