@@ -29,8 +29,9 @@ HIPCC_FLAGS = [
 ]
 
 # per-source flags.  fst_moe.hip: no wave-aggregated expansion of atomics.
-# Its atomics run on one lane, and the expansion reads the returned value at
-# once, so the fused launch's work claim (whose value is used one
+# Its global atomics run on one lane (its LDS atomics have per-lane addresses,
+# which the expansion does not combine), and the expansion reads the returned
+# value at once, so the fused launch's work claim (whose value is used one
 # super-block later) would wait there for every load in flight, the weight
 # prefetch included.
 EXTRA_FLAGS = {
