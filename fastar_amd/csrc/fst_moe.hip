@@ -1555,6 +1555,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 // spin_limit polls a workgroup sets meta[META_TIMEOUT] and the sticky
 // timeout bit and carries on (fst_moe_check and the host-pointer entry
 // points turn that into FST_EHIP).
+#ifndef FST_FU_NB_SMALL
+#define FST_FU_NB_SMALL 1
+#endif
 #ifndef FST_FU_NB
 #define FST_FU_NB 5
 #endif
@@ -1607,7 +1610,9 @@ __device__ __forceinline__ float row16_fmax(float x) {
 // CODEC 0: Q4_K experts, fp16 operands with power-of-two prescales, fp16
 // MFMA; 1: MXFP4 experts, bf16 operands (the input rows as they are, h
 // rounded to bf16), bf16 MFMA, as in q4k_linear_kernel's MXFP4 path.
-template <int HD, int INTER, int CODEC>
+// SMALL: calls of at most 8 tokens (no slot above 8 tokens: no slot splits,
+// no operand phases for down items, no 9..16-token layout compiled in).
+template <int HD, int INTER, int CODEC, bool SMALL>
 __global__ __launch_bounds__(64 * kFuW) __attribute__((amdgpu_waves_per_eu(FST_Q4K_WAVES_PER_EU))) void
 moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
     constexpr bool MX = CODEC == 1;
@@ -1744,7 +1749,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             };
             // (ns0 <= kFuMaxPairs + 1 <= NT: one slot per thread; without
             // large slots, the down items read the gate||up table)
-            const int big = __syncthreads_or(m0 > kFuTD);
+            const int big = SMALL ? 0 : __syncthreads_or(m0 > kFuTD);
             if (big) {
                 split(kFuTD, d_seid, d_sM, d_soff, &s_nds);
                 if (__syncthreads_or(m0 > kFuT)) split(kFuT, r_seid, r_sM, r_soff, &r_meta[META_N_SLOTS]);
@@ -1929,7 +1934,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
                     const int i = 2 * tid + 2 * NT * k;
-                    mv[k] = (k == 0 || kFuTD * aw > 2 * NT)
+                    mv[k] = (k == 0 || (!SMALL && kFuTD * aw > 2 * NT))
                                 ? __builtin_amdgcn_raw_buffer_load_b128(ars, (off * aw + (i < nwd ? i : 0)) * 8, 0, 16)
                                 : u4v_t{0u, 0u, 0u, 0u};
                 }
@@ -1959,7 +1964,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                         // of a row are one wave's)
 #pragma unroll
                         for (int k = 0; k < 2; ++k) {
-                            if (k == 1 && kFuTD * aw <= 2 * NT) break;
+                            if (k == 1 && (SMALL || kFuTD * aw <= 2 * NT)) break;
                             const int i = 2 * tid + 2 * NT * k;
                             float m = 0.0f;
                             if (i < nwd) {
@@ -2105,7 +2110,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             nph = nsb_gu;
             ostr = kFuOpStride16;
             rs = r & 3;
-        } else if (Me <= 8) {  // (every down slot of at most 8 tokens)
+        } else if (SMALL || Me <= 8) {  // (every down slot of at most 8 tokens)
             nph = 8;
             ostr = kFuOpStride;
             rs = r & 7;
@@ -2175,10 +2180,11 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 // the operand's next phase (nph is even: the phases start at
                 // even super-blocks, before the last two)
                 __syncthreads();
-                if (dn)
-                    dn_build(Me, off, sb0, nph, ostr, false);
-                else
-                    gu_build(std::integral_constant<int, FST_FU_NB>{}, Me, off, sb0, nph, ostr);
+                if (dn) {
+                    if constexpr (!SMALL) dn_build(Me, off, sb0, nph, ostr, false);
+                } else {
+                    gu_build(std::integral_constant<int, SMALL ? FST_FU_NB_SMALL : FST_FU_NB>{}, Me, off, sb0, nph, ostr);
+                }
                 __syncthreads();
             }
             step(sb0, J0{});
@@ -2289,31 +2295,45 @@ int launch_moe_fused(hipStream_t st, const Geometry& g, const LayerView& L, int 
     fa.singles = (int)grid.x;
     // with events: they take the dispatch's own start and end times (the
     // kernel's duration, without the gap to the previous launch)
-#define FST_FU(C)                                                                                               \
+#define FST_FU(C, SM)                                                                                         \
     do {                                                                                                        \
         if (ev0)                                                                                                \
-            hipExtLaunchKernelGGL((moe_fused_kernel<4096, 2048, C>), grid, dim3(64 * kFuW), 0, st, ev0, ev1, 0, fa, \
-                                  ra);                                                                          \
+            hipExtLaunchKernelGGL((moe_fused_kernel<4096, 2048, C, SM>), grid, dim3(64 * kFuW), 0, st, ev0, ev1, 0, \
+                                  fa, ra);                                                                      \
         else                                                                                                    \
-            hipLaunchKernelGGL((moe_fused_kernel<4096, 2048, C>), grid, dim3(64 * kFuW), 0, st, fa, ra);         \
+            hipLaunchKernelGGL((moe_fused_kernel<4096, 2048, C, SM>), grid, dim3(64 * kFuW), 0, st, fa, ra);     \
     } while (0)
-    if (g.hd == 4096 && g.inter == 2048 && g.codec == 1)
-        FST_FU(1);
-    else if (g.hd == 4096 && g.inter == 2048)
-        FST_FU(0);
-    else
+    // (at most 8 tokens: no slot holds more than 8)
+    const bool small = M <= 8;
+    if (g.hd == 4096 && g.inter == 2048 && g.codec == 1) {
+        if (small)
+            FST_FU(1, true);
+        else
+            FST_FU(1, false);
+    } else if (g.hd == 4096 && g.inter == 2048) {
+        if (small)
+            FST_FU(0, true);
+        else
+            FST_FU(0, false);
+    } else {
         return set_error(1, "fused MoE launch: geometry without an instantiation");
+    }
 #undef FST_FU
     return 0;
 }
 
 int moe_fused_occupancy(int codec) {
     int n = 0;
+    // (the smaller of the two instantiations' figures)
+    int n2 = 0;
     const hipError_t e =
-        codec == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, moe_fused_kernel<4096, 2048, 1>, 64 * kFuW, 0)
-                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, moe_fused_kernel<4096, 2048, 0>, 64 * kFuW, 0);
-    if (e != hipSuccess) return 0;
-    return std::min(n, 2);
+        codec == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, moe_fused_kernel<4096, 2048, 1, false>, 64 * kFuW, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, moe_fused_kernel<4096, 2048, 0, false>, 64 * kFuW, 0);
+    const hipError_t e2 =
+        codec == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n2, moe_fused_kernel<4096, 2048, 1, true>, 64 * kFuW, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n2, moe_fused_kernel<4096, 2048, 0, true>, 64 * kFuW, 0);
+    if (e != hipSuccess || e2 != hipSuccess) return 0;
+    return std::min(std::min(n, n2), 2);
 }
 
 bool moe_fused_supported(const Geometry& g, int M) {
