@@ -2205,7 +2205,8 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             // (one straight path: clamped to word 0 otherwise)
             int dsl = 0, dti = 0;
             if (tn >= ngu && tn < total) dn_map(tn - ngu, dsl, dti);
-            const bool nd = tn >= ngu && tn < total && !(dn && dsl == slot) && dtab_m[dsl] == 1;
+            // (not in the 8-token instantiation: measured slower there)
+            const bool nd = !SMALL && tn >= ngu && tn < total && !(dn && dsl == slot) && dtab_m[dsl] == 1;
             const int doff = nd ? dtab_o[dsl] : 0;
             const int ql = tid & 255;
             const int ho = nd ? h_off(doff, 0, ql, ql >> 5, tid >> 8) : 0;
