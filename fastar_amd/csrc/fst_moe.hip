@@ -2181,7 +2181,7 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
                 // even super-blocks, before the last two)
                 __syncthreads();
                 if (dn) {
-                    if constexpr (!SMALL) dn_build(Me, off, sb0, nph, ostr, false);
+                    if constexpr (!SMALL && kFuTD > 8) dn_build(Me, off, sb0, nph, ostr, false);
                 } else {
                     gu_build(std::integral_constant<int, SMALL ? FST_FU_NB_SMALL : FST_FU_NB>{}, Me, off, sb0, nph, ostr);
                 }
