@@ -165,6 +165,29 @@ def test_verify_forward_matches_composition_and_oracle(fa, oracle):
         assert rel_l2(logits, ref) < 1e-2
 
 
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 32])
+def test_verify_forward_folded_norms_match_composition(fa, M):
+    """The verify forward folds each next layer's residual add + RMSNorm into
+    the layer's combine launch; over three layers its logits and final
+    residual equal the composition of rmsnorm_dev, moe_layer and lm_head_dev
+    bit for bit, at token counts on both sides of the fused launch's 8-token
+    instantiation."""
+    L, E, tk, V, seed = 3, 8, 2, 1280, 67
+    _log("verify_forward folded norms M=%d" % M)
+    ctx, routers, norms = _layer_stack_ctx(fa, L, E, tk, V, seed)
+    with ctx:
+        h0 = fa.synth_normal_bf16(seed, 3100 + M, (M, HD))
+        logits, h_fin = ctx.verify_forward(h0)
+        h, y = h0, None
+        for l in range(L):
+            x, mn = _rmsnorm_dev(fa, ctx, l, h, y)
+            out, _, _ = ctx.moe_layer(l, mn)
+            h, y = x, out
+        x, _ = _rmsnorm_dev(fa, ctx, L, h, y)
+        assert np.array_equal(x, h_fin)
+        assert np.array_equal(_lm_head_dev(fa, ctx, x), logits)
+
+
 def test_c5_full_verify_step(fa, oracle):
     """BASELINE C5 at full size: 4 sequences x block 8 (M = 32), 8 layers of
     256 routed + 1 shared Q4_K experts (29 GB resident), RMSNorm eps 1e-6 with
