@@ -1751,8 +1751,14 @@ moe_fused_kernel(FusedArgs fa, RouteArgs ra) {
             // large slots, the down items read the gate||up table)
             const int big = SMALL ? 0 : __syncthreads_or(m0 > kFuTD);
             if (big) {
-                split(kFuTD, d_seid, d_sM, d_soff, &s_nds);
-                if (__syncthreads_or(m0 > kFuT)) split(kFuT, r_seid, r_sM, r_soff, &r_meta[META_N_SLOTS]);
+                if constexpr (kFuT == kFuTD) {
+                    // one table for both: the down items read the split gate||up table
+                    split(kFuT, r_seid, r_sM, r_soff, &r_meta[META_N_SLOTS]);
+                    if (tid == 0) s_nds = -1;
+                } else {
+                    split(kFuTD, d_seid, d_sM, d_soff, &s_nds);
+                    if (__syncthreads_or(m0 > kFuT)) split(kFuT, r_seid, r_sM, r_soff, &r_meta[META_N_SLOTS]);
+                }
             } else if (tid == 0) {
                 s_nds = -1;
             }
