@@ -1531,23 +1531,26 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 // separate gate||up launch, and no operand-prep launch runs between them.
 //  - routing: every workgroup computes the call's top-k and bucketing into
 //    LDS first (topk_bucket_block), as the gate||up launch does;
-//  - gate||up items: the arithmetic of q4k_linear_kernel MODE 1 (8 tokens,
-//    8 waves: 64 gate rows in waves 0..3 paired with the same up rows in
-//    waves 4..7), with the item's whole operand copied into LDS once at its
-//    start (a slot of more than 4 tokens: in two halves of K), so that the
-//    super-block loop has no staging loads and no per-super-block barrier;
+//  - gate||up items: the arithmetic of q4k_linear_kernel MODE 1 (16-row MFMA
+//    tiles, 8 waves: 64 gate rows in waves 0..3 paired with the same up rows
+//    in waves 4..7), with the item's operand copied into LDS at its start
+//    (a slot of 5..8 tokens in two halves of K, of 9..16 tokens in four
+//    quarters, rebuilt between them), so that the super-block loop has no
+//    staging loads and no per-super-block barrier;
 //    the up waves write h = silu(g)*u as 64-bit words {epoch, h bits} with
 //    device-coherent stores, and per 16 rows the largest |h| of each token
 //    in the same form (the down operand's prescale needs the row maximum);
 //  - down items: wait until the slot's maxima and h words carry this call's
 //    epoch (coherent loads, bounded polling; for a one-token slot the first
 //    poll's words are loaded during the last super-block of the item before),
-//    then build the slot's whole
-//    fp16 operand (prescale, k-interleave and sub-block sums exactly as
-//    prep_row) in LDS once per item (a slot of more than 8 tokens: in two
-//    halves of K), and stream the down weights with no
-//    staging or barrier inside the super-block loop; y rows go out in fp32
-//    for the combine launch.
+//    then build the slot's fp16 operand (prescale, k-interleave and sub-block
+//    sums exactly as prep_row) in LDS once per item (a slot of 9..16 tokens
+//    in two halves of K), and stream the down weights with no staging or
+//    barrier inside the super-block loop; y rows go out in fp32 for the
+//    combine launch.
+// Slots of more than 16 tokens run as several 16-token slot groups.  Calls of
+// at most 8 tokens use the SMALL instantiation (no slot above 8 tokens: none
+// of the group and phase paths compiled in).
 // Deadlock freedom: every workgroup finishes its gate||up items (lower
 // indices) before it reaches a down item, and the grid never exceeds the
 // workgroups the device holds at once (two per CU), so every item a down
@@ -1555,6 +1558,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 // spin_limit polls a workgroup sets meta[META_TIMEOUT] and the sticky
 // timeout bit and carries on (fst_moe_check and the host-pointer entry
 // points turn that into FST_EHIP).
+// Build-time settings (measured defaults): operand chunks per thread in
+// flight when a gate||up item rebuilds its operand inside the super-block
+// loop (SMALL and general instantiation), and the token rows of a down slot.
 #ifndef FST_FU_NB_SMALL
 #define FST_FU_NB_SMALL 1
 #endif
@@ -1565,7 +1571,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(MF ?
 #define FST_FU_TD 16
 #endif
 constexpr int kFuT = 16;                          // token rows of a gate||up slot (the MFMA's 16 rows)
-constexpr int kFuTD = FST_FU_TD;                          // token rows of a down slot
+constexpr int kFuTD = FST_FU_TD;                  // token rows of a down slot
 constexpr int kFuMaxM = 32;                       // tokens of one call
 constexpr int kFuMaxPairs = 256;                  // routed (token, expert) pairs of one call
 // slots of one call: every routed pair its own expert, the shared expert,
